@@ -1,0 +1,200 @@
+/*
+ * pkv_codec.h -- C ABI of libpkv_hip.so, the MI355X (gfx950) implementation of
+ * proveKV's codec hot path: turbo-quant TQB1, fib-quant fib_k4_n32 FB2 and the
+ * batched pool / shell rehydrate.
+ *
+ * The library replaces the reference's `gpu-backend` crate
+ * (gpu-backend/src/lib.rs:24-249) underneath the unchanged Rust codec
+ * adapters.  Each entry point below names the reference interface it
+ * replaces.  Conventions:
+ *   - every function returns a pkv status code (PKV_OK == 0); nothing throws
+ *     or aborts across the boundary;
+ *   - device pointers are plain `void*` / `uint8_t*` / `float*` into memory the
+ *     caller allocated on the context's device; the library never frees caller
+ *     memory;
+ *   - `stream` is a hipStream_t passed as `void*` (NULL = the null stream);
+ *     kernels are enqueued on it and completion is the caller's to wait for;
+ *   - profiles are immutable after creation and may be shared across threads.
+ * Wire formats are byte-identical to the reference: FB2
+ * (fib-quant/src/codec.rs:195-320) and TQB1 (turbo-quant/src/wire.rs:267-398).
+ */
+#ifndef PKV_CODEC_H
+#define PKV_CODEC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+enum pkv_status {
+    PKV_OK = 0,
+    PKV_ERR_INVALID_ARG = 1,        /* ProveKvError::InvalidPolicy / bad call  */
+    PKV_ERR_DIM_MISMATCH = 2,       /* ProveKvError::DimensionMismatch          */
+    PKV_ERR_OOM = 3,                /* GpuError::OutOfMemory                    */
+    PKV_ERR_DEVICE = 4,             /* GpuError::CudaError (HIP runtime error)  */
+    PKV_ERR_CORRUPT_PAYLOAD = 5,    /* DecompressionFailed / CorruptPayload     */
+    PKV_ERR_UNSUPPORTED = 6,        /* profile outside what the kernels handle  */
+    PKV_ERR_NONFINITE_INPUT = 7,    /* NonFiniteInput                           */
+    PKV_ERR_ZERO_NORM = 8,          /* FibQuantError::ZeroNorm                  */
+    PKV_ERR_NORM_UNREPRESENTABLE = 9, /* encode_norm: not a finite positive f16 */
+    PKV_ERR_EMPTY_BATCH = 10,       /* "empty batch" (wire encode_batch)        */
+    PKV_ERR_CAPACITY = 11,          /* caller buffer too small                  */
+    PKV_ERR_NONFINITE_CODE = 12     /* turbo encode: radius / residual not finite */
+};
+
+/* Returns a static, human-readable name for a status code. */
+const char* pkv_status_string(int status);
+
+/* Detail of the first failure of a batched call. */
+typedef struct pkv_error {
+    int32_t status;      /* pkv_status                                  */
+    int32_t segment;     /* failing segment, -1 when not segment-bound  */
+    uint64_t index;      /* failing vector inside the segment           */
+} pkv_error;
+
+/* ---------------------------------------------------------------- context */
+typedef struct pkv_ctx pkv_ctx;
+typedef struct pkv_profile pkv_profile;
+
+/* Replaces GpuContext::init / is_available (gpu-backend/src/lib.rs:41-58):
+ * binds a context to HIP device `device` (an index, 0 = first). */
+int pkv_ctx_create(int device, pkv_ctx** out);
+void pkv_ctx_destroy(pkv_ctx* ctx);
+/* 1 if a gfx950 device is usable, 0 otherwise (never errors). */
+int pkv_device_available(void);
+
+/* ---------------------------------------------------------------- profiles */
+enum pkv_codec_kind { PKV_CODEC_TURBO = 1, PKV_CODEC_FIB = 2 };
+enum pkv_turbo_mode { PKV_TURBO_POLAR_ONLY = 0, PKV_TURBO_POLAR_WITH_QJL = 1 };
+enum pkv_radii_codec { PKV_RADII_F32 = 0, PKV_RADII_LOG_U8 = 1 };
+enum pkv_dtype { PKV_F32 = 0, PKV_BF16 = 1 };
+
+/* Replaces TurboQuantizer::new_with_mode (turbo-quant/src/turbo.rs:124-188)
+ * as built by TurboQuantAdapter (proveKV/src/codec.rs:249-250): FastHadamard
+ * signs and the QJL matrix are derived from `seed` exactly like the reference
+ * and kept resident on the device.  dim must be 64 or 128. */
+int pkv_turbo_profile_create(pkv_ctx* ctx, uint32_t dim, uint32_t bits, uint32_t projections,
+                             uint64_t seed, int mode, pkv_profile** out);
+/* Same, with the constants supplied by the caller (a Rust host that already
+ * holds `FastHadamardRotation::signs` and `QjlQuantizer::projection_matrix`);
+ * signs: dim floats (+-1), qjl: projections*dim floats row-major. */
+int pkv_turbo_profile_create_with_constants(pkv_ctx* ctx, uint32_t dim, uint32_t bits,
+                                            uint32_t projections, uint64_t seed, int mode,
+                                            const float* signs, const float* qjl,
+                                            pkv_profile** out);
+
+/* Replaces FibQuantAdapter::build_quantizer (proveKV/src/codec.rs:471-499):
+ * paper_default profile with the adapter's training overrides; the codebook
+ * (Lloyd-Max) and the f64 rotation are built on the host once and uploaded.
+ * dim 64 or 128, k 4, n <= 32. */
+int pkv_fib_profile_create(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, uint64_t seed,
+                           uint32_t training_samples, uint32_t lloyd_restarts,
+                           uint32_t lloyd_iterations, pkv_profile** out);
+/* Same, with FibCodebookV1::codewords (n*k f32 row-major) and
+ * StoredRotation::matrix (dim*dim f64 row-major) supplied by the caller. */
+int pkv_fib_profile_create_with_constants(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n,
+                                          const float* codebook, const double* rotation,
+                                          pkv_profile** out);
+void pkv_profile_destroy(pkv_profile* prof);
+
+/* Host-only constant generators (no device needed): the exact constants
+ * pkv_turbo_profile_create / pkv_fib_profile_create derive from a seed.
+ * turbo: signs[dim], qjl[projections*dim] (NULL skips);
+ * fib: codebook[n*k], rotation[dim*dim] (row-major), optional MSEs. */
+int pkv_turbo_constants(uint32_t dim, uint32_t projections, uint64_t seed, float* signs, float* qjl);
+int pkv_fib_constants(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint32_t training_samples,
+                      uint32_t lloyd_restarts, uint32_t lloyd_iterations, float* codebook,
+                      double* rotation, double* init_mse, double* training_mse);
+
+/* Copies the profile constants out (host memory).  turbo: a = signs[dim],
+ * b = float qjl[proj*dim]; fib: a = float codebook[n*k], b = double rot[dim*dim]. */
+int pkv_profile_constants(const pkv_profile* prof, void* a, size_t a_bytes, void* b, size_t b_bytes);
+
+/* Wire sizing: per-vector payload bytes, header bytes (38 TQB1 / 19 FB2) and
+ * the blob size of an n-vector batch. radii_codec is ignored for fib. */
+uint32_t pkv_payload_len(const pkv_profile* prof, int radii_codec);
+uint32_t pkv_header_len(const pkv_profile* prof);
+uint64_t pkv_blob_len(const pkv_profile* prof, int radii_codec, uint64_t n_vectors);
+
+/* ---------------------------------------------------------------- segments
+ * One segment = one FB2/TQB1 blob <-> n_vectors dim-sized f32 (or bf16)
+ * vectors of a strided tensor.  Vector i of the segment starts at element
+ *     elem_offset + (i / group) * stride_outer + (i % group) * stride_inner
+ * which expresses the proveKV gather order (vector i = token * H + head;
+ * proveKV/src/pool.rs:246-257, shell.rs:250-262) and the decode re-layout
+ * (pool.rs:538-558, flatten_heads_tokens 19-33) without a copy.  The blob
+ * (header included) starts at byte wire_offset of the wire buffer.
+ * All (agent, layer, K|V) batches of a pool or of N shells go in ONE launch. */
+typedef struct pkv_seg {
+    uint64_t elem_offset;
+    uint64_t stride_outer;
+    uint64_t stride_inner;
+    uint64_t wire_offset;
+    uint32_t n_vectors;
+    uint32_t group;
+} pkv_seg;
+
+/* Per-segment status words written by the kernels (2 per segment): word 0 =
+ * first input-validation failure, word 1 = first later failure, each packed
+ * as (vector_index << 4) | kind; 0xFFFFFFFF = none.  pkv_segments_status()
+ * turns them into a pkv_error following the reference's precedence. */
+int pkv_segments_status(const pkv_profile* prof, const uint32_t* host_status, uint32_t nseg,
+                        pkv_error* err);
+
+/* Encode every segment: writes complete blobs (header + payloads) into
+ * d_wire.  Replaces the per-(layer, K|V) loops of TurboQuantAdapter /
+ * FibQuantAdapter::encode_batch_compact (proveKV/src/codec.rs:248-291,
+ * 513-525) driven by materialize_shell / SharedKVPool::build_with_policy.
+ * d_status: 2*nseg uint32 device words (may be NULL).  The call validates the
+ * segment table against in_elems / wire_bytes before launching. */
+int pkv_encode_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, int in_dtype,
+                        const void* d_in, uint64_t in_elems, const pkv_seg* segs, uint32_t nseg,
+                        uint8_t* d_wire, uint64_t wire_bytes, uint32_t* d_status, void* stream);
+
+/* Decode every segment into f32 at the segment's strided positions.
+ * radii_codec: the TQB1 radii codec the caller expects (ignored for fib);
+ * each header is checked against the profile and the segment on the device
+ * (a mismatch marks the segment corrupt and leaves its output untouched).
+ * Replaces decode_batch_compact (proveKV/src/codec.rs:295-326, 530-569) under
+ * SharedKVPool::decompress_layer (pool.rs:471-614) and
+ * AgentShell::decompress_all_layers_with_seed (shell.rs:92-141). */
+int pkv_decode_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec,
+                        const uint8_t* d_wire, uint64_t wire_bytes, const pkv_seg* segs,
+                        uint32_t nseg, float* d_out, uint64_t out_elems, uint32_t* d_status,
+                        void* stream);
+
+/* ---------------------------------------------------------------- host-buffer
+ * Drop-ins for the adapters' inherent batch methods: host slices in, wire
+ * bytes out (and back), with the H2D / launch / D2H / sync inside, exactly the
+ * contract of TurboQuantAdapter::encode_batch_compact /
+ * decode_batch_compact (proveKV/src/codec.rs:248-326) and the FibQuantAdapter
+ * pair (513-569).  vectors: n*dim f32 row-major.  For decode, the header is
+ * parsed and validated on the host with the reference's checks
+ * (turbo-quant/src/wire.rs:401-568; fib-quant/src/codec.rs:323-424). */
+int pkv_encode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec,
+                             const float* vectors, uint64_t n, uint8_t* out, uint64_t out_cap,
+                             uint64_t* out_len, pkv_error* err);
+int pkv_decode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, const uint8_t* payload,
+                             uint64_t len, float* out, uint64_t out_cap_vectors, uint64_t* n_out,
+                             pkv_error* err);
+
+/* Parses a TQB1 / FB2 header against the profile (host memory) and reports
+ * the number of vectors and the radii codec; PKV_ERR_CORRUPT_PAYLOAD on any
+ * mismatch the reference decoder rejects. */
+int pkv_parse_header(const pkv_profile* prof, const uint8_t* blob, uint64_t len,
+                     uint64_t* n_vectors, int* radii_codec);
+
+/* ---------------------------------------------------------------- host math
+ * Host builds of the exact scalar routines the kernels use (test hooks):
+ * angle bins of (a[i], b[i]) for pbits, and logf / expf over arrays. */
+void pkv_host_angle_bins(const float* a, const float* b, uint64_t n, uint32_t pbits, uint32_t* out);
+void pkv_host_logf(const float* x, uint64_t n, float* out);
+void pkv_host_expf(const float* x, uint64_t n, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PKV_CODEC_H */

@@ -1,0 +1,357 @@
+"""ctypes wrapper around the CPU oracle (oracle/pkv_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()``
+and by the ``cpu_baseline`` leg of ``bench.py`` -- never by the
+``provekv_amd`` product.  Builds the shared library on first use when it is
+missing (``make -C oracle``); on the GPU box the prebuilt
+``oracle/_build/libpkv_oracle.so`` travels with the tree.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "libpkv_oracle.so")
+
+ERRORS = {
+    0: "ok",
+    -1: "invalid_arg",
+    -2: "nonfinite_input",
+    -3: "zero_norm",
+    -4: "norm_unrepresentable",
+    -5: "malformed",
+    -6: "radius",
+    -7: "residual",
+    -8: "capacity",
+    -9: "empty",
+    -10: "numerical",
+}
+
+
+class OracleError(RuntimeError):
+    def __init__(self, code: int, index: int | None = None):
+        self.code = code
+        self.kind = ERRORS.get(code, str(code))
+        self.index = index
+        super().__init__(f"oracle error {self.kind} (index={index})")
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = C.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+P = C.c_void_p
+U32 = C.c_uint32
+U64 = C.c_uint64
+I32 = C.c_int
+
+
+def _declare(L):
+    L.ora_chacha_words.argtypes = [P, I32, U64, P, U64]
+    L.ora_seed_key.argtypes = [U64, P]
+    L.ora_rng_u64.argtypes = [U64, P, U64]
+    L.ora_normal_f64.argtypes = [U64, P, U64]
+    L.ora_gamma_f64.argtypes = [U64, C.c_double, P, U64]
+    L.ora_zig_tables.argtypes = [P, P, P]
+    L.ora_stored_rotation.argtypes = [U32, U64, P, P]
+    L.ora_stored_rotation.restype = I32
+    L.ora_fib_codebook.argtypes = [U32, U32, U32, U64, U32, U32, U32, P, P, P]
+    L.ora_fib_codebook.restype = I32
+    L.ora_inv_norm_cdf.argtypes = [C.c_double]
+    L.ora_inv_norm_cdf.restype = C.c_double
+    L.ora_beta_inv.argtypes = [C.c_double, C.c_double, C.c_double]
+    L.ora_beta_inv.restype = C.c_double
+    L.ora_radius_quantile.argtypes = [U32, U32, U32, U32]
+    L.ora_radius_quantile.restype = C.c_double
+    L.ora_roberts_kronecker.argtypes = [U32, U32, P]
+    L.ora_roberts_kronecker.restype = I32
+    L.ora_turbo_constants.argtypes = [U32, U32, U64, P, P]
+    L.ora_turbo_constants.restype = I32
+    L.ora_turbo_rotate.argtypes = [U32, P, P, P]
+    L.ora_turbo_rotate_inverse.argtypes = [U32, P, P, P]
+    L.ora_turbo_encode_vector.argtypes = [U32, U32, U32, I32, P, P, P, P, P, P]
+    L.ora_turbo_encode_vector.restype = I32
+    L.ora_turbo_payload_len.argtypes = [U32, U32, U32, I32, I32]
+    L.ora_turbo_payload_len.restype = U32
+    L.ora_turbo_encode_batch.argtypes = [U32, U32, U32, U64, I32, I32, P, P, P, U64, P, U64, P, P]
+    L.ora_turbo_encode_batch.restype = I32
+    L.ora_turbo_decode_batch.argtypes = [U32, U32, U32, U64, I32, P, P, U64, P, U64, P, P]
+    L.ora_turbo_decode_batch.restype = I32
+    L.ora_f32_to_f16.argtypes = [C.c_float]
+    L.ora_f32_to_f16.restype = C.c_uint16
+    L.ora_f16_to_f32.argtypes = [C.c_uint16]
+    L.ora_f16_to_f32.restype = C.c_float
+    L.ora_nearest_codeword_k4.argtypes = [P, P, I32]
+    L.ora_nearest_codeword_k4.restype = I32
+    L.ora_nearest_codeword_scalar.argtypes = [P, P, I32, I32]
+    L.ora_nearest_codeword_scalar.restype = I32
+    L.ora_fib_encode_batch.argtypes = [U32, U32, U32, P, P, P, U64, P, U64, P, P]
+    L.ora_fib_encode_batch.restype = I32
+    L.ora_fib_decode_batch.argtypes = [U32, U32, U32, P, P, P, U64, P, U64, P, P]
+    L.ora_fib_decode_batch.restype = I32
+    L.ora_pack_bits.argtypes = [P, U64, I32, P]
+    L.ora_unpack_bits.argtypes = [P, U64, I32, P]
+    L.ora_unpack_bits.restype = I32
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# ---------------------------------------------------------------- RNG pins
+def chacha_words(key8, rounds: int, n: int, skip: int = 0) -> np.ndarray:
+    key = np.ascontiguousarray(key8, dtype=np.uint32)
+    out = np.zeros(n, dtype=np.uint32)
+    lib().ora_chacha_words(_p(key), rounds, skip, _p(out), n)
+    return out
+
+
+def seed_key(seed: int) -> np.ndarray:
+    out = np.zeros(8, dtype=np.uint32)
+    lib().ora_seed_key(seed, _p(out))
+    return out
+
+
+def rng_u64(seed: int, n: int) -> np.ndarray:
+    out = np.zeros(n, dtype=np.uint64)
+    lib().ora_rng_u64(seed, _p(out), n)
+    return out
+
+
+def normal_f64(seed: int, n: int) -> np.ndarray:
+    out = np.zeros(n, dtype=np.float64)
+    lib().ora_normal_f64(seed, _p(out), n)
+    return out
+
+
+def gamma_f64(seed: int, shape: float, n: int) -> np.ndarray:
+    out = np.zeros(n, dtype=np.float64)
+    lib().ora_gamma_f64(seed, shape, _p(out), n)
+    return out
+
+
+def zig_tables():
+    x = np.zeros(257)
+    f = np.zeros(257)
+    r = np.zeros(1)
+    lib().ora_zig_tables(_p(x), _p(f), _p(r))
+    return x, f, float(r[0])
+
+
+def stored_rotation(d: int, seed: int):
+    m = np.zeros((d, d))
+    g = np.zeros(d * d)
+    rc = lib().ora_stored_rotation(d, seed, _p(m), _p(g))
+    if rc:
+        raise OracleError(rc)
+    return m, g.reshape(d, d).T.copy()   # gaussian as a row-major [row, col] matrix
+
+
+def fib_codebook(d=64, k=4, n=32, seed=42, training=2048, restarts=4, iterations=8):
+    out = np.zeros(n * k, dtype=np.float32)
+    i_mse = np.zeros(1)
+    t_mse = np.zeros(1)
+    rc = lib().ora_fib_codebook(d, k, n, seed, training, restarts, iterations, _p(out), _p(i_mse), _p(t_mse))
+    if rc:
+        raise OracleError(rc)
+    return out.reshape(n, k), float(i_mse[0]), float(t_mse[0])
+
+
+def inv_norm_cdf(p: float) -> float:
+    return lib().ora_inv_norm_cdf(p)
+
+
+def beta_inv(q: float, a: float, b: float) -> float:
+    return lib().ora_beta_inv(q, a, b)
+
+
+def radius_quantile(d, k, idx, n) -> float:
+    return lib().ora_radius_quantile(d, k, idx, n)
+
+
+def roberts_kronecker(k, n) -> np.ndarray:
+    out = np.zeros(k * n)
+    rc = lib().ora_roberts_kronecker(k, n, _p(out))
+    if rc:
+        raise OracleError(rc)
+    return out.reshape(n, k)
+
+
+# ---------------------------------------------------------------- turbo
+def turbo_constants(dim: int, proj: int, seed: int):
+    signs = np.zeros(dim, dtype=np.float32)
+    G = np.zeros(max(proj, 1) * dim, dtype=np.float32)
+    rc = lib().ora_turbo_constants(dim, proj, seed, _p(signs), _p(G))
+    if rc:
+        raise OracleError(rc)
+    return signs, G[: proj * dim].reshape(proj, dim)
+
+
+def turbo_rotate(signs: np.ndarray, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.zeros_like(x)
+    lib().ora_turbo_rotate(len(signs), _p(np.ascontiguousarray(signs, np.float32)), _p(x), _p(y))
+    return y
+
+
+def turbo_rotate_inverse(signs: np.ndarray, y: np.ndarray) -> np.ndarray:
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    x = np.zeros_like(y)
+    lib().ora_turbo_rotate_inverse(len(signs), _p(np.ascontiguousarray(signs, np.float32)), _p(y), _p(x))
+    return x
+
+
+def turbo_payload_len(dim, bits=4, proj=32, mode=1, radii_codec=0) -> int:
+    return int(lib().ora_turbo_payload_len(dim, bits, proj, mode, radii_codec))
+
+
+def turbo_encode_vector(x, signs, G, bits=4, proj=32, mode=1):
+    dim = len(signs)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    radii = np.zeros(dim // 2, dtype=np.float32)
+    idx = np.zeros(dim // 2, dtype=np.uint16)
+    sb = np.zeros(max(1, (proj + 7) // 8), dtype=np.uint8)
+    Gc = np.ascontiguousarray(G, dtype=np.float32)
+    rc = lib().ora_turbo_encode_vector(dim, bits, proj, mode, _p(np.ascontiguousarray(signs, np.float32)),
+                                       _p(Gc), _p(x), _p(radii), _p(idx), _p(sb))
+    if rc:
+        raise OracleError(rc)
+    return radii, idx, sb
+
+
+def turbo_encode_batch(x: np.ndarray, seed: int, bits=4, proj=32, mode=1, radii_codec=0,
+                       signs=None, G=None) -> bytes:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, dim = x.shape
+    if signs is None:
+        signs, G = turbo_constants(dim, proj if mode else 0, seed)
+    if G is None or G.size == 0:
+        G = np.zeros((1, dim), dtype=np.float32)
+    plen = turbo_payload_len(dim, bits, proj, mode, radii_codec)
+    cap = 38 + n * plen
+    out = np.zeros(max(cap, 1), dtype=np.uint8)
+    out_len = np.zeros(1, dtype=np.uint64)
+    fail = np.zeros(1, dtype=np.uint64)
+    rc = lib().ora_turbo_encode_batch(dim, bits, proj, seed, mode, radii_codec, _p(signs),
+                                      _p(np.ascontiguousarray(G, np.float32)), _p(x), n, _p(out), cap,
+                                      _p(out_len), _p(fail))
+    if rc:
+        raise OracleError(rc, int(fail[0]))
+    return out[: int(out_len[0])].tobytes()
+
+
+def turbo_decode_batch(blob: bytes, dim: int, seed: int, bits=4, proj=32, mode=1, signs=None) -> np.ndarray:
+    if signs is None:
+        signs, _ = turbo_constants(dim, 0, seed)
+    buf = np.frombuffer(blob, dtype=np.uint8).copy()
+    if buf.size == 0:
+        buf = np.zeros(1, dtype=np.uint8)
+    n_out = np.zeros(1, dtype=np.uint64)
+    fail = np.zeros(1, dtype=np.uint64)
+    n_guess = max(1, len(blob))
+    # first call sizes the output
+    rc = lib().ora_turbo_decode_batch(dim, bits, proj, seed, mode, _p(signs), _p(buf), len(blob), None, 0,
+                                      _p(n_out), _p(fail))
+    if rc not in (0, -8):
+        raise OracleError(rc, int(fail[0]))
+    n = int(n_out[0])
+    out = np.zeros((max(n, 1), dim), dtype=np.float32)
+    rc = lib().ora_turbo_decode_batch(dim, bits, proj, seed, mode, _p(signs), _p(buf), len(blob), _p(out), n,
+                                      _p(n_out), _p(fail))
+    if rc:
+        raise OracleError(rc, int(fail[0]))
+    del n_guess
+    return out[:n]
+
+
+# ---------------------------------------------------------------- fib
+def f32_to_f16(v: float) -> int:
+    return int(lib().ora_f32_to_f16(v))
+
+
+def f16_to_f32(h: int) -> float:
+    return float(lib().ora_f16_to_f32(h))
+
+
+def nearest_codeword_k4(s, cb) -> int:
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    cb = np.ascontiguousarray(cb, dtype=np.float32)
+    return int(lib().ora_nearest_codeword_k4(_p(s), _p(cb), cb.size // 4))
+
+
+def nearest_codeword_scalar(s, cb, k) -> int:
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    cb = np.ascontiguousarray(cb, dtype=np.float32)
+    return int(lib().ora_nearest_codeword_scalar(_p(s), _p(cb), k, cb.size // k))
+
+
+def fib_encode_batch(x: np.ndarray, codebook: np.ndarray, rotation: np.ndarray) -> bytes:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, d = x.shape
+    N, k = codebook.shape
+    cb = np.ascontiguousarray(codebook, dtype=np.float32)
+    rot = np.ascontiguousarray(rotation, dtype=np.float64)
+    bits = int(N - 1).bit_length()
+    plen = 2 + (d // k * bits + 7) // 8
+    cap = 19 + n * plen
+    out = np.zeros(max(cap, 1), dtype=np.uint8)
+    out_len = np.zeros(1, dtype=np.uint64)
+    fail = np.zeros(1, dtype=np.uint64)
+    rc = lib().ora_fib_encode_batch(d, k, N, _p(cb), _p(rot), _p(x), n, _p(out), cap, _p(out_len), _p(fail))
+    if rc:
+        raise OracleError(rc, int(fail[0]))
+    return out[: int(out_len[0])].tobytes()
+
+
+def fib_decode_batch(blob: bytes, codebook: np.ndarray, rotation: np.ndarray, d: int = 64) -> np.ndarray:
+    N, k = codebook.shape
+    cb = np.ascontiguousarray(codebook, dtype=np.float32)
+    rot = np.ascontiguousarray(rotation, dtype=np.float64)
+    buf = np.frombuffer(blob, dtype=np.uint8).copy()
+    if buf.size == 0:
+        buf = np.zeros(1, dtype=np.uint8)
+    n_out = np.zeros(1, dtype=np.uint64)
+    fail = np.zeros(1, dtype=np.uint64)
+    rc = lib().ora_fib_decode_batch(d, k, N, _p(cb), _p(rot), _p(buf), len(blob), None, 0, _p(n_out), _p(fail))
+    if rc not in (0, -8):
+        raise OracleError(rc, int(fail[0]))
+    n = int(n_out[0])
+    out = np.zeros((max(n, 1), d), dtype=np.float32)
+    rc = lib().ora_fib_decode_batch(d, k, N, _p(cb), _p(rot), _p(buf), len(blob), _p(out), n, _p(n_out), _p(fail))
+    if rc:
+        raise OracleError(rc, int(fail[0]))
+    return out[:n]
+
+
+def pack_bits(values, bits: int) -> bytes:
+    v = np.ascontiguousarray(values, dtype=np.uint32)
+    out = np.zeros(max(1, (len(v) * bits + 7) // 8), dtype=np.uint8)
+    lib().ora_pack_bits(_p(v), len(v), bits, _p(out))
+    return out[: (len(v) * bits + 7) // 8].tobytes()
+
+
+def unpack_bits(data: bytes, n: int, bits: int) -> np.ndarray:
+    buf = np.frombuffer(data, dtype=np.uint8).copy()
+    out = np.zeros(max(n, 1), dtype=np.uint32)
+    rc = lib().ora_unpack_bits(_p(buf), n, bits, _p(out))
+    if rc:
+        raise OracleError(rc)
+    return out[:n]

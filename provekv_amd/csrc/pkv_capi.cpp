@@ -1,0 +1,725 @@
+// pkv_capi.cpp -- host half of libpkv_hip.so: the C ABI declared in
+// include/pkv_codec.h.  Owns contexts, profiles (constants resident on the
+// device), segment-table validation and upload, kernel launches, and the
+// host-buffer drop-ins for the adapters' encode_batch_compact /
+// decode_batch_compact (proveKV/src/codec.rs:248-326, 513-569).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "pkv_internal.h"
+#include "pkv_math.h"
+
+using namespace pkv;
+
+namespace {
+
+constexpr int kSlots = 8;
+
+struct Slot {
+    void* dev = nullptr;         // segs | tile_start | status
+    void* host = nullptr;        // pinned staging
+    size_t cap = 0;
+    hipEvent_t done = nullptr;
+    bool used = false;
+};
+
+}  // namespace
+
+struct pkv_ctx {
+    int device = 0;
+    std::mutex mu;
+    Slot slots[kSlots];
+    int next = 0;
+    hipStream_t own_stream = nullptr;   // for the host-buffer entry points
+    void* scratch = nullptr;            // host-buffer entry points: in + out
+    size_t scratch_cap = 0;
+};
+
+struct pkv_profile {
+    pkv_ctx* ctx = nullptr;
+    int kind = 0;
+    uint32_t dim = 0;
+    // turbo
+    uint32_t bits = 0, pbits = 0, proj = 0, mode = 0;
+    uint64_t seed = 0;
+    std::vector<float> signs, qjl, cs;
+    float* d_signs = nullptr;
+    float* d_qjl = nullptr;
+    float* d_cs = nullptr;
+    // fib
+    uint32_t k = 0, n = 0, wbits = 0;
+    std::vector<float> codebook, rot32t;
+    std::vector<double> rot;
+    float* d_cb = nullptr;
+    double* d_rot = nullptr;
+    float* d_rot32t = nullptr;
+};
+
+namespace {
+
+int hip_status(hipError_t e) {
+    if (e == hipSuccess) return PKV_OK;
+    if (e == hipErrorOutOfMemory) return PKV_ERR_OOM;
+    return PKV_ERR_DEVICE;
+}
+
+#define HIP_TRY(expr)                          \
+    do {                                       \
+        hipError_t _e = (expr);                \
+        if (_e != hipSuccess) return hip_status(_e); \
+    } while (0)
+
+template <typename T>
+int upload(T** dptr, const std::vector<T>& v) {
+    size_t bytes = std::max<size_t>(v.size() * sizeof(T), sizeof(T));
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(dptr), bytes));
+    if (!v.empty()) HIP_TRY(hipMemcpy(*dptr, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice));
+    return PKV_OK;
+}
+
+uint32_t turbo_plen(const pkv_profile* p, int radii) {
+    uint32_t pairs = p->dim / 2;
+    uint32_t rad = radii == PKV_RADII_LOG_U8 ? pairs + 8 : 4 * pairs;
+    uint32_t ang = (pairs * p->pbits + 7) / 8;
+    uint32_t sig = p->mode ? (p->proj + 7) / 8 : 0;
+    return rad + ang + sig;
+}
+
+uint32_t fib_plen(const pkv_profile* p) { return 2 + ((p->dim / p->k) * p->wbits + 7) / 8; }
+
+uint32_t hdr_len(const pkv_profile* p) { return p->kind == PKV_CODEC_TURBO ? 38u : 19u; }
+
+bool mul_add_ok(uint64_t a, uint64_t b, uint64_t c, uint64_t* out) {
+    uint64_t t;
+    if (__builtin_mul_overflow(a, b, &t)) return false;
+    if (__builtin_add_overflow(t, c, out)) return false;
+    return true;
+}
+
+// Highest element index (exclusive) a segment touches in the f32 tensor.
+bool seg_extent(const pkv_seg& s, uint32_t dim, uint64_t* end) {
+    uint64_t n = s.n_vectors;
+    if (n == 0) { *end = 0; return true; }
+    uint64_t q = (n - 1) / s.group;
+    uint64_t r = std::min<uint64_t>(s.group - 1, n - 1);
+    uint64_t a, b;
+    if (!mul_add_ok(q, s.stride_outer, 0, &a)) return false;
+    if (!mul_add_ok(r, s.stride_inner, a, &b)) return false;
+    if (__builtin_add_overflow(b, s.elem_offset, &b)) return false;
+    if (__builtin_add_overflow(b, dim, &b)) return false;
+    *end = b;
+    return true;
+}
+
+int validate_segments(const pkv_profile* p, int radii, bool encode, int dtype, const void* d_f32,
+                      uint64_t f32_elems, const pkv_seg* segs, uint32_t nseg, const void* d_wire,
+                      uint64_t wire_bytes, std::vector<uint32_t>& tile_start) {
+    if (!segs || nseg == 0) return PKV_ERR_INVALID_ARG;
+    if (!d_f32 || !d_wire) return PKV_ERR_INVALID_ARG;
+    const uint32_t align = dtype == PKV_BF16 ? 8u : 4u;
+    if (reinterpret_cast<uintptr_t>(d_f32) % 16 != 0) return PKV_ERR_INVALID_ARG;
+    const uint32_t plen = p->kind == PKV_CODEC_TURBO ? turbo_plen(p, radii) : fib_plen(p);
+    const uint32_t hdr = hdr_len(p);
+    tile_start.assign(nseg + 1, 0);
+    std::vector<std::pair<uint64_t, uint64_t>> blobs;
+    blobs.reserve(nseg);
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < nseg; ++i) {
+        const pkv_seg& s = segs[i];
+        if (s.group == 0) return PKV_ERR_INVALID_ARG;
+        if (s.n_vectors > MAX_SEG_VECTORS) return PKV_ERR_INVALID_ARG;
+        if (encode && s.n_vectors == 0) return PKV_ERR_EMPTY_BATCH;
+        if (s.elem_offset % align || s.stride_outer % align || s.stride_inner % align) return PKV_ERR_INVALID_ARG;
+        uint64_t end;
+        if (!seg_extent(s, p->dim, &end) || end > f32_elems) return PKV_ERR_DIM_MISMATCH;
+        uint64_t blob_end;
+        if (!mul_add_ok(s.n_vectors, plen, hdr, &blob_end) ||
+            __builtin_add_overflow(blob_end, s.wire_offset, &blob_end) || blob_end > wire_bytes)
+            return PKV_ERR_CAPACITY;
+        blobs.emplace_back(s.wire_offset, blob_end);
+        uint64_t tiles = (static_cast<uint64_t>(s.n_vectors) + TILE - 1) / TILE;
+        if (tiles == 0) tiles = 1;   // an empty blob still gets its header checked
+        tile_start[i] = static_cast<uint32_t>(total);
+        total += tiles;
+        if (total > 0x7fffffffull) return PKV_ERR_INVALID_ARG;
+    }
+    tile_start[nseg] = static_cast<uint32_t>(total);
+    if (encode) {   // encoded blobs are written by different workgroups: no overlap
+        std::sort(blobs.begin(), blobs.end());
+        for (size_t i = 1; i < blobs.size(); ++i)
+            if (blobs[i].first < blobs[i - 1].second) return PKV_ERR_INVALID_ARG;
+    }
+    return PKV_OK;
+}
+
+// Stage the segment table + tile prefix (+ status words when the caller gave
+// none) into a ring slot and copy it to the device on `stream`.
+int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vector<uint32_t>& tiles,
+                bool need_status, hipStream_t stream, Slot** out_slot, SegDev** d_segs, uint32_t** d_tiles,
+                uint32_t** d_status) {
+    const size_t seg_bytes = sizeof(pkv_seg) * nseg;
+    const size_t tile_bytes = sizeof(uint32_t) * (nseg + 1);
+    const size_t tile_off = (seg_bytes + 255) & ~static_cast<size_t>(255);
+    const size_t stat_off = (tile_off + tile_bytes + 255) & ~static_cast<size_t>(255);
+    const size_t total = stat_off + (need_status ? sizeof(uint32_t) * 2 * nseg : 0) + 256;
+    Slot& sl = ctx->slots[ctx->next];
+    ctx->next = (ctx->next + 1) % kSlots;
+    if (sl.used) HIP_TRY(hipEventSynchronize(sl.done));
+    if (sl.cap < total) {
+        if (sl.dev) HIP_TRY(hipFree(sl.dev));
+        if (sl.host) HIP_TRY(hipHostFree(sl.host));
+        sl.dev = sl.host = nullptr;
+        size_t cap = std::max<size_t>(total, 64 * 1024);
+        HIP_TRY(hipMalloc(&sl.dev, cap));
+        HIP_TRY(hipHostMalloc(&sl.host, cap, hipHostMallocDefault));
+        sl.cap = cap;
+    }
+    if (!sl.done) HIP_TRY(hipEventCreateWithFlags(&sl.done, hipEventDisableTiming));
+    auto* h = static_cast<uint8_t*>(sl.host);
+    std::memcpy(h, segs, seg_bytes);
+    std::memcpy(h + tile_off, tiles.data(), tile_bytes);
+    HIP_TRY(hipMemcpyAsync(sl.dev, sl.host, stat_off, hipMemcpyHostToDevice, stream));
+    auto* d = static_cast<uint8_t*>(sl.dev);
+    *d_segs = reinterpret_cast<SegDev*>(d);
+    *d_tiles = reinterpret_cast<uint32_t*>(d + tile_off);
+    *d_status = need_status ? reinterpret_cast<uint32_t*>(d + stat_off) : nullptr;
+    *out_slot = &sl;
+    return PKV_OK;
+}
+
+int finish_slot(Slot* sl, hipStream_t stream) {
+    HIP_TRY(hipEventRecord(sl->done, stream));
+    sl->used = true;
+    return PKV_OK;
+}
+
+TurboDev turbo_dev(const pkv_profile* p) {
+    TurboDev t;
+    t.signs = p->d_signs;
+    t.qjl = p->d_qjl;
+    t.cs = p->d_cs;
+    t.seed = p->seed;
+    t.dim = p->dim;
+    t.pbits = p->pbits;
+    t.proj = p->proj;
+    t.mode = p->mode;
+    return t;
+}
+
+FibDev fib_dev(const pkv_profile* p) {
+    FibDev f;
+    f.codebook = p->d_cb;
+    f.rot = p->d_rot;
+    f.rot32t = p->d_rot32t;
+    f.dim = p->dim;
+    f.k = p->k;
+    f.n = p->n;
+    f.bits = p->wbits;
+    return f;
+}
+
+// Caller holds ctx->mu.
+int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool encode, int dtype,
+                        const void* d_f32, uint64_t f32_elems, const pkv_seg* segs, uint32_t nseg,
+                        const uint8_t* d_wire, uint64_t wire_bytes, uint32_t* d_status, hipStream_t stream) {
+    if (!ctx || !prof) return PKV_ERR_INVALID_ARG;
+    if (prof->kind == PKV_CODEC_TURBO && radii != PKV_RADII_F32 && radii != PKV_RADII_LOG_U8)
+        return PKV_ERR_INVALID_ARG;
+    if (prof->kind == PKV_CODEC_FIB) radii = PKV_RADII_F32;
+    if (dtype != PKV_F32 && dtype != PKV_BF16) return PKV_ERR_INVALID_ARG;
+    if (!encode && dtype != PKV_F32) return PKV_ERR_INVALID_ARG;
+    std::vector<uint32_t> tiles;
+    int rc = validate_segments(prof, radii, encode, dtype, d_f32, f32_elems, segs, nseg, d_wire, wire_bytes, tiles);
+    if (rc) return rc;
+    HIP_TRY(hipSetDevice(ctx->device));
+    Slot* sl;
+    SegDev* dsegs;
+    uint32_t *dtiles, *dstat;
+    rc = stage_table(ctx, segs, nseg, tiles, d_status == nullptr, stream, &sl, &dsegs, &dtiles, &dstat);
+    if (rc) return rc;
+    uint32_t* status = d_status ? d_status : dstat;
+    rc = launch_fill_u32(status, STATUS_NONE, 2ull * nseg, stream);
+    if (rc) { finish_slot(sl, stream); return hip_status(static_cast<hipError_t>(rc)); }
+    LaunchCommon lc;
+    lc.segs = dsegs;
+    lc.tile_start = dtiles;
+    lc.nseg = nseg;
+    lc.status = status;
+    lc.radii = static_cast<uint32_t>(radii);
+    lc.plen = prof->kind == PKV_CODEC_TURBO ? turbo_plen(prof, radii) : fib_plen(prof);
+    lc.in_bf16 = dtype == PKV_BF16 ? 1u : 0u;
+    const uint32_t nblocks = tiles[nseg];
+    int e;
+    if (prof->kind == PKV_CODEC_TURBO) {
+        e = encode ? launch_turbo_encode(lc, turbo_dev(prof), d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
+                   : launch_turbo_decode(lc, turbo_dev(prof), d_wire, static_cast<float*>(const_cast<void*>(d_f32)),
+                                         nblocks, stream);
+    } else {
+        e = encode ? launch_fib_encode(lc, fib_dev(prof), d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
+                   : launch_fib_decode(lc, fib_dev(prof), d_wire, static_cast<float*>(const_cast<void*>(d_f32)),
+                                       nblocks, stream);
+    }
+    int rc2 = finish_slot(sl, stream);
+    if (e) return hip_status(static_cast<hipError_t>(e));
+    return rc2;
+}
+
+int run_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool encode, int dtype, const void* d_f32,
+                 uint64_t f32_elems, const pkv_seg* segs, uint32_t nseg, const uint8_t* d_wire,
+                 uint64_t wire_bytes, uint32_t* d_status, hipStream_t stream) {
+    if (!ctx) return PKV_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    return run_segments_locked(ctx, prof, radii, encode, dtype, d_f32, f32_elems, segs, nseg, d_wire, wire_bytes,
+                               d_status, stream);
+}
+
+int ensure_scratch(pkv_ctx* ctx, size_t bytes) {
+    if (ctx->scratch_cap >= bytes) return PKV_OK;
+    if (ctx->scratch) HIP_TRY(hipFree(ctx->scratch));
+    ctx->scratch = nullptr;
+    ctx->scratch_cap = 0;
+    size_t cap = std::max<size_t>(bytes, 1 << 20);
+    HIP_TRY(hipMalloc(&ctx->scratch, cap));
+    ctx->scratch_cap = cap;
+    return PKV_OK;
+}
+
+int resolve_status(const pkv_profile* p, const uint32_t* st, uint32_t nseg, const pkv_seg* segs, pkv_error* err) {
+    for (uint32_t s = 0; s < nseg; ++s) {
+        uint32_t w0 = st[2 * s], w1 = st[2 * s + 1];
+        if (w0 == STATUS_NONE && w1 == STATUS_NONE) continue;
+        uint32_t pick;
+        if (p->kind == PKV_CODEC_FIB && segs && segs[s].n_vectors >= 4)
+            pick = w0 != STATUS_NONE ? w0 : w1;   // batch validation precedes norm encoding
+        else
+            pick = std::min(w0, w1);              // per-vector order
+        uint32_t kind = pick & 15u;
+        int code;
+        switch (kind) {
+            case KIND_NONFINITE_INPUT: code = PKV_ERR_NONFINITE_INPUT; break;
+            case KIND_ZERO_NORM: code = PKV_ERR_ZERO_NORM; break;
+            case KIND_NORM16: code = PKV_ERR_NORM_UNREPRESENTABLE; break;
+            case KIND_NONFINITE_RADIUS:
+            case KIND_NONFINITE_RESIDUAL: code = PKV_ERR_NONFINITE_CODE; break;
+            default: code = PKV_ERR_CORRUPT_PAYLOAD; break;
+        }
+        if (err) {
+            err->status = code;
+            err->segment = static_cast<int32_t>(s);
+            err->index = pick >> 4;
+        }
+        return code;
+    }
+    if (err) { err->status = PKV_OK; err->segment = -1; err->index = 0; }
+    return PKV_OK;
+}
+
+uint16_t rd16(const uint8_t* b) { return static_cast<uint16_t>(b[0] | (b[1] << 8)); }
+uint32_t rd32(const uint8_t* b) {
+    return static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8) | (static_cast<uint32_t>(b[2]) << 16) |
+           (static_cast<uint32_t>(b[3]) << 24);
+}
+uint64_t rd64(const uint8_t* b) { return rd32(b) | (static_cast<uint64_t>(rd32(b + 4)) << 32); }
+
+}  // namespace
+
+// =====================================================================
+extern "C" {
+
+const char* pkv_status_string(int status) {
+    switch (status) {
+        case PKV_OK: return "ok";
+        case PKV_ERR_INVALID_ARG: return "invalid argument";
+        case PKV_ERR_DIM_MISMATCH: return "dimension mismatch";
+        case PKV_ERR_OOM: return "out of device memory";
+        case PKV_ERR_DEVICE: return "HIP runtime error";
+        case PKV_ERR_CORRUPT_PAYLOAD: return "corrupt payload";
+        case PKV_ERR_UNSUPPORTED: return "unsupported profile";
+        case PKV_ERR_NONFINITE_INPUT: return "non-finite input";
+        case PKV_ERR_ZERO_NORM: return "zero norm";
+        case PKV_ERR_NORM_UNREPRESENTABLE: return "norm cannot be represented as finite positive fp16";
+        case PKV_ERR_EMPTY_BATCH: return "empty batch";
+        case PKV_ERR_CAPACITY: return "buffer too small";
+        case PKV_ERR_NONFINITE_CODE: return "non-finite radius or residual";
+        default: return "unknown status";
+    }
+}
+
+int pkv_device_available(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return 0;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, 0) != hipSuccess) return 0;
+    return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+int pkv_ctx_create(int device, pkv_ctx** out) {
+    if (!out) return PKV_ERR_INVALID_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return PKV_ERR_DEVICE;
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return PKV_ERR_UNSUPPORTED;
+    HIP_TRY(hipSetDevice(device));
+    pkv_ctx* c = new (std::nothrow) pkv_ctx();
+    if (!c) return PKV_ERR_OOM;
+    c->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) { delete c; return hip_status(e); }
+    *out = c;
+    return PKV_OK;
+}
+
+void pkv_ctx_destroy(pkv_ctx* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    for (Slot& s : ctx->slots) {
+        if (s.used) (void)hipEventSynchronize(s.done);
+        if (s.done) (void)hipEventDestroy(s.done);
+        if (s.dev) (void)hipFree(s.dev);
+        if (s.host) (void)hipHostFree(s.host);
+    }
+    if (ctx->own_stream) {
+        (void)hipStreamSynchronize(ctx->own_stream);
+        (void)hipStreamDestroy(ctx->own_stream);
+    }
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    delete ctx;
+}
+
+static int turbo_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t bits, uint32_t proj, uint64_t seed, int mode,
+                                const float* signs, const float* qjl, pkv_profile** out) {
+    if (!ctx || !out) return PKV_ERR_INVALID_ARG;
+    *out = nullptr;
+    // reference validity (turbo-quant/src/turbo.rs:148-164)
+    if (dim == 0 || dim % 2 != 0) return PKV_ERR_INVALID_ARG;
+    if (mode != PKV_TURBO_POLAR_ONLY && mode != PKV_TURBO_POLAR_WITH_QJL) return PKV_ERR_INVALID_ARG;
+    if (mode == PKV_TURBO_POLAR_WITH_QJL ? (bits < 2 || bits > 16) : (bits < 1 || bits > 16))
+        return PKV_ERR_INVALID_ARG;
+    if (mode == PKV_TURBO_POLAR_WITH_QJL && proj == 0) return PKV_ERR_INVALID_ARG;
+    // what the kernels implement
+    const uint32_t pbits = mode == PKV_TURBO_POLAR_WITH_QJL ? bits - 1 : bits;
+    if (dim != 64 && dim != 128) return PKV_ERR_UNSUPPORTED;
+    if (pbits > 8) return PKV_ERR_UNSUPPORTED;
+    if (mode == PKV_TURBO_POLAR_WITH_QJL && proj != 32 && proj != 64) return PKV_ERR_UNSUPPORTED;
+    pkv_profile* p = new (std::nothrow) pkv_profile();
+    if (!p) return PKV_ERR_OOM;
+    p->ctx = ctx;
+    p->kind = PKV_CODEC_TURBO;
+    p->dim = dim;
+    p->bits = bits;
+    p->pbits = pbits;
+    p->proj = mode == PKV_TURBO_POLAR_WITH_QJL ? proj : 0;
+    p->mode = static_cast<uint32_t>(mode);
+    p->seed = seed;
+    if (signs) {
+        p->signs.assign(signs, signs + dim);
+        if (p->proj) p->qjl.assign(qjl, qjl + static_cast<size_t>(p->proj) * dim);
+    } else {
+        make_turbo_constants(dim, p->proj, seed, p->signs, p->qjl);
+    }
+    // (cos, sin) of every dequantized angle, host libm (polar.rs:91-95, 312-313)
+    const uint32_t levels = 1u << pbits;
+    p->cs.resize(2 * levels);
+    const float PI = 3.14159265358979323846f;
+    for (uint32_t i = 0; i < levels; ++i) {
+        float th = (static_cast<float>(i) / static_cast<float>(levels)) * (2.0f * PI) - PI;
+        p->cs[2 * i] = std::cos(th);
+        p->cs[2 * i + 1] = std::sin(th);
+    }
+    int rc = hip_status(hipSetDevice(ctx->device));
+    if (!rc) rc = upload(&p->d_signs, p->signs);
+    if (!rc) rc = upload(&p->d_qjl, p->qjl);
+    if (!rc) rc = upload(&p->d_cs, p->cs);
+    if (rc) { pkv_profile_destroy(p); return rc; }
+    *out = p;
+    return PKV_OK;
+}
+
+int pkv_turbo_profile_create(pkv_ctx* ctx, uint32_t dim, uint32_t bits, uint32_t projections, uint64_t seed,
+                             int mode, pkv_profile** out) {
+    return turbo_profile_common(ctx, dim, bits, projections, seed, mode, nullptr, nullptr, out);
+}
+
+int pkv_turbo_profile_create_with_constants(pkv_ctx* ctx, uint32_t dim, uint32_t bits, uint32_t projections,
+                                            uint64_t seed, int mode, const float* signs, const float* qjl,
+                                            pkv_profile** out) {
+    if (!signs || (mode == PKV_TURBO_POLAR_WITH_QJL && !qjl)) return PKV_ERR_INVALID_ARG;
+    return turbo_profile_common(ctx, dim, bits, projections, seed, mode, signs, qjl, out);
+}
+
+static int fib_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, std::vector<float> cb,
+                              std::vector<double> rot, pkv_profile** out) {
+    pkv_profile* p = new (std::nothrow) pkv_profile();
+    if (!p) return PKV_ERR_OOM;
+    p->ctx = ctx;
+    p->kind = PKV_CODEC_FIB;
+    p->dim = dim;
+    p->k = k;
+    p->n = n;
+    p->wbits = 5;
+    p->codebook = std::move(cb);
+    p->rot = std::move(rot);
+    p->rot32t.resize(static_cast<size_t>(dim) * dim);
+    for (uint32_t r = 0; r < dim; ++r)
+        for (uint32_t c = 0; c < dim; ++c)
+            p->rot32t[static_cast<size_t>(c) * dim + r] = static_cast<float>(p->rot[static_cast<size_t>(r) * dim + c]);
+    int rc = hip_status(hipSetDevice(ctx->device));
+    if (!rc) rc = upload(&p->d_cb, p->codebook);
+    if (!rc) rc = upload(&p->d_rot, p->rot);
+    if (!rc) rc = upload(&p->d_rot32t, p->rot32t);
+    if (rc) { pkv_profile_destroy(p); return rc; }
+    *out = p;
+    return PKV_OK;
+}
+
+static int fib_check(uint32_t dim, uint32_t k, uint32_t n) {
+    if (dim == 0 || k == 0 || dim % k != 0) return PKV_ERR_INVALID_ARG;   // FibQuantAdapter::new
+    if (n < 2) return PKV_ERR_INVALID_ARG;
+    if (dim != 64 || k != 4 || n != 32) return PKV_ERR_UNSUPPORTED;      // fib_k4_n32 at head_dim 64
+    return PKV_OK;
+}
+
+int pkv_fib_profile_create(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, uint64_t seed,
+                           uint32_t training_samples, uint32_t lloyd_restarts, uint32_t lloyd_iterations,
+                           pkv_profile** out) {
+    if (!ctx || !out) return PKV_ERR_INVALID_ARG;
+    *out = nullptr;
+    int rc = fib_check(dim, k, n);
+    if (rc) return rc;
+    // FibQuantProfileV1::validate (fib-quant/src/profile.rs:176-263)
+    if (lloyd_restarts == 0 || lloyd_restarts > 1024) return PKV_ERR_INVALID_ARG;
+    if (lloyd_iterations == 0 || lloyd_iterations > 100000) return PKV_ERR_INVALID_ARG;
+    if (training_samples < n || training_samples > 10000000) return PKV_ERR_INVALID_ARG;
+    std::vector<float> cb;
+    std::vector<double> rot;
+    rc = make_fib_codebook(dim, k, n, seed, training_samples, lloyd_restarts, lloyd_iterations, cb, nullptr, nullptr);
+    if (rc) return rc;
+    rc = make_fib_rotation(dim, seed, rot);
+    if (rc) return rc;
+    return fib_profile_common(ctx, dim, k, n, std::move(cb), std::move(rot), out);
+}
+
+int pkv_fib_profile_create_with_constants(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, const float* codebook,
+                                          const double* rotation, pkv_profile** out) {
+    if (!ctx || !out || !codebook || !rotation) return PKV_ERR_INVALID_ARG;
+    *out = nullptr;
+    int rc = fib_check(dim, k, n);
+    if (rc) return rc;
+    for (uint32_t i = 0; i < n * k; ++i)
+        if (!std::isfinite(codebook[i])) return PKV_ERR_INVALID_ARG;   // FibCodebookV1::validate
+    std::vector<float> cb(codebook, codebook + n * k);
+    std::vector<double> rot(rotation, rotation + static_cast<size_t>(dim) * dim);
+    return fib_profile_common(ctx, dim, k, n, std::move(cb), std::move(rot), out);
+}
+
+void pkv_profile_destroy(pkv_profile* p) {
+    if (!p) return;
+    if (p->ctx) (void)hipSetDevice(p->ctx->device);
+    (void)hipDeviceSynchronize();
+    for (void* d : {static_cast<void*>(p->d_signs), static_cast<void*>(p->d_qjl), static_cast<void*>(p->d_cs),
+                    static_cast<void*>(p->d_cb), static_cast<void*>(p->d_rot), static_cast<void*>(p->d_rot32t)})
+        if (d) (void)hipFree(d);
+    delete p;
+}
+
+int pkv_profile_constants(const pkv_profile* p, void* a, size_t a_bytes, void* b, size_t b_bytes) {
+    if (!p) return PKV_ERR_INVALID_ARG;
+    if (p->kind == PKV_CODEC_TURBO) {
+        size_t na = p->signs.size() * sizeof(float), nb = p->qjl.size() * sizeof(float);
+        if ((a && a_bytes < na) || (b && b_bytes < nb)) return PKV_ERR_CAPACITY;
+        if (a) std::memcpy(a, p->signs.data(), na);
+        if (b && nb) std::memcpy(b, p->qjl.data(), nb);
+    } else {
+        size_t na = p->codebook.size() * sizeof(float), nb = p->rot.size() * sizeof(double);
+        if ((a && a_bytes < na) || (b && b_bytes < nb)) return PKV_ERR_CAPACITY;
+        if (a) std::memcpy(a, p->codebook.data(), na);
+        if (b) std::memcpy(b, p->rot.data(), nb);
+    }
+    return PKV_OK;
+}
+
+uint32_t pkv_payload_len(const pkv_profile* p, int radii_codec) {
+    if (!p) return 0;
+    return p->kind == PKV_CODEC_TURBO ? turbo_plen(p, radii_codec) : fib_plen(p);
+}
+
+uint32_t pkv_header_len(const pkv_profile* p) { return p ? hdr_len(p) : 0; }
+
+uint64_t pkv_blob_len(const pkv_profile* p, int radii_codec, uint64_t n) {
+    if (!p) return 0;
+    return hdr_len(p) + n * pkv_payload_len(p, radii_codec);
+}
+
+int pkv_segments_status(const pkv_profile* prof, const uint32_t* host_status, uint32_t nseg, pkv_error* err) {
+    if (!prof || (!host_status && nseg)) return PKV_ERR_INVALID_ARG;
+    return resolve_status(prof, host_status, nseg, nullptr, err);
+}
+
+int pkv_encode_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, int in_dtype, const void* d_in,
+                        uint64_t in_elems, const pkv_seg* segs, uint32_t nseg, uint8_t* d_wire, uint64_t wire_bytes,
+                        uint32_t* d_status, void* stream) {
+    return run_segments(ctx, prof, radii_codec, true, in_dtype, d_in, in_elems, segs, nseg, d_wire, wire_bytes,
+                        d_status, static_cast<hipStream_t>(stream));
+}
+
+int pkv_decode_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, const uint8_t* d_wire,
+                        uint64_t wire_bytes, const pkv_seg* segs, uint32_t nseg, float* d_out, uint64_t out_elems,
+                        uint32_t* d_status, void* stream) {
+    return run_segments(ctx, prof, radii_codec, false, PKV_F32, d_out, out_elems, segs, nseg, d_wire, wire_bytes,
+                        d_status, static_cast<hipStream_t>(stream));
+}
+
+int pkv_parse_header(const pkv_profile* p, const uint8_t* b, uint64_t len, uint64_t* n_vectors, int* radii_codec) {
+    if (!p || !b) return PKV_ERR_INVALID_ARG;
+    if (p->kind == PKV_CODEC_TURBO) {
+        // TurboCodeWireV1::decode_batch (turbo-quant/src/wire.rs:401-503, 566)
+        if (len < 38) return PKV_ERR_CORRUPT_PAYLOAD;
+        if (std::memcmp(b, "TQB1", 4) != 0 || rd16(b + 4) != 1 || rd16(b + 6) != 1 || b[8] != 2)
+            return PKV_ERR_CORRUPT_PAYLOAD;
+        if (b[15] > 1) return PKV_ERR_CORRUPT_PAYLOAD;
+        const int rc = b[15];
+        if (rd32(b + 10) != p->dim || rd32(b + 18) != p->proj || rd64(b + 22) != p->seed) return PKV_ERR_CORRUPT_PAYLOAD;
+        if (b[14] != p->pbits) return PKV_ERR_CORRUPT_PAYLOAD;
+        const uint64_t n = rd32(b + 30);
+        if (rd32(b + 34) != turbo_plen(p, rc)) return PKV_ERR_CORRUPT_PAYLOAD;
+        if (len != 38 + n * turbo_plen(p, rc)) return PKV_ERR_CORRUPT_PAYLOAD;   // short, or trailing bytes
+        if (n_vectors) *n_vectors = n;
+        if (radii_codec) *radii_codec = rc;
+        return PKV_OK;
+    }
+    // FibCodeV1::decode_batch (fib-quant/src/codec.rs:323-402); trailing bytes allowed
+    if (len < 19) return PKV_ERR_CORRUPT_PAYLOAD;
+    if (std::memcmp(b, "FB2", 3) != 0 || b[3] != 1) return PKV_ERR_CORRUPT_PAYLOAD;
+    if (b[4] != p->wbits || rd32(b + 6) != p->dim / p->k) return PKV_ERR_CORRUPT_PAYLOAD;
+    const uint64_t n = rd32(b + 10);
+    if (b[14] != 0) return PKV_ERR_CORRUPT_PAYLOAD;
+    const uint64_t nlen = rd16(b + 15), ilen = rd16(b + 17);
+    if (len < 19 + n * (nlen + ilen)) return PKV_ERR_CORRUPT_PAYLOAD;
+    if (ilen != fib_plen(p) - 2) return PKV_ERR_CORRUPT_PAYLOAD;
+    if (n > 0 && nlen != 2) return PKV_ERR_CORRUPT_PAYLOAD;
+    if (n_vectors) *n_vectors = n;
+    if (radii_codec) *radii_codec = 0;
+    return PKV_OK;
+}
+
+int pkv_encode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, const float* vectors, uint64_t n,
+                             uint8_t* out, uint64_t out_cap, uint64_t* out_len, pkv_error* err) {
+    if (err) { err->status = PKV_OK; err->segment = -1; err->index = 0; }
+    if (!ctx || !prof || (!vectors && n)) return PKV_ERR_INVALID_ARG;
+    if (prof->kind == PKV_CODEC_FIB) radii_codec = PKV_RADII_F32;
+    if (radii_codec != PKV_RADII_F32 && radii_codec != PKV_RADII_LOG_U8) return PKV_ERR_INVALID_ARG;
+    const uint64_t blob = pkv_blob_len(prof, radii_codec, n);
+    if (out_len) *out_len = blob;
+    if (n == 0) return PKV_ERR_EMPTY_BATCH;
+    if (n > MAX_SEG_VECTORS) return PKV_ERR_INVALID_ARG;
+    if (!out || out_cap < blob) return PKV_ERR_CAPACITY;
+    const uint64_t in_bytes = n * prof->dim * sizeof(float);
+    const uint64_t in_pad = (in_bytes + 255) & ~static_cast<uint64_t>(255);
+    std::lock_guard<std::mutex> lock(ctx->mu);   // serialises use of ctx->scratch
+    HIP_TRY(hipSetDevice(ctx->device));
+    int rc = ensure_scratch(ctx, in_pad + blob + 256 + 64);
+    if (rc) return rc;
+    auto* d_in = static_cast<uint8_t*>(ctx->scratch);
+    uint8_t* d_wire = d_in + in_pad;
+    uint32_t* d_stat = reinterpret_cast<uint32_t*>(d_wire + ((blob + 255) & ~static_cast<uint64_t>(255)));
+    hipStream_t st = ctx->own_stream;
+    HIP_TRY(hipMemcpyAsync(d_in, vectors, in_bytes, hipMemcpyHostToDevice, st));
+    pkv_seg seg{0, 0, prof->dim, 0, static_cast<uint32_t>(n), static_cast<uint32_t>(n)};
+    rc = run_segments_locked(ctx, prof, radii_codec, true, PKV_F32, d_in, n * prof->dim, &seg, 1, d_wire, blob,
+                             d_stat, st);
+    if (rc) { (void)hipStreamSynchronize(st); return rc; }
+    uint32_t hs[2];
+    HIP_TRY(hipMemcpyAsync(hs, d_stat, sizeof hs, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(out, d_wire, blob, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    return resolve_status(prof, hs, 1, &seg, err);
+}
+
+int pkv_decode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, const uint8_t* payload, uint64_t len, float* out,
+                             uint64_t out_cap_vectors, uint64_t* n_out, pkv_error* err) {
+    if (err) { err->status = PKV_OK; err->segment = -1; err->index = 0; }
+    if (!ctx || !prof || !payload) return PKV_ERR_INVALID_ARG;
+    uint64_t n = 0;
+    int radii = 0;
+    int rc = pkv_parse_header(prof, payload, len, &n, &radii);
+    if (rc) { if (err) err->status = rc; return rc; }
+    if (n_out) *n_out = n;
+    if (n == 0) return PKV_OK;
+    if (n > MAX_SEG_VECTORS) return PKV_ERR_INVALID_ARG;
+    if (!out || out_cap_vectors < n) return PKV_ERR_CAPACITY;
+    const uint64_t blob = pkv_blob_len(prof, radii, n);
+    const uint64_t out_bytes = n * prof->dim * sizeof(float);
+    const uint64_t out_pad = (out_bytes + 255) & ~static_cast<uint64_t>(255);
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    rc = ensure_scratch(ctx, out_pad + blob + 256 + 64);
+    if (rc) return rc;
+    auto* d_out = static_cast<uint8_t*>(ctx->scratch);
+    uint8_t* d_wire = d_out + out_pad;
+    uint32_t* d_stat = reinterpret_cast<uint32_t*>(d_wire + ((blob + 255) & ~static_cast<uint64_t>(255)));
+    hipStream_t st = ctx->own_stream;
+    HIP_TRY(hipMemcpyAsync(d_wire, payload, blob, hipMemcpyHostToDevice, st));
+    pkv_seg seg{0, 0, prof->dim, 0, static_cast<uint32_t>(n), static_cast<uint32_t>(n)};
+    rc = run_segments_locked(ctx, prof, radii, false, PKV_F32, d_out, n * prof->dim, &seg, 1, d_wire, blob, d_stat,
+                             st);
+    if (rc) { (void)hipStreamSynchronize(st); return rc; }
+    uint32_t hs[2];
+    HIP_TRY(hipMemcpyAsync(hs, d_stat, sizeof hs, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(out, d_out, out_bytes, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    return resolve_status(prof, hs, 1, &seg, err);
+}
+
+int pkv_turbo_constants(uint32_t dim, uint32_t projections, uint64_t seed, float* signs, float* qjl) {
+    if (dim == 0 || (dim & (dim - 1)) != 0 || dim > 4096 || !signs) return PKV_ERR_INVALID_ARG;
+    std::vector<float> s, g;
+    make_turbo_constants(dim, qjl ? projections : 0, seed, s, g);
+    std::memcpy(signs, s.data(), s.size() * sizeof(float));
+    if (qjl && !g.empty()) std::memcpy(qjl, g.data(), g.size() * sizeof(float));
+    return PKV_OK;
+}
+
+int pkv_fib_constants(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint32_t training_samples,
+                      uint32_t lloyd_restarts, uint32_t lloyd_iterations, float* codebook, double* rotation,
+                      double* init_mse, double* training_mse) {
+    if (dim == 0 || k == 0 || dim % k != 0 || n < 2 || dim > 4096) return PKV_ERR_INVALID_ARG;
+    if (lloyd_restarts == 0 || lloyd_iterations == 0 || training_samples < n) return PKV_ERR_INVALID_ARG;
+    if (codebook) {
+        std::vector<float> cb;
+        int rc = make_fib_codebook(dim, k, n, seed, training_samples, lloyd_restarts, lloyd_iterations, cb, init_mse,
+                                   training_mse);
+        if (rc) return rc;
+        std::memcpy(codebook, cb.data(), cb.size() * sizeof(float));
+    }
+    if (rotation) {
+        std::vector<double> rot;
+        int rc = make_fib_rotation(dim, seed, rot);
+        if (rc) return rc;
+        std::memcpy(rotation, rot.data(), rot.size() * sizeof(double));
+    }
+    return PKV_OK;
+}
+
+void pkv_host_angle_bins(const float* a, const float* b, uint64_t n, uint32_t pbits, uint32_t* out) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = pbits == 3 ? angle_bin3(a[i], b[i]) : angle_bin_exact(a[i], b[i], pbits);
+}
+
+void pkv_host_logf(const float* x, uint64_t n, float* out) {
+    static const LogfEntry tab[16] = {PKV_LOGF_TABLE};
+    for (uint64_t i = 0; i < n; ++i) out[i] = og_logf_normal(x[i], tab);
+}
+
+void pkv_host_expf(const float* x, uint64_t n, float* out) {
+    static const uint64_t tab[32] = {PKV_EXP2F_TABLE};
+    for (uint64_t i = 0; i < n; ++i) out[i] = og_expf(x[i], tab);
+}
+
+}  // extern "C"

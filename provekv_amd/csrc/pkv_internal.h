@@ -1,0 +1,84 @@
+// pkv_internal.h -- declarations shared by the host and device halves of
+// libpkv_hip.so (not part of the C ABI).
+#pragma once
+#include <stdint.h>
+#include <vector>
+
+#include "../../include/pkv_codec.h"
+
+namespace pkv {
+
+// Status-word kinds (low 4 bits of a per-segment status word; the vector
+// index sits above them).
+enum Kind : uint32_t {
+    KIND_NONFINITE_INPUT = 0,
+    KIND_ZERO_NORM = 1,
+    KIND_NORM16 = 2,
+    KIND_NONFINITE_RADIUS = 3,
+    KIND_NONFINITE_RESIDUAL = 4,
+    KIND_CORRUPT = 5,
+    KIND_HEADER = 6,
+    KIND_DECODE_NONFINITE = 7,
+};
+constexpr uint32_t STATUS_NONE = 0xFFFFFFFFu;
+constexpr uint32_t MAX_SEG_VECTORS = (1u << 28) - 1;
+
+// Segment record as the kernels read it (same layout as pkv_seg).
+struct SegDev {
+    uint64_t elem_offset;
+    uint64_t stride_outer;
+    uint64_t stride_inner;
+    uint64_t wire_offset;
+    uint32_t n_vectors;
+    uint32_t group;
+};
+static_assert(sizeof(SegDev) == sizeof(pkv_seg), "segment layout");
+
+// Vectors handled by one workgroup (4 waves x 64 lanes, one vector per lane).
+constexpr uint32_t TILE = 256;
+
+struct TurboDev {
+    const float* signs;     // dim
+    const float* qjl;       // proj * dim, row-major
+    const float* cs;        // 2 * levels: cos, sin of each dequantized angle
+    uint64_t seed;
+    uint32_t dim, pbits, proj, mode;
+};
+
+struct FibDev {
+    const float* codebook;  // n * k
+    const double* rot;      // dim * dim, row-major (encode)
+    const float* rot32t;    // dim * dim, f32(rot) transposed: [col][row] (decode)
+    uint32_t dim, k, n, bits;
+};
+
+struct LaunchCommon {
+    const SegDev* segs;
+    const uint32_t* tile_start;   // nseg + 1 prefix of workgroups per segment
+    uint32_t nseg;
+    uint32_t* status;             // 2 * nseg words, or a dummy
+    uint32_t radii;               // turbo radii codec
+    uint32_t plen;                // payload bytes per vector
+    uint32_t in_bf16;             // encode input dtype
+};
+
+// Host-side profile construction (pkv_profile.cpp).
+int make_turbo_constants(uint32_t dim, uint32_t proj, uint64_t seed, std::vector<float>& signs,
+                         std::vector<float>& G);
+int make_fib_rotation(uint32_t dim, uint64_t seed, std::vector<double>& rot);
+int make_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint32_t training,
+                      uint32_t restarts, uint32_t iterations, std::vector<float>& codebook,
+                      double* init_mse, double* train_mse);
+
+// Kernel launchers (pkv_kernels.hip).  Return a hipError_t as int.
+int launch_turbo_encode(const LaunchCommon& lc, const TurboDev& td, const void* in, uint8_t* wire,
+                        uint32_t nblocks, void* stream);
+int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_t* wire, float* out,
+                        uint32_t nblocks, void* stream);
+int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire,
+                      uint32_t nblocks, void* stream);
+int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, float* out,
+                      uint32_t nblocks, void* stream);
+int launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, void* stream);
+
+}  // namespace pkv

@@ -1,0 +1,818 @@
+// pkv_kernels.hip -- gfx950 kernels for proveKV's codec hot path.
+//
+// Work decomposition (all kernels): one workgroup = 4 waves = 256 vectors of
+// ONE segment (one FB2/TQB1 blob); one lane owns one vector end to end.
+// Every (agent, layer, K|V) segment of a call is in the same grid; a
+// workgroup finds its segment by binary search over a prefix table.
+//
+// HBM traffic is staged through LDS so both sides stay coalesced whatever the
+// strides of the f32 tensor and the byte alignment of the blob:
+//   * f32 rows: 16 lanes cover one 256 B row with 16 B loads/stores; each lane
+//     then reads its own row from LDS (row pitch dim+4 floats: conflict-free
+//     ds_read_b128);
+//   * wire bytes: a wave's 64 payloads are one contiguous byte range; it is
+//     moved with aligned dword accesses and v_alignbyte, independent of the
+//     38 B (TQB1) / 19 B (FB2) header offset.
+//
+// Arithmetic follows the reference operation by operation (compiled with
+// -ffp-contract=off): the FWHT butterfly order of fwht_normalized
+// (turbo-quant/src/rotation.rs:379-398), sequential f32 QJL dots
+// (qjl.rs:215), sequential f64 norm / rotation sums (fib-quant/src/codec.rs:
+// 1049-1057, rotation.rs:107-113), the AVX2 pairwise argmin order
+// (gpu-backend/src/simd_nearest.rs:44-104) and the sequential f32 inverse
+// rotation of decode_batch_fast (rotation.rs:136-149).  Host-libm
+// transcendentals come from pkv_math.h.
+#include <hip/hip_runtime.h>
+
+#include "pkv_internal.h"
+#include "pkv_math.h"
+
+namespace pkv {
+namespace {
+
+constexpr int WAVE = 64;
+constexpr int WAVES = TILE / WAVE;
+
+__constant__ LogfEntry c_logf_tab[16] = {PKV_LOGF_TABLE};
+__constant__ uint64_t c_exp2f_tab[32] = {PKV_EXP2F_TABLE};
+
+// ------------------------------------------------------------ helpers
+__device__ __forceinline__ uint32_t find_segment(const uint32_t* __restrict__ tile_start, uint32_t nseg,
+                                                 uint32_t blk) {
+    uint32_t lo = 0, hi = nseg;
+    while (hi - lo > 1) {
+        uint32_t mid = (lo + hi) >> 1;
+        if (tile_start[mid] <= blk) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+__device__ __forceinline__ uint64_t vec_elem_offset(const SegDev& s, uint64_t i) {
+    return s.elem_offset + (i / s.group) * s.stride_outer + (i % s.group) * s.stride_inner;
+}
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ uint32_t lds_byte(const uint32_t* lds, uint32_t off) {
+    return (lds[off >> 2] >> (8 * (off & 3))) & 0xffu;
+}
+
+// Move nbytes from LDS (LDS byte 0 == dst byte 0) to global memory at any
+// byte alignment.  Needs one readable padding dword after the staged bytes.
+__device__ void lds_to_global(uint8_t* __restrict__ dst, const uint32_t* lds, uint32_t nbytes, int lane) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(dst);
+    uint32_t head = static_cast<uint32_t>((4u - (a & 3u)) & 3u);
+    if (head > nbytes) head = nbytes;
+    if (static_cast<uint32_t>(lane) < head) dst[lane] = static_cast<uint8_t>(lds_byte(lds, lane));
+    const uint32_t body = (nbytes - head) >> 2;
+    uint32_t* d32 = reinterpret_cast<uint32_t*>(dst + head);
+    const uint32_t sh = head;   // 0..3
+    for (uint32_t k = lane; k < body; k += WAVE) {
+        const uint32_t q = (head >> 2) + k;    // head < 4, so q == k
+        uint32_t w0 = lds[q], w1 = lds[q + 1];
+        d32[k] = sh ? __builtin_amdgcn_alignbyte(w1, w0, sh) : w0;
+    }
+    const uint32_t t0 = head + (body << 2);
+    const uint32_t tail = nbytes - t0;
+    if (static_cast<uint32_t>(lane) < tail) dst[t0 + lane] = static_cast<uint8_t>(lds_byte(lds, t0 + lane));
+}
+
+// Move nbytes from global memory at any byte alignment into LDS (LDS byte 0 ==
+// src byte 0).  Only aligned dwords holding at least one source byte are read.
+__device__ void global_to_lds(uint32_t* lds, const uint8_t* __restrict__ src, uint32_t nbytes, int lane) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(src);
+    const uint32_t* s32 = reinterpret_cast<const uint32_t*>(a & ~static_cast<uintptr_t>(3));
+    const uint32_t sh = static_cast<uint32_t>(a & 3u);
+    const uint32_t ndw = (nbytes + 3u) >> 2;
+    const uintptr_t last = a + nbytes - 1;   // last valid byte
+    for (uint32_t k = lane; k < ndw; k += WAVE) {
+        uint32_t w0 = s32[k];
+        uint32_t v = w0;
+        if (sh) {
+            uintptr_t next = (a & ~static_cast<uintptr_t>(3)) + 4u * (k + 1);
+            uint32_t w1 = (next <= last) ? s32[k + 1] : 0u;
+            v = __builtin_amdgcn_alignbyte(w1, w0, sh);
+        }
+        lds[k] = v;
+    }
+}
+
+// Stage nv rows of DIM values (f32, or bf16 upcast) into LDS rows of pitch
+// DIM+4 floats.  16-byte loads; DIM/4 (f32) lanes cover one row.
+template <int DIM>
+__device__ void stage_rows_in(float* stage, const void* __restrict__ in, bool bf16, const SegDev& s,
+                              uint32_t v0, uint32_t nv, int lane) {
+    constexpr int PITCH = DIM + 4;
+    if (!bf16) {
+        const float* fin = static_cast<const float*>(in);
+        constexpr int Q = DIM / 4;
+        for (uint32_t i = lane; i < nv * Q; i += WAVE) {
+            uint32_t r = i / Q, c = i % Q;
+            uint64_t off = vec_elem_offset(s, v0 + r);
+            float4 v = *reinterpret_cast<const float4*>(fin + off + 4 * c);
+            *reinterpret_cast<float4*>(stage + r * PITCH + 4 * c) = v;
+        }
+    } else {
+        const uint16_t* hin = static_cast<const uint16_t*>(in);
+        constexpr int Q = DIM / 8;
+        for (uint32_t i = lane; i < nv * Q; i += WAVE) {
+            uint32_t r = i / Q, c = i % Q;
+            uint64_t off = vec_elem_offset(s, v0 + r);
+            uint4 v = *reinterpret_cast<const uint4*>(hin + off + 8 * c);
+            float* d = stage + r * PITCH + 8 * c;
+            uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                d[2 * t] = u2f(w[t] << 16);
+                d[2 * t + 1] = u2f(w[t] & 0xffff0000u);
+            }
+        }
+    }
+}
+
+template <int DIM>
+__device__ void stage_rows_out(float* __restrict__ out, const float* stage, const SegDev& s, uint32_t v0,
+                               uint32_t nv, uint32_t skip_mask_lo, uint32_t skip_mask_hi, int lane) {
+    constexpr int PITCH = DIM + 4;
+    constexpr int Q = DIM / 4;
+    for (uint32_t i = lane; i < nv * Q; i += WAVE) {
+        uint32_t r = i / Q, c = i % Q;
+        uint32_t skip = r < 32 ? (skip_mask_lo >> r) & 1u : (skip_mask_hi >> (r - 32)) & 1u;
+        if (skip) continue;
+        uint64_t off = vec_elem_offset(s, v0 + r);
+        *reinterpret_cast<float4*>(out + off + 4 * c) = *reinterpret_cast<const float4*>(stage + r * PITCH + 4 * c);
+    }
+}
+
+// In-register fwht_normalized (turbo-quant/src/rotation.rs:379-398): stages
+// step = 1, 2, 4, ...; (a + b, a - b) at (start+off, start+off+step).
+template <int DIM>
+__device__ __forceinline__ void fwht(float (&v)[DIM]) {
+#pragma unroll
+    for (int step = 1; step < DIM; step *= 2) {
+#pragma unroll
+        for (int start = 0; start < DIM; start += 2 * step) {
+#pragma unroll
+            for (int off = 0; off < step; ++off) {
+                float a = v[start + off], b = v[start + off + step];
+                v[start + off] = a + b;
+                v[start + off + step] = a - b;
+            }
+        }
+    }
+}
+
+// (n as f32).sqrt().recip(): 0.125 for 64; 1/f32(sqrt(128)) for 128.
+template <int DIM>
+__device__ __forceinline__ float fwht_scale() {
+    return DIM == 64 ? 0.125f : 1.0f / __builtin_sqrtf(static_cast<float>(DIM));
+}
+
+__device__ __forceinline__ void status_fail(uint32_t* status, uint32_t seg, int word, uint32_t index,
+                                            uint32_t kind) {
+    atomicMin(status + 2 * seg + word, (index << 4) | kind);
+}
+
+// TQB1 header byte i (turbo-quant/src/wire.rs:267-346).
+__device__ __forceinline__ uint32_t tqb1_byte(uint32_t i, uint32_t dim, uint32_t pbits, uint32_t radii,
+                                              uint32_t proj, uint64_t seed, uint32_t n, uint32_t plen) {
+    if (i < 4) return (0x31425154u >> (8 * i)) & 0xffu;          // "TQB1"
+    if (i == 4) return 1u;
+    if (i == 6) return 1u;                                       // FastHadamard
+    if (i == 8) return 2u;
+    if (i >= 10 && i < 14) return (dim >> (8 * (i - 10))) & 0xffu;
+    if (i == 14) return pbits;
+    if (i == 15) return radii ? 1u : 0u;
+    if (i >= 18 && i < 22) return (proj >> (8 * (i - 18))) & 0xffu;
+    if (i >= 22 && i < 30) return static_cast<uint32_t>(seed >> (8 * (i - 22))) & 0xffu;
+    if (i >= 30 && i < 34) return (n >> (8 * (i - 30))) & 0xffu;
+    if (i >= 34 && i < 38) return (plen >> (8 * (i - 34))) & 0xffu;
+    return 0u;
+}
+
+// Bytes the TQB1 decoder checks (wire.rs:401-503): all but 9, 16, 17.
+__device__ __forceinline__ bool tqb1_checked(uint32_t i) { return i < 38 && i != 9 && i != 16 && i != 17; }
+
+// FB2 header byte i (fib-quant/src/codec.rs:195-320), n_blocks = n.
+__device__ __forceinline__ uint32_t fb2_byte(uint32_t i, uint32_t bits, uint32_t blocks, uint32_t n,
+                                             uint32_t ilen) {
+    if (i < 3) return (0x324246u >> (8 * i)) & 0xffu;             // "FB2"
+    if (i == 3) return 1u;
+    if (i == 4) return bits;
+    if (i >= 6 && i < 10) return (blocks >> (8 * (i - 6))) & 0xffu;
+    if (i >= 10 && i < 14) return (n >> (8 * (i - 10))) & 0xffu;
+    if (i == 15) return 2u;
+    if (i == 17) return ilen & 0xffu;
+    if (i == 18) return (ilen >> 8) & 0xffu;
+    return 0u;
+}
+
+// Bytes the FB2 decoder checks (codec.rs:323-424): all but 5; the norm length
+// only matters when there is at least one vector (decode_norm, 1025-1031).
+__device__ __forceinline__ bool fb2_checked(uint32_t i, uint32_t n) {
+    if (i == 5) return false;
+    if ((i == 15 || i == 16) && n == 0) return false;
+    return i < 19;
+}
+
+// ------------------------------------------------------------ turbo encode
+template <int DIM, int PB>
+__global__ __launch_bounds__(TILE) void turbo_encode_kernel(
+    LaunchCommon lc, const void* __restrict__ in, uint8_t* __restrict__ wire,
+    const float* __restrict__ signs, const float* __restrict__ qjl, const float* __restrict__ cs_tab,
+    uint64_t seed, uint32_t pbits_rt, uint32_t proj, uint32_t mode) {
+    constexpr int PITCH = DIM + 4;
+    constexpr int PAIRS = DIM / 2;
+    constexpr int WAVE_FLOATS = WAVE * PITCH + 8;
+    extern __shared__ float smem[];
+    __shared__ float cs_lds[512];
+    __shared__ LogfEntry logf_lds[16];
+
+    const uint32_t pbits = PB ? static_cast<uint32_t>(PB) : pbits_rt;
+    const uint32_t levels = 1u << pbits;
+    for (uint32_t t = threadIdx.x; t < 2 * levels; t += blockDim.x) cs_lds[t] = cs_tab[t];
+    if (threadIdx.x < 16) logf_lds[threadIdx.x] = c_logf_tab[threadIdx.x];
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* stage = smem + wave * WAVE_FLOATS;
+    const uint32_t blk = blockIdx.x;
+    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const SegDev seg = lc.segs[sidx];
+    const uint32_t tile = blk - lc.tile_start[sidx];
+    const uint32_t v0 = tile * TILE + wave * WAVE;
+    const uint32_t plen = lc.plen;
+    uint8_t* blob = wire + seg.wire_offset;
+
+    if (v0 < seg.n_vectors) {
+        const uint32_t nv = min(static_cast<uint32_t>(WAVE), seg.n_vectors - v0);
+        stage_rows_in<DIM>(stage, in, lc.in_bf16 != 0, seg, v0, nv, lane);
+        wave_sync();
+
+        const bool active = static_cast<uint32_t>(lane) < nv;
+        const float* xr = stage + lane * PITCH;
+        const float scale = fwht_scale<DIM>();
+        // Lanes past the segment end compute on stale LDS; their results are
+        // never stored.
+        float y[DIM];
+        bool finite = true;
+#pragma unroll
+        for (int c = 0; c < DIM; ++c) {
+            float xv = xr[c];
+            finite &= isfinite_f(xv);
+            y[c] = xv * signs[c];
+        }
+        fwht<DIM>(y);
+#pragma unroll
+        for (int c = 0; c < DIM; ++c) y[c] *= scale;
+
+        // radii and angle bins (polar.rs:246-266, 413-421): octant fast path;
+        // pairs near an octant line (and every pair when pbits != 3) take the
+        // exact libm formula in a rolled loop below.  Bins are kept packed
+        // LSB-first exactly as the wire stores them (bitpack.rs:21-35).
+        constexpr int NW = PB ? (PAIRS * PB + 31) / 32 : 1;
+        float r[PAIRS];
+        uint32_t bw[PB ? NW : 1];
+        uint32_t bins_rt[PB ? 1 : PAIRS];
+#pragma unroll
+        for (int t = 0; t < (PB ? NW : 1); ++t) bw[t] = 0u;
+        uint64_t slow = 0;
+        bool rfinite = true;
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+            float a = y[2 * i], b = y[2 * i + 1];
+            float aa = a * a, bb = b * b;
+            r[i] = __builtin_sqrtf(aa + bb);
+            rfinite &= isfinite_f(r[i]);
+            bool safe = false;
+            if (PB == 3) {
+                const uint32_t bin = octant_bin(a, b, safe);
+                const int bit = 3 * i;
+                bw[bit >> 5] |= bin << (bit & 31);
+                if ((bit & 31) > 29) bw[(bit >> 5) + 1] |= bin >> (32 - (bit & 31));
+            }
+            if (!safe) slow |= 1ull << i;
+        }
+        if (slow) {
+            for (int i = 0; i < PAIRS; ++i) {
+                if (!((slow >> i) & 1ull)) continue;
+                float a = 0.0f, b = 0.0f;
+#pragma unroll
+                for (int k = 0; k < PAIRS; ++k) {
+                    a = (k == i) ? y[2 * k] : a;
+                    b = (k == i) ? y[2 * k + 1] : b;
+                }
+                const uint32_t bin = angle_bin_exact(a, b, pbits);
+                if (PB == 3) {
+                    const uint32_t bit = 3u * static_cast<uint32_t>(i);
+                    const uint32_t wd = bit >> 5, sh = bit & 31u;
+#pragma unroll
+                    for (int t = 0; t < (PB ? NW : 1); ++t) {
+                        if (static_cast<uint32_t>(t) == wd) bw[t] = (bw[t] & ~(7u << sh)) | (bin << sh);
+                        if (sh > 29 && static_cast<uint32_t>(t) == wd + 1)
+                            bw[t] = (bw[t] & ~(7u >> (32 - sh))) | (bin >> (32 - sh));
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < (PB ? 1 : PAIRS); ++k) bins_rt[k] = (k == i) ? bin : bins_rt[k];
+                }
+            }
+        }
+        auto bin_of = [&](int i) -> uint32_t {
+            if (PB == 3) {
+                const int bit = 3 * i;
+                uint32_t v = bw[bit >> 5] >> (bit & 31);
+                if ((bit & 31) > 29) v |= bw[(bit >> 5) + 1] << (32 - (bit & 31));
+                return v & 7u;
+            }
+            return bins_rt[PB ? 0 : i];
+        };
+
+        uint32_t sbits0 = 0u, sbits1 = 0u;
+        bool resfinite = true;
+        if (mode) {
+            // polar decode of the code just produced (polar.rs:272-278, 306-316)
+#pragma unroll
+            for (int i = 0; i < PAIRS; ++i) {
+                const uint32_t bin = bin_of(i);
+                y[2 * i] = r[i] * cs_lds[2 * bin];
+                y[2 * i + 1] = r[i] * cs_lds[2 * bin + 1];
+            }
+            fwht<DIM>(y);
+#pragma unroll
+            for (int c = 0; c < DIM; ++c) {
+                float z = (y[c] * scale) * signs[c];
+                y[c] = xr[c] - z;                 // residual (turbo.rs:269-273)
+                resfinite &= isfinite_f(y[c]);
+            }
+            // QJL sketch (qjl.rs:203-220): sequential f32 dot per row.
+            for (uint32_t j = 0; j < proj; ++j) {
+                const float* g = qjl + static_cast<size_t>(j) * DIM;
+                float dot = 0.0f;
+#pragma unroll
+                for (int c = 0; c < DIM; ++c) dot = dot + g[c] * y[c];
+                const uint32_t bit = dot >= 0.0f ? 1u << (j & 31) : 0u;
+                if (j < 32) sbits0 |= bit; else sbits1 |= bit;
+            }
+        }
+
+        // status: first failing vector (turbo encode is per-vector in order)
+        if (active) {
+            uint32_t vi = v0 + lane;
+            if (!finite) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_INPUT);
+            else if (!rfinite) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RADIUS);
+            else if (mode && !resfinite) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RESIDUAL);
+        }
+        wave_sync();   // every lane is done reading its staged row
+
+        // payload into LDS (plen is a dword multiple for every profile the
+        // host accepts; every field starts dword aligned).
+        uint32_t* pw = reinterpret_cast<uint32_t*>(stage) + lane * (plen >> 2);
+        if (active) {
+            uint32_t w = 0;
+            if (lc.radii == PKV_RADII_F32) {
+#pragma unroll
+                for (int i = 0; i < PAIRS; ++i) pw[w++] = f2u(r[i]);
+            } else {
+                // CompressedRadiiV1 BlockLogU8 (turbo-quant/src/radius.rs:58-77)
+                float lg[PAIRS];
+                float mn = u2f(0x7f800000u), mx = u2f(0xff800000u);
+#pragma unroll
+                for (int i = 0; i < PAIRS; ++i) {
+                    float v = r[i] < 1.17549435e-38f ? 1.17549435e-38f : r[i];
+                    lg[i] = og_logf_normal(v, logf_lds);
+                    mn = __builtin_fminf(mn, lg[i]);
+                    mx = __builtin_fmaxf(mx, lg[i]);
+                }
+                float span = __builtin_fmaxf(mx - mn, 1.1920929e-07f);
+#pragma unroll
+                for (int i = 0; i < PAIRS; i += 4) {
+                    uint32_t packed = 0;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        float nrm = (lg[i + t] - mn) / span;
+                        nrm = nrm < 0.0f ? 0.0f : (nrm > 1.0f ? 1.0f : nrm);
+                        float q = __builtin_roundf(nrm * 255.0f);
+                        packed |= static_cast<uint32_t>(q) << (8 * t);
+                    }
+                    pw[w++] = packed;
+                }
+                pw[w++] = f2u(mn);
+                pw[w++] = f2u(mx);
+            }
+            // angle indices, pbits each, LSB-first (bitpack.rs:21-35)
+            if (PB == 3) {
+#pragma unroll
+                for (int t = 0; t < (PB ? NW : 1); ++t) pw[w++] = bw[t];
+            } else {
+                uint64_t acc = 0;
+                uint32_t nb = 0;
+                for (int i = 0; i < PAIRS; ++i) {
+                    acc |= static_cast<uint64_t>(bin_of(i)) << nb;
+                    nb += pbits;
+                    if (nb >= 32) { pw[w++] = static_cast<uint32_t>(acc); acc >>= 32; nb -= 32; }
+                }
+                if (nb) pw[w++] = static_cast<uint32_t>(acc);
+            }
+            if (mode) {
+                pw[w++] = sbits0;
+                if (proj > 32) pw[w++] = sbits1;
+            }
+        }
+        wave_sync();
+        lds_to_global(blob + 38 + static_cast<uint64_t>(v0) * plen, reinterpret_cast<uint32_t*>(stage),
+                      nv * plen, lane);
+    }
+    if (tile == 0 && threadIdx.x < 38) {
+        blob[threadIdx.x] = static_cast<uint8_t>(
+            tqb1_byte(threadIdx.x, DIM, pbits, lc.radii, mode ? proj : 0u, seed, seg.n_vectors, plen));
+    }
+}
+
+// ------------------------------------------------------------ turbo decode
+template <int DIM, int PB>
+__global__ __launch_bounds__(TILE) void turbo_decode_kernel(
+    LaunchCommon lc, const uint8_t* __restrict__ wire, float* __restrict__ out,
+    const float* __restrict__ signs, const float* __restrict__ cs_tab, uint64_t seed, uint32_t pbits_rt,
+    uint32_t proj, uint32_t mode) {
+    constexpr int PITCH = DIM + 4;
+    constexpr int PAIRS = DIM / 2;
+    constexpr int WAVE_FLOATS = WAVE * PITCH + 8;
+    extern __shared__ float smem[];
+    __shared__ float cs_lds[512];
+    __shared__ uint64_t exp_lds[32];
+
+    const uint32_t pbits = PB ? static_cast<uint32_t>(PB) : pbits_rt;
+    const uint32_t levels = 1u << pbits;
+    for (uint32_t t = threadIdx.x; t < 2 * levels; t += blockDim.x) cs_lds[t] = cs_tab[t];
+    if (threadIdx.x < 32) exp_lds[threadIdx.x] = c_exp2f_tab[threadIdx.x];
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* stage = smem + wave * WAVE_FLOATS;
+    const uint32_t blk = blockIdx.x;
+    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const SegDev seg = lc.segs[sidx];
+    const uint32_t tile = blk - lc.tile_start[sidx];
+    const uint32_t v0 = tile * TILE + wave * WAVE;
+    const uint32_t plen = lc.plen;
+    const uint8_t* blob = wire + seg.wire_offset;
+
+    // header check (every wave; 38 bytes)
+    const uint32_t psign = mode ? proj : 0u;
+    uint32_t hb = lane < 38 ? blob[lane] : 0u;
+    bool bad = lane < 38 && tqb1_checked(lane) &&
+               hb != tqb1_byte(lane, DIM, pbits, lc.radii, psign, seed, seg.n_vectors, plen);
+    if (__ballot(bad) != 0ull) {
+        if (lane == 0) status_fail(lc.status, sidx, 0, 0u, KIND_HEADER);
+        return;
+    }
+    if (v0 >= seg.n_vectors) return;
+    const uint32_t nv = min(static_cast<uint32_t>(WAVE), seg.n_vectors - v0);
+    uint32_t* sw = reinterpret_cast<uint32_t*>(stage);
+    global_to_lds(sw, blob + 38 + static_cast<uint64_t>(v0) * plen, nv * plen, lane);
+    wave_sync();
+
+    const bool active = static_cast<uint32_t>(lane) < nv;
+    const uint32_t* pw = sw + lane * (plen >> 2);
+    float r[PAIRS];
+    uint32_t bins[PAIRS];
+    bool ok = true;
+    uint32_t w = 0;
+    if (active) {
+        if (lc.radii == PKV_RADII_F32) {
+#pragma unroll
+            for (int i = 0; i < PAIRS; ++i) {
+                r[i] = u2f(pw[w++]);
+                ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);   // radius.rs:88-104
+            }
+        } else {
+            uint32_t q[PAIRS / 4];
+#pragma unroll
+            for (int i = 0; i < PAIRS / 4; ++i) q[i] = pw[w++];
+            float mn = u2f(pw[w++]), mx = u2f(pw[w++]);
+            ok &= isfinite_f(mn) && isfinite_f(mx) && !(mn > mx);   // radius.rs:171-177
+            float span = mx - mn;
+#pragma unroll
+            for (int i = 0; i < PAIRS; ++i) {
+                float u = static_cast<float>((q[i >> 2] >> (8 * (i & 3))) & 0xffu);
+                r[i] = og_expf(mn + span * (u / 255.0f), exp_lds);   // radius.rs:128-145
+                ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);     // polar.rs:127-133
+            }
+        }
+        uint64_t acc = 0;
+        uint32_t nb = 0;
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+            if (nb < pbits) { acc |= static_cast<uint64_t>(pw[w++]) << nb; nb += 32; }
+            bins[i] = static_cast<uint32_t>(acc) & (levels - 1u);
+            acc >>= pbits;
+            nb -= pbits;
+        }
+        // padding of the last angle word must be zero (bitpack.rs:88-109);
+        // dword-multiple angle fields have none, the check stays for safety.
+        if (acc != 0) ok = false;
+        if (mode && (proj & 31u)) {
+            uint32_t last = pw[w + ((proj - 1) >> 5)];
+            if (last >> (proj & 31u)) ok = false;
+        }
+    }
+    wave_sync();   // payload words are in registers now
+
+    uint32_t skip_lo = 0, skip_hi = 0;
+    if (active) {
+        float y[DIM];
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+            y[2 * i] = r[i] * cs_lds[2 * bins[i]];
+            y[2 * i + 1] = r[i] * cs_lds[2 * bins[i] + 1];
+        }
+        fwht<DIM>(y);
+        const float scale = fwht_scale<DIM>();
+        float* orow = stage + lane * PITCH;
+#pragma unroll
+        for (int c = 0; c < DIM; ++c) orow[c] = (y[c] * scale) * signs[c];
+        if (!ok) status_fail(lc.status, sidx, 1, v0 + lane, KIND_CORRUPT);
+    }
+    uint64_t badmask = __ballot(active && !ok);
+    skip_lo = static_cast<uint32_t>(badmask);
+    skip_hi = static_cast<uint32_t>(badmask >> 32);
+    wave_sync();
+    stage_rows_out<DIM>(out, stage, seg, v0, nv, skip_lo, skip_hi, lane);
+}
+
+// ------------------------------------------------------------ fib encode
+// FibQuantizer::encode_batch (fib-quant/src/codec.rs:578-729; n < 4 takes
+// FibQuantizer::encode, 471-516) + FibCodeV1::encode_batch (FB2, 225-320).
+template <int DIM>
+__global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const void* __restrict__ in,
+                                                          uint8_t* __restrict__ wire,
+                                                          const double* __restrict__ rot,
+                                                          const float* __restrict__ cb) {
+    constexpr int PITCH = DIM + 4;
+    constexpr int BLOCKS = DIM / 4;
+    constexpr int WAVE_FLOATS = WAVE * PITCH + 8;
+    constexpr uint32_t PLEN = 2 + (BLOCKS * 5 + 7) / 8;
+    extern __shared__ float smem[];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* stage = smem + wave * WAVE_FLOATS;
+    const uint32_t blk = blockIdx.x;
+    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const SegDev seg = lc.segs[sidx];
+    const uint32_t tile = blk - lc.tile_start[sidx];
+    const uint32_t v0 = tile * TILE + wave * WAVE;
+    uint8_t* blob = wire + seg.wire_offset;
+    const bool small = seg.n_vectors < 4;
+
+    if (v0 < seg.n_vectors) {
+        const uint32_t nv = min(static_cast<uint32_t>(WAVE), seg.n_vectors - v0);
+        stage_rows_in<DIM>(stage, in, lc.in_bf16 != 0, seg, v0, nv, lane);
+        wave_sync();
+        const bool active = static_cast<uint32_t>(lane) < nv;
+        const float* xr = stage + lane * PITCH;
+
+        // l2_norm (codec.rs:1049-1057) and finiteness (check_finite)
+        bool finite = true;
+        double ss = 0.0;
+#pragma unroll
+        for (int c = 0; c < DIM; ++c) {
+            float xv = active ? xr[c] : 1.0f;
+            finite &= isfinite_f(xv);
+            double dv = static_cast<double>(xv);
+            ss = ss + dv * dv;
+        }
+        const double nrm = __builtin_sqrt(ss);
+        const bool zero = finite && nrm == 0.0;
+        const double safe_nrm = (finite && !zero) ? nrm : 1.0;
+
+        // x_hat = f32(x / norm) on the batch path (codec.rs:608) and
+        // rho = f32(Pi x_hat), each row a sequential f64 sum
+        // (rotation.rs:107-113); the single-vector path (n < 4, codec.rs:481)
+        // keeps x / norm in f64 and recomputes it per row.
+        float xh[DIM];
+#pragma unroll
+        for (int c = 0; c < DIM; ++c)
+            xh[c] = static_cast<float>(static_cast<double>(active ? xr[c] : 0.0f) / safe_nrm);
+        uint64_t lo = 0, hi = 0;   // 16 x 5-bit indices, LSB-first
+        for (int b = 0; b < BLOCKS; ++b) {
+            float s4[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const double* m = rot + static_cast<size_t>(4 * b + t) * DIM;
+                double acc = 0.0;
+                if (!small) {
+#pragma unroll
+                    for (int c = 0; c < DIM; ++c) acc = acc + m[c] * static_cast<double>(xh[c]);
+                } else {
+                    for (int c = 0; c < DIM; ++c)
+                        acc = acc + m[c] * (static_cast<double>(active ? xr[c] : 0.0f) / safe_nrm);
+                }
+                s4[t] = static_cast<float>(acc);
+            }
+            // argmin: AVX2 pairwise order, strict <, lowest index wins
+            float bd = u2f(0x7f800000u);
+            uint32_t best = 0;
+#pragma unroll 8
+            for (int wv = 0; wv < 32; ++wv) {
+                const float* c = cb + 4 * wv;
+                float e0 = c[0] - s4[0], e1 = c[1] - s4[1], e2 = c[2] - s4[2], e3 = c[3] - s4[3];
+                float d = (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
+                if (d < bd) { bd = d; best = static_cast<uint32_t>(wv); }
+            }
+            const int bit = 5 * b;
+            if (bit < 64) {
+                lo |= static_cast<uint64_t>(best) << bit;
+                if (bit > 59) hi |= static_cast<uint64_t>(best) >> (64 - bit);
+            } else {
+                hi |= static_cast<uint64_t>(best) << (bit - 64);
+            }
+        }
+        // encode_norm Fp16Paper (codec.rs:994-1020)
+        const uint16_t h = f32_to_f16(static_cast<float>(nrm));
+        const bool h_ok = (h & 0x7c00u) != 0x7c00u && (h & 0x7fffu) != 0 && !(h & 0x8000u);
+
+        if (active) {
+            uint32_t vi = v0 + lane;
+            if (!finite) status_fail(lc.status, sidx, 0, vi, KIND_NONFINITE_INPUT);
+            else if (zero) status_fail(lc.status, sidx, 0, vi, KIND_ZERO_NORM);
+            else if (!h_ok) status_fail(lc.status, sidx, 1, vi, KIND_NORM16);
+        }
+        wave_sync();
+        // payload: [f16 norm][16 x 5-bit indices] = 12 bytes, dword aligned
+        uint32_t* pw = reinterpret_cast<uint32_t*>(stage) + lane * (PLEN / 4);
+        if (active) {
+            pw[0] = static_cast<uint32_t>(h) | (static_cast<uint32_t>(lo) << 16);
+            pw[1] = static_cast<uint32_t>(lo >> 16);
+            pw[2] = static_cast<uint32_t>(lo >> 48) | (static_cast<uint32_t>(hi) << 16);
+        }
+        wave_sync();
+        lds_to_global(blob + 19 + static_cast<uint64_t>(v0) * PLEN, reinterpret_cast<uint32_t*>(stage),
+                      nv * PLEN, lane);
+    }
+    if (tile == 0 && threadIdx.x < 19)
+        blob[threadIdx.x] = static_cast<uint8_t>(fb2_byte(threadIdx.x, 5u, BLOCKS, seg.n_vectors, PLEN - 2));
+}
+
+// ------------------------------------------------------------ fib decode
+// FibCodeV1::decode_batch (codec.rs:323-424) + decode_batch_fast (797-844).
+template <int DIM>
+__global__ __launch_bounds__(TILE) void fib_decode_kernel(LaunchCommon lc, const uint8_t* __restrict__ wire,
+                                                          float* __restrict__ out,
+                                                          const float* __restrict__ rot32t,
+                                                          const float* __restrict__ cb) {
+    constexpr int PITCH = DIM + 4;
+    constexpr int BLOCKS = DIM / 4;
+    constexpr int WAVE_FLOATS = WAVE * PITCH + 8;
+    constexpr uint32_t PLEN = 2 + (BLOCKS * 5 + 7) / 8;
+    extern __shared__ float smem[];
+    __shared__ float cb_lds[32 * 4];
+    if (threadIdx.x < 128) cb_lds[threadIdx.x] = cb[threadIdx.x];
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* stage = smem + wave * WAVE_FLOATS;
+    const uint32_t blk = blockIdx.x;
+    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const SegDev seg = lc.segs[sidx];
+    const uint32_t tile = blk - lc.tile_start[sidx];
+    const uint32_t v0 = tile * TILE + wave * WAVE;
+    const uint8_t* blob = wire + seg.wire_offset;
+
+    uint32_t hb = lane < 19 ? blob[lane] : 0u;
+    bool bad = lane < 19 && fb2_checked(lane, seg.n_vectors) &&
+               hb != fb2_byte(lane, 5u, BLOCKS, seg.n_vectors, PLEN - 2);
+    if (lane == 14 && hb != 0u) bad = true;   // norm format must be Fp16Paper
+    if (__ballot(bad) != 0ull) {
+        if (lane == 0) status_fail(lc.status, sidx, 0, 0u, KIND_HEADER);
+        return;
+    }
+    if (v0 >= seg.n_vectors) return;
+    const uint32_t nv = min(static_cast<uint32_t>(WAVE), seg.n_vectors - v0);
+    uint32_t* sw = reinterpret_cast<uint32_t*>(stage);
+    global_to_lds(sw, blob + 19 + static_cast<uint64_t>(v0) * PLEN, nv * PLEN, lane);
+    wave_sync();
+    const bool active = static_cast<uint32_t>(lane) < nv;
+    uint32_t p0 = 0, p1 = 0, p2 = 0;
+    if (active) {
+        const uint32_t* pw = sw + lane * (PLEN / 4);
+        p0 = pw[0]; p1 = pw[1]; p2 = pw[2];
+    }
+    wave_sync();
+    const uint16_t h = static_cast<uint16_t>(p0 & 0xffffu);
+    const float nv32 = f16_to_f32(h);
+    bool ok = isfinite_f(nv32) && nv32 > 0.0f;
+    const uint64_t lo = (static_cast<uint64_t>(p0) >> 16) | (static_cast<uint64_t>(p1) << 16) |
+                        (static_cast<uint64_t>(p2) << 48);
+    const uint32_t hi = p2 >> 16;
+    float c[DIM];
+#pragma unroll
+    for (int b = 0; b < BLOCKS; ++b) {
+        const int bit = 5 * b;
+        uint32_t w;
+        if (bit + 5 <= 64) w = static_cast<uint32_t>(lo >> bit) & 31u;
+        else if (bit >= 64) w = (hi >> (bit - 64)) & 31u;
+        else w = (static_cast<uint32_t>(lo >> bit) | (hi << (64 - bit))) & 31u;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) c[4 * b + t] = cb_lds[4 * w + t];
+    }
+    float* orow = stage + lane * PITCH;
+    bool ofinite = true;
+    for (int col = 0; col < DIM; ++col) {
+        float s = 0.0f;
+#pragma unroll
+        for (int row = 0; row < DIM; ++row) s = s + rot32t[col * DIM + row] * c[row];
+        float o = s * nv32;
+        ofinite &= isfinite_f(o);
+        if (active) orow[col] = o;
+    }
+    if (active) {
+        if (!ok) status_fail(lc.status, sidx, 1, v0 + lane, KIND_CORRUPT);
+        else if (!ofinite) status_fail(lc.status, sidx, 1, v0 + lane, KIND_DECODE_NONFINITE);
+    }
+    uint64_t badmask = __ballot(active && !(ok && ofinite));
+    wave_sync();
+    stage_rows_out<DIM>(out, stage, seg, v0, nv, static_cast<uint32_t>(badmask),
+                        static_cast<uint32_t>(badmask >> 32), lane);
+}
+
+__global__ void fill_u32_kernel(uint32_t* p, uint32_t value, uint64_t n) {
+    uint64_t i = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+    if (i < n) p[i] = value;
+}
+
+template <int DIM>
+constexpr size_t stage_bytes() {
+    return static_cast<size_t>(WAVES) * (WAVE * (DIM + 4) + 8) * sizeof(float);
+}
+
+}  // namespace
+
+int launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, void* stream) {
+    if (n == 0) return hipSuccess;
+    uint32_t blocks = static_cast<uint32_t>((n + 255) / 256);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), p, value, n);
+    return hipGetLastError();
+}
+
+int launch_turbo_encode(const LaunchCommon& lc, const TurboDev& td, const void* in, uint8_t* wire,
+                        uint32_t nblocks, void* stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (td.dim == 64) {
+        if (td.pbits == 3)
+            hipLaunchKernelGGL((turbo_encode_kernel<64, 3>), dim3(nblocks), dim3(TILE), stage_bytes<64>(), st, lc, in,
+                               wire, td.signs, td.qjl, td.cs, td.seed, td.pbits, td.proj, td.mode);
+        else
+            hipLaunchKernelGGL((turbo_encode_kernel<64, 0>), dim3(nblocks), dim3(TILE), stage_bytes<64>(), st, lc, in,
+                               wire, td.signs, td.qjl, td.cs, td.seed, td.pbits, td.proj, td.mode);
+    } else {
+        if (td.pbits == 3)
+            hipLaunchKernelGGL((turbo_encode_kernel<128, 3>), dim3(nblocks), dim3(TILE), stage_bytes<128>(), st, lc,
+                               in, wire, td.signs, td.qjl, td.cs, td.seed, td.pbits, td.proj, td.mode);
+        else
+            hipLaunchKernelGGL((turbo_encode_kernel<128, 0>), dim3(nblocks), dim3(TILE), stage_bytes<128>(), st, lc,
+                               in, wire, td.signs, td.qjl, td.cs, td.seed, td.pbits, td.proj, td.mode);
+    }
+    return hipGetLastError();
+}
+
+int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_t* wire, float* out,
+                        uint32_t nblocks, void* stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (td.dim == 64) {
+        if (td.pbits == 3)
+            hipLaunchKernelGGL((turbo_decode_kernel<64, 3>), dim3(nblocks), dim3(TILE), stage_bytes<64>(), st, lc, wire,
+                               out, td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode);
+        else
+            hipLaunchKernelGGL((turbo_decode_kernel<64, 0>), dim3(nblocks), dim3(TILE), stage_bytes<64>(), st, lc, wire,
+                               out, td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode);
+    } else {
+        if (td.pbits == 3)
+            hipLaunchKernelGGL((turbo_decode_kernel<128, 3>), dim3(nblocks), dim3(TILE), stage_bytes<128>(), st, lc,
+                               wire, out, td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode);
+        else
+            hipLaunchKernelGGL((turbo_decode_kernel<128, 0>), dim3(nblocks), dim3(TILE), stage_bytes<128>(), st, lc,
+                               wire, out, td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode);
+    }
+    return hipGetLastError();
+}
+
+int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire, uint32_t nblocks,
+                      void* stream) {
+    hipLaunchKernelGGL((fib_encode_kernel<64>), dim3(nblocks), dim3(TILE), stage_bytes<64>(),
+                       static_cast<hipStream_t>(stream), lc, in, wire, fd.rot, fd.codebook);
+    return hipGetLastError();
+}
+
+int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, float* out, uint32_t nblocks,
+                      void* stream) {
+    hipLaunchKernelGGL((fib_decode_kernel<64>), dim3(nblocks), dim3(TILE), stage_bytes<64>(),
+                       static_cast<hipStream_t>(stream), lc, wire, out, fd.rot32t, fd.codebook);
+    return hipGetLastError();
+}
+
+}  // namespace pkv

@@ -1,0 +1,266 @@
+"""Device-level API: contexts, profiles and segment tables over torch tensors.
+
+Thin Python view of the C ABI in include/pkv_codec.h.  torch supplies device
+memory and streams only; every byte of codec work runs in libpkv_hip.so.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+
+import numpy as np
+
+from . import _lib as L
+
+SEG_DTYPE = np.dtype([
+    ("elem_offset", "<u8"),
+    ("stride_outer", "<u8"),
+    ("stride_inner", "<u8"),
+    ("wire_offset", "<u8"),
+    ("n_vectors", "<u4"),
+    ("group", "<u4"),
+])
+assert SEG_DTYPE.itemsize == C.sizeof(L.Seg)
+
+
+def segments(rows) -> np.ndarray:
+    """Build a segment table from (elem_offset, stride_outer, stride_inner,
+    wire_offset, n_vectors, group) tuples."""
+    return np.array([tuple(int(v) for v in r) for r in rows], dtype=SEG_DTYPE)
+
+
+def contiguous_segment(elem_offset: int, n: int, dim: int, wire_offset: int) -> tuple:
+    """n row-major dim-vectors starting at elem_offset, one blob at wire_offset."""
+    return (elem_offset, 0, dim, wire_offset, n, max(n, 1))
+
+
+def _torch():
+    import torch  # noqa: F401  (binds the library to torch's HIP runtime)
+    return torch
+
+
+def _stream_ptr(stream):
+    torch = _torch()
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return C.c_void_p(stream.cuda_stream)
+
+
+class Context:
+    """pkv_ctx bound to one HIP device."""
+
+    def __init__(self, device: int = 0):
+        _torch()
+        self._ptr = C.c_void_p()
+        L.check(L.lib().pkv_ctx_create(device, C.byref(self._ptr)), "pkv_ctx_create")
+        self.device = device
+        self._profiles: dict = {}
+        self._lock = threading.Lock()
+
+    @property
+    def ptr(self):
+        return self._ptr
+
+    def close(self):
+        for p in list(self._profiles.values()):
+            p.close()
+        self._profiles.clear()
+        if self._ptr:
+            L.lib().pkv_ctx_destroy(self._ptr)
+            self._ptr = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # profiles are cached per parameters: the reference rebuilds its codebook,
+    # rotation and QJL matrix on every adapter call (proveKV/src/codec.rs:249,
+    # 296, 471-499); here they are built once and stay resident.
+    def turbo_profile(self, dim: int, bits: int, projections: int, seed: int,
+                      mode: int = L.TURBO_POLAR_WITH_QJL) -> "Profile":
+        key = ("turbo", dim, bits, projections, seed, mode)
+        with self._lock:
+            if key not in self._profiles:
+                self._profiles[key] = Profile._turbo(self, dim, bits, projections, seed, mode)
+            return self._profiles[key]
+
+    def fib_profile(self, dim: int, k: int, n: int, seed: int, training_samples: int = 2048,
+                    lloyd_restarts: int = 4, lloyd_iterations: int = 8) -> "Profile":
+        key = ("fib", dim, k, n, seed, training_samples, lloyd_restarts, lloyd_iterations)
+        with self._lock:
+            if key not in self._profiles:
+                self._profiles[key] = Profile._fib(self, dim, k, n, seed, training_samples, lloyd_restarts,
+                                                   lloyd_iterations)
+            return self._profiles[key]
+
+
+_default_ctx = None
+_default_lock = threading.Lock()
+
+
+def default_context() -> Context:
+    global _default_ctx
+    with _default_lock:
+        if _default_ctx is None:
+            _default_ctx = Context(0)
+        return _default_ctx
+
+
+class Profile:
+    """pkv_profile: constants resident on the device."""
+
+    def __init__(self, ctx: Context, ptr: C.c_void_p, kind: int, dim: int, **params):
+        self.ctx = ctx
+        self._ptr = ptr
+        self.kind = kind
+        self.dim = dim
+        self.params = params
+
+    @classmethod
+    def _turbo(cls, ctx, dim, bits, projections, seed, mode):
+        ptr = C.c_void_p()
+        L.check(L.lib().pkv_turbo_profile_create(ctx.ptr, dim, bits, projections, seed, mode, C.byref(ptr)),
+                "pkv_turbo_profile_create")
+        return cls(ctx, ptr, L.CODEC_TURBO, dim, bits=bits, projections=projections, seed=seed, mode=mode)
+
+    @classmethod
+    def _fib(cls, ctx, dim, k, n, seed, training, restarts, iterations):
+        ptr = C.c_void_p()
+        L.check(L.lib().pkv_fib_profile_create(ctx.ptr, dim, k, n, seed, training, restarts, iterations,
+                                               C.byref(ptr)), "pkv_fib_profile_create")
+        return cls(ctx, ptr, L.CODEC_FIB, dim, k=k, n=n, seed=seed)
+
+    @property
+    def ptr(self):
+        return self._ptr
+
+    def close(self):
+        if self._ptr:
+            L.lib().pkv_profile_destroy(self._ptr)
+            self._ptr = C.c_void_p()
+
+    def payload_len(self, radii: int = L.RADII_F32) -> int:
+        return int(L.lib().pkv_payload_len(self._ptr, radii))
+
+    def header_len(self) -> int:
+        return int(L.lib().pkv_header_len(self._ptr))
+
+    def blob_len(self, n: int, radii: int = L.RADII_F32) -> int:
+        return int(L.lib().pkv_blob_len(self._ptr, radii, n))
+
+    def constants(self):
+        if self.kind == L.CODEC_TURBO:
+            a = np.zeros(self.dim, np.float32)
+            b = np.zeros(max(1, self.params["projections"]) * self.dim, np.float32)
+        else:
+            a = np.zeros(self.params["n"] * self.params["k"], np.float32)
+            b = np.zeros(self.dim * self.dim, np.float64)
+        L.check(L.lib().pkv_profile_constants(self._ptr, a.ctypes.data, a.nbytes, b.ctypes.data, b.nbytes),
+                "pkv_profile_constants")
+        return a, b
+
+    # ------------------------------------------------------------ segments
+    def encode_segments(self, inp, segs: np.ndarray, wire, radii: int = L.RADII_F32, status=None,
+                        stream=None) -> None:
+        """Encode every segment of `segs` from device tensor `inp` (f32 or
+        bf16) into device uint8 tensor `wire` in one launch."""
+        torch = _torch()
+        segs = np.ascontiguousarray(segs, dtype=SEG_DTYPE)
+        dtype = L.DT_BF16 if inp.dtype == torch.bfloat16 else L.DT_F32
+        if inp.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError("encode input must be float32 or bfloat16")
+        if wire.dtype != torch.uint8:
+            raise TypeError("wire must be uint8")
+        if not (inp.is_contiguous() and wire.is_contiguous()):
+            raise ValueError("tensors must be contiguous")
+        st = status.data_ptr() if status is not None else None
+        rc = L.lib().pkv_encode_segments(self.ctx.ptr, self._ptr, radii, dtype, inp.data_ptr(), inp.numel(),
+                                         segs.ctypes.data, len(segs), wire.data_ptr(), wire.numel(), st,
+                                         _stream_ptr(stream))
+        L.check(rc, "pkv_encode_segments")
+
+    def decode_segments(self, wire, segs: np.ndarray, out, radii: int = L.RADII_F32, status=None,
+                        stream=None) -> None:
+        torch = _torch()
+        segs = np.ascontiguousarray(segs, dtype=SEG_DTYPE)
+        if out.dtype != torch.float32 or wire.dtype != torch.uint8:
+            raise TypeError("decode writes float32 from a uint8 wire")
+        if not (out.is_contiguous() and wire.is_contiguous()):
+            raise ValueError("tensors must be contiguous")
+        st = status.data_ptr() if status is not None else None
+        rc = L.lib().pkv_decode_segments(self.ctx.ptr, self._ptr, radii, wire.data_ptr(), wire.numel(),
+                                         segs.ctypes.data, len(segs), out.data_ptr(), out.numel(), st,
+                                         _stream_ptr(stream))
+        L.check(rc, "pkv_decode_segments")
+
+    def status_error(self, status_host: np.ndarray, segs: np.ndarray | None = None):
+        """Turn per-segment status words (2 per segment, host copy) into a
+        PkvError (or None).  The fib batch path reports input-validation
+        failures before norm-encoding failures (fib-quant/src/codec.rs:592-610
+        precede 694-704); everything else reports the first failing vector."""
+        st = np.ascontiguousarray(status_host, dtype=np.uint32).reshape(-1, 2)
+        for s, (w0, w1) in enumerate(st):
+            if w0 == 0xFFFFFFFF and w1 == 0xFFFFFFFF:
+                continue
+            if self.kind == L.CODEC_FIB and (segs is None or int(segs[s]["n_vectors"]) >= 4):
+                pick = int(w0) if w0 != 0xFFFFFFFF else int(w1)
+            else:
+                pick = min(int(w0), int(w1))
+            kind = pick & 15
+            code = {0: L.ERR_NONFINITE_INPUT, 1: L.ERR_ZERO_NORM, 2: L.ERR_NORM_UNREPRESENTABLE,
+                    3: L.ERR_NONFINITE_CODE, 4: L.ERR_NONFINITE_CODE}.get(kind, L.ERR_CORRUPT_PAYLOAD)
+            return L.PkvError(code, "segment status", s, pick >> 4)
+        return None
+
+    # ------------------------------------------------------------ host buffers
+    def encode_batch_compact(self, vectors: np.ndarray, radii: int = L.RADII_F32) -> bytes:
+        x = np.ascontiguousarray(vectors, dtype=np.float32)
+        if x.ndim != 2 or x.shape[1] != self.dim:
+            raise L.PkvError(L.ERR_DIM_MISMATCH, "encode_batch_compact")
+        n = x.shape[0]
+        cap = self.blob_len(n, radii)
+        out = np.zeros(max(cap, 1), np.uint8)
+        out_len = C.c_uint64()
+        err = L.Error()
+        rc = L.lib().pkv_encode_batch_compact(self.ctx.ptr, self._ptr, radii, x.ctypes.data if n else None, n,
+                                              out.ctypes.data, cap, C.byref(out_len), C.byref(err))
+        if rc:
+            raise L.PkvError(rc, "encode_batch_compact", err.segment, err.index)
+        return out[: out_len.value].tobytes()
+
+    def decode_batch_compact(self, payload: bytes) -> np.ndarray:
+        buf = np.frombuffer(payload, dtype=np.uint8)
+        n = C.c_uint64()
+        radii = C.c_int()
+        rc = L.lib().pkv_parse_header(self._ptr, buf.ctypes.data, len(payload), C.byref(n), C.byref(radii))
+        if rc:
+            raise L.PkvError(rc, "decode_batch_compact")
+        out = np.zeros((max(n.value, 1), self.dim), np.float32)
+        n_out = C.c_uint64()
+        err = L.Error()
+        rc = L.lib().pkv_decode_batch_compact(self.ctx.ptr, self._ptr, buf.ctypes.data, len(payload),
+                                              out.ctypes.data, n.value, C.byref(n_out), C.byref(err))
+        if rc:
+            raise L.PkvError(rc, "decode_batch_compact", err.segment, err.index)
+        return out[: n_out.value]
+
+
+# ---------------------------------------------------------------- host only
+def turbo_constants(dim: int, projections: int, seed: int):
+    signs = np.zeros(dim, np.float32)
+    G = np.zeros(max(projections, 1) * dim, np.float32)
+    L.check(L.lib().pkv_turbo_constants(dim, projections, seed, signs.ctypes.data,
+                                        G.ctypes.data if projections else None), "pkv_turbo_constants")
+    return signs, G[: projections * dim].reshape(projections, dim)
+
+
+def fib_constants(dim: int = 64, k: int = 4, n: int = 32, seed: int = 42, training: int = 2048,
+                  restarts: int = 4, iterations: int = 8):
+    cb = np.zeros(n * k, np.float32)
+    rot = np.zeros(dim * dim, np.float64)
+    im, tm = C.c_double(), C.c_double()
+    L.check(L.lib().pkv_fib_constants(dim, k, n, seed, training, restarts, iterations, cb.ctypes.data,
+                                      rot.ctypes.data, C.byref(im), C.byref(tm)), "pkv_fib_constants")
+    return cb.reshape(n, k), rot.reshape(dim, dim), im.value, tm.value

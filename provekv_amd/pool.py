@@ -1,0 +1,133 @@
+"""Batched two-tier pool + shell build and rehydrate on one GPU.
+
+The reference builds the cold tier (SharedKVPool::build_with_policy,
+proveKV/src/pool.rs:157-392: one FB2 blob per (layer, K|V) over the shared
+prefix, vectors gathered token-major / head-minor at pool.rs:246-257) and one
+hot-tier shell per agent (shell::materialize_shell, shell.rs:148-376: one
+TQB1 blob per (layer, K|V)), each (layer, K|V) through its own adapter call on
+a rayon worker.  Decode goes back through decompress_layer (pool.rs:471-614)
+and AgentShell::decompress_all_layers_with_seed (shell.rs:92-141), which
+re-lay every layer as [tokens][heads][head_dim] f32.
+
+Here every blob of a tier is one segment of ONE launch: the segment strides
+read the corpus layout [tokens][layers][heads][K|V][head_dim] in place (no
+gather copy), and decode writes each layer's [tokens][heads][head_dim] block
+directly.  Blob bytes are identical to the reference's.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib as L
+from .device import SEG_DTYPE
+
+
+@dataclass
+class TierLayout:
+    """Segment tables of one tier (pool or all shells)."""
+    enc: np.ndarray          # segments over the corpus tensor
+    dec: np.ndarray          # segments over the rehydrated output tensor
+    wire_bytes: int
+    out_elems: int
+    blob_offsets: list       # (owner, layer, side, wire_offset, blob_len)
+
+
+def _tier(owners, layers: int, heads: int, dim: int, corpus_tokens: int, hdr: int, plen: int) -> TierLayout:
+    """owners: list of (name, first_token, n_tokens) ranges of the corpus."""
+    tok_stride = layers * heads * 2 * dim           # elements per corpus token
+    enc, dec, blobs = [], [], []
+    wire = 0
+    out = 0
+    for name, t0, nt in owners:
+        n = nt * heads
+        for layer in range(layers):
+            for side in (0, 1):
+                blob = hdr + n * plen
+                enc.append((t0 * tok_stride + layer * heads * 2 * dim + side * dim,
+                            tok_stride, 2 * dim, wire, n, heads))
+                dec.append((out, 0, dim, wire, n, max(n, 1)))
+                blobs.append((name, layer, side, wire, blob))
+                wire += blob
+                out += n * dim
+    del corpus_tokens
+    return TierLayout(np.array(enc, dtype=SEG_DTYPE), np.array(dec, dtype=SEG_DTYPE), wire, out, blobs)
+
+
+class TwoTierPlan:
+    """Pool over tokens [0, prefix) with fib_k4_n32 (FB2); one turbo (TQB1)
+    shell per agent over its own token range.  Decode output per tier is
+    [owner][layer][K|V][tokens][heads][head_dim] f32."""
+
+    def __init__(self, ctx, layers: int, heads: int, dim: int, prefix: int, agent_tokens: list,
+                 seed: int = 42, turbo_bits: int = 4, projections: int = 32, lossy: bool = False,
+                 fib_training: int = 2048, fib_restarts: int = 4, fib_iterations: int = 8):
+        self.ctx = ctx
+        self.layers, self.heads, self.dim = layers, heads, dim
+        self.prefix = prefix
+        self.agent_tokens = list(agent_tokens)
+        self.tokens = prefix + sum(self.agent_tokens)
+        self.radii = L.RADII_LOG_U8 if lossy else L.RADII_F32
+        self.fib = ctx.fib_profile(dim, 4, 32, seed, fib_training, fib_restarts, fib_iterations)
+        self.turbo = ctx.turbo_profile(dim, turbo_bits, projections, seed)
+        self.pool = _tier([("pool", 0, prefix)], layers, heads, dim, self.tokens, 19, self.fib.payload_len())
+        owners, t = [], prefix
+        for a, nt in enumerate(self.agent_tokens):
+            owners.append((f"agent{a}", t, nt))
+            t += nt
+        self.shells = _tier(owners, layers, heads, dim, self.tokens, 38, self.turbo.payload_len(self.radii))
+
+    @property
+    def corpus_elems(self) -> int:
+        return self.tokens * self.layers * self.heads * 2 * self.dim
+
+    def alloc(self, device="cuda"):
+        import torch
+        return {
+            "pool_wire": torch.empty(self.pool.wire_bytes, dtype=torch.uint8, device=device),
+            "shell_wire": torch.empty(self.shells.wire_bytes, dtype=torch.uint8, device=device),
+            "pool_out": torch.empty(self.pool.out_elems, dtype=torch.float32, device=device),
+            "shell_out": torch.empty(self.shells.out_elems, dtype=torch.float32, device=device),
+            "pool_status": torch.empty(2 * len(self.pool.enc), dtype=torch.int32, device=device),
+            "shell_status": torch.empty(2 * len(self.shells.enc), dtype=torch.int32, device=device),
+            "pool_dstatus": torch.empty(2 * len(self.pool.dec), dtype=torch.int32, device=device),
+            "shell_dstatus": torch.empty(2 * len(self.shells.dec), dtype=torch.int32, device=device),
+        }
+
+    def encode(self, corpus, bufs, stream=None):
+        """Pool build + all shells: two launches (fib, turbo)."""
+        self.fib.encode_segments(corpus, self.pool.enc, bufs["pool_wire"], status=bufs["pool_status"],
+                                 stream=stream)
+        self.turbo.encode_segments(corpus, self.shells.enc, bufs["shell_wire"], radii=self.radii,
+                                   status=bufs["shell_status"], stream=stream)
+
+    def decode(self, bufs, stream=None):
+        """Rehydrate the pool once and every shell: two launches."""
+        self.fib.decode_segments(bufs["pool_wire"], self.pool.dec, bufs["pool_out"],
+                                 status=bufs["pool_dstatus"], stream=stream)
+        self.turbo.decode_segments(bufs["shell_wire"], self.shells.dec, bufs["shell_out"], radii=self.radii,
+                                   status=bufs["shell_dstatus"], stream=stream)
+
+    def check(self, bufs):
+        """Raise the first failure recorded by the last encode/decode."""
+        for prof, key, segs in ((self.fib, "pool_status", self.pool.enc), (self.turbo, "shell_status", self.shells.enc),
+                                (self.fib, "pool_dstatus", self.pool.dec),
+                                (self.turbo, "shell_dstatus", self.shells.dec)):
+            st = bufs[key].cpu().numpy().view(np.uint32)
+            err = prof.status_error(st, segs)
+            if err is not None:
+                raise err
+
+    # ------------------------------------------------------------ receipts
+    def compressed_bytes(self) -> dict:
+        """CLAIMS.json-style byte math: pool FB2 + shells TQB1(-L)."""
+        return {"pool": self.pool.wire_bytes, "shells": self.shells.wire_bytes,
+                "total": self.pool.wire_bytes + self.shells.wire_bytes,
+                "per_agent_shell": self.shells.wire_bytes // max(1, len(self.agent_tokens))}
+
+    def blob(self, bufs, tier: str, index: int) -> bytes:
+        t = self.pool if tier == "pool" else self.shells
+        _, _, _, off, ln = t.blob_offsets[index]
+        w = bufs["pool_wire" if tier == "pool" else "shell_wire"]
+        return w[off:off + ln].cpu().numpy().tobytes()

@@ -1,0 +1,155 @@
+"""GPU parity: libpkv_hip.so (through the C ABI) against the CPU oracle.
+
+Bar: TQB1 / FB2 bytes bit-exact; decoded f32 within 1e-6 relative
+(per vector, max|d| / max|ref|) -- the kernels are in fact expected to match
+the oracle bit for bit, and the tests report exact equality separately.
+"""
+import struct
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from provekv_amd import _lib as L
+from provekv_amd import synth
+from provekv_amd.codec import (CompressionFailed, DecompressionFailed, FibQuantAdapter, RadiiCompression,
+                               TurboQuantAdapter)
+
+pytestmark = pytest.mark.gpu
+SEED = 42
+
+
+def rel_err(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    den = np.maximum(np.abs(b).max(axis=-1), 1e-30)
+    return (np.abs(a - b).max(axis=-1) / den).max()
+
+
+def kv_vectors(seed, n, dim=64):
+    K, V = synth.kv_cache(seed, 1, 4, (n + 7) // 8, dim)
+    x = np.concatenate([K.reshape(-1, dim), V.reshape(-1, dim)])[:n]
+    assert x.shape == (n, dim)
+    return np.ascontiguousarray(x)
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 63, 64, 65, 255, 256, 257, 1000])
+@pytest.mark.parametrize("lossy", [False, True])
+def test_turbo_encode_decode_bit_exact(ctx, n, lossy):
+    x = kv_vectors(n, n)
+    ad = TurboQuantAdapter(64, 4, 32, RadiiCompression.Lossy if lossy else RadiiCompression.Lossless)
+    blob = ad.encode_batch_compact(x, SEED)
+    ref = O.turbo_encode_batch(x, SEED, radii_codec=1 if lossy else 0)
+    assert blob == ref
+    dec = ad.decode_batch_compact(blob, SEED)
+    dref = O.turbo_decode_batch(ref, 64, SEED)
+    assert rel_err(dec, dref) <= 1e-6
+    assert np.array_equal(dec.view(np.uint32), dref.view(np.uint32))
+
+
+def test_turbo_dim128_bit_exact(ctx):
+    x = kv_vectors(5, 300, 128)
+    for lossy in (False, True):
+        ad = TurboQuantAdapter(128, 4, 32, RadiiCompression.Lossy if lossy else RadiiCompression.Lossless)
+        blob = ad.encode_batch_compact(x, SEED)
+        assert blob == O.turbo_encode_batch(x, SEED, radii_codec=int(lossy))
+        dec = ad.decode_batch_compact(blob, SEED)
+        assert rel_err(dec, O.turbo_decode_batch(blob, 128, SEED)) <= 1e-6
+
+
+@pytest.mark.parametrize("bits,mode", [(8, 1), (4, 0), (2, 1)])
+def test_turbo_other_bit_widths(ctx, bits, mode):
+    x = kv_vectors(7, 200)
+    prof = ctx.turbo_profile(64, bits, 32, SEED, mode)
+    blob = prof.encode_batch_compact(x)
+    assert blob == O.turbo_encode_batch(x, SEED, bits=bits, mode=mode)
+    dec = prof.decode_batch_compact(blob)
+    assert rel_err(dec, O.turbo_decode_batch(blob, 64, SEED, bits=bits, mode=mode)) <= 1e-6
+
+
+def test_turbo_edge_inputs(ctx):
+    rng = np.random.RandomState(3)
+    x = rng.randn(64, 64).astype(np.float32)
+    x[0] = 0.0                      # all-zero vector: r = 0, theta = 0 -> bin 4
+    x[1] = -0.0
+    x[2, ::2] = 0.0                 # many pairs on the octant lines
+    x[3] = 1e-30                    # tiny values (denormal products)
+    x[4] = np.float32(1e18)
+    x[5, :] = np.arange(64, dtype=np.float32)
+    ad = TurboQuantAdapter(64, 4, 32)
+    assert ad.encode_batch_compact(x, SEED) == O.turbo_encode_batch(x, SEED)
+    adl = TurboQuantAdapter(64, 4, 32, RadiiCompression.Lossy)
+    assert adl.encode_batch_compact(x, SEED) == O.turbo_encode_batch(x, SEED, radii_codec=1)
+
+
+def test_turbo_errors(ctx):
+    ad = TurboQuantAdapter(64, 4, 32)
+    x = kv_vectors(11, 100)
+    bad = x.copy()
+    bad[37, 5] = np.inf
+    with pytest.raises(CompressionFailed, match="non-finite input.*vector 37"):
+        ad.encode_batch_compact(bad, SEED)
+    with pytest.raises(O.OracleError) as e:
+        O.turbo_encode_batch(bad, SEED)
+    assert e.value.index == 37
+    huge = x.copy()
+    huge[12] = 3e38                  # rotated values overflow -> non-finite radius
+    with pytest.raises(CompressionFailed, match="non-finite radius"):
+        ad.encode_batch_compact(huge, SEED)
+    with pytest.raises(CompressionFailed):
+        ad.encode_batch_compact(np.zeros((0, 64), np.float32), SEED)
+    blob = bytearray(ad.encode_batch_compact(x, SEED))
+    neg = bytearray(blob)
+    struct.pack_into("<f", neg, 38 + 144 * 9 + 4, -1.0)
+    with pytest.raises(DecompressionFailed, match="vector 9"):
+        ad.decode_batch_compact(bytes(neg), SEED)
+    with pytest.raises(DecompressionFailed):
+        ad.decode_batch_compact(bytes(blob) + b"\0", SEED)     # trailing bytes
+    with pytest.raises(DecompressionFailed):
+        ad.decode_batch_compact(bytes(blob), SEED + 1)          # seed mismatch
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 64, 257, 1000])
+def test_fib_encode_decode_bit_exact(ctx, n):
+    x = kv_vectors(100 + n, n)
+    ad = FibQuantAdapter(64, 4, 32, 2048, 4, 8)
+    blob = ad.encode_batch_compact(x, SEED)
+    prof = ad.build_quantizer(SEED)
+    cb, rot = prof.constants()
+    ref = O.fib_encode_batch(x, cb.reshape(32, 4), rot.reshape(64, 64))
+    assert blob == ref
+    dec = ad.decode_batch_compact(blob, SEED)
+    dref = O.fib_decode_batch(ref, cb.reshape(32, 4), rot.reshape(64, 64))
+    assert rel_err(dec, dref) <= 1e-6
+    assert np.array_equal(dec.view(np.uint32), dref.view(np.uint32))
+
+
+def test_fib_errors(ctx):
+    ad = FibQuantAdapter(64, 4, 32, 2048, 4, 8)
+    x = kv_vectors(21, 50)
+    z = x.copy()
+    z[7] = 0
+    z[30] *= 1e6     # later failure of another kind: validation pass wins
+    with pytest.raises(CompressionFailed, match="zero norm.*vector 7"):
+        ad.encode_batch_compact(z, SEED)
+    nf = x.copy()
+    nf[44, 1] = np.nan
+    with pytest.raises(CompressionFailed, match="non-finite input.*vector 44"):
+        ad.encode_batch_compact(nf, SEED)
+    big = x.copy()
+    big[30] *= 1e6
+    with pytest.raises(CompressionFailed, match="fp16.*vector 30"):
+        ad.encode_batch_compact(big, SEED)
+    blob = bytearray(ad.encode_batch_compact(x, SEED))
+    zero_norm = bytearray(blob)
+    zero_norm[19 + 12 * 3] = 0
+    zero_norm[19 + 12 * 3 + 1] = 0
+    with pytest.raises(DecompressionFailed, match="vector 3"):
+        ad.decode_batch_compact(bytes(zero_norm), SEED)
+    hdr = bytearray(blob)
+    hdr[4] = 6
+    with pytest.raises(DecompressionFailed):
+        ad.decode_batch_compact(bytes(hdr), SEED)
+    # trailing bytes are accepted (fib-quant/src/codec.rs:380-386)
+    out = ad.decode_batch_compact(bytes(blob) + b"\1\2\3", SEED)
+    assert out.shape == (50, 64)
