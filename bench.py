@@ -34,7 +34,7 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(corpus: np.ndarray, plan, budget_s: float = 12.0) -> dict:
+def cpu_baseline(corpus: np.ndarray, plan, budget_s: float = 16.0) -> dict:
     """Oracle (one thread) encode + decode of sampled (layer, K|V) blobs of
     both tiers, scaled to the f32-KV GB/s of the whole workload."""
     from oracle import oracle as O
@@ -43,7 +43,7 @@ def cpu_baseline(corpus: np.ndarray, plan, budget_s: float = 12.0) -> dict:
     rot = rot.reshape(plan.dim, plan.dim)
     layers, dim = plan.layers, plan.dim
     # fib: one (layer, K) blob of the prefix, truncated to a fixed vector count
-    x_pool = np.ascontiguousarray(corpus[:plan.prefix, 0, :, 0, :].reshape(-1, dim))[:16384]
+    x_pool = np.ascontiguousarray(corpus[:plan.prefix, 0, :, 0, :].reshape(-1, dim))[:25600]
     x_shell = np.ascontiguousarray(corpus[plan.prefix:plan.prefix + plan.agent_tokens[0], 0, :, 0, :]
                                    .reshape(-1, dim))
     t0 = time.perf_counter()
@@ -57,7 +57,7 @@ def cpu_baseline(corpus: np.ndarray, plan, budget_s: float = 12.0) -> dict:
         tb = O.turbo_encode_batch(x_shell, plan.fib.params["seed"], radii_codec=plan.radii)
         O.turbo_decode_batch(tb, dim, plan.fib.params["seed"])
         reps += 1
-        if time.perf_counter() - t3 > min(3.0, budget_s / 4):
+        if time.perf_counter() - t3 > budget_s / 2:
             break
     t4 = time.perf_counter()
     fib_s_per_vec = ((t1 - t0) + (t2 - t1)) / x_pool.shape[0]
@@ -80,6 +80,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--lossy", action="store_true", help="TQB1-L shells (BlockLogU8 radii)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run a 256 MiB device copy (reference kernel for rocprofv3 --pmc byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1",
@@ -180,6 +182,22 @@ def main():
                      "algorithmic_bytes": alg[dom]},
         "compressed_bytes": plan.compressed_bytes(),
     }
+    # STREAM-style copy: the achievable HBM bandwidth on this box
+    src = torch.empty(1 << 28, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0.record(stream)
+    for _ in range(10):
+        dst.copy_(src)
+    c1.record(stream)
+    torch.cuda.synchronize()
+    out["copy_gbs"] = round(2 * src.numel() * 10 / (c0.elapsed_time(c1) * 1e-3) / 1e9, 1)
+    if args.copy_calib:
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+    del src, dst
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle, bounded sample)")
         out["cpu_baseline"] = cpu_baseline(corpus, plan)

@@ -416,14 +416,15 @@ static int turbo_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t bits, uint3
     p->dim = dim;
     p->bits = bits;
     p->pbits = pbits;
-    p->proj = mode == PKV_TURBO_POLAR_WITH_QJL ? proj : 0;
+    p->proj = proj;   // written to TQB1 bytes 18..21 in every mode (wire.rs:311, 343)
     p->mode = static_cast<uint32_t>(mode);
     p->seed = seed;
+    const uint32_t qrows = mode == PKV_TURBO_POLAR_WITH_QJL ? proj : 0;
     if (signs) {
         p->signs.assign(signs, signs + dim);
-        if (p->proj) p->qjl.assign(qjl, qjl + static_cast<size_t>(p->proj) * dim);
+        if (qrows) p->qjl.assign(qjl, qjl + static_cast<size_t>(qrows) * dim);
     } else {
-        make_turbo_constants(dim, p->proj, seed, p->signs, p->qjl);
+        make_turbo_constants(dim, qrows, seed, p->signs, p->qjl);
     }
     // (cos, sin) of every dequantized angle, host libm (polar.rs:91-95, 312-313)
     const uint32_t levels = 1u << pbits;

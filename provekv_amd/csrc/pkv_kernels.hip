@@ -429,7 +429,7 @@ __global__ __launch_bounds__(TILE) void turbo_encode_kernel(
     }
     if (tile == 0 && threadIdx.x < 38) {
         blob[threadIdx.x] = static_cast<uint8_t>(
-            tqb1_byte(threadIdx.x, DIM, pbits, lc.radii, mode ? proj : 0u, seed, seg.n_vectors, plen));
+            tqb1_byte(threadIdx.x, DIM, pbits, lc.radii, proj, seed, seg.n_vectors, plen));
     }
 }
 
@@ -463,10 +463,9 @@ __global__ __launch_bounds__(TILE) void turbo_decode_kernel(
     const uint8_t* blob = wire + seg.wire_offset;
 
     // header check (every wave; 38 bytes)
-    const uint32_t psign = mode ? proj : 0u;
     uint32_t hb = lane < 38 ? blob[lane] : 0u;
     bool bad = lane < 38 && tqb1_checked(lane) &&
-               hb != tqb1_byte(lane, DIM, pbits, lc.radii, psign, seed, seg.n_vectors, plen);
+               hb != tqb1_byte(lane, DIM, pbits, lc.radii, proj, seed, seg.n_vectors, plen);
     if (__ballot(bad) != 0ull) {
         if (lane == 0) status_fail(lc.status, sidx, 0, 0u, KIND_HEADER);
         return;
@@ -750,6 +749,13 @@ constexpr size_t stage_bytes() {
     return static_cast<size_t>(WAVES) * (WAVE * (DIM + 4) + 8) * sizeof(float);
 }
 
+// Dynamic LDS above 64 KiB must be allowed per kernel before launch.
+template <typename K>
+hipError_t allow_lds(K kernel, size_t bytes) {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(bytes));
+}
+
 }  // namespace
 
 int launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, void* stream) {
@@ -759,60 +765,56 @@ int launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, void* stream) {
     return hipGetLastError();
 }
 
+template <typename K, typename... Args>
+hipError_t launch_big_lds(K kernel, uint32_t nblocks, size_t lds, hipStream_t st, Args... args) {
+    hipError_t e = allow_lds(kernel, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kernel, dim3(nblocks), dim3(TILE), lds, st, args...);
+    return hipGetLastError();
+}
+
 int launch_turbo_encode(const LaunchCommon& lc, const TurboDev& td, const void* in, uint8_t* wire,
                         uint32_t nblocks, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (td.dim == 64) {
-        if (td.pbits == 3)
-            hipLaunchKernelGGL((turbo_encode_kernel<64, 3>), dim3(nblocks), dim3(TILE), stage_bytes<64>(), st, lc, in,
-                               wire, td.signs, td.qjl, td.cs, td.seed, td.pbits, td.proj, td.mode);
-        else
-            hipLaunchKernelGGL((turbo_encode_kernel<64, 0>), dim3(nblocks), dim3(TILE), stage_bytes<64>(), st, lc, in,
-                               wire, td.signs, td.qjl, td.cs, td.seed, td.pbits, td.proj, td.mode);
-    } else {
-        if (td.pbits == 3)
-            hipLaunchKernelGGL((turbo_encode_kernel<128, 3>), dim3(nblocks), dim3(TILE), stage_bytes<128>(), st, lc,
-                               in, wire, td.signs, td.qjl, td.cs, td.seed, td.pbits, td.proj, td.mode);
-        else
-            hipLaunchKernelGGL((turbo_encode_kernel<128, 0>), dim3(nblocks), dim3(TILE), stage_bytes<128>(), st, lc,
-                               in, wire, td.signs, td.qjl, td.cs, td.seed, td.pbits, td.proj, td.mode);
-    }
-    return hipGetLastError();
+    if (td.dim == 64)
+        return td.pbits == 3
+                   ? launch_big_lds(turbo_encode_kernel<64, 3>, nblocks, stage_bytes<64>(), st, lc, in, wire, td.signs,
+                                    td.qjl, td.cs, td.seed, td.pbits, td.proj, td.mode)
+                   : launch_big_lds(turbo_encode_kernel<64, 0>, nblocks, stage_bytes<64>(), st, lc, in, wire, td.signs,
+                                    td.qjl, td.cs, td.seed, td.pbits, td.proj, td.mode);
+    return td.pbits == 3
+               ? launch_big_lds(turbo_encode_kernel<128, 3>, nblocks, stage_bytes<128>(), st, lc, in, wire, td.signs,
+                                td.qjl, td.cs, td.seed, td.pbits, td.proj, td.mode)
+               : launch_big_lds(turbo_encode_kernel<128, 0>, nblocks, stage_bytes<128>(), st, lc, in, wire, td.signs,
+                                td.qjl, td.cs, td.seed, td.pbits, td.proj, td.mode);
 }
 
 int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_t* wire, float* out,
                         uint32_t nblocks, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (td.dim == 64) {
-        if (td.pbits == 3)
-            hipLaunchKernelGGL((turbo_decode_kernel<64, 3>), dim3(nblocks), dim3(TILE), stage_bytes<64>(), st, lc, wire,
-                               out, td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode);
-        else
-            hipLaunchKernelGGL((turbo_decode_kernel<64, 0>), dim3(nblocks), dim3(TILE), stage_bytes<64>(), st, lc, wire,
-                               out, td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode);
-    } else {
-        if (td.pbits == 3)
-            hipLaunchKernelGGL((turbo_decode_kernel<128, 3>), dim3(nblocks), dim3(TILE), stage_bytes<128>(), st, lc,
-                               wire, out, td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode);
-        else
-            hipLaunchKernelGGL((turbo_decode_kernel<128, 0>), dim3(nblocks), dim3(TILE), stage_bytes<128>(), st, lc,
-                               wire, out, td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode);
-    }
-    return hipGetLastError();
+    if (td.dim == 64)
+        return td.pbits == 3
+                   ? launch_big_lds(turbo_decode_kernel<64, 3>, nblocks, stage_bytes<64>(), st, lc, wire, out, td.signs,
+                                    td.cs, td.seed, td.pbits, td.proj, td.mode)
+                   : launch_big_lds(turbo_decode_kernel<64, 0>, nblocks, stage_bytes<64>(), st, lc, wire, out, td.signs,
+                                    td.cs, td.seed, td.pbits, td.proj, td.mode);
+    return td.pbits == 3
+               ? launch_big_lds(turbo_decode_kernel<128, 3>, nblocks, stage_bytes<128>(), st, lc, wire, out, td.signs,
+                                td.cs, td.seed, td.pbits, td.proj, td.mode)
+               : launch_big_lds(turbo_decode_kernel<128, 0>, nblocks, stage_bytes<128>(), st, lc, wire, out, td.signs,
+                                td.cs, td.seed, td.pbits, td.proj, td.mode);
 }
 
 int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire, uint32_t nblocks,
                       void* stream) {
-    hipLaunchKernelGGL((fib_encode_kernel<64>), dim3(nblocks), dim3(TILE), stage_bytes<64>(),
-                       static_cast<hipStream_t>(stream), lc, in, wire, fd.rot, fd.codebook);
-    return hipGetLastError();
+    return launch_big_lds(fib_encode_kernel<64>, nblocks, stage_bytes<64>(), static_cast<hipStream_t>(stream), lc, in,
+                          wire, fd.rot, fd.codebook);
 }
 
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, float* out, uint32_t nblocks,
                       void* stream) {
-    hipLaunchKernelGGL((fib_decode_kernel<64>), dim3(nblocks), dim3(TILE), stage_bytes<64>(),
-                       static_cast<hipStream_t>(stream), lc, wire, out, fd.rot32t, fd.codebook);
-    return hipGetLastError();
+    return launch_big_lds(fib_decode_kernel<64>, nblocks, stage_bytes<64>(), static_cast<hipStream_t>(stream), lc,
+                          wire, out, fd.rot32t, fd.codebook);
 }
 
 }  // namespace pkv

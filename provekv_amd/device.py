@@ -153,7 +153,8 @@ class Profile:
     def constants(self):
         if self.kind == L.CODEC_TURBO:
             a = np.zeros(self.dim, np.float32)
-            b = np.zeros(max(1, self.params["projections"]) * self.dim, np.float32)
+            rows = self.params["projections"] if self.params["mode"] == L.TURBO_POLAR_WITH_QJL else 0
+            b = np.zeros(max(1, rows) * self.dim, np.float32)
         else:
             a = np.zeros(self.params["n"] * self.params["k"], np.float32)
             b = np.zeros(self.dim * self.dim, np.float64)
@@ -162,6 +163,15 @@ class Profile:
         return a, b
 
     # ------------------------------------------------------------ segments
+    @staticmethod
+    def _status_ptr(status, nseg: int):
+        """The kernels write 2 uint32 words per segment into `status`."""
+        if status is None:
+            return None
+        if status.element_size() != 4 or status.numel() < 2 * nseg or not status.is_contiguous():
+            raise ValueError(f"status must be a contiguous 32-bit tensor of >= {2 * nseg} elements")
+        return status.data_ptr()
+
     def encode_segments(self, inp, segs: np.ndarray, wire, radii: int = L.RADII_F32, status=None,
                         stream=None) -> None:
         """Encode every segment of `segs` from device tensor `inp` (f32 or
@@ -175,7 +185,7 @@ class Profile:
             raise TypeError("wire must be uint8")
         if not (inp.is_contiguous() and wire.is_contiguous()):
             raise ValueError("tensors must be contiguous")
-        st = status.data_ptr() if status is not None else None
+        st = self._status_ptr(status, len(segs))
         rc = L.lib().pkv_encode_segments(self.ctx.ptr, self._ptr, radii, dtype, inp.data_ptr(), inp.numel(),
                                          segs.ctypes.data, len(segs), wire.data_ptr(), wire.numel(), st,
                                          _stream_ptr(stream))
@@ -189,7 +199,7 @@ class Profile:
             raise TypeError("decode writes float32 from a uint8 wire")
         if not (out.is_contiguous() and wire.is_contiguous()):
             raise ValueError("tensors must be contiguous")
-        st = status.data_ptr() if status is not None else None
+        st = self._status_ptr(status, len(segs))
         rc = L.lib().pkv_decode_segments(self.ctx.ptr, self._ptr, radii, wire.data_ptr(), wire.numel(),
                                          segs.ctypes.data, len(segs), out.data_ptr(), out.numel(), st,
                                          _stream_ptr(stream))
