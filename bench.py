@@ -73,6 +73,25 @@ def cpu_baseline(corpus: np.ndarray, plan, budget_s: float = 16.0) -> dict:
             "encode_decode_s_projected": round(total_s, 2)}
 
 
+KERNEL_SYMBOL = {"fib_encode": "fib_encode_kernel<64>", "turbo_encode": "turbo_encode_kernel<64, 3>",
+                 "fib_decode": "fib_decode_kernel<64>", "turbo_decode": "turbo_decode_kernel<64, 3>"}
+
+
+def profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (calibrated FETCH_SIZE + WRITE_SIZE), or None."""
+    path = os.path.join(ROOT, "profiles", "codec_kernels_config3.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = line.strip().rsplit(" ", 1)
+        if line.startswith("traffic_bytes ") and len(parts) == 2:
+            name = parts[0][len("traffic_bytes "):]
+            if name == KERNEL_SYMBOL[kernel]:
+                return int(parts[1])
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -178,7 +197,8 @@ def main():
         "kernels_ms": {n: round(per[n], 4) for n in names},
         "kernels_gbs": {n: round(kern_gbs[n], 1) for n in names},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(kern_gbs[dom], 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(kern_gbs[dom] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(kern_gbs[dom] / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic(dom),
                      "algorithmic_bytes": alg[dom]},
         "compressed_bytes": plan.compressed_bytes(),
     }
