@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <limits>
 #include <mutex>
 #include <new>
 #include <vector>
@@ -54,11 +55,14 @@ struct pkv_profile {
     float* d_cs = nullptr;
     // fib
     uint32_t k = 0, n = 0, wbits = 0;
-    std::vector<float> codebook, rot32t;
+    std::vector<float> codebook, rot32t, rot32, kc;
     std::vector<double> rot;
     float* d_cb = nullptr;
     double* d_rot = nullptr;
     float* d_rot32t = nullptr;
+    float* d_rot32 = nullptr;
+    float* d_kc = nullptr;
+    float thr = 0.0f;
 };
 
 namespace {
@@ -217,6 +221,9 @@ FibDev fib_dev(const pkv_profile* p) {
     f.codebook = p->d_cb;
     f.rot = p->d_rot;
     f.rot32t = p->d_rot32t;
+    f.rot32 = p->d_rot32;
+    f.kc = p->d_kc;
+    f.thr = p->thr;
     f.dim = p->dim;
     f.k = p->k;
     f.n = p->n;
@@ -456,6 +463,45 @@ int pkv_turbo_profile_create_with_constants(pkv_ctx* ctx, uint32_t dim, uint32_t
     return turbo_profile_common(ctx, dim, bits, projections, seed, mode, signs, qjl, out);
 }
 
+// Constants of the encode kernel's approximate argmin and its acceptance
+// margin.  key_w = |c_w|^2 + off - 2 c_w . rho' (f32 FMA) approximates the
+// reference distance D_w (+ off - |rho|^2, common to all w) within
+//   E = E_score + E_D + E_key, where
+//   E_score = 2^-23 (rounding of |c|^2 + off) + 4 * 2^-24 (FMA roundings)
+//             + 2 |c|_1 * eps_rho,  eps_rho = 69 * 2^-24 (|rho' - rho| bound:
+//             64 FMA roundings + x_hat' and Pi32 representation, with
+//             sum|Pi_rc x_c| <= |Pi_r| |x| = 1),
+//   E_D     = 8 * 2^-24 * (|c| + 1)^2 (the reference's f32 distance formula),
+//   E_key   = 31 * 2^-23 (index bits in the key, values in (0, 2)).
+// A gap above 2E between the two smallest keys proves the reference's strict
+// argmin; thr = 2.5 E leaves extra room.  With the codebook's |c| <= 0.35
+// every key stays in (0.5, 2); otherwise every block takes the exact path.
+static void fib_argmin_constants(pkv_profile* p) {
+    const uint32_t n = p->n, k = p->k;
+    const double off = 1.25;
+    double cmax = 0.0, l1max = 0.0;
+    p->kc.assign(static_cast<size_t>(n) * 8, 0.0f);
+    for (uint32_t w = 0; w < n; ++w) {
+        double sq = 0.0, l1 = 0.0;
+        for (uint32_t t = 0; t < k; ++t) {
+            const double c = p->codebook[w * k + t];
+            sq += c * c;
+            l1 += std::fabs(c);
+            p->kc[w * 8 + t] = -2.0f * p->codebook[w * k + t];
+        }
+        p->kc[w * 8 + 4] = static_cast<float>(sq + off);
+        cmax = std::max(cmax, std::sqrt(sq));
+        l1max = std::max(l1max, l1);
+    }
+    const double u = std::ldexp(1.0, -24);
+    const double eps_rho = 69.0 * u * 1.001;
+    const double e_score = 2.0 * u + 4.0 * u + 2.0 * l1max * eps_rho;
+    const double e_d = 8.0 * u * (cmax + 1.0) * (cmax + 1.0);
+    const double e_key = 31.0 * 2.0 * u;
+    const double e = e_score + e_d + e_key;
+    p->thr = cmax <= 0.35 ? static_cast<float>(2.5 * e) : std::numeric_limits<float>::infinity();
+}
+
 static int fib_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, std::vector<float> cb,
                               std::vector<double> rot, pkv_profile** out) {
     pkv_profile* p = new (std::nothrow) pkv_profile();
@@ -469,13 +515,20 @@ static int fib_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n
     p->codebook = std::move(cb);
     p->rot = std::move(rot);
     p->rot32t.resize(static_cast<size_t>(dim) * dim);
+    p->rot32.resize(static_cast<size_t>(dim) * dim);
     for (uint32_t r = 0; r < dim; ++r)
-        for (uint32_t c = 0; c < dim; ++c)
-            p->rot32t[static_cast<size_t>(c) * dim + r] = static_cast<float>(p->rot[static_cast<size_t>(r) * dim + c]);
+        for (uint32_t c = 0; c < dim; ++c) {
+            const float v = static_cast<float>(p->rot[static_cast<size_t>(r) * dim + c]);
+            p->rot32t[static_cast<size_t>(c) * dim + r] = v;
+            p->rot32[static_cast<size_t>(r) * dim + c] = v;
+        }
+    fib_argmin_constants(p);
     int rc = hip_status(hipSetDevice(ctx->device));
     if (!rc) rc = upload(&p->d_cb, p->codebook);
     if (!rc) rc = upload(&p->d_rot, p->rot);
     if (!rc) rc = upload(&p->d_rot32t, p->rot32t);
+    if (!rc) rc = upload(&p->d_rot32, p->rot32);
+    if (!rc) rc = upload(&p->d_kc, p->kc);
     if (rc) { pkv_profile_destroy(p); return rc; }
     *out = p;
     return PKV_OK;
@@ -526,7 +579,8 @@ void pkv_profile_destroy(pkv_profile* p) {
     if (p->ctx) (void)hipSetDevice(p->ctx->device);
     (void)hipDeviceSynchronize();
     for (void* d : {static_cast<void*>(p->d_signs), static_cast<void*>(p->d_qjl), static_cast<void*>(p->d_cs),
-                    static_cast<void*>(p->d_cb), static_cast<void*>(p->d_rot), static_cast<void*>(p->d_rot32t)})
+                    static_cast<void*>(p->d_cb), static_cast<void*>(p->d_rot), static_cast<void*>(p->d_rot32t),
+                    static_cast<void*>(p->d_rot32), static_cast<void*>(p->d_kc)})
         if (d) (void)hipFree(d);
     delete p;
 }

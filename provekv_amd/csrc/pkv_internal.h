@@ -49,6 +49,9 @@ struct FibDev {
     const float* codebook;  // n * k
     const double* rot;      // dim * dim, row-major (encode)
     const float* rot32t;    // dim * dim, f32(rot) transposed: [col][row] (decode)
+    const float* rot32;     // dim * dim, f32(rot) row-major (encode approximation)
+    const float* kc;        // per codeword: -2c0..-2c3, |c|^2 + off, pad x3
+    float thr;              // argmin acceptance margin for the approximate keys
     uint32_t dim, k, n, bits;
 };
 

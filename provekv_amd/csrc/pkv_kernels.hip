@@ -547,11 +547,58 @@ __global__ __launch_bounds__(TILE) void turbo_decode_kernel(
 // ------------------------------------------------------------ fib encode
 // FibQuantizer::encode_batch (fib-quant/src/codec.rs:578-729; n < 4 takes
 // FibQuantizer::encode, 471-516) + FibCodeV1::encode_batch (FB2, 225-320).
+//
+// The reference computes rho = f32(Pi x_hat) with sequential f64 rows and
+// then, per 4-block, an exact f32 argmin over 32 codewords.  Only the argmin
+// reaches the wire, so the kernel decides it from cheap approximations and
+// proves the decision:
+//   rho'  = Pi32 x_hat' by f32 FMA chains.  Rows of Pi and x_hat are unit
+//           vectors, so sum|terms| <= 1 and |rho' - rho| <= 69 * 2^-24.
+//   key_w = bits(|c_w|^2 + off - 2 c_w . rho') with the codeword index in the
+//           5 low bits; the two smallest keys are tracked.
+// If the second smallest key exceeds the smallest by more than `thr` (twice
+// the host-computed worst-case error of a key against the reference's f32
+// distance), the smallest key's codeword is the reference's strict argmin.
+// Otherwise (about 1e-3 of blocks) the block is redone exactly: f64
+// sequential rows of the exact x_hat and the AVX2-order f32 distances.
+
+// Exact reference block: rho for rows 4b..4b+3 and the AVX2-order argmin.
+__device__ __noinline__ uint32_t fib_exact_block(const float* xrow, bool small, double nrm, const double* rot,
+                                                 const float* cb, int b) {
+    float s4[4];
+    for (int t = 0; t < 4; ++t) {
+        const double* m = rot + static_cast<size_t>(4 * b + t) * 64;
+        double acc = 0.0;
+        for (int c = 0; c < 64; ++c) {
+            // batch path: x_hat = f32(x / norm) already stored in the row;
+            // single-vector path: x / norm in f64 (codec.rs:481 vs 608)
+            double xh = small ? static_cast<double>(xrow[c]) / nrm : static_cast<double>(xrow[c]);
+            acc = acc + m[c] * xh;
+        }
+        s4[t] = static_cast<float>(acc);
+    }
+    float bd = u2f(0x7f800000u);
+    uint32_t best = 0;
+    for (int wv = 0; wv < 32; ++wv) {
+        const float* c = cb + 4 * wv;
+        float e0 = c[0] - s4[0], e1 = c[1] - s4[1], e2 = c[2] - s4[2], e3 = c[3] - s4[3];
+        float d = (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
+        if (d < bd) { bd = d; best = static_cast<uint32_t>(wv); }
+    }
+    return best;
+}
+
+__device__ __forceinline__ uint32_t umed3(uint32_t a, uint32_t b, uint32_t c) {
+    return max(min(a, b), min(max(a, b), c));
+}
+
 template <int DIM>
 __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const void* __restrict__ in,
                                                           uint8_t* __restrict__ wire,
                                                           const double* __restrict__ rot,
-                                                          const float* __restrict__ cb) {
+                                                          const float* __restrict__ rot32,
+                                                          const float* __restrict__ cb,
+                                                          const float* __restrict__ kc, float thr) {
     constexpr int PITCH = DIM + 4;
     constexpr int BLOCKS = DIM / 4;
     constexpr int WAVE_FLOATS = WAVE * PITCH + 8;
@@ -573,56 +620,51 @@ __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const
         stage_rows_in<DIM>(stage, in, lc.in_bf16 != 0, seg, v0, nv, lane);
         wave_sync();
         const bool active = static_cast<uint32_t>(lane) < nv;
-        const float* xr = stage + lane * PITCH;
+        float* xr = stage + lane * PITCH;
 
-        // l2_norm (codec.rs:1049-1057) and finiteness (check_finite)
-        bool finite = true;
+        // l2_norm (codec.rs:1049-1057); a non-finite element makes the sum
+        // non-finite, so one test covers check_finite.
+        float xv[DIM];
         double ss = 0.0;
 #pragma unroll
         for (int c = 0; c < DIM; ++c) {
-            float xv = active ? xr[c] : 1.0f;
-            finite &= isfinite_f(xv);
-            double dv = static_cast<double>(xv);
+            xv[c] = active ? xr[c] : 1.0f;
+            double dv = static_cast<double>(xv[c]);
             ss = ss + dv * dv;
         }
         const double nrm = __builtin_sqrt(ss);
-        const bool zero = finite && nrm == 0.0;
-        const double safe_nrm = (finite && !zero) ? nrm : 1.0;
-
-        // x_hat = f32(x / norm) on the batch path (codec.rs:608) and
-        // rho = f32(Pi x_hat), each row a sequential f64 sum
-        // (rotation.rs:107-113); the single-vector path (n < 4, codec.rs:481)
-        // keeps x / norm in f64 and recomputes it per row.
-        float xh[DIM];
+        const bool finite_all = ss == ss && ss < __builtin_inf();
+        const bool zero = finite_all && nrm == 0.0;
+        const double safe_nrm = (finite_all && !zero) ? nrm : 1.0;
+        const float r32 = static_cast<float>(1.0 / safe_nrm);
 #pragma unroll
-        for (int c = 0; c < DIM; ++c)
-            xh[c] = static_cast<float>(static_cast<double>(active ? xr[c] : 0.0f) / safe_nrm);
+        for (int c = 0; c < DIM; ++c) xv[c] = xv[c] * r32;   // x_hat' (within 2^-23 of x / norm)
+
         uint64_t lo = 0, hi = 0;   // 16 x 5-bit indices, LSB-first
+        uint32_t redo = small ? 0xFFFFu : 0u;
         for (int b = 0; b < BLOCKS; ++b) {
-            float s4[4];
+            float rho[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const double* m = rot + static_cast<size_t>(4 * b + t) * DIM;
-                double acc = 0.0;
-                if (!small) {
+                const float* m = rot32 + (4 * b + t) * DIM;
+                float acc = 0.0f;
 #pragma unroll
-                    for (int c = 0; c < DIM; ++c) acc = acc + m[c] * static_cast<double>(xh[c]);
-                } else {
-                    for (int c = 0; c < DIM; ++c)
-                        acc = acc + m[c] * (static_cast<double>(active ? xr[c] : 0.0f) / safe_nrm);
-                }
-                s4[t] = static_cast<float>(acc);
+                for (int c = 0; c < DIM; ++c) acc = __builtin_fmaf(m[c], xv[c], acc);
+                rho[t] = acc;
             }
-            // argmin: AVX2 pairwise order, strict <, lowest index wins
-            float bd = u2f(0x7f800000u);
-            uint32_t best = 0;
-#pragma unroll 8
+            uint32_t m1 = 0xFFFFFFFFu, m2 = 0xFFFFFFFFu;
+#pragma unroll
             for (int wv = 0; wv < 32; ++wv) {
-                const float* c = cb + 4 * wv;
-                float e0 = c[0] - s4[0], e1 = c[1] - s4[1], e2 = c[2] - s4[2], e3 = c[3] - s4[3];
-                float d = (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
-                if (d < bd) { bd = d; best = static_cast<uint32_t>(wv); }
+                const float* k = kc + 8 * wv;   // -2c0, -2c1, -2c2, -2c3, |c|^2 + off
+                float v = __builtin_fmaf(k[0], rho[0],
+                          __builtin_fmaf(k[1], rho[1], __builtin_fmaf(k[2], rho[2], __builtin_fmaf(k[3], rho[3], k[4]))));
+                uint32_t key = (f2u(v) & ~31u) | static_cast<uint32_t>(wv);
+                m2 = umed3(m1, m2, key);
+                m1 = min(m1, key);
             }
+            const float gap = u2f(m2 & ~31u) - u2f(m1 & ~31u);
+            if (!(gap > thr)) redo |= 1u << b;
+            const uint32_t best = m1 & 31u;
             const int bit = 5 * b;
             if (bit < 64) {
                 lo |= static_cast<uint64_t>(best) << bit;
@@ -631,13 +673,29 @@ __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const
                 hi |= static_cast<uint64_t>(best) << (bit - 64);
             }
         }
+        if (active && redo && finite_all && !zero) {
+            if (!small)   // exact x_hat = f32(x / norm) in place (codec.rs:608)
+                for (int c = 0; c < DIM; ++c)
+                    xr[c] = static_cast<float>(static_cast<double>(xr[c]) / safe_nrm);
+            for (int b = 0; b < BLOCKS; ++b) {
+                if (!((redo >> b) & 1u)) continue;
+                const uint64_t best = fib_exact_block(xr, small, safe_nrm, rot, cb, b);
+                const uint32_t bit = 5u * static_cast<uint32_t>(b);
+                if (bit < 64) {
+                    lo = (lo & ~(31ull << bit)) | (best << bit);
+                    if (bit > 59) hi = (hi & ~(31ull >> (64 - bit))) | (best >> (64 - bit));
+                } else {
+                    hi = (hi & ~(31ull << (bit - 64))) | (best << (bit - 64));
+                }
+            }
+        }
         // encode_norm Fp16Paper (codec.rs:994-1020)
         const uint16_t h = f32_to_f16(static_cast<float>(nrm));
         const bool h_ok = (h & 0x7c00u) != 0x7c00u && (h & 0x7fffu) != 0 && !(h & 0x8000u);
 
         if (active) {
             uint32_t vi = v0 + lane;
-            if (!finite) status_fail(lc.status, sidx, 0, vi, KIND_NONFINITE_INPUT);
+            if (!finite_all) status_fail(lc.status, sidx, 0, vi, KIND_NONFINITE_INPUT);
             else if (zero) status_fail(lc.status, sidx, 0, vi, KIND_ZERO_NORM);
             else if (!h_ok) status_fail(lc.status, sidx, 1, vi, KIND_NORM16);
         }
@@ -808,7 +866,7 @@ int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_
 int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire, uint32_t nblocks,
                       void* stream) {
     return launch_big_lds(fib_encode_kernel<64>, nblocks, stage_bytes<64>(), static_cast<hipStream_t>(stream), lc, in,
-                          wire, fd.rot, fd.codebook);
+                          wire, fd.rot, fd.rot32, fd.codebook, fd.kc, fd.thr);
 }
 
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, float* out, uint32_t nblocks,

@@ -153,3 +153,27 @@ def test_fib_errors(ctx):
     # trailing bytes are accepted (fib-quant/src/codec.rs:380-386)
     out = ad.decode_batch_compact(bytes(blob) + b"\1\2\3", SEED)
     assert out.shape == (50, 64)
+
+
+def test_fib_encode_near_ties_take_exact_path(ctx):
+    """Vectors whose rotated blocks sit on the bisector of two codewords: the
+    approximate argmin cannot decide them, the exact path must, and the bytes
+    must still equal the reference's."""
+    ad = FibQuantAdapter(64, 4, 32, 2048, 4, 8)
+    prof = ad.build_quantizer(SEED)
+    cb, rot = prof.constants()
+    cb = cb.reshape(32, 4).astype(np.float64)
+    rot = rot.reshape(64, 64)
+    rng = np.random.RandomState(17)
+    xs = []
+    for _ in range(300):
+        rho = np.zeros(64)
+        for b in range(16):
+            w1, w2 = rng.choice(32, 2, replace=False)
+            t = 0.5 + rng.choice([0.0, 1e-9, -1e-9, 1e-7, 3e-6])
+            rho[4 * b:4 * b + 4] = t * cb[w1] + (1 - t) * cb[w2]
+        x = rot.T @ rho
+        xs.append(x * rng.uniform(0.5, 4.0))
+    x = np.array(xs, np.float32)
+    blob = ad.encode_batch_compact(x, SEED)
+    assert blob == O.fib_encode_batch(x, cb.astype(np.float32), rot)
