@@ -25,6 +25,9 @@ FLAGS = [
     "-fno-fast-math",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs (gfx950 allows it): no v_accvgpr_read per
+    # result element in the fib encode scoring loop
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -28,6 +28,8 @@ struct Slot {
     size_t cap = 0;
     hipEvent_t done = nullptr;
     bool used = false;
+    void* redo = nullptr;        // fib encode redo queue: count word + entries
+    size_t redo_cap = 0;
 };
 
 }  // namespace
@@ -55,13 +57,13 @@ struct pkv_profile {
     float* d_cs = nullptr;
     // fib
     uint32_t k = 0, n = 0, wbits = 0;
-    std::vector<float> codebook, rot32t, rot32, kc;
+    std::vector<float> codebook, rot32t;
+    std::vector<uint32_t> mf;
     std::vector<double> rot;
     float* d_cb = nullptr;
     double* d_rot = nullptr;
     float* d_rot32t = nullptr;
-    float* d_rot32 = nullptr;
-    float* d_kc = nullptr;
+    uint32_t* d_mf = nullptr;
     float thr = 0.0f;
 };
 
@@ -221,14 +223,37 @@ FibDev fib_dev(const pkv_profile* p) {
     f.codebook = p->d_cb;
     f.rot = p->d_rot;
     f.rot32t = p->d_rot32t;
-    f.rot32 = p->d_rot32;
-    f.kc = p->d_kc;
+    f.mf = p->d_mf;
     f.thr = p->thr;
     f.dim = p->dim;
     f.k = p->k;
     f.n = p->n;
     f.bits = p->wbits;
     return f;
+}
+
+// fib encode: size the slot's per-workgroup redo queues (a count and TILE
+// entries per workgroup), then run the MFMA kernel and the exact fixup.
+int launch_fib_encode_queued(Slot* sl, const LaunchCommon& lc, const pkv_profile* prof, const void* d_in,
+                             uint8_t* d_wire, uint32_t nblocks, hipStream_t stream) {
+    const size_t counts_bytes = (4 * static_cast<size_t>(nblocks) + 255) & ~static_cast<size_t>(255);
+    const size_t need = counts_bytes + 4 * static_cast<size_t>(TILE) * nblocks;
+    if (sl->redo_cap < need) {
+        if (sl->redo) {
+            hipError_t e = hipFree(sl->redo);
+            if (e != hipSuccess) return e;
+        }
+        sl->redo = nullptr;
+        sl->redo_cap = 0;
+        const size_t cap = std::max<size_t>(need + need / 4, 1 << 16);
+        hipError_t e = hipMalloc(&sl->redo, cap);
+        if (e != hipSuccess) return e;
+        sl->redo_cap = cap;
+    }
+    FibRedo rq;
+    rq.counts = static_cast<uint32_t*>(sl->redo);
+    rq.entries = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(sl->redo) + counts_bytes);
+    return launch_fib_encode(lc, fib_dev(prof), d_in, d_wire, nblocks, rq, stream);
 }
 
 // Caller holds ctx->mu.
@@ -268,7 +293,7 @@ int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool e
                    : launch_turbo_decode(lc, turbo_dev(prof), d_wire, static_cast<float*>(const_cast<void*>(d_f32)),
                                          nblocks, stream);
     } else {
-        e = encode ? launch_fib_encode(lc, fib_dev(prof), d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
+        e = encode ? launch_fib_encode_queued(sl, lc, prof, d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
                    : launch_fib_decode(lc, fib_dev(prof), d_wire, static_cast<float*>(const_cast<void*>(d_f32)),
                                        nblocks, stream);
     }
@@ -392,6 +417,7 @@ void pkv_ctx_destroy(pkv_ctx* ctx) {
         if (s.done) (void)hipEventDestroy(s.done);
         if (s.dev) (void)hipFree(s.dev);
         if (s.host) (void)hipHostFree(s.host);
+        if (s.redo) (void)hipFree(s.redo);
     }
     if (ctx->own_stream) {
         (void)hipStreamSynchronize(ctx->own_stream);
@@ -476,30 +502,94 @@ int pkv_turbo_profile_create_with_constants(pkv_ctx* ctx, uint32_t dim, uint32_t
 // A gap above 2E between the two smallest keys proves the reference's strict
 // argmin; thr = 2.5 E leaves extra room.  With the codebook's |c| <= 0.35
 // every key stays in (0.5, 2); otherwise every block takes the exact path.
-static void fib_argmin_constants(pkv_profile* p) {
-    const uint32_t n = p->n, k = p->k;
+// f16 halves of v: hi = f16(v), lo = f16(v - hi), both round-to-nearest-even.
+static void f16_split(double v, uint16_t* hi, uint16_t* lo) {
+    const _Float16 h = static_cast<_Float16>(v);
+    const _Float16 l = static_cast<_Float16>(v - static_cast<double>(h));
+    std::memcpy(hi, &h, 2);
+    std::memcpy(lo, &l, 2);
+}
+
+// Operands of the fib encode MFMA path and the acceptance margin `thr` of its
+// approximate argmin.  u = 2^-24; f16 splits: RNE on the host (|v - hi - lo|
+// <= 2^-22 |v| + 2^-25), round-toward-zero in the kernel (<= 2^-20 |v| +
+// 2^-24).  Per rotated component, against the reference's
+// rho = f32(sum_c Pi[j][c] f64(f32(x_c / |x|))) (sequential f64), with unit
+// rows and a unit x_hat (sum_c |Pi[j][c] x_c| <= 1, sum_c |Pi[j][c]| <= 8,
+// sum_c |x_c| <= 8):
+//   x_hat' = x * f32(1 / |x|)                        2.01u
+//   kernel split of x_hat' (2^-20 + 8 * 2^-24)       24u
+//   host split of Pi (2^-22 + 8 * 2^-25)              8u
+//   dropped Pi_lo * x_lo                              8u
+//   f32 accumulation: the 128 small cross products first (< 1u), then 64
+//     hi * hi products, counted as 128 roundings of at most u (twice the
+//     sequential round-to-nearest count: truncating adders are covered)   128u
+//   the reference's own x_hat and rho roundings       2u
+// so |rho' - rho| <= eps_rho = 175u.  A key is the scoring MFMA's
+// f32(|c|^2 + off - 2 c . rho') (16 products of f16 halves, C = 0: 32u S,
+// S the largest sum of |terms|; kernel split of rho' 2 l1 17u; host splits
+// of -2c and of |c|^2 + off (8 l1 + 2 + 4 kmax)u; dropped lo * lo 16 l1 u)
+// with its 5 low bits replaced by the index (31 ulp).  Against the
+// reference's f32 distance (shifted by |rho_b|^2, common to all codewords)
+// a key is off by at most
+//   E = e_score + 2 l1max eps_rho + 8u (cmax + 1)^2 + 31 ulp(kmax),
+// so a gap > 2E between the two smallest keys fixes the reference's argmin;
+// thr = 2.5E.  Keys must stay positive (off - 2 cmax > 0) for the unsigned
+// order to be the float order; otherwise thr = inf and every block is redone.
+static void fib_mfma_constants(pkv_profile* p) {
+    const uint32_t n = p->n, k = p->k, dim = p->dim;
     const double off = 1.25;
     double cmax = 0.0, l1max = 0.0;
-    p->kc.assign(static_cast<size_t>(n) * 8, 0.0f);
+    std::vector<double> sq(n);
     for (uint32_t w = 0; w < n; ++w) {
-        double sq = 0.0, l1 = 0.0;
+        double q = 0.0, l1 = 0.0;
         for (uint32_t t = 0; t < k; ++t) {
             const double c = p->codebook[w * k + t];
-            sq += c * c;
+            q += c * c;
             l1 += std::fabs(c);
-            p->kc[w * 8 + t] = -2.0f * p->codebook[w * k + t];
         }
-        p->kc[w * 8 + 4] = static_cast<float>(sq + off);
-        cmax = std::max(cmax, std::sqrt(sq));
+        sq[w] = q;
+        cmax = std::max(cmax, std::sqrt(q));
         l1max = std::max(l1max, l1);
     }
+    p->mf.assign(MF_WORDS, 0u);
+    auto pack = [](uint16_t a, uint16_t b) { return static_cast<uint32_t>(a) | static_cast<uint32_t>(b) << 16; };
+    for (uint32_t t = 0; t < 2; ++t)
+        for (uint32_t q = 0; q < 4; ++q)
+            for (uint32_t lane = 0; lane < 64; ++lane)
+                for (uint32_t i = 0; i < 4; ++i) {
+                    const uint32_t row = fib_mfma_row(t, lane % 32);
+                    const uint32_t col = 32 * (lane / 32) + 8 * q + 2 * i;
+                    uint16_t h0, l0, h1, l1;
+                    f16_split(p->rot[row * dim + col], &h0, &l0);
+                    f16_split(p->rot[row * dim + col + 1], &h1, &l1);
+                    p->mf[MF_ROT + (((t * 4 + q) * 2 + 0) * 64 + lane) * 4 + i] = pack(h0, h1);
+                    p->mf[MF_ROT + (((t * 4 + q) * 2 + 1) * 64 + lane) * 4 + i] = pack(l0, l1);
+                }
+    for (uint32_t lane = 0; lane < 64; ++lane) {
+        const uint32_t w = lane % 32, h = lane / 32;
+        uint16_t ah, al, bh, bl, kh = 0, kl = 0;
+        f16_split(-2.0 * static_cast<double>(p->codebook[w * k + h]), &ah, &al);
+        f16_split(-2.0 * static_cast<double>(p->codebook[w * k + 2 + h]), &bh, &bl);
+        if (h == 0) f16_split(static_cast<double>(static_cast<float>(sq[w] + off)), &kh, &kl);
+        uint32_t* m = &p->mf[MF_SCA + lane * 4];
+        m[0] = pack(ah, bh);
+        m[1] = pack(ah, bh);
+        m[2] = pack(al, bl);
+        m[3] = pack(kh, kl);
+    }
     const double u = std::ldexp(1.0, -24);
-    const double eps_rho = 69.0 * u * 1.001;
-    const double e_score = 2.0 * u + 4.0 * u + 2.0 * l1max * eps_rho;
-    const double e_d = 8.0 * u * (cmax + 1.0) * (cmax + 1.0);
-    const double e_key = 31.0 * 2.0 * u;
-    const double e = e_score + e_d + e_key;
-    p->thr = cmax <= 0.35 ? static_cast<float>(2.5 * e) : std::numeric_limits<float>::infinity();
+    const double eps_rho = 175.0 * u;
+    const double kmax = off + cmax * cmax + 2.0 * cmax * (1.0 + eps_rho);
+    const double S = off + cmax * cmax + 2.0 * l1max * (1.0 + eps_rho);
+    int ex;
+    (void)std::frexp(kmax, &ex);   // kmax in [2^(ex-1), 2^ex)
+    const double ulp = std::ldexp(1.0, ex - 24);
+    const double e_score = 32.0 * u * S + 2.0 * l1max * 17.0 * u + (8.0 * l1max + 2.0 + 4.0 * kmax) * u +
+                           16.0 * l1max * u;
+    const double e = e_score + 2.0 * l1max * eps_rho + 8.0 * u * (cmax + 1.0) * (cmax + 1.0) + 31.0 * ulp;
+    const bool positive = off - 2.0 * cmax * (1.0 + eps_rho) > 0.25;
+    p->thr = positive ? static_cast<float>(2.5 * e) : std::numeric_limits<float>::infinity();
 }
 
 static int fib_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, std::vector<float> cb,
@@ -515,20 +605,17 @@ static int fib_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n
     p->codebook = std::move(cb);
     p->rot = std::move(rot);
     p->rot32t.resize(static_cast<size_t>(dim) * dim);
-    p->rot32.resize(static_cast<size_t>(dim) * dim);
     for (uint32_t r = 0; r < dim; ++r)
         for (uint32_t c = 0; c < dim; ++c) {
             const float v = static_cast<float>(p->rot[static_cast<size_t>(r) * dim + c]);
             p->rot32t[static_cast<size_t>(c) * dim + r] = v;
-            p->rot32[static_cast<size_t>(r) * dim + c] = v;
         }
-    fib_argmin_constants(p);
+    fib_mfma_constants(p);
     int rc = hip_status(hipSetDevice(ctx->device));
     if (!rc) rc = upload(&p->d_cb, p->codebook);
     if (!rc) rc = upload(&p->d_rot, p->rot);
     if (!rc) rc = upload(&p->d_rot32t, p->rot32t);
-    if (!rc) rc = upload(&p->d_rot32, p->rot32);
-    if (!rc) rc = upload(&p->d_kc, p->kc);
+    if (!rc) rc = upload(&p->d_mf, p->mf);
     if (rc) { pkv_profile_destroy(p); return rc; }
     *out = p;
     return PKV_OK;
@@ -580,7 +667,7 @@ void pkv_profile_destroy(pkv_profile* p) {
     (void)hipDeviceSynchronize();
     for (void* d : {static_cast<void*>(p->d_signs), static_cast<void*>(p->d_qjl), static_cast<void*>(p->d_cs),
                     static_cast<void*>(p->d_cb), static_cast<void*>(p->d_rot), static_cast<void*>(p->d_rot32t),
-                    static_cast<void*>(p->d_rot32), static_cast<void*>(p->d_kc)})
+                    static_cast<void*>(p->d_mf)})
         if (d) (void)hipFree(d);
     delete p;
 }

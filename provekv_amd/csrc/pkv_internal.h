@@ -45,14 +45,44 @@ struct TurboDev {
     uint32_t dim, pbits, proj, mode;
 };
 
+// Per-profile constants of the fib encode MFMA path (32-bit words, each two
+// f16, built on the host, read by fib_encode_kernel):
+//   MF_ROT  [t 2][q 4][part 2][lane 64][4]: A operand of the rotation MFMAs:
+//           f16 hi (part 0) / lo (part 1) halves of
+//           Pi[fib_mfma_row(t, lane % 32)][32 (lane / 32) + 8q + j], j = 0..7
+//   MF_SCA  [lane 64][4]: A operand of the scoring MFMA for codeword
+//           w = lane % 32, h = lane / 32: f16 halves j = 0..7 of
+//           (-2c[w][h])hi, (-2c[w][2+h])hi, same, same, (-2c[w][h])lo,
+//           (-2c[w][2+h])lo, then (|c_w|^2 + off) hi, lo (h = 0) or 0, 0
+constexpr int MF_ROT = 0;
+constexpr int MF_SCA = 4096;
+constexpr int MF_WORDS = MF_SCA + 256;
+
+// Logical rotation row held by physical row m (0..31) of MFMA row tile t:
+// the 32x32 accumulator keeps rows 8(r/4) + 4h + r%4 in register r of lane
+// half h, and the scoring step wants rho[4b + 2s + h] of block b = 8t + r/2,
+// K-step s = r % 2, in that register.
+constexpr uint32_t fib_mfma_row(uint32_t t, uint32_t m) {
+    return 4 * (8 * t + (4 * (m >> 3) + (m & 3)) / 2) + 2 * ((4 * (m >> 3) + (m & 3)) % 2) + ((m >> 2) & 1);
+}
+
 struct FibDev {
     const float* codebook;  // n * k
-    const double* rot;      // dim * dim, row-major (encode)
+    const double* rot;      // dim * dim, row-major (exact encode fixup)
     const float* rot32t;    // dim * dim, f32(rot) transposed: [col][row] (decode)
-    const float* rot32;     // dim * dim, f32(rot) row-major (encode approximation)
-    const float* kc;        // per codeword: -2c0..-2c3, |c|^2 + off, pad x3
+    const uint32_t* mf;     // MF_WORDS (encode MFMA operands)
     float thr;              // argmin acceptance margin for the approximate keys
     uint32_t dim, k, n, bits;
+};
+
+// Per-workgroup queues of vectors whose approximate argmin was not proven,
+// filled by fib_encode_kernel and drained by fib_fixup_kernel.  Workgroup b
+// (TILE vectors of one segment) owns entries[b * TILE ..] and writes their
+// number to counts[b]; an entry is (vector index within the workgroup) |
+// (mask of undecided blocks) << 8.
+struct FibRedo {
+    uint32_t* counts;       // one per workgroup
+    uint32_t* entries;      // TILE per workgroup
 };
 
 struct LaunchCommon {
@@ -79,7 +109,7 @@ int launch_turbo_encode(const LaunchCommon& lc, const TurboDev& td, const void* 
 int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_t* wire, float* out,
                         uint32_t nblocks, void* stream);
 int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire,
-                      uint32_t nblocks, void* stream);
+                      uint32_t nblocks, const FibRedo& rq, void* stream);
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, float* out,
                       uint32_t nblocks, void* stream);
 int launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, void* stream);

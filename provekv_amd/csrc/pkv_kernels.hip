@@ -550,169 +550,439 @@ __global__ __launch_bounds__(TILE) void turbo_decode_kernel(
 //
 // The reference computes rho = f32(Pi x_hat) with sequential f64 rows and
 // then, per 4-block, an exact f32 argmin over 32 codewords.  Only the argmin
-// reaches the wire, so the kernel decides it from cheap approximations and
-// proves the decision:
-//   rho'  = Pi32 x_hat' by f32 FMA chains.  Rows of Pi and x_hat are unit
-//           vectors, so sum|terms| <= 1 and |rho' - rho| <= 69 * 2^-24.
-//   key_w = bits(|c_w|^2 + off - 2 c_w . rho') with the codeword index in the
-//           5 low bits; the two smallest keys are tracked.
-// If the second smallest key exceeds the smallest by more than `thr` (twice
-// the host-computed worst-case error of a key against the reference's f32
+// reaches the wire, so the main kernel decides it on the matrix cores from
+// approximations and proves every decision:
+//   rho'  = Pi x_hat' by v_mfma_f32_32x32x16_f16 on f16 hi/lo halves
+//           (hi*hi + hi*lo + lo*hi, f32 accumulation): per wave 64 rows x 32
+//           vectors.  The rows of Pi are permuted (fib_mfma_row) so that the
+//           accumulator layout is already what the scoring step needs: lane
+//           (h, n) holds rho'[4b + 2m + h] of vector n in register
+//           2(b % 8) + m of row tile b / 8.
+//   key_w = bits(|c_w|^2 + off - 2 c_w . rho') for the 32 codewords of one
+//           block: one more 32x32x16 f16 MFMA whose K holds the split
+//           products and |c_w|^2 + off (times 1.0); codeword index in the 5
+//           low bits; each half-wave keeps its two smallest keys and the
+//           halves meet through v_permlane32_swap.
+// If the second smallest key exceeds the smallest by more than `thr` (2.5x
+// the host-derived worst-case error of a key against the reference's f32
 // distance), the smallest key's codeword is the reference's strict argmin.
-// Otherwise (about 1e-3 of blocks) the block is redone exactly: f64
+// Otherwise the vector is queued with the mask of its undecided blocks (a
+// few % of vectors) and fib_fixup_kernel redoes those blocks exactly: f64
 // sequential rows of the exact x_hat and the AVX2-order f32 distances.
+// Segments of fewer than 4 vectors (the reference's single-vector path with
+// an f64 x_hat) queue all 16 blocks.
 
-// Exact reference block: rho for rows 4b..4b+3 and the AVX2-order argmin.
-__device__ __noinline__ uint32_t fib_exact_block(const float* xrow, bool small, double nrm, const double* rot,
-                                                 const float* cb, int b) {
-    float s4[4];
-    for (int t = 0; t < 4; ++t) {
-        const double* m = rot + static_cast<size_t>(4 * b + t) * 64;
-        double acc = 0.0;
-        for (int c = 0; c < 64; ++c) {
-            // batch path: x_hat = f32(x / norm) already stored in the row;
-            // single-vector path: x / norm in f64 (codec.rs:481 vs 608)
-            double xh = small ? static_cast<double>(xrow[c]) / nrm : static_cast<double>(xrow[c]);
-            acc = acc + m[c] * xh;
-        }
-        s4[t] = static_cast<float>(acc);
-    }
-    float bd = u2f(0x7f800000u);
-    uint32_t best = 0;
-    for (int wv = 0; wv < 32; ++wv) {
-        const float* c = cb + 4 * wv;
-        float e0 = c[0] - s4[0], e1 = c[1] - s4[1], e2 = c[2] - s4[2], e3 = c[3] - s4[3];
-        float d = (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
-        if (d < bd) { bd = d; best = static_cast<uint32_t>(wv); }
-    }
-    return best;
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// f16 halves of a, b by round-toward-zero: hi = (a_hi, b_hi), lo = the
+// rounded remainders; a - a_hi is exact in f32.
+__device__ __forceinline__ uint2 split2(float a, float b) {
+    const auto h = __builtin_amdgcn_cvt_pkrtz(a, b);
+    const float ra = a - static_cast<float>(h[0]), rb = b - static_cast<float>(h[1]);
+    return make_uint2(__builtin_bit_cast(uint32_t, h), __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(ra, rb)));
+}
+
+__device__ __forceinline__ v16f mfma16(const v4u& a, const v4u& b, const v16f& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
 }
 
 __device__ __forceinline__ uint32_t umed3(uint32_t a, uint32_t b, uint32_t c) {
-    return max(min(a, b), min(max(a, b), c));
+    uint32_t r;
+    asm("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
 }
+
+// Elements 32h .. 32h + 31 of vector vi as 8 float4 (f32, or bf16 widened);
+// all loads are issued before any use.
+__device__ __forceinline__ void load_half_row(float4 (&v)[8], const void* __restrict__ in, bool bf16,
+                                              const SegDev& s, uint32_t vi, int h) {
+    const uint64_t off = vec_elem_offset(s, vi) + 32u * static_cast<uint32_t>(h);
+    if (!bf16) {
+        const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(in) + off);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = p[k];
+    } else {
+        const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(in) + off);
+        uint4 w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = p[k];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[2 * k] = make_float4(u2f(w[k].x << 16), u2f(w[k].x & 0xffff0000u), u2f(w[k].y << 16),
+                                   u2f(w[k].y & 0xffff0000u));
+            v[2 * k + 1] = make_float4(u2f(w[k].z << 16), u2f(w[k].z & 0xffff0000u), u2f(w[k].w << 16),
+                                       u2f(w[k].w & 0xffff0000u));
+        }
+    }
+}
+
+// Value of `x` in lane (l % 32) + 32 * from_h, for every lane l.
+__device__ __forceinline__ uint32_t half_lane(uint32_t x, int from_h) {
+    const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return from_h ? p[1] : p[0];
+}
+__device__ __forceinline__ double half_lane(double x, int from_h) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = half_lane(static_cast<uint32_t>(b), from_h);
+    const uint32_t hi = half_lane(static_cast<uint32_t>(b >> 32), from_h);
+    return __builtin_bit_cast(double, static_cast<uint64_t>(hi) << 32 | lo);
+}
+
+// Phase 1 of one 32-vector MFMA tile of fib_encode_kernel: norm and rotated
+// components.  Lane (h, n) = (lane / 32, lane % 32) holds elements
+// 32h .. 32h + 31 of vector v0 + n in x.
+struct FibTileRot {
+    v16f acc0, acc1;   // rho' rows, accumulator layout of row tiles 0 and 1
+    double nrm;
+    bool finite_all, zero;
+};
+
+__device__ __forceinline__ void fib_encode_rotate(FibTileRot& t, const float4 (&x)[8], const uint32_t* rot_lds,
+                                                  int lane) {
+    // l2_norm (codec.rs:1049-1057): sequential f64 sum of squares.  A square
+    // of an f32 is exact in f64, so fma(d, d, s) rounds like s + d * d.
+    // Half 0 sums elements 0..31, hands the partial to half 1, which adds
+    // 32..63; a non-finite element makes the sum non-finite (check_finite).
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float e[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const double d = static_cast<double>(e[j]);
+            ss = __builtin_fma(d, d, ss);
+        }
+    }
+    ss = half_lane(ss, 0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float e[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const double d = static_cast<double>(e[j]);
+            ss = __builtin_fma(d, d, ss);
+        }
+    }
+    ss = half_lane(ss, 1);
+    t.nrm = __builtin_sqrt(ss);
+    t.finite_all = ss == ss && ss < __builtin_inf();
+    t.zero = t.finite_all && t.nrm == 0.0;
+    const double safe_nrm = (t.finite_all && !t.zero) ? t.nrm : 1.0;
+    const float r32 = static_cast<float>(1.0 / safe_nrm);
+
+    // B operands: f16 halves of x_hat' elements 32h + 8q .. 32h + 8q + 7
+    v4u xh[4], xl[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 u = x[2 * q], v = x[2 * q + 1];
+        const uint2 s0 = split2(u.x * r32, u.y * r32), s1 = split2(u.z * r32, u.w * r32);
+        const uint2 s2 = split2(v.x * r32, v.y * r32), s3 = split2(v.z * r32, v.w * r32);
+        xh[q] = v4u{s0.x, s1.x, s2.x, s3.x};
+        xl[q] = v4u{s0.y, s1.y, s2.y, s3.y};
+    }
+    const v4u* rl = reinterpret_cast<const v4u*>(rot_lds);   // [t][q][part][lane]
+    v16f acc0 = {}, acc1 = {};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {   // small cross products first
+        acc0 = mfma16(rl[((0 * 4 + q) * 2 + 0) * 64 + lane], xl[q], acc0);
+        acc1 = mfma16(rl[((1 * 4 + q) * 2 + 0) * 64 + lane], xl[q], acc1);
+        acc0 = mfma16(rl[((0 * 4 + q) * 2 + 1) * 64 + lane], xh[q], acc0);
+        acc1 = mfma16(rl[((1 * 4 + q) * 2 + 1) * 64 + lane], xh[q], acc1);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        acc0 = mfma16(rl[((0 * 4 + q) * 2 + 0) * 64 + lane], xh[q], acc0);
+        acc1 = mfma16(rl[((1 * 4 + q) * 2 + 0) * 64 + lane], xh[q], acc1);
+    }
+    t.acc0 = acc0;
+    t.acc1 = acc1;
+}
+
+// Phase 2: approximate argmin per block, status, redo queue, payload out.
+template <int DIM>
+__device__ __forceinline__ void fib_encode_score(const LaunchCommon& lc, const SegDev& seg, uint32_t sidx,
+                                                 uint8_t* __restrict__ blob, uint32_t v0, const FibTileRot& t,
+                                                 uint32_t* pay, const v4u& sa, float thr, uint32_t* q_count,
+                                                 uint32_t* q_entries, uint32_t tile_v0, int lane) {
+    constexpr uint32_t PLEN = 12;   // f16 norm + 16 x 5 bits
+    const int h = lane >> 5, n = lane & 31;
+    const uint32_t nv = min(32u, seg.n_vectors - v0);
+    const bool active = static_cast<uint32_t>(n) < nv;   // other lanes repeat the last vector
+    const bool small = seg.n_vectors < 4;
+    const v16f& acc0 = t.acc0;
+    const v16f& acc1 = t.acc1;
+    const double nrm = t.nrm;
+    const bool finite_all = t.finite_all, zero = t.zero;
+
+    uint64_t ia = 0, ib = 0;   // indices of blocks 0..7 and 8..15, 5 bits each
+    uint32_t redo = 0;
+    const v16f zero16 = {};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {   // blocks i (row tile 0) and i + 8 (row tile 1)
+        // B: (p0 hi, p1 hi), (p0 lo, p1 lo), (p0 hi, p1 hi), (1, 1) with
+        // p0 = rho'[4b + h], p1 = rho'[4b + 2 + h]
+        const uint2 qa = split2(acc0[2 * i], acc0[2 * i + 1]), qb = split2(acc1[2 * i], acc1[2 * i + 1]);
+        const v4u ba = {qa.x, qa.y, qa.x, 0x3C003C00u}, bb = {qb.x, qb.y, qb.x, 0x3C003C00u};
+        const v16f d0 = mfma16(sa, ba, zero16);
+        const v16f d1 = mfma16(sa, bb, zero16);
+        // keys of accumulator rows w = 8(r/4) + 4h + r%4; two smallest per
+        // half-wave, two keys per step: m2 = min(m2, med3(m1, k, k')),
+        // m1 = min3(m1, k, k') (m1 <= m2 throughout)
+        uint32_t a1 = 0xFFFFFFFFu, a2 = 0xFFFFFFFFu, b1 = 0xFFFFFFFFu, b2 = 0xFFFFFFFFu;
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+            const uint32_t w0 = static_cast<uint32_t>(8 * (r >> 2) + (r & 3)), w1 = w0 + 1;
+            const uint32_t ka = (f2u(d0[r]) & ~31u) | w0, kA = (f2u(d0[r + 1]) & ~31u) | w1;
+            const uint32_t kb = (f2u(d1[r]) & ~31u) | w0, kB = (f2u(d1[r + 1]) & ~31u) | w1;
+            a2 = min(a2, umed3(a1, ka, kA));
+            a1 = min(a1, min(ka, kA));
+            b2 = min(b2, umed3(b1, kb, kB));
+            b1 = min(b1, min(kb, kB));
+        }
+        const uint32_t hb = static_cast<uint32_t>(h) << 2;
+        a1 |= hb; a2 |= hb; b1 |= hb; b2 |= hb;
+        const auto pa = __builtin_amdgcn_permlane32_swap(a1, a1, false, false);
+        const auto pA = __builtin_amdgcn_permlane32_swap(a2, a2, false, false);
+        const auto pb = __builtin_amdgcn_permlane32_swap(b1, b1, false, false);
+        const auto pB = __builtin_amdgcn_permlane32_swap(b2, b2, false, false);
+        const uint32_t ka1 = min(pa[0], pa[1]), ka2 = min(max(pa[0], pa[1]), min(pA[0], pA[1]));
+        const uint32_t kb1 = min(pb[0], pb[1]), kb2 = min(max(pb[0], pb[1]), min(pB[0], pB[1]));
+        if (!(u2f(ka2 & ~31u) - u2f(ka1 & ~31u) > thr)) redo |= 1u << i;
+        if (!(u2f(kb2 & ~31u) - u2f(kb1 & ~31u) > thr)) redo |= 1u << (i + 8);
+        ia |= static_cast<uint64_t>(ka1 & 31u) << (5 * i);
+        ib |= static_cast<uint64_t>(kb1 & 31u) << (5 * i);
+        __builtin_amdgcn_sched_barrier(0);   // keep one block pair's results live at a time
+    }
+    const uint64_t ilo = ia | (ib << 40);
+    const uint32_t iw[3] = {static_cast<uint32_t>(ilo), static_cast<uint32_t>(ilo >> 32),
+                            static_cast<uint32_t>(ib >> 24)};
+
+    // encode_norm Fp16Paper (codec.rs:994-1020)
+    const uint16_t h16 = f32_to_f16(static_cast<float>(nrm));
+    const bool h_ok = (h16 & 0x7c00u) != 0x7c00u && (h16 & 0x7fffu) != 0 && !(h16 & 0x8000u);
+    const bool owner = active && h == 0;
+    const uint32_t vi = v0 + static_cast<uint32_t>(n);
+    if (owner) {
+        if (!finite_all) status_fail(lc.status, sidx, 0, vi, KIND_NONFINITE_INPUT);
+        else if (zero) status_fail(lc.status, sidx, 0, vi, KIND_ZERO_NORM);
+        else if (!h_ok) status_fail(lc.status, sidx, 1, vi, KIND_NORM16);
+    }
+    const bool queue = owner && finite_all && !zero && (small || redo != 0);
+    const uint64_t qmask = __ballot(queue);
+    if (qmask) {   // workgroup-local queue: an LDS counter, no device atomics
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(q_count, static_cast<uint32_t>(__popcll(qmask)));
+        base = __shfl(base, 0);
+        if (queue) {
+            const uint32_t slot = base + static_cast<uint32_t>(__popcll(qmask & ((1ull << lane) - 1ull)));
+            q_entries[slot] = (vi - tile_v0) | (small ? 0xFFFFu : redo) << 8;
+        }
+    }
+    // payload [f16 norm][16 x 5-bit indices] = 12 bytes via LDS, so the
+    // wave's 32 payloads leave as one byte range
+    if (owner) {
+        pay[3 * n + 0] = static_cast<uint32_t>(h16) | (iw[0] << 16);
+        pay[3 * n + 1] = (iw[0] >> 16) | (iw[1] << 16);
+        pay[3 * n + 2] = (iw[1] >> 16) | (iw[2] << 16);
+    }
+    wave_sync();
+    lds_to_global(blob + 19 + static_cast<uint64_t>(v0) * PLEN, pay, nv * PLEN, lane);
+    wave_sync();
+}
+
+constexpr int FIB_PAY_WORDS = 32 * 3 + 4;
 
 template <int DIM>
 __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const void* __restrict__ in,
-                                                          uint8_t* __restrict__ wire,
-                                                          const double* __restrict__ rot,
-                                                          const float* __restrict__ rot32,
-                                                          const float* __restrict__ cb,
-                                                          const float* __restrict__ kc, float thr) {
-    constexpr int PITCH = DIM + 4;
-    constexpr int BLOCKS = DIM / 4;
-    constexpr int WAVE_FLOATS = WAVE * PITCH + 8;
-    constexpr uint32_t PLEN = 2 + (BLOCKS * 5 + 7) / 8;
-    extern __shared__ float smem[];
-
+                                                          uint8_t* __restrict__ wire, const uint32_t* __restrict__ mf,
+                                                          float thr, FibRedo rq) {
+    static_assert(DIM == 64, "the MFMA layout is built for head_dim 64");
+    extern __shared__ uint32_t smem_u[];
+    uint32_t* rot_lds = smem_u;   // MF_ROT block (MF_SCA words)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    float* stage = smem + wave * WAVE_FLOATS;
+    uint32_t* pay = smem_u + MF_SCA + wave * FIB_PAY_WORDS;
+
     const uint32_t blk = blockIdx.x;
     const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
     const SegDev seg = lc.segs[sidx];
     const uint32_t tile = blk - lc.tile_start[sidx];
-    const uint32_t v0 = tile * TILE + wave * WAVE;
     uint8_t* blob = wire + seg.wire_offset;
-    const bool small = seg.n_vectors < 4;
+    const int h = lane >> 5, n = lane & 31;
+    const uint32_t v0 = tile * TILE + wave * WAVE;
+    const bool bf16 = lc.in_bf16 != 0;
 
+    // tile 0's input rows first: their latency overlaps the set-up (lanes
+    // past the end re-read the last vector; their results are dropped)
+    float4 xa[8], xb[8];
+    const uint32_t last = seg.n_vectors - 1;
+    if (v0 < seg.n_vectors) load_half_row(xa, in, bf16, seg, min(v0 + n, last), h);
+    {
+        const uint4* src = reinterpret_cast<const uint4*>(mf + MF_ROT);
+        uint4* dst = reinterpret_cast<uint4*>(rot_lds);
+        uint4 t[MF_SCA / 4 / TILE];
+#pragma unroll
+        for (int k = 0; k < MF_SCA / 4 / TILE; ++k) t[k] = src[threadIdx.x + k * TILE];
+#pragma unroll
+        for (int k = 0; k < MF_SCA / 4 / TILE; ++k) dst[threadIdx.x + k * TILE] = t[k];
+    }
+    const uint4 sa4 = reinterpret_cast<const uint4*>(mf + MF_SCA)[lane];
+    const v4u sa = {sa4.x, sa4.y, sa4.z, sa4.w};
+    __shared__ uint32_t q_count;
+    if (threadIdx.x == 0) q_count = 0;
+    uint32_t* q_entries = rq.entries + static_cast<uint64_t>(blk) * TILE;
+    const uint32_t tile_v0 = tile * TILE;
+    __syncthreads();
+
+    // tile 1's loads are issued once tile 0's rotation has consumed its
+    // inputs, and land while tile 0 is scored
     if (v0 < seg.n_vectors) {
-        const uint32_t nv = min(static_cast<uint32_t>(WAVE), seg.n_vectors - v0);
-        stage_rows_in<DIM>(stage, in, lc.in_bf16 != 0, seg, v0, nv, lane);
-        wave_sync();
-        const bool active = static_cast<uint32_t>(lane) < nv;
-        float* xr = stage + lane * PITCH;
-
-        // l2_norm (codec.rs:1049-1057); a non-finite element makes the sum
-        // non-finite, so one test covers check_finite.
-        float xv[DIM];
-        double ss = 0.0;
-#pragma unroll
-        for (int c = 0; c < DIM; ++c) {
-            xv[c] = active ? xr[c] : 1.0f;
-            double dv = static_cast<double>(xv[c]);
-            ss = ss + dv * dv;
-        }
-        const double nrm = __builtin_sqrt(ss);
-        const bool finite_all = ss == ss && ss < __builtin_inf();
-        const bool zero = finite_all && nrm == 0.0;
-        const double safe_nrm = (finite_all && !zero) ? nrm : 1.0;
-        const float r32 = static_cast<float>(1.0 / safe_nrm);
-#pragma unroll
-        for (int c = 0; c < DIM; ++c) xv[c] = xv[c] * r32;   // x_hat' (within 2^-23 of x / norm)
-
-        uint64_t lo = 0, hi = 0;   // 16 x 5-bit indices, LSB-first
-        uint32_t redo = small ? 0xFFFFu : 0u;
-        for (int b = 0; b < BLOCKS; ++b) {
-            float rho[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const float* m = rot32 + (4 * b + t) * DIM;
-                float acc = 0.0f;
-#pragma unroll
-                for (int c = 0; c < DIM; ++c) acc = __builtin_fmaf(m[c], xv[c], acc);
-                rho[t] = acc;
-            }
-            uint32_t m1 = 0xFFFFFFFFu, m2 = 0xFFFFFFFFu;
-#pragma unroll
-            for (int wv = 0; wv < 32; ++wv) {
-                const float* k = kc + 8 * wv;   // -2c0, -2c1, -2c2, -2c3, |c|^2 + off
-                float v = __builtin_fmaf(k[0], rho[0],
-                          __builtin_fmaf(k[1], rho[1], __builtin_fmaf(k[2], rho[2], __builtin_fmaf(k[3], rho[3], k[4]))));
-                uint32_t key = (f2u(v) & ~31u) | static_cast<uint32_t>(wv);
-                m2 = umed3(m1, m2, key);
-                m1 = min(m1, key);
-            }
-            const float gap = u2f(m2 & ~31u) - u2f(m1 & ~31u);
-            if (!(gap > thr)) redo |= 1u << b;
-            const uint32_t best = m1 & 31u;
-            const int bit = 5 * b;
-            if (bit < 64) {
-                lo |= static_cast<uint64_t>(best) << bit;
-                if (bit > 59) hi |= static_cast<uint64_t>(best) >> (64 - bit);
-            } else {
-                hi |= static_cast<uint64_t>(best) << (bit - 64);
-            }
-        }
-        if (active && redo && finite_all && !zero) {
-            if (!small)   // exact x_hat = f32(x / norm) in place (codec.rs:608)
-                for (int c = 0; c < DIM; ++c)
-                    xr[c] = static_cast<float>(static_cast<double>(xr[c]) / safe_nrm);
-            for (int b = 0; b < BLOCKS; ++b) {
-                if (!((redo >> b) & 1u)) continue;
-                const uint64_t best = fib_exact_block(xr, small, safe_nrm, rot, cb, b);
-                const uint32_t bit = 5u * static_cast<uint32_t>(b);
-                if (bit < 64) {
-                    lo = (lo & ~(31ull << bit)) | (best << bit);
-                    if (bit > 59) hi = (hi & ~(31ull >> (64 - bit))) | (best >> (64 - bit));
-                } else {
-                    hi = (hi & ~(31ull << (bit - 64))) | (best << (bit - 64));
-                }
-            }
-        }
-        // encode_norm Fp16Paper (codec.rs:994-1020)
-        const uint16_t h = f32_to_f16(static_cast<float>(nrm));
-        const bool h_ok = (h & 0x7c00u) != 0x7c00u && (h & 0x7fffu) != 0 && !(h & 0x8000u);
-
-        if (active) {
-            uint32_t vi = v0 + lane;
-            if (!finite_all) status_fail(lc.status, sidx, 0, vi, KIND_NONFINITE_INPUT);
-            else if (zero) status_fail(lc.status, sidx, 0, vi, KIND_ZERO_NORM);
-            else if (!h_ok) status_fail(lc.status, sidx, 1, vi, KIND_NORM16);
-        }
-        wave_sync();
-        // payload: [f16 norm][16 x 5-bit indices] = 12 bytes, dword aligned
-        uint32_t* pw = reinterpret_cast<uint32_t*>(stage) + lane * (PLEN / 4);
-        if (active) {
-            pw[0] = static_cast<uint32_t>(h) | (static_cast<uint32_t>(lo) << 16);
-            pw[1] = static_cast<uint32_t>(lo >> 16);
-            pw[2] = static_cast<uint32_t>(lo >> 48) | (static_cast<uint32_t>(hi) << 16);
-        }
-        wave_sync();
-        lds_to_global(blob + 19 + static_cast<uint64_t>(v0) * PLEN, reinterpret_cast<uint32_t*>(stage),
-                      nv * PLEN, lane);
+        FibTileRot t;
+        fib_encode_rotate(t, xa, rot_lds, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        if (v0 + 32 < seg.n_vectors) load_half_row(xb, in, bf16, seg, min(v0 + 32 + n, last), h);
+        fib_encode_score<DIM>(lc, seg, sidx, blob, v0, t, pay, sa, thr, &q_count, q_entries, tile_v0, lane);
+    }
+    if (v0 + 32 < seg.n_vectors) {
+        FibTileRot t;
+        fib_encode_rotate(t, xb, rot_lds, lane);
+        fib_encode_score<DIM>(lc, seg, sidx, blob, v0 + 32, t, pay, sa, thr, &q_count, q_entries, tile_v0, lane);
     }
     if (tile == 0 && threadIdx.x < 19)
-        blob[threadIdx.x] = static_cast<uint8_t>(fb2_byte(threadIdx.x, 5u, BLOCKS, seg.n_vectors, PLEN - 2));
+        blob[threadIdx.x] = static_cast<uint8_t>(fb2_byte(threadIdx.x, 5u, DIM / 4, seg.n_vectors, 10u));
+    __syncthreads();
+    if (threadIdx.x == 0) rq.counts[blk] = q_count;
+}
+
+// Exact redo of the queued (vector, block) decisions of fib_encode_kernel.
+// Wave w of workgroup b drains the queue of encode workgroup 4b + w, 16
+// entries at a time: 4 lanes per vector rebuild x_hat exactly (sequential f64
+// norm; f32(x / norm), or x / norm in f64 for segments of fewer than 4
+// vectors), then 16 undecided blocks at a time get one lane per rho row
+// (sequential f64 dot, rotation.rs:107-113) and a quarter of the codewords
+// per lane in the AVX2 distance order with strict < (simd_nearest.rs:44-104);
+// the entry's owner lane patches the 5-bit fields.
+template <int DIM>
+__global__ __launch_bounds__(TILE) void fib_fixup_kernel(LaunchCommon lc, const void* __restrict__ in,
+                                                         uint8_t* __restrict__ wire, const double* __restrict__ rot,
+                                                         const float* __restrict__ cb, FibRedo rq, uint32_t ntiles) {
+    constexpr int G = 16;
+    __shared__ double xh_s[WAVES][G][DIM];
+    __shared__ float xf_s[WAVES][G][DIM];
+    __shared__ float part_s[WAVES][G][4][2];
+    __shared__ float rho_s[WAVES][G][4];
+    __shared__ uint32_t mask_s[WAVES][G];
+    __shared__ uint8_t res_s[WAVES][G][DIM / 4];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int e = lane >> 2, t = lane & 3;
+    const uint32_t tb = blockIdx.x * WAVES + wave;
+    if (tb >= ntiles) return;
+    const uint32_t count = min(rq.counts[tb], TILE);
+    if (count == 0) return;
+    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, tb);
+    const SegDev seg = lc.segs[sidx];
+    const bool small = seg.n_vectors < 4;
+    const uint32_t tile_v0 = (tb - lc.tile_start[sidx]) * TILE;
+    const uint32_t* ents = rq.entries + static_cast<uint64_t>(tb) * TILE;
+    for (uint32_t g0 = 0; g0 < count; g0 += G) {
+        const uint32_t ne = min(static_cast<uint32_t>(G), count - g0);
+        const bool has = static_cast<uint32_t>(e) < ne;
+        uint32_t vi = 0, mask = 0;
+        if (has) {
+            const uint32_t ent = ents[g0 + e];
+            vi = tile_v0 + (ent & 0xFFu);
+            mask = ent >> 8;
+        }
+        if (has) {
+            const uint64_t off = vec_elem_offset(seg, vi);
+            for (int c = 16 * t; c < 16 * t + 16; ++c)
+                xf_s[wave][e][c] = lc.in_bf16 ? u2f(static_cast<uint32_t>(static_cast<const uint16_t*>(in)[off + c]) << 16)
+                                              : static_cast<const float*>(in)[off + c];
+            if (t == 0) mask_s[wave][e] = mask;
+        }
+        wave_sync();
+        double nrm = 1.0;
+        if (has && t == 0) {
+            double s = 0.0;
+            for (int c = 0; c < DIM; ++c) {
+                const double dv = static_cast<double>(xf_s[wave][e][c]);
+                s = s + dv * dv;
+            }
+            nrm = __builtin_sqrt(s);
+        }
+        nrm = __shfl(nrm, lane & ~3);
+        if (has)
+            for (int c = 16 * t; c < 16 * t + 16; ++c) {
+                const double q = static_cast<double>(xf_s[wave][e][c]) / nrm;
+                xh_s[wave][e][c] = small ? q : static_cast<double>(static_cast<float>(q));
+            }
+        wave_sync();
+        uint32_t total = 0;
+        for (uint32_t j = 0; j < ne; ++j) total += __popc(mask_s[wave][j]);
+        for (uint32_t p0 = 0; p0 < total; p0 += G) {
+            const uint32_t qi = p0 + static_cast<uint32_t>(e);
+            int pe = -1, pb = 0;
+            if (qi < total) {
+                uint32_t acc = 0;
+                for (uint32_t j = 0; j < ne; ++j) {
+                    uint32_t m = mask_s[wave][j];
+                    const uint32_t c = __popc(m);
+                    if (qi < acc + c) {
+                        for (uint32_t k = qi - acc; k > 0; --k) m &= m - 1u;
+                        pe = static_cast<int>(j);
+                        pb = __ffs(m) - 1;
+                        break;
+                    }
+                    acc += c;
+                }
+            }
+            if (pe >= 0) {
+                const double* row = rot + static_cast<size_t>(4 * pb + t) * DIM;
+                double a = 0.0;
+                for (int c = 0; c < DIM; ++c) a = a + row[c] * xh_s[wave][pe][c];
+                rho_s[wave][e][t] = static_cast<float>(a);
+            }
+            wave_sync();
+            if (pe >= 0) {
+                const float s0 = rho_s[wave][e][0], s1 = rho_s[wave][e][1];
+                const float s2 = rho_s[wave][e][2], s3 = rho_s[wave][e][3];
+                float bd = u2f(0x7f800000u);
+                uint32_t bw = 0;
+                for (int w = 8 * t; w < 8 * t + 8; ++w) {
+                    const float* c = cb + 4 * w;
+                    const float e0 = c[0] - s0, e1 = c[1] - s1, e2 = c[2] - s2, e3 = c[3] - s3;
+                    const float dd = (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
+                    if (dd < bd) { bd = dd; bw = static_cast<uint32_t>(w); }
+                }
+                part_s[wave][e][t][0] = bd;
+                part_s[wave][e][t][1] = u2f(bw);
+            }
+            wave_sync();
+            if (pe >= 0 && t == 0) {
+                float bd = part_s[wave][e][0][0];
+                uint32_t bw = f2u(part_s[wave][e][0][1]);
+                for (int u = 1; u < 4; ++u)
+                    if (part_s[wave][e][u][0] < bd) { bd = part_s[wave][e][u][0]; bw = f2u(part_s[wave][e][u][1]); }
+                res_s[wave][pe][pb] = static_cast<uint8_t>(bw);
+            }
+            wave_sync();
+        }
+        if (has && t == 0) {
+            uint8_t* p = wire + seg.wire_offset + 19 + static_cast<uint64_t>(vi) * 12 + 2;
+            uint32_t iw[3] = {0u, 0u, 0u};
+            for (int i = 0; i < 10; ++i) iw[i >> 2] |= static_cast<uint32_t>(p[i]) << (8 * (i & 3));
+            for (int b = 0; b < DIM / 4; ++b) {
+                if (!((mask >> b) & 1u)) continue;
+                const uint32_t w = res_s[wave][e][b];
+                const int bit = 5 * b, wd = bit >> 5, sh = bit & 31;
+                iw[wd] = (iw[wd] & ~(31u << sh)) | (w << sh);
+                if (sh > 27) iw[wd + 1] = (iw[wd + 1] & ~(31u >> (32 - sh))) | (w >> (32 - sh));
+            }
+            for (int i = 0; i < 10; ++i) p[i] = static_cast<uint8_t>(iw[i >> 2] >> (8 * (i & 3)));
+        }
+        wave_sync();
+    }
 }
 
 // ------------------------------------------------------------ fib decode
@@ -864,9 +1134,14 @@ int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_
 }
 
 int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire, uint32_t nblocks,
-                      void* stream) {
-    return launch_big_lds(fib_encode_kernel<64>, nblocks, stage_bytes<64>(), static_cast<hipStream_t>(stream), lc, in,
-                          wire, fd.rot, fd.rot32, fd.codebook, fd.kc, fd.thr);
+                      const FibRedo& rq, void* stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    constexpr size_t lds = (MF_SCA + WAVES * FIB_PAY_WORDS) * sizeof(uint32_t);
+    hipError_t e = launch_big_lds(fib_encode_kernel<64>, nblocks, lds, st, lc, in, wire, fd.mf, fd.thr, rq);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(fib_fixup_kernel<64>, dim3((nblocks + WAVES - 1) / WAVES), dim3(TILE), 0, st, lc, in, wire,
+                       fd.rot, fd.codebook, rq, nblocks);
+    return hipGetLastError();
 }
 
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, float* out, uint32_t nblocks,
