@@ -57,12 +57,14 @@ struct pkv_profile {
     float* d_cs = nullptr;
     // fib
     uint32_t k = 0, n = 0, wbits = 0;
-    std::vector<float> codebook, rot32t;
+    std::vector<float> codebook, rot32t, rot32;
     std::vector<uint32_t> mf;
-    std::vector<double> rot;
+    std::vector<double> rot, rot_t;
     float* d_cb = nullptr;
-    double* d_rot = nullptr;
+    double* d_rot_t = nullptr;
     float* d_rot32t = nullptr;
+    float* d_rot32 = nullptr;
+    int mfma_decode = 0;
     uint32_t* d_mf = nullptr;
     float thr = 0.0f;
 };
@@ -221,8 +223,10 @@ TurboDev turbo_dev(const pkv_profile* p) {
 FibDev fib_dev(const pkv_profile* p) {
     FibDev f;
     f.codebook = p->d_cb;
-    f.rot = p->d_rot;
+    f.rot_t = p->d_rot_t;
     f.rot32t = p->d_rot32t;
+    f.rot32 = p->d_rot32;
+    f.mfma_decode = p->mfma_decode;
     f.mf = p->d_mf;
     f.thr = p->thr;
     f.dim = p->dim;
@@ -232,11 +236,11 @@ FibDev fib_dev(const pkv_profile* p) {
     return f;
 }
 
-// fib encode: size the slot's per-workgroup redo queues (a count and TILE
-// entries per workgroup), then run the MFMA kernel and the exact fixup.
+// fib encode: size the slot's per-workgroup redo queues (a 4-word head and
+// TILE entries per workgroup), then run the MFMA kernel and the exact fixup.
 int launch_fib_encode_queued(Slot* sl, const LaunchCommon& lc, const pkv_profile* prof, const void* d_in,
                              uint8_t* d_wire, uint32_t nblocks, hipStream_t stream) {
-    const size_t counts_bytes = (4 * static_cast<size_t>(nblocks) + 255) & ~static_cast<size_t>(255);
+    const size_t counts_bytes = (16 * static_cast<size_t>(nblocks) + 255) & ~static_cast<size_t>(255);
     const size_t need = counts_bytes + 4 * static_cast<size_t>(TILE) * nblocks;
     if (sl->redo_cap < need) {
         if (sl->redo) {
@@ -251,7 +255,7 @@ int launch_fib_encode_queued(Slot* sl, const LaunchCommon& lc, const pkv_profile
         sl->redo_cap = cap;
     }
     FibRedo rq;
-    rq.counts = static_cast<uint32_t*>(sl->redo);
+    rq.heads = static_cast<uint32_t*>(sl->redo);
     rq.entries = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(sl->redo) + counts_bytes);
     return launch_fib_encode(lc, fib_dev(prof), d_in, d_wire, nblocks, rq, stream);
 }
@@ -592,6 +596,22 @@ static void fib_mfma_constants(pkv_profile* p) {
     p->thr = positive ? static_cast<float>(2.5 * e) : std::numeric_limits<float>::infinity();
 }
 
+// The matrix-core decode is used only if every product it can form equals
+// f32 multiplication for this profile's rotation and codebook.
+static int fib_verify_mfma_products(pkv_ctx* ctx, pkv_profile* p) {
+    uint32_t* d_bad = nullptr;
+    HIP_TRY(hipMalloc(&d_bad, sizeof(uint32_t)));
+    uint32_t bad = 1;
+    hipError_t e = hipMemsetAsync(d_bad, 0, sizeof(uint32_t), ctx->own_stream);
+    if (e == hipSuccess) e = static_cast<hipError_t>(launch_fib_product_check(p->d_rot32, p->d_cb, d_bad, ctx->own_stream));
+    if (e == hipSuccess) e = hipMemcpyAsync(&bad, d_bad, sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->own_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->own_stream);
+    (void)hipFree(d_bad);
+    if (e != hipSuccess) return hip_status(e);
+    p->mfma_decode = bad == 0 ? 1 : 0;
+    return PKV_OK;
+}
+
 static int fib_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, std::vector<float> cb,
                               std::vector<double> rot, pkv_profile** out) {
     pkv_profile* p = new (std::nothrow) pkv_profile();
@@ -605,17 +625,23 @@ static int fib_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n
     p->codebook = std::move(cb);
     p->rot = std::move(rot);
     p->rot32t.resize(static_cast<size_t>(dim) * dim);
+    p->rot_t.resize(static_cast<size_t>(dim) * dim);
+    p->rot32.resize(static_cast<size_t>(dim) * dim);
     for (uint32_t r = 0; r < dim; ++r)
         for (uint32_t c = 0; c < dim; ++c) {
             const float v = static_cast<float>(p->rot[static_cast<size_t>(r) * dim + c]);
             p->rot32t[static_cast<size_t>(c) * dim + r] = v;
+            p->rot32[static_cast<size_t>(r) * dim + c] = v;
+            p->rot_t[static_cast<size_t>(c) * dim + r] = p->rot[static_cast<size_t>(r) * dim + c];
         }
     fib_mfma_constants(p);
     int rc = hip_status(hipSetDevice(ctx->device));
     if (!rc) rc = upload(&p->d_cb, p->codebook);
-    if (!rc) rc = upload(&p->d_rot, p->rot);
+    if (!rc) rc = upload(&p->d_rot_t, p->rot_t);
     if (!rc) rc = upload(&p->d_rot32t, p->rot32t);
     if (!rc) rc = upload(&p->d_mf, p->mf);
+    if (!rc) rc = upload(&p->d_rot32, p->rot32);
+    if (!rc) rc = fib_verify_mfma_products(ctx, p);
     if (rc) { pkv_profile_destroy(p); return rc; }
     *out = p;
     return PKV_OK;
@@ -640,7 +666,7 @@ int pkv_fib_profile_create(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, u
     if (lloyd_iterations == 0 || lloyd_iterations > 100000) return PKV_ERR_INVALID_ARG;
     if (training_samples < n || training_samples > 10000000) return PKV_ERR_INVALID_ARG;
     std::vector<float> cb;
-    std::vector<double> rot;
+    std::vector<double> rot, rot_t;
     rc = make_fib_codebook(dim, k, n, seed, training_samples, lloyd_restarts, lloyd_iterations, cb, nullptr, nullptr);
     if (rc) return rc;
     rc = make_fib_rotation(dim, seed, rot);
@@ -666,8 +692,8 @@ void pkv_profile_destroy(pkv_profile* p) {
     if (p->ctx) (void)hipSetDevice(p->ctx->device);
     (void)hipDeviceSynchronize();
     for (void* d : {static_cast<void*>(p->d_signs), static_cast<void*>(p->d_qjl), static_cast<void*>(p->d_cs),
-                    static_cast<void*>(p->d_cb), static_cast<void*>(p->d_rot), static_cast<void*>(p->d_rot32t),
-                    static_cast<void*>(p->d_mf)})
+                    static_cast<void*>(p->d_cb), static_cast<void*>(p->d_rot_t), static_cast<void*>(p->d_rot32t),
+                    static_cast<void*>(p->d_mf), static_cast<void*>(p->d_rot32)})
         if (d) (void)hipFree(d);
     delete p;
 }
@@ -842,7 +868,7 @@ int pkv_fib_constants(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint3
         std::memcpy(codebook, cb.data(), cb.size() * sizeof(float));
     }
     if (rotation) {
-        std::vector<double> rot;
+        std::vector<double> rot, rot_t;
         int rc = make_fib_rotation(dim, seed, rot);
         if (rc) return rc;
         std::memcpy(rotation, rot.data(), rot.size() * sizeof(double));

@@ -68,8 +68,10 @@ constexpr uint32_t fib_mfma_row(uint32_t t, uint32_t m) {
 
 struct FibDev {
     const float* codebook;  // n * k
-    const double* rot;      // dim * dim, row-major (exact encode fixup)
-    const float* rot32t;    // dim * dim, f32(rot) transposed: [col][row] (decode)
+    const double* rot_t;    // dim * dim, transposed: [col][row] (exact encode fixup)
+    const float* rot32t;    // dim * dim, f32(rot) transposed: [col][row] (VALU decode)
+    const float* rot32;     // dim * dim, f32(rot) row-major (MFMA decode)
+    int mfma_decode;        // matrix-core products verified bit-exact for this profile
     const uint32_t* mf;     // MF_WORDS (encode MFMA operands)
     float thr;              // argmin acceptance margin for the approximate keys
     uint32_t dim, k, n, bits;
@@ -77,11 +79,11 @@ struct FibDev {
 
 // Per-workgroup queues of vectors whose approximate argmin was not proven,
 // filled by fib_encode_kernel and drained by fib_fixup_kernel.  Workgroup b
-// (TILE vectors of one segment) owns entries[b * TILE ..] and writes their
-// number to counts[b]; an entry is (vector index within the workgroup) |
-// (mask of undecided blocks) << 8.
+// (TILE vectors of one segment) writes heads[4b ..] = {entry count, segment,
+// first vector index, 0} and owns entries[b * TILE ..]; an entry is (vector
+// index within the workgroup) | (mask of undecided blocks) << 8.
 struct FibRedo {
-    uint32_t* counts;       // one per workgroup
+    uint32_t* heads;        // 4 words per workgroup
     uint32_t* entries;      // TILE per workgroup
 };
 
@@ -113,5 +115,6 @@ int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, 
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, float* out,
                       uint32_t nblocks, void* stream);
 int launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, void* stream);
+int launch_fib_product_check(const float* rot32, const float* cb, uint32_t* bad, void* stream);
 
 }  // namespace pkv

@@ -82,53 +82,86 @@ __device__ void lds_to_global(uint8_t* __restrict__ dst, const uint32_t* lds, ui
 }
 
 // Move nbytes from global memory at any byte alignment into LDS (LDS byte 0 ==
-// src byte 0).  Only aligned dwords holding at least one source byte are read.
+// src byte 0).  Only aligned dwords holding at least one source byte are read;
+// each lane issues up to 8 loads before it waits on any of them.
 __device__ void global_to_lds(uint32_t* lds, const uint8_t* __restrict__ src, uint32_t nbytes, int lane) {
+    constexpr uint32_t BATCH = 8;
     const uintptr_t a = reinterpret_cast<uintptr_t>(src);
     const uint32_t* s32 = reinterpret_cast<const uint32_t*>(a & ~static_cast<uintptr_t>(3));
     const uint32_t sh = static_cast<uint32_t>(a & 3u);
     const uint32_t ndw = (nbytes + 3u) >> 2;
-    const uintptr_t last = a + nbytes - 1;   // last valid byte
-    for (uint32_t k = lane; k < ndw; k += WAVE) {
-        uint32_t w0 = s32[k];
-        uint32_t v = w0;
-        if (sh) {
-            uintptr_t next = (a & ~static_cast<uintptr_t>(3)) + 4u * (k + 1);
-            uint32_t w1 = (next <= last) ? s32[k + 1] : 0u;
-            v = __builtin_amdgcn_alignbyte(w1, w0, sh);
+    // dwords of the aligned window [a & ~3, a + nbytes): the last one may be
+    // the only reader of the tail bytes
+    const uint32_t nwin = static_cast<uint32_t>(((a + nbytes + 3u) & ~static_cast<uintptr_t>(3)) -
+                                                (a & ~static_cast<uintptr_t>(3))) >> 2;
+    for (uint32_t k0 = 0; k0 < ndw; k0 += BATCH * WAVE) {
+        uint32_t w0[BATCH], w1[BATCH];
+#pragma unroll
+        for (uint32_t j = 0; j < BATCH; ++j) {
+            const uint32_t k = k0 + j * WAVE + static_cast<uint32_t>(lane);
+            w0[j] = k < ndw ? s32[k] : 0u;
+            w1[j] = (sh && k < ndw && k + 1 < nwin) ? s32[k + 1] : 0u;
         }
-        lds[k] = v;
+#pragma unroll
+        for (uint32_t j = 0; j < BATCH; ++j) {
+            const uint32_t k = k0 + j * WAVE + static_cast<uint32_t>(lane);
+            if (k < ndw) lds[k] = sh ? __builtin_amdgcn_alignbyte(w1[j], w0[j], sh) : w0[j];
+        }
     }
 }
 
-// Stage nv rows of DIM values (f32, or bf16 upcast) into LDS rows of pitch
-// DIM+4 floats.  16-byte loads; DIM/4 (f32) lanes cover one row.
+// Stage nv (<= 64) rows of DIM values (f32, or bf16 upcast) into LDS rows of
+// pitch DIM+4 floats with 16-byte loads; each lane issues 8 loads before it
+// waits on any of them.  Lane r computes row r's offset once; the loads fetch
+// it with __shfl.
 template <int DIM>
 __device__ void stage_rows_in(float* stage, const void* __restrict__ in, bool bf16, const SegDev& s,
                               uint32_t v0, uint32_t nv, int lane) {
     constexpr int PITCH = DIM + 4;
+    constexpr int BATCH = 8;
+    const unsigned long long my_off = vec_elem_offset(s, v0 + min(static_cast<uint32_t>(lane), nv - 1));
     if (!bf16) {
         const float* fin = static_cast<const float*>(in);
-        constexpr int Q = DIM / 4;
-        for (uint32_t i = lane; i < nv * Q; i += WAVE) {
-            uint32_t r = i / Q, c = i % Q;
-            uint64_t off = vec_elem_offset(s, v0 + r);
-            float4 v = *reinterpret_cast<const float4*>(fin + off + 4 * c);
-            *reinterpret_cast<float4*>(stage + r * PITCH + 4 * c) = v;
+        constexpr int Q = DIM / 4;       // float4 per row
+        constexpr int RPI = WAVE / Q;    // rows per load instruction
+        for (uint32_t r0 = 0; r0 < nv; r0 += RPI * BATCH) {
+            float4 v[BATCH];
+#pragma unroll
+            for (int k = 0; k < BATCH; ++k) {
+                const uint32_t r = r0 + k * RPI + lane / Q;
+                const unsigned long long off = __shfl(my_off, static_cast<int>(r & 63u));
+                if (r < nv) v[k] = *reinterpret_cast<const float4*>(fin + off + 4 * (lane % Q));
+            }
+#pragma unroll
+            for (int k = 0; k < BATCH; ++k) {
+                const uint32_t r = r0 + k * RPI + lane / Q;
+                if (r < nv) *reinterpret_cast<float4*>(stage + r * PITCH + 4 * (lane % Q)) = v[k];
+            }
         }
     } else {
         const uint16_t* hin = static_cast<const uint16_t*>(in);
-        constexpr int Q = DIM / 8;
-        for (uint32_t i = lane; i < nv * Q; i += WAVE) {
-            uint32_t r = i / Q, c = i % Q;
-            uint64_t off = vec_elem_offset(s, v0 + r);
-            uint4 v = *reinterpret_cast<const uint4*>(hin + off + 8 * c);
-            float* d = stage + r * PITCH + 8 * c;
-            uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        constexpr int Q = DIM / 8;       // uint4 (8 bf16) per row
+        constexpr int RPI = WAVE / Q;
+        for (uint32_t r0 = 0; r0 < nv; r0 += RPI * BATCH) {
+            uint4 v[BATCH];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                d[2 * t] = u2f(w[t] << 16);
-                d[2 * t + 1] = u2f(w[t] & 0xffff0000u);
+            for (int k = 0; k < BATCH; ++k) {
+                const uint32_t r = r0 + k * RPI + lane / Q;
+                const unsigned long long off = __shfl(my_off, static_cast<int>(r & 63u));
+                if (r < nv) v[k] = *reinterpret_cast<const uint4*>(hin + off + 8 * (lane % Q));
+            }
+#pragma unroll
+            for (int k = 0; k < BATCH; ++k) {
+                const uint32_t r = r0 + k * RPI + lane / Q;
+                if (r < nv) {
+                    float* d = stage + r * PITCH + 8 * (lane % Q);
+                    const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        d[2 * t] = u2f(w[t] << 16);
+                        d[2 * t + 1] = u2f(w[t] & 0xffff0000u);
+                    }
+                }
             }
         }
     }
@@ -852,24 +885,27 @@ __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const
     if (tile == 0 && threadIdx.x < 19)
         blob[threadIdx.x] = static_cast<uint8_t>(fb2_byte(threadIdx.x, 5u, DIM / 4, seg.n_vectors, 10u));
     __syncthreads();
-    if (threadIdx.x == 0) rq.counts[blk] = q_count;
+    if (threadIdx.x == 0)
+        *reinterpret_cast<uint4*>(rq.heads + 4ull * blk) = make_uint4(q_count, sidx, tile_v0, 0u);
 }
 
 // Exact redo of the queued (vector, block) decisions of fib_encode_kernel.
 // Wave w of workgroup b drains the queue of encode workgroup 4b + w, 16
-// entries at a time: 4 lanes per vector rebuild x_hat exactly (sequential f64
-// norm; f32(x / norm), or x / norm in f64 for segments of fewer than 4
-// vectors), then 16 undecided blocks at a time get one lane per rho row
-// (sequential f64 dot, rotation.rs:107-113) and a quarter of the codewords
-// per lane in the AVX2 distance order with strict < (simd_nearest.rs:44-104);
-// the entry's owner lane patches the 5-bit fields.
+// entries at a time: 4 lanes per vector load it, one lane takes the
+// sequential f64 norm and the 4 lanes form x_hat = f32(x / norm) (segments of
+// fewer than 4 vectors keep x / norm in f64, codec.rs:481 vs 608); then 16
+// undecided blocks at a time get one lane per rho row (sequential f64 dot,
+// rotation.rs:107-113) and a quarter of the codewords per lane in the AVX2
+// distance order with strict < (simd_nearest.rs:44-104); the entry's owner
+// lane patches the 5-bit fields.
 template <int DIM>
 __global__ __launch_bounds__(TILE) void fib_fixup_kernel(LaunchCommon lc, const void* __restrict__ in,
-                                                         uint8_t* __restrict__ wire, const double* __restrict__ rot,
+                                                         uint8_t* __restrict__ wire, const double* __restrict__ rot_t,
                                                          const float* __restrict__ cb, FibRedo rq, uint32_t ntiles) {
+    static_assert(DIM == 64, "four lanes of 16 elements per vector");
     constexpr int G = 16;
-    __shared__ double xh_s[WAVES][G][DIM];
-    __shared__ float xf_s[WAVES][G][DIM];
+    __shared__ float x_s[WAVES][G][DIM + 4];   // x, then x_hat (segments of >= 4 vectors); padded rows
+    __shared__ double nrm_s[WAVES][G];
     __shared__ float part_s[WAVES][G][4][2];
     __shared__ float rho_s[WAVES][G][4];
     __shared__ uint32_t mask_s[WAVES][G];
@@ -878,12 +914,12 @@ __global__ __launch_bounds__(TILE) void fib_fixup_kernel(LaunchCommon lc, const 
     const int e = lane >> 2, t = lane & 3;
     const uint32_t tb = blockIdx.x * WAVES + wave;
     if (tb >= ntiles) return;
-    const uint32_t count = min(rq.counts[tb], TILE);
+    const uint4 head = *reinterpret_cast<const uint4*>(rq.heads + 4ull * tb);
+    const uint32_t count = min(head.x, TILE);
     if (count == 0) return;
-    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, tb);
-    const SegDev seg = lc.segs[sidx];
+    const SegDev seg = lc.segs[head.y];
     const bool small = seg.n_vectors < 4;
-    const uint32_t tile_v0 = (tb - lc.tile_start[sidx]) * TILE;
+    const uint32_t tile_v0 = head.z;
     const uint32_t* ents = rq.entries + static_cast<uint64_t>(tb) * TILE;
     for (uint32_t g0 = 0; g0 < count; g0 += G) {
         const uint32_t ne = min(static_cast<uint32_t>(G), count - g0);
@@ -893,30 +929,40 @@ __global__ __launch_bounds__(TILE) void fib_fixup_kernel(LaunchCommon lc, const 
             const uint32_t ent = ents[g0 + e];
             vi = tile_v0 + (ent & 0xFFu);
             mask = ent >> 8;
-        }
-        if (has) {
-            const uint64_t off = vec_elem_offset(seg, vi);
-            for (int c = 16 * t; c < 16 * t + 16; ++c)
-                xf_s[wave][e][c] = lc.in_bf16 ? u2f(static_cast<uint32_t>(static_cast<const uint16_t*>(in)[off + c]) << 16)
-                                              : static_cast<const float*>(in)[off + c];
+            const uint64_t off = vec_elem_offset(seg, vi) + 16u * static_cast<uint32_t>(t);
+            float4* dst = reinterpret_cast<float4*>(&x_s[wave][e][16 * t]);
+            if (!lc.in_bf16) {
+                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(in) + off);
+                const float4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
+                dst[0] = v0; dst[1] = v1; dst[2] = v2; dst[3] = v3;
+            } else {
+                const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(in) + off);
+                const uint4 w0 = src[0], w1 = src[1];
+                const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    dst[k] = make_float4(u2f(w[2 * k] << 16), u2f(w[2 * k] & 0xffff0000u), u2f(w[2 * k + 1] << 16),
+                                         u2f(w[2 * k + 1] & 0xffff0000u));
+            }
             if (t == 0) mask_s[wave][e] = mask;
         }
         wave_sync();
-        double nrm = 1.0;
-        if (has && t == 0) {
-            double s = 0.0;
+        if (has && t == 0) {   // l2_norm: sequential f64; a square of an f32 is exact, so fma == s + d * d
+            double s2 = 0.0;
+#pragma unroll 16
             for (int c = 0; c < DIM; ++c) {
-                const double dv = static_cast<double>(xf_s[wave][e][c]);
-                s = s + dv * dv;
+                const double d = static_cast<double>(x_s[wave][e][c]);
+                s2 = __builtin_fma(d, d, s2);
             }
-            nrm = __builtin_sqrt(s);
+            nrm_s[wave][e] = __builtin_sqrt(s2);
         }
-        nrm = __shfl(nrm, lane & ~3);
-        if (has)
-            for (int c = 16 * t; c < 16 * t + 16; ++c) {
-                const double q = static_cast<double>(xf_s[wave][e][c]) / nrm;
-                xh_s[wave][e][c] = small ? q : static_cast<double>(static_cast<float>(q));
-            }
+        wave_sync();
+        if (has && !small) {
+            const double nrm = nrm_s[wave][e];
+#pragma unroll
+            for (int c = 16 * t; c < 16 * t + 16; ++c)
+                x_s[wave][e][c] = static_cast<float>(static_cast<double>(x_s[wave][e][c]) / nrm);
+        }
         wave_sync();
         uint32_t total = 0;
         for (uint32_t j = 0; j < ne; ++j) total += __popc(mask_s[wave][j]);
@@ -937,10 +983,17 @@ __global__ __launch_bounds__(TILE) void fib_fixup_kernel(LaunchCommon lc, const 
                     acc += c;
                 }
             }
-            if (pe >= 0) {
-                const double* row = rot + static_cast<size_t>(4 * pb + t) * DIM;
+            if (pe >= 0) {   // Pi^T: at step c all lanes read within one 512 B row
+                const double* col = rot_t + (4 * pb + t);
+                const float* xr = x_s[wave][pe];
                 double a = 0.0;
-                for (int c = 0; c < DIM; ++c) a = a + row[c] * xh_s[wave][pe][c];
+                if (!small) {
+#pragma unroll 16
+                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * static_cast<double>(xr[c]);
+                } else {
+                    const double nrm = nrm_s[wave][pe];
+                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * (static_cast<double>(xr[c]) / nrm);
+                }
                 rho_s[wave][e][t] = static_cast<float>(a);
             }
             wave_sync();
@@ -949,6 +1002,7 @@ __global__ __launch_bounds__(TILE) void fib_fixup_kernel(LaunchCommon lc, const 
                 const float s2 = rho_s[wave][e][2], s3 = rho_s[wave][e][3];
                 float bd = u2f(0x7f800000u);
                 uint32_t bw = 0;
+#pragma unroll
                 for (int w = 8 * t; w < 8 * t + 8; ++w) {
                     const float* c = cb + 4 * w;
                     const float e0 = c[0] - s0, e1 = c[1] - s1, e2 = c[2] - s2, e3 = c[3] - s3;
@@ -987,22 +1041,28 @@ __global__ __launch_bounds__(TILE) void fib_fixup_kernel(LaunchCommon lc, const 
 
 // ------------------------------------------------------------ fib decode
 // FibCodeV1::decode_batch (codec.rs:323-424) + decode_batch_fast (797-844).
+//
+// One lane per output column: lane `col` keeps column col of f32(Pi) (row
+// `row` at f32(Pi)[row][col]) in 64 VGPRs and rebuilds
+//   x[col] = (((0 + P[0][col] c_0) + P[1][col] c_1) + ...) * norm
+// with every product and sum rounded (the reference's sequential f32 loop),
+// where c_row = codebook[w_{row/4}][row % 4] is the same for every lane:
+// the indices are decoded once per vector and the codeword components are
+// scalar loads, so each term costs one v_mul_f32 and one v_add_f32 with an
+// SGPR operand.  A wave walks its 64 vectors one by one and stores each
+// decoded row as one coalesced 256-byte write.
 template <int DIM>
 __global__ __launch_bounds__(TILE) void fib_decode_kernel(LaunchCommon lc, const uint8_t* __restrict__ wire,
                                                           float* __restrict__ out,
                                                           const float* __restrict__ rot32t,
                                                           const float* __restrict__ cb) {
-    constexpr int PITCH = DIM + 4;
+    static_assert(DIM == 64, "one lane per column of a 64-wide vector");
     constexpr int BLOCKS = DIM / 4;
-    constexpr int WAVE_FLOATS = WAVE * PITCH + 8;
-    constexpr uint32_t PLEN = 2 + (BLOCKS * 5 + 7) / 8;
-    extern __shared__ float smem[];
-    __shared__ float cb_lds[32 * 4];
-    if (threadIdx.x < 128) cb_lds[threadIdx.x] = cb[threadIdx.x];
-    __syncthreads();
+    constexpr uint32_t PLEN = 2 + (BLOCKS * 5 + 7) / 8;   // 12
+    constexpr int PAY_WORDS = WAVE * PLEN / 4 + 4;
+    __shared__ uint32_t pay_s[WAVES][PAY_WORDS];
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    float* stage = smem + wave * WAVE_FLOATS;
     const uint32_t blk = blockIdx.x;
     const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
     const SegDev seg = lc.segs[sidx];
@@ -1020,51 +1080,207 @@ __global__ __launch_bounds__(TILE) void fib_decode_kernel(LaunchCommon lc, const
     }
     if (v0 >= seg.n_vectors) return;
     const uint32_t nv = min(static_cast<uint32_t>(WAVE), seg.n_vectors - v0);
-    uint32_t* sw = reinterpret_cast<uint32_t*>(stage);
+
+    // column `lane` of f32(Pi): rot32t is [col][row]
+    float pc[DIM];
+    {
+        const float4* src = reinterpret_cast<const float4*>(rot32t + lane * DIM);
+#pragma unroll
+        for (int k = 0; k < DIM / 4; ++k) {
+            const float4 v = src[k];
+            pc[4 * k] = v.x; pc[4 * k + 1] = v.y; pc[4 * k + 2] = v.z; pc[4 * k + 3] = v.w;
+        }
+    }
+    // the wave's payloads into LDS (coalesced), then lane v keeps vector v's
+    // three payload words and output offset for the walk below
+    uint32_t* sw = pay_s[wave];
     global_to_lds(sw, blob + 19 + static_cast<uint64_t>(v0) * PLEN, nv * PLEN, lane);
     wave_sync();
-    const bool active = static_cast<uint32_t>(lane) < nv;
-    uint32_t p0 = 0, p1 = 0, p2 = 0;
-    if (active) {
-        const uint32_t* pw = sw + lane * (PLEN / 4);
-        p0 = pw[0]; p1 = pw[1]; p2 = pw[2];
-    }
-    wave_sync();
-    const uint16_t h = static_cast<uint16_t>(p0 & 0xffffu);
-    const float nv32 = f16_to_f32(h);
-    bool ok = isfinite_f(nv32) && nv32 > 0.0f;
-    const uint64_t lo = (static_cast<uint64_t>(p0) >> 16) | (static_cast<uint64_t>(p1) << 16) |
-                        (static_cast<uint64_t>(p2) << 48);
-    const uint32_t hi = p2 >> 16;
-    float c[DIM];
+    // lane v decodes vector v: norm bits, output offset and the byte offsets
+    // of its 16 codewords in the codebook; the walk below reads them with
+    // v_readlane, so the scalar unit only issues the loads
+    const uint32_t mine = min(static_cast<uint32_t>(lane), nv - 1);
+    const uint32_t q0 = sw[3 * mine], q1 = sw[3 * mine + 1], q2 = sw[3 * mine + 2];
+    const uint64_t my_off = vec_elem_offset(seg, v0 + mine);
+    uint32_t cofs[BLOCKS];
+    {
+        // 16 x 5-bit indices, LSB-first, starting at payload byte 2
+        const uint64_t lo = (static_cast<uint64_t>(q0) >> 16) | (static_cast<uint64_t>(q1) << 16) |
+                            (static_cast<uint64_t>(q2) << 48);
+        const uint32_t hi = q2 >> 16;
 #pragma unroll
-    for (int b = 0; b < BLOCKS; ++b) {
-        const int bit = 5 * b;
-        uint32_t w;
-        if (bit + 5 <= 64) w = static_cast<uint32_t>(lo >> bit) & 31u;
-        else if (bit >= 64) w = (hi >> (bit - 64)) & 31u;
-        else w = (static_cast<uint32_t>(lo >> bit) | (hi << (64 - bit))) & 31u;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) c[4 * b + t] = cb_lds[4 * w + t];
+        for (int b = 0; b < BLOCKS; ++b) {
+            const int bit = 5 * b;
+            uint32_t w;
+            if (bit + 5 <= 64) w = static_cast<uint32_t>(lo >> bit) & 31u;
+            else if (bit >= 64) w = (hi >> (bit - 64)) & 31u;
+            else w = (static_cast<uint32_t>(lo >> bit) | (hi << (64 - bit))) & 31u;
+            cofs[b] = w * 16u;
+        }
     }
-    float* orow = stage + lane * PITCH;
-    bool ofinite = true;
-    for (int col = 0; col < DIM; ++col) {
+    const char* cbb = reinterpret_cast<const char*>(cb);
+    for (uint32_t v = 0; v < nv; ++v) {
+        float4 c[BLOCKS];
+#pragma unroll
+        for (int b = 0; b < BLOCKS; ++b)
+            c[b] = *reinterpret_cast<const float4*>(
+                cbb + static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(cofs[b], v))));
         float s = 0.0f;
 #pragma unroll
-        for (int row = 0; row < DIM; ++row) s = s + rot32t[col * DIM + row] * c[row];
-        float o = s * nv32;
-        ofinite &= isfinite_f(o);
-        if (active) orow[col] = o;
+        for (int b = 0; b < BLOCKS; ++b) {
+            s = s + pc[4 * b + 0] * c[b].x;
+            s = s + pc[4 * b + 1] * c[b].y;
+            s = s + pc[4 * b + 2] * c[b].z;
+            s = s + pc[4 * b + 3] * c[b].w;
+        }
+        const uint32_t olo = __builtin_amdgcn_readlane(static_cast<uint32_t>(my_off), v);
+        const uint32_t ohi = __builtin_amdgcn_readlane(static_cast<uint32_t>(my_off >> 32), v);
+        const uint64_t off = static_cast<uint64_t>(ohi) << 32 | olo;
+        const float nrm = f16_to_f32(static_cast<uint16_t>(__builtin_amdgcn_readlane(q0, v) & 0xffffu));
+        const bool ok = isfinite_f(nrm) && nrm > 0.0f;
+        const float o = s * nrm;
+        const bool ofinite = __ballot(!isfinite_f(o)) == 0ull;
+        const uint32_t vi = v0 + v;
+        if (!ok) {
+            if (lane == 0) status_fail(lc.status, sidx, 1, vi, KIND_CORRUPT);
+        } else if (!ofinite) {
+            if (lane == 0) status_fail(lc.status, sidx, 1, vi, KIND_DECODE_NONFINITE);
+        } else {
+            out[off + lane] = o;
+        }
     }
-    if (active) {
-        if (!ok) status_fail(lc.status, sidx, 1, v0 + lane, KIND_CORRUPT);
-        else if (!ofinite) status_fail(lc.status, sidx, 1, v0 + lane, KIND_DECODE_NONFINITE);
+}
+
+// Decode with the products on the matrix cores.  For one rotation row r the
+// products of all columns and vectors form the rank-1 matrix
+// f32(Pi)[r][:] x c_r[:], so v_mfma_f32_32x32x1_2b_f32 with a zero
+// accumulator yields them (2 x 32 columns x 32 vectors per instruction); the
+// VALU keeps only the sequential f32 additions, in the reference's order.
+// A product from the matrix core must equal f32 multiplication bit for bit:
+// fib_product_check_kernel checks every product this kernel can form
+// (64 rows x 64 columns x 32 codewords) when a profile is created, and the
+// profile falls back to fib_decode_kernel on any difference.
+typedef float v32f __attribute__((ext_vector_type(32)));
+
+template <int DIM>
+__global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, const uint8_t* __restrict__ wire,
+                                                               float* __restrict__ out,
+                                                               const float* __restrict__ rot32,
+                                                               const float* __restrict__ cb) {
+    static_assert(DIM == 64, "two 32-column MFMA blocks");
+    constexpr int BLOCKS = DIM / 4;
+    constexpr uint32_t PLEN = 2 + (BLOCKS * 5 + 7) / 8;   // 12
+    constexpr int PAY_WORDS = WAVE * PLEN / 4 + 4;
+    __shared__ float rot_s[DIM * DIM];   // f32(Pi), row-major
+    __shared__ float4 cb_s[32];
+    __shared__ uint32_t pay_s[WAVES][PAY_WORDS];
+    {
+        const float4* src = reinterpret_cast<const float4*>(rot32);
+        float4* dst = reinterpret_cast<float4*>(rot_s);
+        float4 t[DIM * DIM / 4 / TILE];
+#pragma unroll
+        for (int k = 0; k < DIM * DIM / 4 / TILE; ++k) t[k] = src[threadIdx.x + k * TILE];
+#pragma unroll
+        for (int k = 0; k < DIM * DIM / 4 / TILE; ++k) dst[threadIdx.x + k * TILE] = t[k];
+        if (threadIdx.x < 32) cb_s[threadIdx.x] = reinterpret_cast<const float4*>(cb)[threadIdx.x];
     }
-    uint64_t badmask = __ballot(active && !(ok && ofinite));
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int h = lane >> 5, n = lane & 31;
+    const uint32_t blk = blockIdx.x;
+    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const SegDev seg = lc.segs[sidx];
+    const uint32_t tile = blk - lc.tile_start[sidx];
+    const uint32_t v0 = tile * TILE + wave * WAVE;
+    const uint8_t* blob = wire + seg.wire_offset;
+
+    uint32_t hb = lane < 19 ? blob[lane] : 0u;
+    bool bad = lane < 19 && fb2_checked(lane, seg.n_vectors) &&
+               hb != fb2_byte(lane, 5u, BLOCKS, seg.n_vectors, PLEN - 2);
+    if (lane == 14 && hb != 0u) bad = true;   // norm format must be Fp16Paper
+    if (__ballot(bad) != 0ull) {
+        if (lane == 0) status_fail(lc.status, sidx, 0, 0u, KIND_HEADER);
+        return;
+    }
+    if (v0 >= seg.n_vectors) return;
+    const uint32_t nv = min(static_cast<uint32_t>(WAVE), seg.n_vectors - v0);
+    uint32_t* sw = pay_s[wave];
+    global_to_lds(sw, blob + 19 + static_cast<uint64_t>(v0) * PLEN, nv * PLEN, lane);
     wave_sync();
-    stage_rows_out<DIM>(out, stage, seg, v0, nv, static_cast<uint32_t>(badmask),
-                        static_cast<uint32_t>(badmask >> 32), lane);
+
+    for (uint32_t sub = 0; sub < 2; ++sub) {
+        const uint32_t t0 = 32 * sub;   // first vector of this tile within the wave
+        if (t0 >= nv) break;
+        const uint32_t my = min(t0 + static_cast<uint32_t>(n), nv - 1);   // lanes past the end repeat the last
+        const uint32_t q0 = sw[3 * my], q1 = sw[3 * my + 1], q2 = sw[3 * my + 2];
+        const uint64_t lo = (static_cast<uint64_t>(q0) >> 16) | (static_cast<uint64_t>(q1) << 16) |
+                            (static_cast<uint64_t>(q2) << 48);
+        const uint32_t hi = q2 >> 16;
+        const v32f zero = {};
+        v32f acc = {};
+#pragma unroll 2
+        for (int b = 0; b < BLOCKS; ++b) {
+            const int bit = 5 * b;
+            // 5-bit index b, LSB-first from payload byte 2 (bit may straddle the 64-bit word)
+            const uint32_t w = static_cast<uint32_t>(bit < 64 ? (lo >> bit) | (bit > 59 ? static_cast<uint64_t>(hi) << (64 - bit) : 0ull)
+                                                             : static_cast<uint64_t>(hi >> (bit - 64))) & 31u;
+            const float4 c = cb_s[w];
+            const float cr[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(rot_s[(4 * b + t) * DIM + lane], cr[t], zero, 0, 0, 0);
+#pragma unroll
+                for (int q = 0; q < 32; ++q) acc[q] = acc[q] + p[q];
+            }
+        }
+        const float nrm = f16_to_f32(static_cast<uint16_t>(q0 & 0xffffu));
+        const bool ok = isfinite_f(nrm) && nrm > 0.0f;
+        bool fin = true;
+#pragma unroll
+        for (int q = 0; q < 32; ++q) {
+            acc[q] = acc[q] * nrm;
+            fin &= isfinite_f(acc[q]);
+        }
+        // a vector is bad if either half-wave saw a bad value
+        const uint64_t badm = __ballot(!(ok && fin));
+        const bool vbad = ((badm >> n) | (badm >> (n + 32))) & 1ull;
+        const bool active = t0 + static_cast<uint32_t>(n) < nv;
+        const uint32_t vi = v0 + t0 + static_cast<uint32_t>(n);
+        if (active && h == 0 && vbad) status_fail(lc.status, sidx, 1, vi, ok ? KIND_DECODE_NONFINITE : KIND_CORRUPT);
+        if (active && !vbad) {
+            float* orow = out + vec_elem_offset(seg, vi);
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int q = 16 * bb + 4 * g;   // registers q .. q + 3: columns 32bb + 8g + 4h .. + 3
+                    *reinterpret_cast<float4*>(orow + 32 * bb + 8 * g + 4 * h) =
+                        make_float4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3]);
+                }
+        }
+    }
+}
+
+// Counts the products of (f32(Pi)[r][col], codeword component c[j][r % 4])
+// whose matrix-core result differs from f32 multiplication, over every row,
+// column and codeword, with the operand placement of fib_decode_mfma_kernel.
+__global__ __launch_bounds__(64) void fib_product_check_kernel(const float* __restrict__ rot32,
+                                                               const float* __restrict__ cb, uint32_t* bad) {
+    const int lane = threadIdx.x, h = lane >> 5, j = lane & 31;
+    const v32f zero = {};
+    uint32_t cnt = 0;
+    for (int r = 0; r < 64; ++r) {
+        const float a = rot32[r * 64 + lane], b = cb[j * 4 + (r & 3)];
+        const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, zero, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 32; ++q) {
+            const int col = 32 * (q >> 4) + 8 * ((q & 15) >> 2) + 4 * h + (q & 3);
+            const float e = rot32[r * 64 + col] * b;
+            cnt += f2u(p[q]) != f2u(e) ? 1u : 0u;
+        }
+    }
+    if (cnt) atomicAdd(bad, cnt);
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t value, uint64_t n) {
@@ -1140,14 +1356,24 @@ int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, 
     hipError_t e = launch_big_lds(fib_encode_kernel<64>, nblocks, lds, st, lc, in, wire, fd.mf, fd.thr, rq);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(fib_fixup_kernel<64>, dim3((nblocks + WAVES - 1) / WAVES), dim3(TILE), 0, st, lc, in, wire,
-                       fd.rot, fd.codebook, rq, nblocks);
+                       fd.rot_t, fd.codebook, rq, nblocks);
     return hipGetLastError();
 }
 
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, float* out, uint32_t nblocks,
                       void* stream) {
-    return launch_big_lds(fib_decode_kernel<64>, nblocks, stage_bytes<64>(), static_cast<hipStream_t>(stream), lc,
-                          wire, out, fd.rot32t, fd.codebook);
+    if (fd.mfma_decode)
+        hipLaunchKernelGGL(fib_decode_mfma_kernel<64>, dim3(nblocks), dim3(TILE), 0, static_cast<hipStream_t>(stream),
+                           lc, wire, out, fd.rot32, fd.codebook);
+    else
+        hipLaunchKernelGGL(fib_decode_kernel<64>, dim3(nblocks), dim3(TILE), 0, static_cast<hipStream_t>(stream), lc,
+                           wire, out, fd.rot32t, fd.codebook);
+    return hipGetLastError();
+}
+
+int launch_fib_product_check(const float* rot32, const float* cb, uint32_t* bad, void* stream) {
+    hipLaunchKernelGGL(fib_product_check_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), rot32, cb, bad);
+    return hipGetLastError();
 }
 
 }  // namespace pkv
