@@ -51,10 +51,12 @@ struct pkv_profile {
     // turbo
     uint32_t bits = 0, pbits = 0, proj = 0, mode = 0;
     uint64_t seed = 0;
-    std::vector<float> signs, qjl, cs;
+    std::vector<float> signs, qjl, cs, qa, qb;
     float* d_signs = nullptr;
     float* d_qjl = nullptr;
     float* d_cs = nullptr;
+    float* d_qa = nullptr;
+    float* d_qb = nullptr;
     // fib
     uint32_t k = 0, n = 0, wbits = 0;
     std::vector<float> codebook, rot32t, rot32;
@@ -212,6 +214,8 @@ TurboDev turbo_dev(const pkv_profile* p) {
     t.signs = p->d_signs;
     t.qjl = p->d_qjl;
     t.cs = p->d_cs;
+    t.qa = p->d_qa;
+    t.qb = p->d_qb;
     t.seed = p->seed;
     t.dim = p->dim;
     t.pbits = p->pbits;
@@ -431,6 +435,31 @@ void pkv_ctx_destroy(pkv_ctx* ctx) {
     delete ctx;
 }
 
+// Operands of the head_dim-64 QJL MFMA path (layout in TurboDev).
+static void turbo_qjl_mfma_constants(pkv_profile* p) {
+    const uint32_t dim = p->dim, tiles = p->proj / 32;
+    p->qa.assign(static_cast<size_t>(tiles) * 32 * 64, 0.0f);
+    p->qb.assign(static_cast<size_t>(tiles) * 16 * 64, 0.0f);
+    const double u = std::ldexp(1.0, -24);
+    for (uint32_t t = 0; t < tiles; ++t)
+        for (uint32_t lane = 0; lane < 64; ++lane) {
+            for (uint32_t c = 0; c < 32; ++c)
+                p->qa[(t * 32 + c) * 64 + lane] = p->qjl[static_cast<size_t>(32 * t + lane % 32) * dim + 32 * (lane / 32) + c];
+            for (uint32_t q = 0; q < 16; ++q) {
+                const uint32_t j = 32 * t + 8 * (q / 4) + 4 * (lane / 32) + q % 4;
+                double g2 = 0.0;
+                for (uint32_t c = 0; c < dim; ++c) {
+                    const double g = p->qjl[static_cast<size_t>(j) * dim + c];
+                    g2 += g * g;
+                }
+                const double b = 200.0 * u * std::sqrt(g2) * (1.0 + std::ldexp(1.0, -10));
+                float bf = static_cast<float>(b);
+                if (static_cast<double>(bf) < b) bf = std::nextafter(bf, std::numeric_limits<float>::infinity());
+                p->qb[(t * 16 + q) * 64 + lane] = bf;
+            }
+        }
+}
+
 static int turbo_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t bits, uint32_t proj, uint64_t seed, int mode,
                                 const float* signs, const float* qjl, pkv_profile** out) {
     if (!ctx || !out) return PKV_ERR_INVALID_ARG;
@@ -476,6 +505,11 @@ static int turbo_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t bits, uint3
     if (!rc) rc = upload(&p->d_signs, p->signs);
     if (!rc) rc = upload(&p->d_qjl, p->qjl);
     if (!rc) rc = upload(&p->d_cs, p->cs);
+    if (!rc && dim == 64 && qrows) {
+        turbo_qjl_mfma_constants(p);
+        rc = upload(&p->d_qa, p->qa);
+        if (!rc) rc = upload(&p->d_qb, p->qb);
+    }
     if (rc) { pkv_profile_destroy(p); return rc; }
     *out = p;
     return PKV_OK;
@@ -692,6 +726,7 @@ void pkv_profile_destroy(pkv_profile* p) {
     if (p->ctx) (void)hipSetDevice(p->ctx->device);
     (void)hipDeviceSynchronize();
     for (void* d : {static_cast<void*>(p->d_signs), static_cast<void*>(p->d_qjl), static_cast<void*>(p->d_cs),
+                    static_cast<void*>(p->d_qa), static_cast<void*>(p->d_qb),
                     static_cast<void*>(p->d_cb), static_cast<void*>(p->d_rot_t), static_cast<void*>(p->d_rot32t),
                     static_cast<void*>(p->d_mf), static_cast<void*>(p->d_rot32)})
         if (d) (void)hipFree(d);

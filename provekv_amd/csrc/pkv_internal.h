@@ -41,6 +41,12 @@ struct TurboDev {
     const float* signs;     // dim
     const float* qjl;       // proj * dim, row-major
     const float* cs;        // 2 * levels: cos, sin of each dequantized angle
+    // QJL sketch on the matrix cores (head_dim 64 with QJL), per 32-projection tile p:
+    //   qa [p][c 32][lane 64] = G[32p + lane % 32][32 (lane / 32) + c]
+    //   qb [p][q 16][lane 64] = 200 * 2^-24 * |G_j| * (1 + 2^-10), rounded up, for
+    //                           j = 32p + 8(q/4) + 4(lane/32) + q%4
+    const float* qa;
+    const float* qb;
     uint64_t seed;
     uint32_t dim, pbits, proj, mode;
 };

@@ -33,6 +33,10 @@ namespace {
 constexpr int WAVE = 64;
 constexpr int WAVES = TILE / WAVE;
 
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
 __constant__ LogfEntry c_logf_tab[16] = {PKV_LOGF_TABLE};
 __constant__ uint64_t c_exp2f_tab[32] = {PKV_EXP2F_TABLE};
 
@@ -466,6 +470,341 @@ __global__ __launch_bounds__(TILE) void turbo_encode_kernel(
     }
 }
 
+// ------------------------------------------------------------ turbo encode, QJL on the matrix cores
+// TurboQuantizer::encode with PolarWithQjl at head_dim 64 (turbo.rs:240-300).
+// Two lanes per vector: lane (h, n) = (lane / 32, lane % 32) holds elements
+// 32h .. 32h + 31 of vector n of a 32-vector tile.  The arithmetic is the
+// reference's, operation for operation: FWHT stages 1..16 run in registers
+// and stage 32 pairs the halves through v_permlane32_swap (same operands,
+// same rounding); radii and angle bins are per pair; the residual is exact.
+// Of the QJL sketch only the signs of the 32 (or 64) sequential f32 dots
+// reach the wire (qjl.rs:203-220), and this layout is already the B operand
+// of v_mfma_f32_32x32x2_f32 (K-step c: dimension 32h + c), so the dots come
+// from the matrix cores.  A sign is taken when |dot'| > bound_j * |res|,
+// where bound_j = 200 * 2^-24 * |g_j| (1 + 2^-10) covers the reference's
+// rounding (64 products and sums, <= 66u sum|g_c res_c|) and the MFMA's
+// (<= 130u, twice the sequential count) with sum|g_c res_c| <= |g_j| |res|;
+// the other dots (about 1e-4 of them) are recomputed in the reference's
+// order, the first half's partial sum handed to the second half.
+constexpr int QA_PER_TILE = 32 * 64;   // A operand floats of one 32-projection tile
+constexpr int QB_PER_TILE = 16 * 64;   // bound floats of one 32-projection tile
+
+// Value of the other half-wave's lane (l ^ 32).
+__device__ __forceinline__ uint32_t partner(uint32_t x, int h) {
+    const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return h ? p[0] : p[1];
+}
+
+// fwht_normalized stages (turbo-quant/src/rotation.rs:379-398) on a vector
+// split over the two halves of the wave: 32 elements per lane.
+__device__ __forceinline__ void fwht_split(float (&v)[32], int h) {
+#pragma unroll
+    for (int step = 1; step < 32; step *= 2) {
+#pragma unroll
+        for (int start = 0; start < 32; start += 2 * step) {
+#pragma unroll
+            for (int off = 0; off < step; ++off) {
+                const float a = v[start + off], b = v[start + off + step];
+                v[start + off] = a + b;
+                v[start + off + step] = a - b;
+            }
+        }
+    }
+    // step 32: element c (half 0) with c + 32 (half 1): (a + b, a - b)
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+        const float o = u2f(partner(f2u(v[c]), h));
+        v[c] = h ? o - v[c] : v[c] + o;
+    }
+}
+
+template <int PB>
+__global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
+    LaunchCommon lc, const void* __restrict__ in, uint8_t* __restrict__ wire, const float* __restrict__ signs,
+    const float* __restrict__ qjl, const float* __restrict__ cs_tab, const float* __restrict__ qa,
+    const float* __restrict__ qb, uint64_t seed, uint32_t pbits_rt, uint32_t proj) {
+    constexpr int DIM = 64;
+    constexpr int HP = 16;   // pairs per lane
+    extern __shared__ uint32_t smem_u[];   // per wave: 32 payloads (+ f32 radii for BlockLogU8)
+    __shared__ float cs_lds[512];
+    __shared__ LogfEntry logf_lds[16];
+
+    const uint32_t pbits = PB ? static_cast<uint32_t>(PB) : pbits_rt;
+    const uint32_t levels = 1u << pbits;
+    for (uint32_t t = threadIdx.x; t < 2 * levels; t += blockDim.x) cs_lds[t] = cs_tab[t];
+    if (threadIdx.x < 16) logf_lds[threadIdx.x] = c_logf_tab[threadIdx.x];
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int h = lane >> 5, n = lane & 31;
+    // two workgroups per TILE-vector tile, one 32-vector group per wave
+    const uint32_t blk = blockIdx.x >> 1;
+    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const SegDev seg = lc.segs[sidx];
+    const uint32_t tile = blk - lc.tile_start[sidx];
+    const uint32_t plen = lc.plen, pwd = plen >> 2;
+    const bool f32r = lc.radii == PKV_RADII_F32;
+    // per vector: the payload, then (BlockLogU8 radii only) its 32 f32 radii
+    const uint32_t vec_words = pwd + (f32r ? 0u : 32u);
+    uint32_t* pay = smem_u + wave * (32 * vec_words + 4);
+    uint8_t* blob = wire + seg.wire_offset;
+    const bool bf16 = lc.in_bf16 != 0;
+    const float scale = fwht_scale<DIM>();
+    const uint32_t rwords = f32r ? 32u : 32u / 4 + 2;          // radii words in the payload
+    const uint32_t bwords = (32u * pbits + 31) / 32;            // angle index words
+
+    // signs of this lane's half, read where they are used
+    auto load_signs = [&](float (&sg)[32]) {
+        const float4* sp = reinterpret_cast<const float4*>(signs + 32 * h);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float4 v = sp[k];
+            sg[4 * k] = v.x; sg[4 * k + 1] = v.y; sg[4 * k + 2] = v.z; sg[4 * k + 3] = v.w;
+        }
+    };
+
+    do {
+        const uint32_t t0 = tile * TILE + (blockIdx.x & 1u) * (TILE / 2) + 32u * static_cast<uint32_t>(wave);
+        if (t0 >= seg.n_vectors) break;
+        const uint32_t nv = min(32u, seg.n_vectors - t0);
+        const bool active = static_cast<uint32_t>(n) < nv;   // other lanes repeat the last vector
+        const uint64_t off = vec_elem_offset(seg, t0 + min(static_cast<uint32_t>(n), nv - 1)) + 32u * h;
+        uint32_t* pv = pay + n * vec_words;          // this vector's payload
+        uint32_t* rw = pv + (f32r ? 0u : pwd);       // its f32 radii
+
+        float y[32];
+        auto load_half = [&](float (&v)[32]) {
+            if (!bf16) {
+                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(in) + off);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float4 q = src[k];
+                    v[4 * k] = q.x; v[4 * k + 1] = q.y; v[4 * k + 2] = q.z; v[4 * k + 3] = q.w;
+                }
+            } else {
+                const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(in) + off);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint4 q = src[k];
+                    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        v[8 * k + 2 * t] = u2f(w[t] << 16);
+                        v[8 * k + 2 * t + 1] = u2f(w[t] & 0xffff0000u);
+                    }
+                }
+            }
+        };
+        load_half(y);
+        bool finite = true;
+        {
+            float sg[32];
+            load_signs(sg);
+#pragma unroll
+            for (int c = 0; c < 32; ++c) {
+                finite &= isfinite_f(y[c]);
+                y[c] = y[c] * sg[c];
+            }
+        }
+        fwht_split(y, h);
+#pragma unroll
+        for (int c = 0; c < 32; ++c) y[c] *= scale;
+
+        // zero this vector's angle index words: both halves OR into them
+        if (h == 0 && active)
+            for (uint32_t k = 0; k < bwords; ++k) pv[rwords + k] = 0u;
+        wave_sync();
+
+        // radii and angle bins (polar.rs:246-266, 413-421) of pairs 16h + i
+        float r[HP];
+        bool rfinite = true;
+        uint64_t pk = 0;
+        uint32_t slow = 0;
+#pragma unroll
+        for (int i = 0; i < HP; ++i) {
+            const float a = y[2 * i], b = y[2 * i + 1];
+            const float aa = a * a, bb = b * b;
+            r[i] = __builtin_sqrtf(aa + bb);
+            rfinite &= isfinite_f(r[i]);
+            uint32_t safe = 0u;
+            const uint32_t bin = PB == 3 ? octant_bin_u(a, b, safe) : 0u;
+            pk |= static_cast<uint64_t>(bin) << (static_cast<uint32_t>(i) * pbits);
+            slow |= (safe ^ 1u) << i;
+        }
+        if (slow) {   // pairs near an octant line (every pair at other widths): the exact formula
+            float ys[32];
+#pragma unroll
+            for (int c = 0; c < 32; ++c) ys[c] = y[c];
+            for (uint32_t m = slow; m; m &= m - 1u) {
+                const uint32_t i = static_cast<uint32_t>(__ffs(m) - 1);
+                const uint64_t bin = angle_bin_exact(ys[2 * i], ys[2 * i + 1], pbits);
+                pk = (pk & ~(static_cast<uint64_t>(levels - 1u) << (i * pbits))) | (bin << (i * pbits));
+            }
+        }
+        // angle indices, pbits each, LSB-first (bitpack.rs:21-35): this half's
+        // 16 * pbits bits start at bit 16 * pbits * h
+        if (active) {
+            const uint32_t bit0 = 16u * pbits * static_cast<uint32_t>(h);
+            const uint32_t nb = 16u * pbits;   // <= 128 bits: pk holds up to 64, pbits <= 4 here
+            uint32_t* bwp = pv + rwords + (bit0 >> 5);
+            const uint32_t sh = bit0 & 31u;
+            const uint32_t w0 = static_cast<uint32_t>(pk << sh);
+            const uint32_t w1 = static_cast<uint32_t>((pk << sh) >> 32) | (sh ? static_cast<uint32_t>(pk >> (64 - sh)) : 0u);
+            const uint32_t w2 = sh ? static_cast<uint32_t>(pk >> (96 - sh)) : 0u;
+            atomicOr(bwp, w0);
+            if (sh + nb > 32) atomicOr(bwp + 1, w1);
+            if (sh + nb > 64) atomicOr(bwp + 2, w2);
+        }
+        if (f32r) {
+            if (active)
+#pragma unroll
+                for (int i = 0; i < HP; ++i) rw[16 * h + i] = f2u(r[i]);
+        } else {
+            // CompressedRadiiV1 BlockLogU8 (turbo-quant/src/radius.rs:58-77)
+            float lg[HP];
+            float mn = u2f(0x7f800000u), mx = u2f(0xff800000u);
+#pragma unroll
+            for (int i = 0; i < HP; ++i) {
+                const float v = r[i] < 1.17549435e-38f ? 1.17549435e-38f : r[i];
+                lg[i] = og_logf_normal(v, logf_lds);
+                mn = __builtin_fminf(mn, lg[i]);
+                mx = __builtin_fmaxf(mx, lg[i]);
+            }
+            mn = __builtin_fminf(mn, u2f(partner(f2u(mn), h)));
+            mx = __builtin_fmaxf(mx, u2f(partner(f2u(mx), h)));
+            const float span = __builtin_fmaxf(mx - mn, 1.1920929e-07f);
+            if (active) {
+#pragma unroll
+                for (int i = 0; i < HP; i += 4) {
+                    uint32_t packed = 0;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        float nrm = (lg[i + t] - mn) / span;
+                        nrm = nrm < 0.0f ? 0.0f : (nrm > 1.0f ? 1.0f : nrm);
+                        const float q = __builtin_roundf(nrm * 255.0f);
+                        packed |= static_cast<uint32_t>(q) << (8 * t);
+                    }
+                    pv[4 * h + i / 4] = packed;
+                }
+                if (h == 0) {
+                    pv[8] = f2u(mn);
+                    pv[9] = f2u(mx);
+                }
+#pragma unroll
+                for (int i = 0; i < HP; ++i) rw[16 * h + i] = f2u(r[i]);
+            }
+        }
+        wave_sync();
+
+        // polar decode of the code just produced (polar.rs:272-278, 306-316)
+#pragma unroll
+        for (int i = 0; i < HP; ++i) {
+            const uint32_t bin = static_cast<uint32_t>(pk >> (static_cast<uint32_t>(i) * pbits)) & (levels - 1u);
+            y[2 * i] = r[i] * cs_lds[2 * bin];
+            y[2 * i + 1] = r[i] * cs_lds[2 * bin + 1];
+        }
+        fwht_split(y, h);
+        // residual against x read again (turbo.rs:269-273)
+        asm volatile("" ::: "memory");
+        {
+            float x[32], sg[32];
+            load_half(x);
+            load_signs(sg);
+#pragma unroll
+            for (int c = 0; c < 32; ++c) y[c] = x[c] - (y[c] * scale) * sg[c];
+        }
+        bool resfinite = true;
+        float rn2 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 32; ++c) {
+            resfinite &= isfinite_f(y[c]);
+            rn2 = __builtin_fmaf(y[c], y[c], rn2);
+        }
+        rn2 = rn2 + u2f(partner(f2u(rn2), h));
+        const float rn = __builtin_sqrtf(rn2) * 1.0001f;   // |res|, rounded up far past its f32 error
+
+        uint32_t sbits[2] = {0u, 0u}, unc[2] = {0u, 0u};
+        const uint32_t ptiles = proj / 32;
+#pragma unroll
+        for (uint32_t p = 0; p < 2; ++p) {
+            if (p >= ptiles) break;
+            const float* qa_p = qa + p * QA_PER_TILE;
+            const float* qb_p = qb + p * QB_PER_TILE;
+            v16f acc = {};
+#pragma unroll
+            for (int c = 0; c < 32; ++c)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa_p[c * 64 + lane], y[c], acc, 0, 0, 0);
+            // accumulator register q: projection 32p + 8(q/4) + 4h + q%4 of vector n
+            uint32_t sb = 0, un = 0;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const uint32_t j = static_cast<uint32_t>(8 * (q >> 2) + 4 * h + (q & 3));
+                const float bnd = qb_p[q * 64 + lane] * rn;
+                sb |= (acc[q] >= 0.0f ? 1u : 0u) << j;
+                un |= (__builtin_fabsf(acc[q]) > bnd ? 0u : 1u) << j;
+            }
+            sbits[p] = sb | partner(sb, h);
+            unc[p] = un | partner(un, h);
+        }
+        // undecided signs: the reference's sequential dot, half 0's partial
+        // sum continued by half 1
+        if (__ballot(active && (unc[0] | unc[1]) != 0u)) {
+#pragma unroll
+            for (uint32_t p = 0; p < 2; ++p) {
+                if (p >= ptiles) break;
+                uint32_t m = active ? unc[p] : 0u;
+                // the wave walks the union of its vectors' undecided projections
+                uint32_t any = m;
+                any |= partner(any, h);
+                for (int sh2 = 1; sh2 < 32; sh2 <<= 1) any |= __shfl_xor(any, sh2);
+                while (any) {
+                    const uint32_t j = static_cast<uint32_t>(__ffs(any) - 1);
+                    any &= any - 1u;
+                    const float* g = qjl + static_cast<size_t>(32 * p + j) * DIM + 32 * h;
+                    float dot = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < 32; ++c) dot = dot + g[c] * y[c];   // half 0: dims 0..31 from 0
+                    const float first = u2f(partner(f2u(dot), h));          // half 0's sum, seen by half 1
+                    float d2 = first;
+#pragma unroll
+                    for (int c = 0; c < 32; ++c) d2 = d2 + g[c] * y[c];     // half 1: continues over 32..63
+                    const float full = u2f(h ? f2u(d2) : partner(f2u(d2), h));
+                    if ((m >> j) & 1u) sbits[p] = (sbits[p] & ~(1u << j)) | (full >= 0.0f ? 1u << j : 0u);
+                }
+            }
+        }
+
+        // status (per vector, first failure in vector order) and the QJL words
+        const bool fin_v = finite && partner(finite ? 1u : 0u, h);
+        const bool rfin_v = rfinite && partner(rfinite ? 1u : 0u, h);
+        const bool resfin_v = resfinite && partner(resfinite ? 1u : 0u, h);
+        if (active && h == 0) {
+            const uint32_t vi = t0 + n;
+            if (!fin_v) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_INPUT);
+            else if (!rfin_v) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RADIUS);
+            else if (!resfin_v) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RESIDUAL);
+            pv[rwords + bwords] = sbits[0];
+            if (proj > 32) pv[rwords + bwords + 1] = sbits[1];
+        }
+        wave_sync();
+        if (!f32r) {   // close the gaps left by the f32 radii words
+            uint32_t tmp[(32 / 4 + 2) + 8 + 2];
+            const uint32_t k0 = static_cast<uint32_t>(h) * (pwd / 2 + 1);
+            const uint32_t k1 = h ? pwd : pwd / 2 + 1;
+            for (uint32_t k = k0; k < k1; ++k) tmp[k - k0] = active ? pv[k] : 0u;
+            wave_sync();
+            if (active)
+                for (uint32_t k = k0; k < k1; ++k) pay[n * pwd + k] = tmp[k - k0];
+            wave_sync();
+        }
+        lds_to_global(blob + 38 + static_cast<uint64_t>(t0) * plen, pay, nv * plen, lane);
+    } while (false);
+    if (tile == 0 && (blockIdx.x & 1u) == 0 && threadIdx.x < 38) {
+        blob[threadIdx.x] = static_cast<uint8_t>(
+            tqb1_byte(threadIdx.x, DIM, pbits, lc.radii, proj, seed, seg.n_vectors, plen));
+    }
+}
+
 // ------------------------------------------------------------ turbo decode
 template <int DIM, int PB>
 __global__ __launch_bounds__(TILE) void turbo_decode_kernel(
@@ -605,9 +944,6 @@ __global__ __launch_bounds__(TILE) void turbo_decode_kernel(
 // Segments of fewer than 4 vectors (the reference's single-vector path with
 // an f64 x_hat) queue all 16 blocks.
 
-typedef float v16f __attribute__((ext_vector_type(16)));
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 // f16 halves of a, b by round-toward-zero: hi = (a_hi, b_hi), lo = the
 // rounded remainders; a - a_hi is exact in f32.
@@ -1320,6 +1656,15 @@ hipError_t launch_big_lds(K kernel, uint32_t nblocks, size_t lds, hipStream_t st
 int launch_turbo_encode(const LaunchCommon& lc, const TurboDev& td, const void* in, uint8_t* wire,
                         uint32_t nblocks, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (td.dim == 64 && td.mode && td.qa && td.pbits <= 4) {
+        const size_t vec_words = (lc.plen >> 2) + (lc.radii == PKV_RADII_F32 ? 0u : 32u);
+        const size_t lds = static_cast<size_t>(WAVES) * (32 * vec_words + 4) * sizeof(uint32_t);
+        return td.pbits == 3
+                   ? launch_big_lds(turbo_encode_qjl_kernel<3>, 2 * nblocks, lds, st, lc, in, wire, td.signs, td.qjl,
+                                    td.cs, td.qa, td.qb, td.seed, td.pbits, td.proj)
+                   : launch_big_lds(turbo_encode_qjl_kernel<0>, 2 * nblocks, lds, st, lc, in, wire, td.signs, td.qjl,
+                                    td.cs, td.qa, td.qb, td.seed, td.pbits, td.proj);
+    }
     if (td.dim == 64)
         return td.pbits == 3
                    ? launch_big_lds(turbo_encode_kernel<64, 3>, nblocks, stage_bytes<64>(), st, lc, in, wire, td.signs,

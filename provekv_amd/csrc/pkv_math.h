@@ -142,6 +142,39 @@ PKV_HD uint32_t octant_bin(float a, float b, bool& safe) {
     return bin;
 }
 
+// octant_bin in integer arithmetic on the bit patterns (no compare masks):
+// for finite floats, |x| orders like its bit pattern with the sign cleared,
+// and a difference of two such patterns is negative exactly when the first is
+// smaller.  The bin of (bpos, apos, bsmall) comes from an 8-entry table of
+// 3-bit fields.  Agrees with octant_bin on every input (NaN included: both
+// mark it unsafe).
+PKV_HD uint32_t octant_bin_u(float a, float b, uint32_t& safe) {
+    uint32_t xa, xb;
+    __builtin_memcpy(&xa, &a, 4);
+    __builtin_memcpy(&xb, &b, 4);
+    const uint32_t ua = xa & 0x7fffffffu, ub = xb & 0x7fffffffu;
+    const uint32_t bsmall = (ub - ua) >> 31;                       // |b| < |a|
+    const uint32_t apos = ((0u - xa) & ~xa) >> 31;                 // a > 0
+    const uint32_t bpos = ((0u - xb) & ~xb) >> 31;                 // b > 0
+    const uint32_t idx = (bpos << 2) | (apos << 1) | bsmall;
+    // idx: 0 -> 1, 1 -> 0, 2 -> 2, 3 -> 3, 4 -> 6, 5 -> 7, 6 -> 5, 7 -> 4
+    const uint32_t lut = 1u | 0u << 3 | 2u << 6 | 3u << 9 | 6u << 12 | 7u << 15 | 5u << 18 | 4u << 21;
+    const uint32_t bin = (lut >> (3u * idx)) & 7u;
+    const uint32_t mx = ua > ub ? ua : ub, mn = ua > ub ? ub : ua;
+    // eps = mx * 2^-16 (exact while mx > 2^-110; smaller mx is unsafe below)
+    const uint32_t eps = mx - (16u << 23);
+    float fa, fb;
+    __builtin_memcpy(&fa, &ua, 4);
+    __builtin_memcpy(&fb, &ub, 4);
+    const float g = fa - fb;
+    uint32_t ug;
+    __builtin_memcpy(&ug, &g, 4);
+    ug &= 0x7fffffffu;                                              // |aa - ab|
+    const uint32_t lo = 0x0da24260u, hi = 0x7149f2cau;             // 1e-30f, 1e30f
+    safe = ((eps - mn) & (eps - ug) & (lo - mx) & (mx - hi)) >> 31;
+    return bin;
+}
+
 PKV_HD uint32_t angle_bin3(float a, float b) {
     bool safe;
     uint32_t bin = octant_bin(a, b, safe);
