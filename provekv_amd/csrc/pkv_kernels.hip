@@ -916,6 +916,127 @@ __global__ __launch_bounds__(TILE) void turbo_decode_kernel(
     stage_rows_out<DIM>(out, stage, seg, v0, nv, skip_lo, skip_hi, lane);
 }
 
+// LDS words per wave of turbo_decode_split_kernel: max(payloads, rows).
+__host__ __device__ constexpr uint32_t turbo_split_wave_words(uint32_t pwd) {
+    return (32 * pwd + 4 > 32 * (64 + 4) + 4) ? 32 * pwd + 4 : 32 * (64 + 4) + 4;
+}
+
+// Turbo decode at head_dim 64 (TurboQuantizer::decode, turbo.rs:302-330:
+// the polar part; the QJL words are validated, not used): two lanes per
+// vector as in turbo_encode_qjl_kernel, one 32-vector group per wave, two
+// workgroups per tile.  Each lane rebuilds the 32 elements of its half and
+// stores them straight from registers.
+template <int PB>
+__global__ __launch_bounds__(TILE) void turbo_decode_split_kernel(
+    LaunchCommon lc, const uint8_t* __restrict__ wire, float* __restrict__ out,
+    const float* __restrict__ signs, const float* __restrict__ cs_tab, uint64_t seed, uint32_t pbits_rt,
+    uint32_t proj, uint32_t mode) {
+    constexpr int DIM = 64;
+    constexpr int HP = 16;
+    extern __shared__ uint32_t smem_u[];   // per wave: 32 payloads
+    __shared__ float cs_lds[512];
+    __shared__ uint64_t exp_lds[32];
+
+    const uint32_t pbits = PB ? static_cast<uint32_t>(PB) : pbits_rt;
+    const uint32_t levels = 1u << pbits;
+    for (uint32_t t = threadIdx.x; t < 2 * levels; t += blockDim.x) cs_lds[t] = cs_tab[t];
+    if (threadIdx.x < 32) exp_lds[threadIdx.x] = c_exp2f_tab[threadIdx.x];
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int h = lane >> 5, n = lane & 31;
+    const uint32_t blk = blockIdx.x >> 1;
+    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const SegDev seg = lc.segs[sidx];
+    const uint32_t tile = blk - lc.tile_start[sidx];
+    const uint32_t plen = lc.plen, pwd = plen >> 2;
+    const uint8_t* blob = wire + seg.wire_offset;
+
+    // header check (every wave; 38 bytes)
+    const uint32_t hb = lane < 38 ? blob[lane] : 0u;
+    const bool hbad = lane < 38 && tqb1_checked(lane) &&
+                      hb != tqb1_byte(lane, DIM, pbits, lc.radii, proj, seed, seg.n_vectors, plen);
+    if (__ballot(hbad) != 0ull) {
+        if (lane == 0) status_fail(lc.status, sidx, 0, 0u, KIND_HEADER);
+        return;
+    }
+    const uint32_t t0 = tile * TILE + (blockIdx.x & 1u) * (TILE / 2) + 32u * static_cast<uint32_t>(wave);
+    if (t0 >= seg.n_vectors) return;
+    const uint32_t nv = min(32u, seg.n_vectors - t0);
+    // per wave: the 32 payloads, later the 32 decoded rows (pitch DIM + 4)
+    uint32_t* sw = smem_u + wave * turbo_split_wave_words(pwd);
+    global_to_lds(sw, blob + 38 + static_cast<uint64_t>(t0) * plen, nv * plen, lane);
+    wave_sync();
+
+    const bool active = static_cast<uint32_t>(n) < nv;
+    const uint32_t* pw = sw + min(static_cast<uint32_t>(n), nv - 1) * pwd;
+    const bool f32r = lc.radii == PKV_RADII_F32;
+    const uint32_t rwords = f32r ? 32u : 32u / 4 + 2;
+    bool ok = true;
+    float r[HP];
+    if (f32r) {
+#pragma unroll
+        for (int i = 0; i < HP; ++i) {
+            r[i] = u2f(pw[16 * h + i]);
+            ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);   // radius.rs:88-104
+        }
+    } else {
+        const float mn = u2f(pw[8]), mx = u2f(pw[9]);
+        ok &= isfinite_f(mn) && isfinite_f(mx) && !(mn > mx);   // radius.rs:171-177
+        const float span = mx - mn;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t q = pw[4 * h + k];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float u = static_cast<float>((q >> (8 * t)) & 0xffu);
+                const int i = 4 * k + t;
+                r[i] = og_expf(mn + span * (u / 255.0f), exp_lds);   // radius.rs:128-145
+                ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);             // polar.rs:127-133
+            }
+        }
+    }
+    // this half's 16 angle indices: bits 16 pbits h .. (pbits <= 4: <= 64 bits)
+    const uint32_t bit0 = 16u * pbits * static_cast<uint32_t>(h);
+    const uint32_t* aw = pw + rwords + (bit0 >> 5);
+    const uint32_t sh = bit0 & 31u;
+    const uint64_t lo64 = static_cast<uint64_t>(aw[0]) | static_cast<uint64_t>(aw[1]) << 32;
+    uint64_t pk = lo64 >> sh;
+    if (sh) pk |= static_cast<uint64_t>(aw[2]) << (64 - sh);
+    // the angle field is 32 * pbits bits, a whole number of words: no padding
+    // bits to check (bitpack.rs:88-109); nor in the 32/64-bit QJL field
+    (void)mode;
+
+    float y[32];
+#pragma unroll
+    for (int i = 0; i < HP; ++i) {
+        const uint32_t bin = static_cast<uint32_t>(pk >> (static_cast<uint32_t>(i) * pbits)) & (levels - 1u);
+        y[2 * i] = r[i] * cs_lds[2 * bin];
+        y[2 * i + 1] = r[i] * cs_lds[2 * bin + 1];
+    }
+    fwht_split(y, h);
+    const float scale = fwht_scale<DIM>();
+    const bool vok = ok && partner(ok ? 1u : 0u, h);
+    if (active && h == 0 && !vok) status_fail(lc.status, sidx, 1, t0 + n, KIND_CORRUPT);
+    // rows through LDS (over the consumed payloads) so they leave coalesced
+    wave_sync();
+    float* stage = reinterpret_cast<float*>(sw);
+    {
+        float* srow = stage + n * (DIM + 4) + 32 * h;
+        const float4* sp = reinterpret_cast<const float4*>(signs + 32 * h);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float4 sg = sp[k];
+            *reinterpret_cast<float4*>(srow + 4 * k) =
+                make_float4((y[4 * k] * scale) * sg.x, (y[4 * k + 1] * scale) * sg.y, (y[4 * k + 2] * scale) * sg.z,
+                            (y[4 * k + 3] * scale) * sg.w);
+        }
+    }
+    const uint64_t badm = __ballot(active && h == 0 && !vok);
+    wave_sync();
+    stage_rows_out<DIM>(out, stage, seg, t0, nv, static_cast<uint32_t>(badm), 0u, lane);
+}
+
 // ------------------------------------------------------------ fib encode
 // FibQuantizer::encode_batch (fib-quant/src/codec.rs:578-729; n < 4 takes
 // FibQuantizer::encode, 471-516) + FibCodeV1::encode_batch (FB2, 225-320).
@@ -1681,6 +1802,13 @@ int launch_turbo_encode(const LaunchCommon& lc, const TurboDev& td, const void* 
 int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_t* wire, float* out,
                         uint32_t nblocks, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (td.dim == 64 && td.pbits <= 4) {
+        const size_t lds = static_cast<size_t>(WAVES) * turbo_split_wave_words(lc.plen >> 2) * sizeof(uint32_t);
+        return td.pbits == 3 ? launch_big_lds(turbo_decode_split_kernel<3>, 2 * nblocks, lds, st, lc, wire, out,
+                                              td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode)
+                             : launch_big_lds(turbo_decode_split_kernel<0>, 2 * nblocks, lds, st, lc, wire, out,
+                                              td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode);
+    }
     if (td.dim == 64)
         return td.pbits == 3
                    ? launch_big_lds(turbo_decode_kernel<64, 3>, nblocks, stage_bytes<64>(), st, lc, wire, out, td.signs,
