@@ -22,14 +22,79 @@ namespace {
 
 constexpr int kSlots = 8;
 
+int hip_status(hipError_t e) {
+    if (e == hipSuccess) return PKV_OK;
+    if (e == hipErrorOutOfMemory) return PKV_ERR_OOM;
+    return PKV_ERR_DEVICE;
+}
+
+#define HIP_TRY(expr)                          \
+    do {                                       \
+        hipError_t _e = (expr);                \
+        if (_e != hipSuccess) return hip_status(_e); \
+    } while (0)
+
+
+// Streams that have launched work on a buffer since it was last known idle.
+// No event is recorded per launch: when the buffer must be reused or rewritten
+// the library records an event on each of these streams at that moment (it
+// follows all their earlier work) and waits on it.  Past kMaxUsers streams
+// the device is synchronised instead.
+constexpr int kMaxUsers = 4;
+struct Users {
+    hipStream_t s[kMaxUsers] = {};
+    int n = 0;
+    bool overflow = false;
+    void add(hipStream_t st) {
+        for (int i = 0; i < n; ++i)
+            if (s[i] == st) return;
+        if (n < kMaxUsers) s[n++] = st; else overflow = true;
+    }
+    bool only(hipStream_t st) const { return !overflow && (n == 0 || (n == 1 && s[0] == st)); }
+    // host waits until every recorded user is done
+    int drain_host(hipEvent_t ev) {
+        if (overflow) HIP_TRY(hipDeviceSynchronize());
+        else
+            for (int i = 0; i < n; ++i) {
+                HIP_TRY(hipEventRecord(ev, s[i]));
+                HIP_TRY(hipEventSynchronize(ev));
+            }
+        n = 0;
+        overflow = false;
+        return PKV_OK;
+    }
+    // `st` waits (on the device) until every other recorded user is done
+    int drain_stream(hipEvent_t ev, hipStream_t st) {
+        if (overflow) HIP_TRY(hipDeviceSynchronize());
+        else
+            for (int i = 0; i < n; ++i)
+                if (s[i] != st) {
+                    HIP_TRY(hipEventRecord(ev, s[i]));
+                    HIP_TRY(hipStreamWaitEvent(st, ev, 0));
+                }
+        n = 0;
+        overflow = false;
+        return PKV_OK;
+    }
+};
+
 struct Slot {
     void* dev = nullptr;         // segs | tile_start | status
-    void* host = nullptr;        // pinned staging
+    void* host = nullptr;        // pinned staging (keeps the uploaded table)
     size_t cap = 0;
-    hipEvent_t done = nullptr;
-    bool used = false;
-    void* redo = nullptr;        // fib encode redo queue: count word + entries
-    size_t redo_cap = 0;
+    hipEvent_t ev = nullptr;
+    Users users;                 // streams that read (or wrote status into) the slot
+    bool shared = false;         // table only (no status words): reusable by equal tables
+    uint32_t nseg = 0;
+    uint64_t hash = 0;
+};
+
+// fib encode redo queues, a ring of their own (the kernels write them)
+struct RedoSlot {
+    void* dev = nullptr;
+    size_t cap = 0;
+    hipEvent_t ev = nullptr;
+    Users users;
 };
 
 }  // namespace
@@ -39,6 +104,8 @@ struct pkv_ctx {
     std::mutex mu;
     Slot slots[kSlots];
     int next = 0;
+    RedoSlot redo[kSlots];
+    int redo_next = 0;
     hipStream_t own_stream = nullptr;   // for the host-buffer entry points
     void* scratch = nullptr;            // host-buffer entry points: in + out
     size_t scratch_cap = 0;
@@ -73,17 +140,7 @@ struct pkv_profile {
 
 namespace {
 
-int hip_status(hipError_t e) {
-    if (e == hipSuccess) return PKV_OK;
-    if (e == hipErrorOutOfMemory) return PKV_ERR_OOM;
-    return PKV_ERR_DEVICE;
-}
 
-#define HIP_TRY(expr)                          \
-    do {                                       \
-        hipError_t _e = (expr);                \
-        if (_e != hipSuccess) return hip_status(_e); \
-    } while (0)
 
 template <typename T>
 int upload(T** dptr, const std::vector<T>& v) {
@@ -168,8 +225,18 @@ int validate_segments(const pkv_profile* p, int radii, bool encode, int dtype, c
     return PKV_OK;
 }
 
+uint64_t fnv1a(const void* p, size_t n) {
+    const auto* b = static_cast<const uint8_t*>(p);
+    uint64_t h = 1469598103934665603ull;
+    for (size_t i = 0; i < n; ++i) h = (h ^ b[i]) * 1099511628211ull;
+    return h;
+}
+
 // Stage the segment table + tile prefix (+ status words when the caller gave
-// none) into a ring slot and copy it to the device on `stream`.
+// none) into a ring slot and copy it to the device on `stream`.  A table the
+// device already holds in a table-only slot is reused as is: the kernels only
+// read it, so a launch in flight on it does not matter, and repeated calls
+// over the same segments (every step of a serving loop) upload nothing.
 int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vector<uint32_t>& tiles,
                 bool need_status, hipStream_t stream, Slot** out_slot, SegDev** d_segs, uint32_t** d_tiles,
                 uint32_t** d_status) {
@@ -178,9 +245,28 @@ int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vec
     const size_t tile_off = (seg_bytes + 255) & ~static_cast<size_t>(255);
     const size_t stat_off = (tile_off + tile_bytes + 255) & ~static_cast<size_t>(255);
     const size_t total = stat_off + (need_status ? sizeof(uint32_t) * 2 * nseg : 0) + 256;
+    const uint64_t hash = fnv1a(segs, seg_bytes);
+    if (!need_status) {
+        for (Slot& c : ctx->slots) {
+            if (c.shared && c.nseg == nseg && c.hash == hash && std::memcmp(c.host, segs, seg_bytes) == 0) {
+                auto* d = static_cast<uint8_t*>(c.dev);
+                *d_segs = reinterpret_cast<SegDev*>(d);
+                *d_tiles = reinterpret_cast<uint32_t*>(d + tile_off);
+                *d_status = nullptr;
+                *out_slot = &c;
+                return PKV_OK;
+            }
+        }
+    }
     Slot& sl = ctx->slots[ctx->next];
     ctx->next = (ctx->next + 1) % kSlots;
-    if (sl.used) HIP_TRY(hipEventSynchronize(sl.done));
+    if (!sl.ev) HIP_TRY(hipEventCreateWithFlags(&sl.ev, hipEventDisableTiming));
+    // the pinned copy and the device table are about to be rewritten
+    if (sl.users.n || sl.users.overflow) {
+        int rc = sl.users.drain_host(sl.ev);
+        if (rc) return rc;
+    }
+    sl.shared = false;
     if (sl.cap < total) {
         if (sl.dev) HIP_TRY(hipFree(sl.dev));
         if (sl.host) HIP_TRY(hipHostFree(sl.host));
@@ -190,11 +276,13 @@ int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vec
         HIP_TRY(hipHostMalloc(&sl.host, cap, hipHostMallocDefault));
         sl.cap = cap;
     }
-    if (!sl.done) HIP_TRY(hipEventCreateWithFlags(&sl.done, hipEventDisableTiming));
     auto* h = static_cast<uint8_t*>(sl.host);
     std::memcpy(h, segs, seg_bytes);
     std::memcpy(h + tile_off, tiles.data(), tile_bytes);
     HIP_TRY(hipMemcpyAsync(sl.dev, sl.host, stat_off, hipMemcpyHostToDevice, stream));
+    sl.shared = !need_status;
+    sl.nseg = nseg;
+    sl.hash = hash;
     auto* d = static_cast<uint8_t*>(sl.dev);
     *d_segs = reinterpret_cast<SegDev*>(d);
     *d_tiles = reinterpret_cast<uint32_t*>(d + tile_off);
@@ -204,8 +292,7 @@ int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vec
 }
 
 int finish_slot(Slot* sl, hipStream_t stream) {
-    HIP_TRY(hipEventRecord(sl->done, stream));
-    sl->used = true;
+    sl->users.add(stream);
     return PKV_OK;
 }
 
@@ -240,28 +327,46 @@ FibDev fib_dev(const pkv_profile* p) {
     return f;
 }
 
-// fib encode: size the slot's per-workgroup redo queues (a 4-word head and
-// TILE entries per workgroup), then run the MFMA kernel and the exact fixup.
-int launch_fib_encode_queued(Slot* sl, const LaunchCommon& lc, const pkv_profile* prof, const void* d_in,
+// fib encode: the next redo-queue buffer of the ring (a 4-word head and TILE
+// entries per workgroup), then the MFMA kernel and the exact fixup.
+int launch_fib_encode_queued(pkv_ctx* ctx, const LaunchCommon& lc, const pkv_profile* prof, const void* d_in,
                              uint8_t* d_wire, uint32_t nblocks, hipStream_t stream) {
+    // a redo buffer last used by this stream alone needs no wait (stream order)
+    RedoSlot* pick = nullptr;
+    for (RedoSlot& r : ctx->redo)
+        if (r.dev && r.users.only(stream)) { pick = &r; break; }
+    if (!pick) {
+        pick = &ctx->redo[ctx->redo_next];
+        ctx->redo_next = (ctx->redo_next + 1) % kSlots;
+    }
+    RedoSlot& rs = *pick;
+    hipError_t e = hipSuccess;
+    if (!rs.ev && (e = hipEventCreateWithFlags(&rs.ev, hipEventDisableTiming)) != hipSuccess) return e;
+    if (!rs.users.only(stream)) {
+        int rc = rs.users.drain_stream(rs.ev, stream);
+        if (rc) return hipErrorUnknown;
+    }
     const size_t counts_bytes = (16 * static_cast<size_t>(nblocks) + 255) & ~static_cast<size_t>(255);
     const size_t need = counts_bytes + 4 * static_cast<size_t>(TILE) * nblocks;
-    if (sl->redo_cap < need) {
-        if (sl->redo) {
-            hipError_t e = hipFree(sl->redo);
-            if (e != hipSuccess) return e;
+    if (rs.cap < need) {
+        if (rs.users.n || rs.users.overflow) {
+            int rc = rs.users.drain_host(rs.ev);
+            if (rc) return hipErrorUnknown;
         }
-        sl->redo = nullptr;
-        sl->redo_cap = 0;
+        if (rs.dev && (e = hipFree(rs.dev)) != hipSuccess) return e;
+        rs.dev = nullptr;
+        rs.cap = 0;
         const size_t cap = std::max<size_t>(need + need / 4, 1 << 16);
-        hipError_t e = hipMalloc(&sl->redo, cap);
-        if (e != hipSuccess) return e;
-        sl->redo_cap = cap;
+        if ((e = hipMalloc(&rs.dev, cap)) != hipSuccess) return e;
+        rs.cap = cap;
     }
     FibRedo rq;
-    rq.heads = static_cast<uint32_t*>(sl->redo);
-    rq.entries = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(sl->redo) + counts_bytes);
-    return launch_fib_encode(lc, fib_dev(prof), d_in, d_wire, nblocks, rq, stream);
+    rq.heads = static_cast<uint32_t*>(rs.dev);
+    rq.entries = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(rs.dev) + counts_bytes);
+    int rc = launch_fib_encode(lc, fib_dev(prof), d_in, d_wire, nblocks, rq, stream);
+    if (rc) return rc;
+    rs.users.add(stream);
+    return hipSuccess;
 }
 
 // Caller holds ctx->mu.
@@ -301,7 +406,7 @@ int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool e
                    : launch_turbo_decode(lc, turbo_dev(prof), d_wire, static_cast<float*>(const_cast<void*>(d_f32)),
                                          nblocks, stream);
     } else {
-        e = encode ? launch_fib_encode_queued(sl, lc, prof, d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
+        e = encode ? launch_fib_encode_queued(ctx, lc, prof, d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
                    : launch_fib_decode(lc, fib_dev(prof), d_wire, static_cast<float*>(const_cast<void*>(d_f32)),
                                        nblocks, stream);
     }
@@ -421,11 +526,15 @@ void pkv_ctx_destroy(pkv_ctx* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     for (Slot& s : ctx->slots) {
-        if (s.used) (void)hipEventSynchronize(s.done);
-        if (s.done) (void)hipEventDestroy(s.done);
+        if (s.users.n || s.users.overflow) (void)s.users.drain_host(s.ev);
+        if (s.ev) (void)hipEventDestroy(s.ev);
         if (s.dev) (void)hipFree(s.dev);
         if (s.host) (void)hipHostFree(s.host);
-        if (s.redo) (void)hipFree(s.redo);
+    }
+    for (RedoSlot& r : ctx->redo) {
+        if (r.users.n || r.users.overflow) (void)r.users.drain_host(r.ev);
+        if (r.ev) (void)hipEventDestroy(r.ev);
+        if (r.dev) (void)hipFree(r.dev);
     }
     if (ctx->own_stream) {
         (void)hipStreamSynchronize(ctx->own_stream);
