@@ -15,7 +15,7 @@ duration (HIP events on the launch stream) against 8 TB/s.
 cpu_baseline = the C oracle (a one-thread restatement of the reference Rust
 codecs) timed on a bounded sample of the same workload on the host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--lossy] [--workload pool|legacy]
 """
 from __future__ import annotations
 
@@ -97,6 +97,97 @@ def profiled_traffic(kernel: str):
     return None
 
 
+def bench_legacy(args):
+    """Per-vector KVecCodec records through the host-buffer entry points
+    (pkv_encode_vectors / pkv_decode_vectors, PCIe copies included): a
+    config-1-sized pool as FB1 records and config-2-sized shells as TQW1
+    records.  Prints one JSON line; the kernel durations come from rocprofv3."""
+    import ctypes as C
+
+    import torch
+    from oracle import oracle as O
+    from provekv_amd import _lib as L
+    from provekv_amd import synth
+    from provekv_amd.device import default_context
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU"}))
+        sys.exit(1)
+    ctx = default_context()
+    fib = ctx.fib_profile(64, 4, 32, 42)
+    tur = ctx.turbo_profile(64, 4, 32, 42, 1)
+    log("[bench] generating config-1 / config-2 shaped vectors")
+    x1 = np.ascontiguousarray(synth.corpus_tokens(1, 24, 32, 800, 64).reshape(-1, 64))
+    x2 = np.ascontiguousarray(synth.corpus_tokens(2, 24, 32, 224, 64).reshape(-1, 64))
+
+    def enc(prof, x, each):
+        n, rec = x.shape[0], prof.record_len()
+        out = np.empty(n * rec, np.uint8)
+        ln, err = C.c_uint64(), L.Error()
+        rc = L.lib().pkv_encode_vectors(ctx.ptr, prof.ptr, int(each), x.ctypes.data, n, out.ctypes.data, out.size,
+                                        C.byref(ln), C.byref(err))
+        if rc:
+            raise L.PkvError(rc, "pkv_encode_vectors", err.segment, err.index)
+        return out
+
+    def dec(prof, recs, n, each):
+        off = np.arange(n + 1, dtype=np.uint64) * np.uint64(prof.record_len())
+        out = np.empty((n, 64), np.float32)
+        err = L.Error()
+        rc = L.lib().pkv_decode_vectors(ctx.ptr, prof.ptr, int(each), recs.ctypes.data, off.ctypes.data, n,
+                                        out.ctypes.data, n, C.byref(err))
+        if rc:
+            raise L.PkvError(rc, "pkv_decode_vectors", err.segment, err.index)
+        return out
+
+    def timed(fn):
+        fn()
+        best = float("inf")
+        for _ in range(args.steps):
+            t0 = time.perf_counter()
+            r = fn()
+            best = min(best, time.perf_counter() - t0)
+        return r, best
+
+    ops = {}
+    r_fib, t = timed(lambda: enc(fib, x1, False))
+    ops["fib_fb1_encode_batch"] = (x1.shape[0], t)
+    _, t = timed(lambda: enc(fib, x1, True))
+    ops["fib_fb1_encode_each"] = (x1.shape[0], t)
+    d_fast, t = timed(lambda: dec(fib, r_fib, x1.shape[0], False))
+    ops["fib_fb1_decode_batch"] = (x1.shape[0], t)
+    d_f64, t = timed(lambda: dec(fib, r_fib, x1.shape[0], True))
+    ops["fib_fb1_decode_each_f64"] = (x1.shape[0], t)
+    r_tur, t = timed(lambda: enc(tur, x2, True))
+    ops["turbo_tqw1_encode"] = (x2.shape[0], t)
+    d_tur, t = timed(lambda: dec(tur, r_tur, x2.shape[0], True))
+    ops["turbo_tqw1_decode"] = (x2.shape[0], t)
+    # parity spot check against the oracle on the first records
+    m = 2000
+    cb, rot = fib.constants()
+    cb, rot = cb.reshape(32, 4), rot.reshape(64, 64)
+    rec1 = fib.record_len()
+    ref = O.fib_encode_fb1(x1[:m], cb, rot, each=False)
+    parity = b"".join(ref) == r_fib[:m * rec1].tobytes()
+    parity &= np.array_equal(O.fib_decode_fb1(ref, cb, rot, each=True).view(np.uint32), d_f64[:m].view(np.uint32))
+    rec2 = tur.record_len()
+    ref2 = O.turbo_encode_tqw1(x2[:m], 42)
+    parity &= b"".join(ref2) == r_tur[:m * rec2].tobytes()
+    parity &= np.array_equal(O.turbo_decode_tqw1(ref2, 64, 42).view(np.uint32), d_tur[:m].view(np.uint32))
+    out = {"workload": "legacy per-vector records (KVecCodec::encode/decode): config-1 pool as 1,228,800 FB1 "
+                       "records, config-2 shells as 344,064 TQW1 records, host buffers (PCIe included)",
+           "unit": "GB/s of f32 KV", "steps": args.steps, "parity_first_2000": bool(parity),
+           "ops": {k: {"vectors": n, "ms": round(t * 1e3, 3), "gbs": round(n * 256 / t / 1e9, 2)}
+                   for k, (n, t) in ops.items()}}
+    if args.copy_calib:   # the reference kernel for rocprofv3 --pmc byte counters
+        src = torch.empty(1 << 28, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -106,11 +197,16 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a 256 MiB device copy (reference kernel for rocprofv3 --pmc byte counters)")
+    ap.add_argument("--workload", choices=("pool", "legacy"), default="pool",
+                    help="pool: the config-3 metric (default); legacy: per-vector TQW1 / FB1 records")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1",
                           "n_gpus": args.gpus}), flush=True)
         sys.exit(2)
+    if args.workload == "legacy":
+        bench_legacy(args)
+        return
 
     import torch
     from provekv_amd import synth

@@ -89,7 +89,8 @@ int pkv_turbo_profile_create_with_constants(pkv_ctx* ctx, uint32_t dim, uint32_t
 /* Replaces FibQuantAdapter::build_quantizer (proveKV/src/codec.rs:471-499):
  * paper_default profile with the adapter's training overrides; the codebook
  * (Lloyd-Max) and the f64 rotation are built on the host once and uploaded.
- * dim 64 or 128, k 4, n <= 32. */
+ * The kernels implement fib_k4_n32 at head_dim 64 (dim 64, k 4, n 32);
+ * other shapes return PKV_ERR_UNSUPPORTED. */
 int pkv_fib_profile_create(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, uint64_t seed,
                            uint32_t training_samples, uint32_t lloyd_restarts,
                            uint32_t lloyd_iterations, pkv_profile** out);
@@ -180,6 +181,37 @@ int pkv_encode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, int radii_co
 int pkv_decode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, const uint8_t* payload,
                              uint64_t len, float* out, uint64_t out_cap_vectors, uint64_t* n_out,
                              pkv_error* err);
+
+/* ---------------------------------------------------------------- per-vector
+ * The KVecCodec trait's own methods (proveKV/src/codec.rs:8-66), whose wire
+ * form is one self-describing record per vector: TQW1 for turbo
+ * (TurboCodeWireV1::encode / decode, turbo-quant/src/wire.rs:44-256; always
+ * f32 radii) and compact FB1 for fib (FibCodeV1::to_compact_bytes /
+ * from_compact_bytes, fib-quant/src/codec.rs:81-176).  Legacy pools and
+ * shells store these (pool.rs:569-603).  Records are fixed-size for a
+ * profile: pkv_record_len bytes (190 = 46 + 144 TQW1, 23 = 11 + 12 FB1 at
+ * head_dim 64). */
+uint32_t pkv_record_len(const pkv_profile* prof);
+
+/* Replaces TurboQuantAdapter::encode / KVecCodec::encode_batch (codec.rs:28-30,
+ * 339-365; every vector encoded on its own) and FibQuantAdapter::encode
+ * (each != 0, codec.rs:582-594: FibQuantizer::encode per vector, f64
+ * normalisation) / encode_batch (each == 0, 596-610: FibQuantizer::encode_batch,
+ * f32-rounded normalisation when n >= 4).  Writes n records back to back
+ * (out_len = n * pkv_record_len).  Errors as pkv_encode_batch_compact. */
+int pkv_encode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const float* vectors, uint64_t n,
+                       uint8_t* out, uint64_t out_cap, uint64_t* out_len, pkv_error* err);
+
+/* Replaces TurboQuantAdapter::decode / KVecCodec::decode_batch (codec.rs:367-405,
+ * 34-37) and FibQuantAdapter::decode (each != 0, 612-637: FibQuantizer::decode,
+ * f64 inverse rotation, codec.rs:506-537) / decode_batch (each == 0, 639-665:
+ * every record parsed first, then decode_batch_fast).  Record i is
+ * records[offsets[i] .. offsets[i + 1]) (n + 1 non-decreasing offsets, the
+ * flattening of a `&[&[u8]]`).  A rejected record gives
+ * PKV_ERR_CORRUPT_PAYLOAD with err->index = the record the reference reports.
+ * JSON-serialised codes (the pre-compact envelope) are not decoded. */
+int pkv_decode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const uint8_t* records,
+                       const uint64_t* offsets, uint64_t n, float* out, uint64_t out_cap_vectors, pkv_error* err);
 
 /* Parses a TQB1 / FB2 header against the profile (host memory) and reports
  * the number of vectors and the radii codec; PKV_ERR_CORRUPT_PAYLOAD on any

@@ -107,6 +107,18 @@ def _declare(L):
     L.ora_fib_encode_batch.restype = I32
     L.ora_fib_decode_batch.argtypes = [U32, U32, U32, P, P, P, U64, P, U64, P, P]
     L.ora_fib_decode_batch.restype = I32
+    L.ora_tqw1_record_len.argtypes = [U32, U32, U32, I32]
+    L.ora_tqw1_record_len.restype = U32
+    L.ora_turbo_encode_tqw1.argtypes = [U32, U32, U32, U64, I32, P, P, P, U64, P, U64, P, P]
+    L.ora_turbo_encode_tqw1.restype = I32
+    L.ora_turbo_decode_tqw1.argtypes = [U32, U32, U32, U64, I32, P, P, P, U64, P, P]
+    L.ora_turbo_decode_tqw1.restype = I32
+    L.ora_fb1_record_len.argtypes = [U32, U32, U32]
+    L.ora_fb1_record_len.restype = U32
+    L.ora_fib_encode_fb1.argtypes = [U32, U32, U32, P, P, P, U64, I32, P, U64, P, P]
+    L.ora_fib_encode_fb1.restype = I32
+    L.ora_fib_decode_fb1.argtypes = [U32, U32, U32, P, P, P, P, U64, I32, P, P]
+    L.ora_fib_decode_fb1.restype = I32
     L.ora_pack_bits.argtypes = [P, U64, I32, P]
     L.ora_unpack_bits.argtypes = [P, U64, I32, P]
     L.ora_unpack_bits.restype = I32
@@ -339,6 +351,84 @@ def fib_decode_batch(blob: bytes, codebook: np.ndarray, rotation: np.ndarray, d:
     if rc:
         raise OracleError(rc, int(fail[0]))
     return out[:n]
+
+
+# ---------------------------------------------------------------- legacy per-vector records
+def _records(records):
+    """list of bytes -> (concatenated buffer, n + 1 offsets)."""
+    off = np.zeros(len(records) + 1, dtype=np.uint64)
+    off[1:] = np.cumsum([len(r) for r in records], dtype=np.uint64) if records else []
+    buf = np.frombuffer(b"".join(records), dtype=np.uint8).copy()
+    if buf.size == 0:
+        buf = np.zeros(1, dtype=np.uint8)
+    return buf, off
+
+
+def turbo_encode_tqw1(x: np.ndarray, seed: int, bits=4, proj=32, mode=1) -> list:
+    """TurboQuantAdapter::encode on each row -> list of TQW1 records."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, dim = x.shape
+    signs, G = turbo_constants(dim, proj if mode else 0, seed)
+    if G.size == 0:
+        G = np.zeros((1, dim), dtype=np.float32)
+    rec = int(lib().ora_tqw1_record_len(dim, bits, proj, mode))
+    out = np.zeros(max(n * rec, 1), dtype=np.uint8)
+    out_len = np.zeros(1, dtype=np.uint64)
+    fail = np.zeros(1, dtype=np.uint64)
+    rc = lib().ora_turbo_encode_tqw1(dim, bits, proj, seed, mode, _p(signs), _p(np.ascontiguousarray(G, np.float32)),
+                                     _p(x), n, _p(out), n * rec, _p(out_len), _p(fail))
+    if rc:
+        raise OracleError(rc, int(fail[0]))
+    b = out.tobytes()
+    return [b[i * rec:(i + 1) * rec] for i in range(n)]
+
+
+def turbo_decode_tqw1(records: list, dim: int, seed: int, bits=4, proj=32, mode=1) -> np.ndarray:
+    """TurboQuantAdapter::decode on each TQW1 record (first failure raises)."""
+    signs, _ = turbo_constants(dim, 0, seed)
+    buf, off = _records(records)
+    out = np.zeros((max(len(records), 1), dim), dtype=np.float32)
+    fail = np.zeros(1, dtype=np.uint64)
+    rc = lib().ora_turbo_decode_tqw1(dim, bits, proj, seed, mode, _p(signs), _p(buf), _p(off), len(records),
+                                     _p(out), _p(fail))
+    if rc:
+        raise OracleError(rc, int(fail[0]))
+    return out[:len(records)]
+
+
+def fib_encode_fb1(x: np.ndarray, codebook: np.ndarray, rotation: np.ndarray, each: bool) -> list:
+    """FibQuantAdapter::encode per row (each) or encode_batch -> FB1 records."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, d = x.shape
+    N, k = codebook.shape
+    cb = np.ascontiguousarray(codebook, dtype=np.float32)
+    rot = np.ascontiguousarray(rotation, dtype=np.float64)
+    rec = int(lib().ora_fb1_record_len(d, k, N))
+    out = np.zeros(max(n * rec, 1), dtype=np.uint8)
+    out_len = np.zeros(1, dtype=np.uint64)
+    fail = np.zeros(1, dtype=np.uint64)
+    rc = lib().ora_fib_encode_fb1(d, k, N, _p(cb), _p(rot), _p(x), n, int(each), _p(out), n * rec, _p(out_len),
+                                  _p(fail))
+    if rc:
+        raise OracleError(rc, int(fail[0]))
+    b = out.tobytes()
+    return [b[i * rec:(i + 1) * rec] for i in range(n)]
+
+
+def fib_decode_fb1(records: list, codebook: np.ndarray, rotation: np.ndarray, each: bool, d: int = 64) -> np.ndarray:
+    """FibQuantAdapter::decode per record (each: f64 rotation) or decode_batch
+    (parse every record first, then the f32 decode_batch_fast)."""
+    N, k = codebook.shape
+    cb = np.ascontiguousarray(codebook, dtype=np.float32)
+    rot = np.ascontiguousarray(rotation, dtype=np.float64)
+    buf, off = _records(records)
+    out = np.zeros((max(len(records), 1), d), dtype=np.float32)
+    fail = np.zeros(1, dtype=np.uint64)
+    rc = lib().ora_fib_decode_fb1(d, k, N, _p(cb), _p(rot), _p(buf), _p(off), len(records), int(each), _p(out),
+                                  _p(fail))
+    if rc:
+        raise OracleError(rc, int(fail[0]))
+    return out[:len(records)]
 
 
 def pack_bits(values, bits: int) -> bytes:

@@ -872,6 +872,36 @@ static int turbo_check_profile(uint32_t dim, uint32_t bits, uint32_t proj, int m
     return 1;
 }
 
+/* One vector's payload: [radii (f32, or BlockLogU8 u8s + min + max)]
+ * [packed angle indices][packed QJL signs] (wire.rs:63-95, 350-390). */
+static int turbo_encode_payload(uint32_t dim, uint32_t bits, uint32_t proj, int mode, int radii_codec,
+                                const float* signs, const float* G, const float* xv, uint8_t* p) {
+    int pbits = mode ? (int)bits - 1 : (int)bits;
+    uint32_t pairs = dim / 2;
+    uint32_t plen = turbo_payload_len(dim, pbits, proj, mode, radii_codec);
+    uint32_t angle_bytes = (pairs * (uint32_t)pbits + 7) / 8;
+    float radii[128];
+    uint16_t idx[128];
+    uint8_t sb[128];
+    int rc = ora_turbo_encode_vector(dim, bits, proj, mode, signs, G, xv, radii, idx, sb);
+    if (rc != ORA_OK) return rc;
+    memset(p, 0, plen);
+    if (radii_codec) {
+        float mn, mx;
+        radii_log_u8(radii, (int)pairs, p, &mn, &mx);
+        put_f32(p + pairs, mn);
+        put_f32(p + pairs + 4, mx);
+        p += pairs + 8;
+    } else {
+        for (uint32_t i = 0; i < pairs; ++i) put_f32(p + 4 * i, radii[i]);
+        p += 4 * pairs;
+    }
+    for (uint32_t i = 0; i < pairs; ++i) write_bits(p, (size_t)i * pbits, pbits, idx[i]);
+    p += angle_bytes;
+    if (mode) memcpy(p, sb, (proj + 7) / 8);
+    return ORA_OK;
+}
+
 /* TurboQuantAdapter::encode_batch_compact (proveKV/src/codec.rs:248-291) =
  * per-vector TurboQuantizer::encode + TurboCodeWireV1::encode_batch_with_radii
  * (wire.rs:291-398).  x: n*dim row-major.  radii_codec: 0 F32, 1 BlockLogU8. */
@@ -881,7 +911,6 @@ int ora_turbo_encode_batch(uint32_t dim, uint32_t bits, uint32_t proj, uint64_t 
                            uint64_t* fail_index) {
     if (!turbo_check_profile(dim, bits, proj, mode)) return ORA_ERR_INVALID_ARG;
     int pbits = mode ? (int)bits - 1 : (int)bits;
-    uint32_t pairs = dim / 2;
     uint32_t plen = turbo_payload_len(dim, pbits, proj, mode, radii_codec);
     uint64_t total = 38 + n * (uint64_t)plen;
     if (out_len) *out_len = total;
@@ -899,28 +928,10 @@ int ora_turbo_encode_batch(uint32_t dim, uint32_t bits, uint32_t proj, uint64_t 
     put_u64(out + 22, seed);
     put_u32(out + 30, (uint32_t)n);
     put_u32(out + 34, plen);
-    float radii[128];
-    uint16_t idx[128];
-    uint8_t sb[128];
-    uint32_t angle_bytes = (pairs * (uint32_t)pbits + 7) / 8;
     for (uint64_t v = 0; v < n; ++v) {
-        int rc = ora_turbo_encode_vector(dim, bits, proj, mode, signs, G, x + v * dim, radii, idx, sb);
+        int rc = turbo_encode_payload(dim, bits, proj, mode, radii_codec, signs, G, x + v * dim,
+                                      out + 38 + v * plen);
         if (rc != ORA_OK) { if (fail_index) *fail_index = v; return rc; }
-        uint8_t* p = out + 38 + v * plen;
-        memset(p, 0, plen);
-        if (radii_codec) {
-            float mn, mx;
-            radii_log_u8(radii, (int)pairs, p, &mn, &mx);
-            put_f32(p + pairs, mn);
-            put_f32(p + pairs + 4, mx);
-            p += pairs + 8;
-        } else {
-            for (uint32_t i = 0; i < pairs; ++i) put_f32(p + 4 * i, radii[i]);
-            p += 4 * pairs;
-        }
-        for (uint32_t i = 0; i < pairs; ++i) write_bits(p, (size_t)i * pbits, pbits, idx[i]);
-        p += angle_bytes;
-        if (mode) memcpy(p, sb, (proj + 7) / 8);
     }
     return ORA_OK;
 }
@@ -1115,6 +1126,57 @@ static uint32_t fib_wire_bits(int n) {
     return bits;
 }
 
+/* Payloads [f16 norm][16 x 5-bit indices] of n vectors (plen bytes each).
+ * per_vector = 0: FibQuantizer::encode_batch (codec.rs:578-668): a validation
+ * pass over the whole batch first (592-610), x^ = f32(x / |x|) (608).
+ * per_vector = 1: FibQuantizer::encode on each vector (codec.rs:471-516):
+ * checks vector by vector, x^ = x / |x| kept in f64 (481-483).
+ * Both: rho = f32(Pi x^) row by row in f64 (rotation.rs:104-115), norm f64 ->
+ * f32 -> f16 (994-1020), AVX2 argmin per k-block, indices LSB-first. */
+static int fib_encode_payloads(uint32_t d, uint32_t k, uint32_t N, const float* cb, const double* rot,
+                               const float* x, uint64_t n, int per_vector, uint8_t* pay, uint32_t plen,
+                               uint64_t* fail_index) {
+    uint32_t bits = fib_wire_bits((int)N);
+    uint32_t blocks = d / k;
+    double xn[256], yr[256];
+    float xh[256], rho[256];
+    if (!per_vector) {
+        for (uint64_t v = 0; v < n; ++v) {
+            const float* xv = x + v * d;
+            for (uint32_t i = 0; i < d; ++i)
+                if (!isfinite(xv[i])) { if (fail_index) *fail_index = v; return ORA_ERR_NONFINITE_INPUT; }
+            if (l2_norm_f64(xv, (int)d) == 0.0) { if (fail_index) *fail_index = v; return ORA_ERR_ZERO_NORM; }
+        }
+    }
+    for (uint64_t v = 0; v < n; ++v) {
+        const float* xv = x + v * d;
+        double nrm;
+        if (per_vector) {
+            for (uint32_t i = 0; i < d; ++i)
+                if (!isfinite(xv[i])) { if (fail_index) *fail_index = v; return ORA_ERR_NONFINITE_INPUT; }
+            nrm = l2_norm_f64(xv, (int)d);
+            if (nrm == 0.0) { if (fail_index) *fail_index = v; return ORA_ERR_ZERO_NORM; }
+            for (uint32_t i = 0; i < d; ++i) xn[i] = (double)xv[i] / nrm;          /* codec.rs:481 */
+        } else {
+            nrm = l2_norm_f64(xv, (int)d);
+            for (uint32_t i = 0; i < d; ++i) { xh[i] = (float)((double)xv[i] / nrm); xn[i] = (double)xh[i]; }
+        }
+        rot_apply_f64((int)d, rot, xn, yr);
+        for (uint32_t i = 0; i < d; ++i) rho[i] = (float)yr[i];
+        uint16_t h;
+        int rc = encode_norm16(nrm, &h);
+        if (rc != ORA_OK) { if (fail_index) *fail_index = v; return rc; }
+        uint8_t* p = pay + v * plen;
+        memset(p, 0, plen);
+        put_u16(p, h);
+        for (uint32_t b = 0; b < blocks; ++b) {
+            int w = nearest_dispatch(rho + (size_t)b * k, cb, (int)k, (int)N);
+            write_bits(p + 2, (size_t)b * bits, (int)bits, (uint32_t)w);
+        }
+    }
+    return ORA_OK;
+}
+
 /* FibQuantAdapter::encode_batch_compact (proveKV/src/codec.rs:513-525) =
  * FibQuantizer::encode_batch (codec.rs:578-668; n < 4 takes encode,
  * codec.rs:471-516) + finish_batch_encode (670-729) + FibCodeV1::encode_batch
@@ -1131,17 +1193,6 @@ int ora_fib_encode_batch(uint32_t d, uint32_t k, uint32_t N, const float* cb, co
     if (out_len) *out_len = total;
     if (n == 0) return ORA_ERR_EMPTY;
     if (cap < total) return ORA_ERR_CAPACITY;
-    double xn[256], yr[256];
-    float xh[256], rho[256];
-    if (n >= 4) {
-        /* validation pass over the whole batch first (codec.rs:592-610) */
-        for (uint64_t v = 0; v < n; ++v) {
-            const float* xv = x + v * d;
-            for (uint32_t i = 0; i < d; ++i)
-                if (!isfinite(xv[i])) { if (fail_index) *fail_index = v; return ORA_ERR_NONFINITE_INPUT; }
-            if (l2_norm_f64(xv, (int)d) == 0.0) { if (fail_index) *fail_index = v; return ORA_ERR_ZERO_NORM; }
-        }
-    }
     memcpy(out, "FB2", 3);
     out[3] = 1;
     out[4] = (uint8_t)bits;
@@ -1151,32 +1202,48 @@ int ora_fib_encode_batch(uint32_t d, uint32_t k, uint32_t N, const float* cb, co
     out[14] = 0;                 /* Fp16Paper */
     put_u16(out + 15, 2);
     put_u16(out + 17, (uint16_t)ilen);
-    for (uint64_t v = 0; v < n; ++v) {
-        const float* xv = x + v * d;
-        double nrm;
-        if (n < 4) {
-            for (uint32_t i = 0; i < d; ++i)
-                if (!isfinite(xv[i])) { if (fail_index) *fail_index = v; return ORA_ERR_NONFINITE_INPUT; }
-            nrm = l2_norm_f64(xv, (int)d);
-            if (nrm == 0.0) { if (fail_index) *fail_index = v; return ORA_ERR_ZERO_NORM; }
-            for (uint32_t i = 0; i < d; ++i) xn[i] = (double)xv[i] / nrm;          /* codec.rs:481 */
+    return fib_encode_payloads(d, k, N, cb, rot, x, n, n < 4, out + 19, plen, fail_index);
+}
+
+/* One payload [norm (nlen bytes)][indices (ilen bytes)] -> d floats.
+ * f64_path = 0: decode_batch_fast (codec.rs:797-844): gather f32 codewords,
+ *   out[col] = (sum_row f32(M)[row][col] * c[row], sequential f32 from 0)
+ *   * f32(norm) with StoredRotation::apply_inverse_f32 (rotation.rs:136-149).
+ * f64_path = 1: FibQuantizer::decode (codec.rs:506-537): f64 codewords
+ *   (codebook.rs:118-131), out[col] = f32((sum_row M[row][col] * c[row],
+ *   sequential f64 from 0) * norm_f64) with apply_inverse (rotation.rs:117-128).
+ * Checks in the reference's order: index padding (bitpack.rs:47-90), index <
+ * N, decode_norm (codec.rs:1022-1047: exactly 2 bytes, finite > 0), finite
+ * output (check_finite).  m32: f32(M) row-major. */
+static int fib_decode_payload(uint32_t d, uint32_t k, uint32_t N, const float* cb, const double* rot,
+                              const float* m32, const uint8_t* p, uint32_t nlen, uint32_t ilen, int f64_path,
+                              float* o) {
+    uint32_t bits = fib_wire_bits((int)N);
+    uint32_t blocks = d / k;
+    const uint8_t* ip = p + nlen;
+    if (!padding_zero(ip, (size_t)blocks * bits, ilen)) return ORA_ERR_MALFORMED;
+    float c[256];
+    for (uint32_t b = 0; b < blocks; ++b) {
+        uint32_t w = read_bits(ip, (size_t)b * bits, (int)bits);
+        if (w >= N) return ORA_ERR_MALFORMED;
+        for (uint32_t t = 0; t < k; ++t) c[b * k + t] = cb[(size_t)w * k + t];
+    }
+    if (nlen != 2) return ORA_ERR_MALFORMED;
+    float nv = ora_f16_to_f32(get_u16(p));
+    if (!isfinite(nv) || !(nv > 0.0f)) return ORA_ERR_MALFORMED;
+    for (uint32_t col = 0; col < d; ++col) {
+        if (f64_path) {
+            double s = 0.0;
+            for (uint32_t row = 0; row < d; ++row) s += rot[(size_t)row * d + col] * (double)c[row];
+            o[col] = (float)(s * (double)nv);
         } else {
-            nrm = l2_norm_f64(xv, (int)d);
-            for (uint32_t i = 0; i < d; ++i) { xh[i] = (float)((double)xv[i] / nrm); xn[i] = (double)xh[i]; }
-        }
-        rot_apply_f64((int)d, rot, xn, yr);
-        for (uint32_t i = 0; i < d; ++i) rho[i] = (float)yr[i];
-        uint16_t h;
-        int rc = encode_norm16(nrm, &h);
-        if (rc != ORA_OK) { if (fail_index) *fail_index = v; return rc; }
-        uint8_t* p = out + 19 + v * plen;
-        memset(p, 0, plen);
-        put_u16(p, h);
-        for (uint32_t b = 0; b < blocks; ++b) {
-            int w = nearest_dispatch(rho + (size_t)b * k, cb, (int)k, (int)N);
-            write_bits(p + 2, (size_t)b * bits, (int)bits, (uint32_t)w);
+            float s = 0.0f;
+            for (uint32_t row = 0; row < d; ++row) s += m32[(size_t)row * d + col] * c[row];
+            o[col] = s * nv;
         }
     }
+    for (uint32_t col = 0; col < d; ++col)
+        if (!isfinite(o[col])) return ORA_ERR_MALFORMED;
     return ORA_OK;
 }
 
@@ -1202,32 +1269,204 @@ int ora_fib_decode_batch(uint32_t d, uint32_t k, uint32_t N, const float* cb, co
     if (ilen != (blocks * bits + 7) / 8) return ORA_ERR_MALFORMED;
     if (n_out) *n_out = n;
     if (cap_vectors < n) return ORA_ERR_CAPACITY;
-    float m32[256 * 256];
+    float* m32 = (float*)malloc(sizeof(float) * d * d);
+    if (!m32) return ORA_ERR_CAPACITY;
     for (size_t t = 0; t < (size_t)d * d; ++t) m32[t] = (float)rot[t];
-    float c[256];
+    int rc = ORA_OK;
+    for (uint64_t v = 0; v < n && rc == ORA_OK; ++v) {
+        rc = fib_decode_payload(d, k, N, cb, rot, m32, in + 19 + v * plen, nlen, ilen, 0, out + v * d);
+        if (rc != ORA_OK && fail_index) *fail_index = v;
+    }
+    free(m32);
+    return rc;
+}
+
+/* ======================================================================
+ * 9. Legacy per-vector formats behind KVecCodec::encode / decode and their
+ *    batch forms (proveKV/src/codec.rs:8-66, 339-413, 582-668):
+ *    TQW1 (turbo-quant/src/wire.rs:44-256) and compact FB1
+ *    (fib-quant/src/codec.rs:81-176).  A batch of records is given as one
+ *    byte buffer plus n + 1 offsets (record i = in[off[i] .. off[i+1])).
+ *    Parity: header layouts are pinned by the reference's own tests
+ *    (turbo-quant/tests/wire_format.rs offsets 9/15/22/38/46,
+ *    fib-quant/tests/compact_bytes_roundtrip.rs header literals) and the
+ *    payloads by the TQB1/FB2 paths; the f64 fib decode is pinned against an
+ *    exact rational evaluation (tests/test_oracle_codecs.py).
+ * ====================================================================== */
+
+/* TurboCodeWireV1::encode header (wire.rs:44-90): 46 bytes. */
+static void tqw1_header(uint8_t* h, uint32_t dim, int pbits, uint32_t proj, uint64_t seed, int mode,
+                        uint32_t plen) {
+    memcpy(h, "TQW1", 4);
+    put_u16(h + 4, 1);
+    put_u16(h + 6, 1);            /* FastHadamard (power-of-two dims) */
+    h[8] = 1;                     /* VARIANT_TURBO_CODE */
+    h[9] = 0;
+    put_u32(h + 10, dim);
+    h[14] = (uint8_t)pbits;
+    h[15] = h[16] = h[17] = 0;
+    put_u32(h + 18, proj);
+    put_u64(h + 22, seed);
+    put_u32(h + 30, dim / 2);
+    put_u32(h + 34, mode ? proj : 0);
+    put_u64(h + 38, plen);
+}
+
+uint32_t ora_tqw1_record_len(uint32_t dim, uint32_t bits, uint32_t proj, int mode) {
+    return 46 + ora_turbo_payload_len(dim, bits, proj, mode, 0);
+}
+
+/* TurboQuantAdapter::encode (proveKV/src/codec.rs:339-365) on each vector --
+ * KVecCodec::encode_batch is the trait's default loop (codec.rs:28-30).
+ * out: n records of ora_tqw1_record_len bytes; TQW1 always carries f32 radii. */
+int ora_turbo_encode_tqw1(uint32_t dim, uint32_t bits, uint32_t proj, uint64_t seed, int mode,
+                          const float* signs, const float* G, const float* x, uint64_t n, uint8_t* out,
+                          uint64_t cap, uint64_t* out_len, uint64_t* fail_index) {
+    if (!turbo_check_profile(dim, bits, proj, mode)) return ORA_ERR_INVALID_ARG;
+    int pbits = mode ? (int)bits - 1 : (int)bits;
+    uint32_t plen = turbo_payload_len(dim, pbits, proj, mode, 0);
+    uint64_t rec = 46 + (uint64_t)plen;
+    if (out_len) *out_len = n * rec;
+    if (cap < n * rec) return ORA_ERR_CAPACITY;
     for (uint64_t v = 0; v < n; ++v) {
-        const uint8_t* p = in + 19 + v * plen;
-        /* decode_norm requires exactly 2 bytes (codec.rs:1025-1031) */
-        if (nlen != 2) { if (fail_index) *fail_index = v; return ORA_ERR_MALFORMED; }
-        const uint8_t* ip = p + nlen;
-        if (!padding_zero(ip, (size_t)blocks * bits, ilen)) { if (fail_index) *fail_index = v; return ORA_ERR_MALFORMED; }
-        for (uint32_t b = 0; b < blocks; ++b) {
-            uint32_t w = read_bits(ip, (size_t)b * bits, (int)bits);
-            if (w >= N) { if (fail_index) *fail_index = v; return ORA_ERR_MALFORMED; }
-            for (uint32_t t = 0; t < k; ++t) c[b * k + t] = cb[(size_t)w * k + t];
-        }
-        float nv = ora_f16_to_f32(get_u16(p));
-        if (!isfinite(nv) || !(nv > 0.0f)) { if (fail_index) *fail_index = v; return ORA_ERR_MALFORMED; }
-        float* o = out + v * d;
-        for (uint32_t col = 0; col < d; ++col) {
-            float s = 0.0f;
-            for (uint32_t row = 0; row < d; ++row) s += m32[(size_t)row * d + col] * c[row];
-            o[col] = s * nv;
-        }
-        for (uint32_t col = 0; col < d; ++col)
-            if (!isfinite(o[col])) { if (fail_index) *fail_index = v; return ORA_ERR_MALFORMED; }
+        uint8_t* r = out + v * rec;
+        int rc = turbo_encode_payload(dim, bits, proj, mode, 0, signs, G, x + v * dim, r + 46);
+        if (rc != ORA_OK) { if (fail_index) *fail_index = v; return rc; }
+        tqw1_header(r, dim, pbits, proj, seed, mode, plen);
     }
     return ORA_OK;
+}
+
+/* TurboCodeWireV1::decode (wire.rs:100-256) + PolarQuantizer::decode
+ * (polar.rs:272-278) on each record, as TurboQuantAdapter::decode
+ * (proveKV/src/codec.rs:367-405) looped by KVecCodec::decode_batch.  Any
+ * rejection returns ORA_ERR_MALFORMED with the record's index. */
+int ora_turbo_decode_tqw1(uint32_t dim, uint32_t bits, uint32_t proj, uint64_t seed, int mode,
+                          const float* signs, const uint8_t* in, const uint64_t* off, uint64_t n, float* out,
+                          uint64_t* fail_index) {
+    if (!turbo_check_profile(dim, bits, proj, mode)) return ORA_ERR_INVALID_ARG;
+    int pbits = mode ? (int)bits - 1 : (int)bits;
+    uint32_t pairs = dim / 2;
+    uint32_t plen = turbo_payload_len(dim, pbits, proj, mode, 0);
+    uint32_t angle_bytes = (pairs * (uint32_t)pbits + 7) / 8;
+    uint32_t sign_bytes = mode ? (proj + 7) / 8 : 0;
+    float radii[128];
+    uint16_t idx[128];
+    for (uint64_t v = 0; v < n; ++v) {
+        if (fail_index) *fail_index = v;
+        if (off[v + 1] < off[v]) return ORA_ERR_MALFORMED;
+        const uint8_t* r = in + off[v];
+        uint64_t len = off[v + 1] - off[v];
+        if (len < 46) return ORA_ERR_MALFORMED;                         /* cursor reads */
+        if (memcmp(r, "TQW1", 4) != 0 || get_u16(r + 4) != 1) return ORA_ERR_MALFORMED;
+        if (get_u16(r + 6) != 1 || r[8] != 1 || r[9] != 0) return ORA_ERR_MALFORMED;
+        if (get_u32(r + 10) != dim || r[14] != pbits || get_u32(r + 18) != proj) return ORA_ERR_MALFORMED;
+        if (r[15] || r[16] || r[17]) return ORA_ERR_MALFORMED;
+        if (get_u64(r + 22) != seed) return ORA_ERR_MALFORMED;
+        if (get_u32(r + 30) != pairs || get_u32(r + 34) != (mode ? proj : 0)) return ORA_ERR_MALFORMED;
+        if (get_u64(r + 38) != plen || len != 46 + (uint64_t)plen) return ORA_ERR_MALFORMED;   /* + finish() */
+        const uint8_t* p = r + 46;
+        for (uint32_t i = 0; i < pairs; ++i) radii[i] = get_f32(p + 4 * i);
+        p += 4 * pairs;
+        if (!padding_zero(p, (size_t)pairs * pbits, angle_bytes)) return ORA_ERR_MALFORMED;
+        for (uint32_t i = 0; i < pairs; ++i) idx[i] = (uint16_t)read_bits(p, (size_t)i * pbits, pbits);
+        p += angle_bytes;
+        if (mode && !padding_zero(p, proj, sign_bytes)) return ORA_ERR_MALFORMED;
+        for (uint32_t i = 0; i < pairs; ++i)                            /* validate_for */
+            if (!isfinite(radii[i]) || radii[i] < 0.0f) return ORA_ERR_MALFORMED;
+        polar_decode(dim, signs, radii, idx, pbits, out + v * dim);
+    }
+    if (fail_index) *fail_index = 0;
+    return ORA_OK;
+}
+
+uint32_t ora_fb1_record_len(uint32_t d, uint32_t k, uint32_t N) {
+    return 11 + 2 + ((d / k) * fib_wire_bits((int)N) + 7) / 8;
+}
+
+/* FibQuantAdapter::encode (proveKV/src/codec.rs:582-594; each = 1) or
+ * encode_batch (596-610; each = 0, FibQuantizer::encode_batch semantics),
+ * then FibCodeV1::to_compact_bytes (fib-quant/src/codec.rs:81-92) per code:
+ * "FB1", version 1, wire_index_bits, block_count u32, norm_len u16, norm,
+ * indices. */
+int ora_fib_encode_fb1(uint32_t d, uint32_t k, uint32_t N, const float* cb, const double* rot, const float* x,
+                       uint64_t n, int each, uint8_t* out, uint64_t cap, uint64_t* out_len, uint64_t* fail_index) {
+    if (d == 0 || k == 0 || d % k != 0 || d > 256 || N < 2) return ORA_ERR_INVALID_ARG;
+    uint32_t bits = fib_wire_bits((int)N);
+    uint32_t plen = 2 + ((d / k) * bits + 7) / 8;
+    uint64_t rec = 11 + (uint64_t)plen;
+    if (out_len) *out_len = n * rec;
+    if (cap < n * rec) return ORA_ERR_CAPACITY;
+    if (n == 0) return ORA_OK;
+    uint8_t* pay = (uint8_t*)malloc(n * plen);
+    if (!pay) return ORA_ERR_CAPACITY;
+    int rc = fib_encode_payloads(d, k, N, cb, rot, x, n, each || n < 4, pay, plen, fail_index);
+    if (rc == ORA_OK) {
+        for (uint64_t v = 0; v < n; ++v) {
+            uint8_t* r = out + v * rec;
+            memcpy(r, "FB1", 3);
+            r[3] = 1;
+            r[4] = (uint8_t)bits;
+            put_u32(r + 5, d / k);
+            put_u16(r + 9, 2);
+            memcpy(r + 11, pay + v * plen, plen);
+        }
+    }
+    free(pay);
+    return rc;
+}
+
+/* FibCodeV1::from_compact_bytes (fib-quant/src/codec.rs:100-176): 1 if the
+ * record parses; fills the header fields. */
+static int fb1_parse(const uint8_t* r, uint64_t len, uint32_t* bits, uint32_t* blocks, uint32_t* nlen) {
+    if (len < 11) return 0;
+    if (memcmp(r, "FB1", 3) != 0 || r[3] != 1) return 0;
+    *bits = r[4];
+    *blocks = get_u32(r + 5);
+    *nlen = get_u16(r + 9);
+    if (len < 11 + (uint64_t)*nlen) return 0;
+    uint64_t ilen = len - 11 - *nlen;
+    if (ilen != ((uint64_t)*blocks * *bits + 7) / 8) return 0;
+    return 1;
+}
+
+/* FibQuantAdapter::decode (proveKV/src/codec.rs:612-637; each = 1): per
+ * record parse, FibQuantizer::decode (f64 path), first failure wins.
+ * FibQuantAdapter::decode_batch (639-665; each = 0): every record parsed
+ * first (a parse failure anywhere wins), then decode_batch_fast (f32 path)
+ * with validate_code_header (codec.rs:926-975) per code. */
+int ora_fib_decode_fb1(uint32_t d, uint32_t k, uint32_t N, const float* cb, const double* rot,
+                       const uint8_t* in, const uint64_t* off, uint64_t n, int each, float* out,
+                       uint64_t* fail_index) {
+    if (d == 0 || k == 0 || d % k != 0 || d > 256 || N < 2) return ORA_ERR_INVALID_ARG;
+    uint32_t bits_p = fib_wire_bits((int)N);
+    uint32_t blocks_p = d / k;
+    uint32_t bits, blocks, nlen;
+    if (!each) {
+        for (uint64_t v = 0; v < n; ++v) {
+            if (off[v + 1] < off[v] || !fb1_parse(in + off[v], off[v + 1] - off[v], &bits, &blocks, &nlen)) {
+                if (fail_index) *fail_index = v;
+                return ORA_ERR_MALFORMED;
+            }
+        }
+    }
+    float* m32 = (float*)malloc(sizeof(float) * d * d);
+    if (!m32) return ORA_ERR_CAPACITY;
+    for (size_t t = 0; t < (size_t)d * d; ++t) m32[t] = (float)rot[t];
+    int rc = ORA_OK;
+    for (uint64_t v = 0; v < n && rc == ORA_OK; ++v) {
+        const uint8_t* r = in + off[v];
+        if (off[v + 1] < off[v] || !fb1_parse(r, off[v + 1] - off[v], &bits, &blocks, &nlen))
+            rc = ORA_ERR_MALFORMED;
+        else if (bits != bits_p || blocks != blocks_p)                         /* validate_code_header */
+            rc = ORA_ERR_MALFORMED;
+        else if (fib_decode_payload(d, k, N, cb, rot, m32, r + 11, nlen, (blocks * bits + 7) / 8, each,
+                                    out + v * d) != ORA_OK)
+            rc = ORA_ERR_MALFORMED;
+        if (rc != ORA_OK && fail_index) *fail_index = v;
+    }
+    free(m32);
+    return rc;
 }
 
 /* ======================================================================

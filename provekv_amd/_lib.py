@@ -43,7 +43,8 @@ EXPORTS = (
     "pkv_fib_profile_create_with_constants", "pkv_profile_destroy", "pkv_turbo_constants",
     "pkv_fib_constants", "pkv_profile_constants", "pkv_payload_len", "pkv_header_len", "pkv_blob_len",
     "pkv_segments_status", "pkv_encode_segments", "pkv_decode_segments", "pkv_encode_batch_compact",
-    "pkv_decode_batch_compact", "pkv_parse_header", "pkv_host_angle_bins", "pkv_host_logf", "pkv_host_expf",
+    "pkv_decode_batch_compact", "pkv_parse_header", "pkv_record_len", "pkv_encode_vectors", "pkv_decode_vectors",
+    "pkv_host_angle_bins", "pkv_host_logf", "pkv_host_expf",
 )
 
 
@@ -115,6 +116,9 @@ def _declare(L):
         "pkv_encode_batch_compact": ([P, P, I32, P, U64, P, U64, P, P], I32),
         "pkv_decode_batch_compact": ([P, P, P, U64, P, U64, P, P], I32),
         "pkv_parse_header": ([P, P, U64, P, P], I32),
+        "pkv_record_len": ([P], U32),
+        "pkv_encode_vectors": ([P, P, I32, P, U64, P, U64, P, P], I32),
+        "pkv_decode_vectors": ([P, P, I32, P, P, U64, P, U64, P], I32),
         "pkv_host_angle_bins": ([P, P, U64, U32, P], None),
         "pkv_host_logf": ([P, U64, P], None),
         "pkv_host_expf": ([P, U64, P], None),

@@ -5,7 +5,9 @@ Mirrors proveKV/src/codec.rs: the ``KVecCodec`` trait (8-66), the
 inherent batch methods ``encode_batch_compact`` / ``decode_batch_compact``
 (TQB1 248-326, FB2 513-569), and ``create_codec`` (700-758).  Same names,
 argument meaning and error classes; the work runs in libpkv_hip.so through
-``pkv_encode_batch_compact`` / ``pkv_decode_batch_compact``.
+``pkv_encode_batch_compact`` / ``pkv_decode_batch_compact`` (batched TQB1 /
+FB2 blobs) and ``pkv_encode_vectors`` / ``pkv_decode_vectors`` (the trait's
+per-vector TQW1 / FB1 records).
 """
 from __future__ import annotations
 
@@ -156,6 +158,34 @@ class TurboQuantAdapter(KVecCodec):
         except L.PkvError as e:
             raise _wrap(e, DecompressionFailed, "turbo batched wire decode failed")
 
+    # ---- KVecCodec per-vector methods: one TQW1 record per vector
+    # (codec.rs:339-405; encode_batch / decode_batch are the trait's loops)
+    def encode(self, vector, seed: int) -> bytes:
+        return self.encode_batch([vector], seed)[0]
+
+    def encode_batch(self, vectors, seed: int) -> list:
+        x = _as_batch(vectors, self._dim)
+        prof = self._profile(seed, "encode")
+        try:
+            return prof.encode_vectors(x, each=True)
+        except L.PkvError as e:
+            raise _wrap(e, CompressionFailed, "turbo encode failed")
+
+    def decode(self, payload: bytes, seed: int) -> np.ndarray:
+        return self.decode_batch([payload], seed)[0]
+
+    def decode_batch(self, payloads, seed: int) -> np.ndarray:
+        payloads = [bytes(p) for p in payloads]
+        for i, p in enumerate(payloads):   # not TQW1 -> the reference tries its JSON envelope
+            if p[:4] != b"TQW1":
+                raise DecompressionFailed(f"turbo code deserialize failed: payload {i} is not a TQW1 record "
+                                          "(JSON-serialised codes are not supported)")
+        prof = self._profile(seed, "decode")
+        try:
+            return prof.decode_vectors(payloads, each=True)
+        except L.PkvError as e:
+            raise _wrap(e, DecompressionFailed, "turbo wire decode failed")
+
 
 class FibQuantAdapter(KVecCodec):
     """proveKV/src/codec.rs:429-693 (FB2 batch path)."""
@@ -203,6 +233,48 @@ class FibQuantAdapter(KVecCodec):
             return prof.decode_batch_compact(payload)
         except L.PkvError as e:
             raise _wrap(e, DecompressionFailed, "fib batched wire decode failed")
+
+    # ---- KVecCodec per-vector methods: one compact FB1 record per vector
+    # (codec.rs:582-665)
+    def encode(self, vector, seed: int) -> bytes:
+        x = _as_batch([vector], self._dim)
+        prof = self.build_quantizer(seed)
+        try:
+            return prof.encode_vectors(x, each=True)[0]
+        except L.PkvError as e:
+            raise _wrap(e, CompressionFailed, "fib encode failed")
+
+    def encode_batch(self, vectors, seed: int) -> list:
+        x = _as_batch(vectors, self._dim)
+        prof = self.build_quantizer(seed)
+        try:
+            return prof.encode_vectors(x, each=False)
+        except L.PkvError as e:
+            raise _wrap(e, CompressionFailed, "fib encode_batch failed")
+
+    def _check_magic(self, payloads):
+        for i, p in enumerate(payloads):   # not FB1 -> the reference tries its JSON envelope
+            if p[:3] != b"FB1":
+                raise DecompressionFailed(f"fib code deserialize failed: payload {i} is not an FB1 record "
+                                          "(JSON-serialised codes are not supported)")
+
+    def decode(self, payload: bytes, seed: int) -> np.ndarray:
+        payload = bytes(payload)
+        self._check_magic([payload])
+        prof = self.build_quantizer(seed)
+        try:
+            return prof.decode_vectors([payload], each=True)[0]
+        except L.PkvError as e:
+            raise _wrap(e, DecompressionFailed, "fib decode failed")
+
+    def decode_batch(self, payloads, seed: int) -> np.ndarray:
+        payloads = [bytes(p) for p in payloads]
+        self._check_magic(payloads)
+        prof = self.build_quantizer(seed)
+        try:
+            return prof.decode_vectors(payloads, each=False)
+        except L.PkvError as e:
+            raise _wrap(e, DecompressionFailed, "fib decode_batch_fast failed")
 
 
 def create_codec(codec_id: str, dim: int, fib_config=None, turbo_config=None) -> KVecCodec:

@@ -128,8 +128,9 @@ struct pkv_profile {
     uint32_t k = 0, n = 0, wbits = 0;
     std::vector<float> codebook, rot32t, rot32;
     std::vector<uint32_t> mf;
-    std::vector<double> rot, rot_t;
+    std::vector<double> rot, rot_t, cb64;
     float* d_cb = nullptr;
+    double* d_cb64 = nullptr;
     double* d_rot_t = nullptr;
     float* d_rot32t = nullptr;
     float* d_rot32 = nullptr;
@@ -314,6 +315,7 @@ TurboDev turbo_dev(const pkv_profile* p) {
 FibDev fib_dev(const pkv_profile* p) {
     FibDev f;
     f.codebook = p->d_cb;
+    f.codebook64 = p->d_cb64;
     f.rot_t = p->d_rot_t;
     f.rot32t = p->d_rot32t;
     f.rot32 = p->d_rot32;
@@ -372,7 +374,8 @@ int launch_fib_encode_queued(pkv_ctx* ctx, const LaunchCommon& lc, const pkv_pro
 // Caller holds ctx->mu.
 int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool encode, int dtype,
                         const void* d_f32, uint64_t f32_elems, const pkv_seg* segs, uint32_t nseg,
-                        const uint8_t* d_wire, uint64_t wire_bytes, uint32_t* d_status, hipStream_t stream) {
+                        const uint8_t* d_wire, uint64_t wire_bytes, uint32_t* d_status, hipStream_t stream,
+                        bool per_vector = false) {
     if (!ctx || !prof) return PKV_ERR_INVALID_ARG;
     if (prof->kind == PKV_CODEC_TURBO && radii != PKV_RADII_F32 && radii != PKV_RADII_LOG_U8)
         return PKV_ERR_INVALID_ARG;
@@ -399,6 +402,7 @@ int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool e
     lc.radii = static_cast<uint32_t>(radii);
     lc.plen = prof->kind == PKV_CODEC_TURBO ? turbo_plen(prof, radii) : fib_plen(prof);
     lc.in_bf16 = dtype == PKV_BF16 ? 1u : 0u;
+    lc.per_vector = per_vector ? 1u : 0u;
     const uint32_t nblocks = tiles[nseg];
     int e;
     if (prof->kind == PKV_CODEC_TURBO) {
@@ -435,12 +439,13 @@ int ensure_scratch(pkv_ctx* ctx, size_t bytes) {
     return PKV_OK;
 }
 
-int resolve_status(const pkv_profile* p, const uint32_t* st, uint32_t nseg, const pkv_seg* segs, pkv_error* err) {
+int resolve_status(const pkv_profile* p, const uint32_t* st, uint32_t nseg, const pkv_seg* segs, pkv_error* err,
+                   bool per_vector = false) {
     for (uint32_t s = 0; s < nseg; ++s) {
         uint32_t w0 = st[2 * s], w1 = st[2 * s + 1];
         if (w0 == STATUS_NONE && w1 == STATUS_NONE) continue;
         uint32_t pick;
-        if (p->kind == PKV_CODEC_FIB && segs && segs[s].n_vectors >= 4)
+        if (p->kind == PKV_CODEC_FIB && segs && segs[s].n_vectors >= 4 && !per_vector)
             pick = w0 != STATUS_NONE ? w0 : w1;   // batch validation precedes norm encoding
         else
             pick = std::min(w0, w1);              // per-vector order
@@ -471,6 +476,77 @@ uint32_t rd32(const uint8_t* b) {
            (static_cast<uint32_t>(b[3]) << 24);
 }
 uint64_t rd64(const uint8_t* b) { return rd32(b) | (static_cast<uint64_t>(rd32(b + 4)) << 32); }
+
+// ---- legacy per-vector records: TQW1 (turbo-quant/src/wire.rs:44-98) and
+// compact FB1 (fib-quant/src/codec.rs:81-92).  Every header field is fixed by
+// the profile, so a record is a constant header followed by the payload the
+// batched path writes (TQW1 always carries f32 radii).
+uint32_t record_hdr_len(const pkv_profile* p) { return p->kind == PKV_CODEC_TURBO ? 46u : 11u; }
+
+uint32_t record_plen(const pkv_profile* p) {
+    return p->kind == PKV_CODEC_TURBO ? turbo_plen(p, PKV_RADII_F32) : fib_plen(p);
+}
+
+struct ByteWriter {
+    HdrBytes h{};
+    void put(uint32_t i, uint32_t v) { h.w[i >> 2] |= (v & 0xffu) << (8 * (i & 3)); }
+    void put16(uint32_t i, uint32_t v) { put(i, v); put(i + 1, v >> 8); }
+    void put32(uint32_t i, uint32_t v) { for (uint32_t k = 0; k < 4; ++k) put(i + k, v >> (8 * k)); }
+    void put64(uint32_t i, uint64_t v) { put32(i, static_cast<uint32_t>(v)); put32(i + 4, static_cast<uint32_t>(v >> 32)); }
+};
+
+HdrBytes record_header(const pkv_profile* p) {
+    ByteWriter b;
+    if (p->kind == PKV_CODEC_TURBO) {
+        b.put(0, 'T'); b.put(1, 'Q'); b.put(2, 'W'); b.put(3, '1');
+        b.put16(4, 1);                       // VERSION
+        b.put16(6, 1);                       // rotation flag: FastHadamard (power-of-two dims)
+        b.put(8, 1);                         // VARIANT_TURBO_CODE
+        b.put32(10, p->dim);
+        b.put(14, p->pbits);
+        b.put32(18, p->proj);                // profile.projections(), also without QJL
+        b.put64(22, p->seed);
+        b.put32(30, p->dim / 2);             // polar block count
+        b.put32(34, p->mode ? p->proj : 0);  // QJL sign count
+        b.put64(38, turbo_plen(p, PKV_RADII_F32));
+    } else {
+        b.put(0, 'F'); b.put(1, 'B'); b.put(2, '1');
+        b.put(3, 1);                         // COMPACT_VERSION
+        b.put(4, p->wbits);
+        b.put32(5, p->dim / p->k);           // block_count
+        b.put16(9, 2);                       // fp16 norm length
+    }
+    return b.h;
+}
+
+// Header of the batched blob the records are reshaped into (TQB1 with f32
+// radii, wire.rs:267-346; FB2, codec.rs:195-320).
+HdrBytes blob_header(const pkv_profile* p, uint64_t n) {
+    ByteWriter b;
+    if (p->kind == PKV_CODEC_TURBO) {
+        b.put(0, 'T'); b.put(1, 'Q'); b.put(2, 'B'); b.put(3, '1');
+        b.put16(4, 1);
+        b.put16(6, 1);
+        b.put(8, 2);
+        b.put32(10, p->dim);
+        b.put(14, p->pbits);
+        b.put32(18, p->proj);
+        b.put64(22, p->seed);
+        b.put32(30, static_cast<uint32_t>(n));
+        b.put32(34, turbo_plen(p, PKV_RADII_F32));
+    } else {
+        b.put(0, 'F'); b.put(1, 'B'); b.put(2, '2');
+        b.put(3, 1);
+        b.put(4, p->wbits);
+        b.put32(6, p->dim / p->k);
+        b.put32(10, static_cast<uint32_t>(n));
+        b.put16(15, 2);
+        b.put16(17, fib_plen(p) - 2);
+    }
+    return b.h;
+}
+
+uint64_t pad256(uint64_t v) { return (v + 255) & ~static_cast<uint64_t>(255); }
 
 }  // namespace
 
@@ -778,8 +854,10 @@ static int fib_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n
             p->rot_t[static_cast<size_t>(c) * dim + r] = p->rot[static_cast<size_t>(r) * dim + c];
         }
     fib_mfma_constants(p);
+    p->cb64.assign(p->codebook.begin(), p->codebook.end());   // f64::from(f32), codebook.rs:118-131
     int rc = hip_status(hipSetDevice(ctx->device));
     if (!rc) rc = upload(&p->d_cb, p->codebook);
+    if (!rc) rc = upload(&p->d_cb64, p->cb64);
     if (!rc) rc = upload(&p->d_rot_t, p->rot_t);
     if (!rc) rc = upload(&p->d_rot32t, p->rot32t);
     if (!rc) rc = upload(&p->d_mf, p->mf);
@@ -837,7 +915,7 @@ void pkv_profile_destroy(pkv_profile* p) {
     for (void* d : {static_cast<void*>(p->d_signs), static_cast<void*>(p->d_qjl), static_cast<void*>(p->d_cs),
                     static_cast<void*>(p->d_qa), static_cast<void*>(p->d_qb),
                     static_cast<void*>(p->d_cb), static_cast<void*>(p->d_rot_t), static_cast<void*>(p->d_rot32t),
-                    static_cast<void*>(p->d_mf), static_cast<void*>(p->d_rot32)})
+                    static_cast<void*>(p->d_mf), static_cast<void*>(p->d_rot32), static_cast<void*>(p->d_cb64)})
         if (d) (void)hipFree(d);
     delete p;
 }
@@ -988,6 +1066,107 @@ int pkv_decode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, const uint8_
     HIP_TRY(hipMemcpyAsync(out, d_out, out_bytes, hipMemcpyDeviceToHost, st));
     HIP_TRY(hipStreamSynchronize(st));
     return resolve_status(prof, hs, 1, &seg, err);
+}
+
+uint32_t pkv_record_len(const pkv_profile* prof) { return prof ? record_hdr_len(prof) + record_plen(prof) : 0; }
+
+int pkv_encode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const float* vectors, uint64_t n,
+                       uint8_t* out, uint64_t out_cap, uint64_t* out_len, pkv_error* err) {
+    if (err) { err->status = PKV_OK; err->segment = -1; err->index = 0; }
+    if (!ctx || !prof || (!vectors && n)) return PKV_ERR_INVALID_ARG;
+    const uint32_t plen = record_plen(prof), rh = record_hdr_len(prof), hdr = hdr_len(prof);
+    const uint64_t rec_bytes = n * (static_cast<uint64_t>(rh) + plen);
+    if (out_len) *out_len = rec_bytes;
+    if (n == 0) return PKV_OK;                    // Ok(vec![]) (codec.rs:28-30, 596-610)
+    if (n > MAX_SEG_VECTORS) return PKV_ERR_INVALID_ARG;
+    if (!out || out_cap < rec_bytes) return PKV_ERR_CAPACITY;
+    const uint64_t in_bytes = n * prof->dim * sizeof(float);
+    const uint64_t blob = hdr + n * static_cast<uint64_t>(plen);
+    const uint64_t o_in = 0, o_blob = pad256(in_bytes), o_rec = o_blob + pad256(blob + 4);
+    const uint64_t o_st = o_rec + pad256(rec_bytes + 4);
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    int rc = ensure_scratch(ctx, o_st + 256);
+    if (rc) return rc;
+    auto* base = static_cast<uint8_t*>(ctx->scratch);
+    uint8_t* d_blob = base + o_blob;
+    uint32_t* d_stat = reinterpret_cast<uint32_t*>(base + o_st);
+    hipStream_t st = ctx->own_stream;
+    HIP_TRY(hipMemcpyAsync(base + o_in, vectors, in_bytes, hipMemcpyHostToDevice, st));
+    pkv_seg seg{0, 0, prof->dim, 0, static_cast<uint32_t>(n), static_cast<uint32_t>(n)};
+    const bool per_vector = each != 0 && prof->kind == PKV_CODEC_FIB;
+    rc = run_segments_locked(ctx, prof, PKV_RADII_F32, true, PKV_F32, base + o_in, n * prof->dim, &seg, 1, d_blob,
+                             blob, d_stat, st, per_vector);
+    if (rc) { (void)hipStreamSynchronize(st); return rc; }
+    int e = launch_records_pack(d_blob + hdr, base + o_rec, n, plen, rh, record_header(prof), st);
+    if (e) { (void)hipStreamSynchronize(st); return hip_status(static_cast<hipError_t>(e)); }
+    uint32_t hs[2];
+    HIP_TRY(hipMemcpyAsync(hs, d_stat, sizeof hs, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(out, base + o_rec, rec_bytes, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    return resolve_status(prof, hs, 1, &seg, err, per_vector);
+}
+
+int pkv_decode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const uint8_t* records,
+                       const uint64_t* offsets, uint64_t n, float* out, uint64_t out_cap_vectors, pkv_error* err) {
+    if (err) { err->status = PKV_OK; err->segment = -1; err->index = 0; }
+    if (!ctx || !prof || (n && (!offsets || !records))) return PKV_ERR_INVALID_ARG;
+    if (n == 0) return PKV_OK;
+    if (n > MAX_SEG_VECTORS) return PKV_ERR_INVALID_ARG;
+    if (!out || out_cap_vectors < n) return PKV_ERR_CAPACITY;
+    const uint32_t plen = record_plen(prof), rh = record_hdr_len(prof), hdr = hdr_len(prof);
+    const uint32_t rec_len = rh + plen;
+    bool packed = offsets[0] == 0;   // record i at i * rec_len: every valid batch
+    for (uint64_t i = 0; i < n; ++i) {
+        if (offsets[i + 1] < offsets[i]) return PKV_ERR_INVALID_ARG;
+        packed = packed && offsets[i + 1] - offsets[i] == rec_len;
+    }
+    const uint64_t total = offsets[n];
+    const uint64_t blob = hdr + n * static_cast<uint64_t>(plen);
+    const uint64_t out_bytes = n * prof->dim * sizeof(float);
+    const uint64_t o_out = 0, o_rec = pad256(out_bytes), o_off = o_rec + pad256(total + 4);
+    const uint64_t o_blob = o_off + pad256(8 * (n + 1)), o_st = o_blob + pad256(blob + 4);
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    int rc = ensure_scratch(ctx, o_st + 256);
+    if (rc) return rc;
+    auto* base = static_cast<uint8_t*>(ctx->scratch);
+    const uint8_t* d_rec = base + o_rec;
+    const uint64_t* d_off = reinterpret_cast<const uint64_t*>(base + o_off);
+    uint8_t* d_blob = base + o_blob;
+    uint32_t* d_stat = reinterpret_cast<uint32_t*>(base + o_st);   // [0, 1] decode, [2, 3] records
+    hipStream_t st = ctx->own_stream;
+    if (total) HIP_TRY(hipMemcpyAsync(base + o_rec, records, total, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(base + o_off, offsets, 8 * (n + 1), hipMemcpyHostToDevice, st));
+    const bool fib = prof->kind == PKV_CODEC_FIB;
+    int e = launch_fill_u32(d_stat, STATUS_NONE, 4, st);
+    if (!e)
+        e = launch_records_check(d_rec, d_off, n, rec_len, rh, fib ? 1u : 0u, packed, record_header(prof), d_stat + 2,
+                                 st);
+    if (!e) e = launch_records_gather(d_rec, d_off, n, rec_len, rh, packed, d_blob, hdr, blob_header(prof, n), plen, st);
+    if (e) { (void)hipStreamSynchronize(st); return hip_status(static_cast<hipError_t>(e)); }
+    pkv_seg seg{0, 0, prof->dim, 0, static_cast<uint32_t>(n), static_cast<uint32_t>(n)};
+    if (fib && each) {   // FibQuantizer::decode: f64 inverse rotation
+        e = launch_fib_decode_f64(fib_dev(prof), d_blob + hdr, n, plen, reinterpret_cast<float*>(base + o_out),
+                                  d_stat, st);
+        if (e) { (void)hipStreamSynchronize(st); return hip_status(static_cast<hipError_t>(e)); }
+    } else {
+        rc = run_segments_locked(ctx, prof, PKV_RADII_F32, false, PKV_F32, base + o_out, n * prof->dim, &seg, 1,
+                                 d_blob, blob, d_stat, st);
+        if (rc) { (void)hipStreamSynchronize(st); return rc; }
+    }
+    uint32_t hs[4];
+    HIP_TRY(hipMemcpyAsync(hs, d_stat, sizeof hs, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(out, base + o_out, out_bytes, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    // FibQuantAdapter::decode_batch parses every record before decoding any
+    // (codec.rs:639-665); per-record decoding stops at the first failure.
+    uint32_t pick = std::min(std::min(hs[0], hs[1]), hs[3]);
+    if (fib && !each && hs[2] != STATUS_NONE) pick = hs[2];
+    else pick = std::min(pick, hs[2]);
+    if (pick == STATUS_NONE) return PKV_OK;
+    if (err) { err->status = PKV_ERR_CORRUPT_PAYLOAD; err->segment = 0; err->index = pick >> 4; }
+    return PKV_ERR_CORRUPT_PAYLOAD;
 }
 
 int pkv_turbo_constants(uint32_t dim, uint32_t projections, uint64_t seed, float* signs, float* qjl) {

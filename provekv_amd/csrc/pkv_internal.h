@@ -74,6 +74,7 @@ constexpr uint32_t fib_mfma_row(uint32_t t, uint32_t m) {
 
 struct FibDev {
     const float* codebook;  // n * k
+    const double* codebook64;  // n * k, the same values widened (per-vector f64 decode)
     const double* rot_t;    // dim * dim, transposed: [col][row] (exact encode fixup)
     const float* rot32t;    // dim * dim, f32(rot) transposed: [col][row] (VALU decode)
     const float* rot32;     // dim * dim, f32(rot) row-major (MFMA decode)
@@ -101,6 +102,13 @@ struct LaunchCommon {
     uint32_t radii;               // turbo radii codec
     uint32_t plen;                // payload bytes per vector
     uint32_t in_bf16;             // encode input dtype
+    uint32_t per_vector;          // fib encode: FibQuantizer::encode semantics for every vector
+};
+
+// Up to 48 constant header bytes (TQW1 / FB1 record headers, TQB1 / FB2 blob
+// headers), little-endian packed, passed to kernels by value.
+struct HdrBytes {
+    uint32_t w[12];
 };
 
 // Host-side profile construction (pkv_profile.cpp).
@@ -122,5 +130,19 @@ int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* w
                       uint32_t nblocks, void* stream);
 int launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, void* stream);
 int launch_fib_product_check(const float* rot32, const float* cb, uint32_t* bad, void* stream);
+
+// Legacy per-vector records (pkv_records.hip).  Records are rec_hdr header
+// bytes + one payload; a batch is a byte buffer plus n + 1 offsets.
+int launch_records_pack(const uint8_t* pay, uint8_t* out, uint64_t n, uint32_t plen, uint32_t rec_hdr,
+                        const HdrBytes& hdr, void* stream);
+// packed: record i starts at i * rec_len (no offset table reads); the record
+// buffer is then 4-byte aligned.  Rejections go to status[0] / status[1].
+int launch_records_check(const uint8_t* rec, const uint64_t* off, uint64_t n, uint32_t rec_len, uint32_t rec_hdr,
+                         uint32_t fb1, bool packed, const HdrBytes& hdr, uint32_t* status, void* stream);
+int launch_records_gather(const uint8_t* rec, const uint64_t* off, uint64_t n, uint32_t rec_len, uint32_t rec_hdr,
+                          bool packed, uint8_t* blob, uint32_t blob_hdr, const HdrBytes& bhdr, uint32_t plen,
+                          void* stream);
+int launch_fib_decode_f64(const FibDev& fd, const uint8_t* pay, uint64_t n, uint32_t plen, float* out,
+                          uint32_t* status, void* stream);
 
 }  // namespace pkv

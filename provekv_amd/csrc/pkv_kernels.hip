@@ -1200,7 +1200,7 @@ __device__ __forceinline__ void fib_encode_score(const LaunchCommon& lc, const S
     const int h = lane >> 5, n = lane & 31;
     const uint32_t nv = min(32u, seg.n_vectors - v0);
     const bool active = static_cast<uint32_t>(n) < nv;   // other lanes repeat the last vector
-    const bool small = seg.n_vectors < 4;
+    const bool small = seg.n_vectors < 4 || lc.per_vector != 0;
     const v16f& acc0 = t.acc0;
     const v16f& acc1 = t.acc1;
     const double nrm = t.nrm;
@@ -1375,7 +1375,7 @@ __global__ __launch_bounds__(TILE) void fib_fixup_kernel(LaunchCommon lc, const 
     const uint32_t count = min(head.x, TILE);
     if (count == 0) return;
     const SegDev seg = lc.segs[head.y];
-    const bool small = seg.n_vectors < 4;
+    const bool small = seg.n_vectors < 4 || lc.per_vector != 0;
     const uint32_t tile_v0 = head.z;
     const uint32_t* ents = rq.entries + static_cast<uint64_t>(tb) * TILE;
     for (uint32_t g0 = 0; g0 < count; g0 += G) {

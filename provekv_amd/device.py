@@ -257,6 +257,46 @@ class Profile:
         return out[: n_out.value]
 
 
+    # ---- per-vector records (TQW1 / FB1): the KVecCodec trait's own methods
+    def record_len(self) -> int:
+        return int(L.lib().pkv_record_len(self._ptr))
+
+    def encode_vectors(self, vectors: np.ndarray, each: bool) -> list:
+        """n vectors -> n TQW1 / FB1 records (``each``: FibQuantizer::encode per
+        vector; otherwise encode_batch semantics)."""
+        x = np.ascontiguousarray(vectors, dtype=np.float32)
+        if x.ndim != 2 or x.shape[1] != self.dim:
+            raise L.PkvError(L.ERR_DIM_MISMATCH, "encode_vectors")
+        n = x.shape[0]
+        rec = self.record_len()
+        out = np.zeros(max(n * rec, 1), np.uint8)
+        out_len = C.c_uint64()
+        err = L.Error()
+        rc = L.lib().pkv_encode_vectors(self.ctx.ptr, self._ptr, int(each), x.ctypes.data if n else None, n,
+                                        out.ctypes.data, n * rec, C.byref(out_len), C.byref(err))
+        if rc:
+            raise L.PkvError(rc, "encode_vectors", err.segment, err.index)
+        b = out.tobytes()
+        return [b[i * rec:(i + 1) * rec] for i in range(n)]
+
+    def decode_vectors(self, records, each: bool) -> np.ndarray:
+        """TQW1 / FB1 records -> [n, dim] f32 (``each``: FibQuantizer::decode,
+        f64 rotation; otherwise decode_batch semantics)."""
+        records = [bytes(r) for r in records]
+        n = len(records)
+        off = np.zeros(n + 1, np.uint64)
+        if n:
+            off[1:] = np.cumsum([len(r) for r in records], dtype=np.uint64)
+        buf = np.frombuffer(b"".join(records) or b"\0", dtype=np.uint8)
+        out = np.zeros((max(n, 1), self.dim), np.float32)
+        err = L.Error()
+        rc = L.lib().pkv_decode_vectors(self.ctx.ptr, self._ptr, int(each), buf.ctypes.data, off.ctypes.data, n,
+                                        out.ctypes.data, n, C.byref(err))
+        if rc:
+            raise L.PkvError(rc, "decode_vectors", err.segment, err.index)
+        return out[:n]
+
+
 # ---------------------------------------------------------------- host only
 def turbo_constants(dim: int, projections: int, seed: int):
     signs = np.zeros(dim, np.float32)
