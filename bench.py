@@ -4,11 +4,13 @@ Default workload: the SmolLM2-1.7B-shape N=8 pool --
 24 layers x 32 KV heads x head_dim 64, an 800-token shared prefix in the
 fib_k4_n32 cold tier (FB2) and 8 agents x 28 unique tokens in the turbo b=4
 hot tier (TQB1, lossless radii).  One step = build the pool + all 8 shells
-(encode: 2 launches) and rehydrate the pool once and every shell (decode:
-2 launches), inputs resident in HBM.
+(encode: 2 launches) and rehydrate all 8 agents' full 1024-token KV -- pool
+and every shell, decoded once and written to each agent's cache -- straight
+into HuggingFace-layout KV caches ([1, H, T, D] per layer and K|V, f32;
+decode: 2 launches; 3,221,225,472 B written), inputs resident in HBM.
 
-value = f32 KV bytes of the context (402,653,184 B) / the GPU time of one step
-(events at the two ends of K back-to-back steps).  kernels_ms: a second pass
+value = f32 KV bytes of the context (402,653,184 B, the metric's "f32 in") /
+the GPU time of one step (events at the two ends of K back-to-back steps).  kernels_ms: a second pass
 with events between the four calls.
 roofline = the dominant kernel's algorithmic bytes per launch / its mean
 duration (HIP events on the launch stream) against 8 TB/s.
@@ -75,10 +77,31 @@ def cpu_baseline(corpus: np.ndarray, plan, budget_s: float = 16.0) -> dict:
             "encode_decode_s_projected": round(total_s, 2)}
 
 
+def spot_check_cache(plan, bufs, cache, corpus):
+    """Parity spot check of the rehydrated cache against the oracle on one
+    pool blob and one shell blob (layer 0, K): the cache rows must be the
+    oracle decode (rounded to the cache dtype) in every copy."""
+    import torch
+    from oracle import oracle as O
+    cb, rot = plan.fib.constants()
+    cb, rot = cb.reshape(32, 4), rot.reshape(plan.dim, plan.dim)
+    heads, dim = plan.heads, plan.dim
+    checks = [(0, plan.prefix, O.fib_decode_batch(plan.blob(bufs, "pool", 0), cb, rot))]
+    checks.append((plan.prefix, plan.agent_tokens[0],
+                   O.turbo_decode_batch(plan.blob(bufs, "shell", 0), dim, plan.fib.params["seed"])))
+    for t0, nt, dec in checks:
+        want = torch.from_numpy(np.ascontiguousarray(dec.reshape(nt, heads, dim).transpose(1, 0, 2)))
+        want = want.to(cache.buf.dtype)
+        for c in range(cache.copies):
+            got = cache.buf[c, 0, 0, :, t0:t0 + nt, :].cpu()
+            if not torch.equal(got, want):
+                raise AssertionError(f"rehydrated cache differs from the oracle (copy {c}, tokens {t0}..)")
+
+
 # the kernel each timed span is about (fib_encode's span also holds the exact
 # fixup kernel, turbo/fib spans a status fill of a few microseconds)
 KERNEL_SYMBOL = {"fib_encode": "fib_encode_kernel<64>", "turbo_encode": "turbo_encode_qjl_kernel<3>",
-                 "fib_decode": "fib_decode_mfma_kernel<64>", "turbo_decode": "turbo_decode_split_kernel<3>"}
+                 "fib_decode": "fib_decode_mfma_kernel<64, true>", "turbo_decode": "turbo_decode_split_kernel<3>"}
 SINGLE_KERNEL = ("fib_decode", "turbo_encode", "turbo_decode")
 
 
@@ -197,9 +220,16 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a 256 MiB device copy (reference kernel for rocprofv3 --pmc byte counters)")
+    ap.add_argument("--cache-dtype", choices=("f32", "bf16", "f16"), default="f32",
+                    help="dtype of the KV cache the rehydrate writes (default f32, the metric's)")
+    ap.add_argument("--copies", type=int, default=8,
+                    help="KV caches filled from one decode: config 3 rehydrates all 8 agents' full 1024-token "
+                         "KV (default 8)")
     ap.add_argument("--workload", choices=("pool", "legacy"), default="pool",
                     help="pool: the config-3 metric (default); legacy: per-vector TQW1 / FB1 records")
     args = ap.parse_args()
+    if args.copies == 1:   # one cache: the fib decode stores directly (no LDS staging)
+        KERNEL_SYMBOL["fib_decode"] = "fib_decode_mfma_kernel<64, false>"
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1",
                           "n_gpus": args.gpus}), flush=True)
@@ -211,7 +241,7 @@ def main():
     import torch
     from provekv_amd import synth
     from provekv_amd.device import default_context
-    from provekv_amd.pool import TwoTierPlan
+    from provekv_amd.pool import DeviceKVCache, TwoTierPlan
 
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU"}))
@@ -223,32 +253,39 @@ def main():
     log("[bench] building profiles (fib codebook + rotation, turbo signs + QJL)")
     plan = TwoTierPlan(ctx, layers, heads, dim, prefix, agents, seed=42, lossy=args.lossy)
     bufs = plan.alloc()
+    cache_dtype = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[args.cache_dtype]
+    cache = DeviceKVCache(layers, heads, plan.tokens, dim, dtype=cache_dtype, copies=args.copies)
     dev = torch.from_numpy(corpus.reshape(-1)).cuda()
     stream = torch.cuda.current_stream()
 
     def step(evs=None):
         if evs is None:
             plan.encode(dev, bufs)
-            plan.decode(bufs)
+            plan.rehydrate(bufs, cache)
             return
         e = evs
+        pseg, sseg = plan._cache_segs
+        out = cache.buf.view(-1)
         e[0].record(stream)
         plan.fib.encode_segments(dev, plan.pool.enc, bufs["pool_wire"], status=bufs["pool_status"])
         e[1].record(stream)
         plan.turbo.encode_segments(dev, plan.shells.enc, bufs["shell_wire"], radii=plan.radii,
                                    status=bufs["shell_status"])
         e[2].record(stream)
-        plan.fib.decode_segments(bufs["pool_wire"], plan.pool.dec, bufs["pool_out"], status=bufs["pool_dstatus"])
+        plan.fib.decode_segments(bufs["pool_wire"], pseg, out, status=bufs["pool_cstatus"], fanout=cache.copies,
+                                 fanout_stride=cache.copy_stride)
         e[3].record(stream)
-        plan.turbo.decode_segments(bufs["shell_wire"], plan.shells.dec, bufs["shell_out"], radii=plan.radii,
-                                   status=bufs["shell_dstatus"])
+        plan.turbo.decode_segments(bufs["shell_wire"], sseg, out, radii=plan.radii, status=bufs["shell_cstatus"],
+                                   fanout=cache.copies, fanout_stride=cache.copy_stride)
         e[4].record(stream)
 
     log(f"[bench] warmup {args.warmup}")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    plan.check(bufs)
+    plan.check(bufs, decode=False)
+    plan.check_rehydrate(bufs)
+    spot_check_cache(plan, bufs, cache, corpus)
     # timed region: K whole steps, events only at its two ends
     log(f"[bench] timing {args.steps} steps")
     t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -261,7 +298,8 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     step_gpu_ms = t_start.elapsed_time(t_end) / args.steps
-    plan.check(bufs)
+    plan.check(bufs, decode=False)
+    plan.check_rehydrate(bufs)
     # per-op breakdown from a separate pass with events between the launches
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
     torch.cuda.synchronize()
@@ -277,8 +315,9 @@ def main():
     f32_shell = n_shell * dim * 4
     wire_pool = plan.pool.wire_bytes
     wire_shell = plan.shells.wire_bytes
+    out_scale = args.copies * cache.buf.element_size() / 4   # cache bytes written per f32 input byte
     alg = {"fib_encode": f32_pool + wire_pool, "turbo_encode": f32_shell + wire_shell,
-           "fib_decode": f32_pool + wire_pool, "turbo_decode": f32_shell + wire_shell}
+           "fib_decode": int(f32_pool * out_scale) + wire_pool, "turbo_decode": int(f32_shell * out_scale) + wire_shell}
     kern_gbs = {n: alg[n] / (per[n] * 1e-3) / 1e9 for n in names}
     step_ms = wall / args.steps * 1e3
     f32_total = f32_pool + f32_shell
@@ -302,9 +341,11 @@ def main():
         "data": "synthetic (seeded log-normal K with outlier channels, Gaussian V)",
         "config": {"workload": "config3: N=8 two-tier pool, 24L x 32H x d64, 800-token fib_k4_n32 prefix + "
                                "8 x 28-token turbo b=4 shells" + (" (TQB1-L lossy radii)" if args.lossy else
-                                                                  " (TQB1 lossless radii)"),
+                                                                  " (TQB1 lossless radii)") +
+                               f", rehydrated into {args.copies} x [1,H,T,D] {args.cache_dtype} KV cache(s)",
                    "layers": layers, "kv_heads": heads, "head_dim": dim, "prefix_tokens": prefix,
-                   "agents": len(agents), "agent_tokens": agents[0], "seed": 42},
+                   "agents": len(agents), "agent_tokens": agents[0], "seed": 42,
+                   "cache_dtype": args.cache_dtype, "cache_copies": args.copies},
         "hbm_fraction_codec": round(total_alg / (step_gpu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "kernels_ms": {n: round(per[n], 4) for n in names},
         "kernels_gbs": {n: round(kern_gbs[n], 1) for n in names},
@@ -314,6 +355,7 @@ def main():
                      "traffic": profiled_traffic(dom),
                      "algorithmic_bytes": alg[dom]},
         "compressed_bytes": plan.compressed_bytes(),
+        "rehydrated_bytes": cache.buf.numel() * cache.buf.element_size(),
     }
     # STREAM-style copy: the achievable HBM bandwidth on this box
     src = torch.empty(1 << 28, dtype=torch.uint8, device="cuda")

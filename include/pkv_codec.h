@@ -70,7 +70,7 @@ int pkv_device_available(void);
 enum pkv_codec_kind { PKV_CODEC_TURBO = 1, PKV_CODEC_FIB = 2 };
 enum pkv_turbo_mode { PKV_TURBO_POLAR_ONLY = 0, PKV_TURBO_POLAR_WITH_QJL = 1 };
 enum pkv_radii_codec { PKV_RADII_F32 = 0, PKV_RADII_LOG_U8 = 1 };
-enum pkv_dtype { PKV_F32 = 0, PKV_BF16 = 1 };
+enum pkv_dtype { PKV_F32 = 0, PKV_BF16 = 1, PKV_F16 = 2 };
 
 /* Replaces TurboQuantizer::new_with_mode (turbo-quant/src/turbo.rs:124-188)
  * as built by TurboQuantAdapter (proveKV/src/codec.rs:249-250): FastHadamard
@@ -166,6 +166,28 @@ int pkv_decode_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec,
                         const uint8_t* d_wire, uint64_t wire_bytes, const pkv_seg* segs,
                         uint32_t nseg, float* d_out, uint64_t out_elems, uint32_t* d_status,
                         void* stream);
+
+/* Decode straight into a framework KV-cache layout.  Same as
+ * pkv_decode_segments, plus:
+ *   out_dtype  PKV_F32, PKV_BF16 or PKV_F16: the f32 decode rounded to nearest
+ *              even, the conversion the reference harness applies when it
+ *              patches decoded K/V into a bf16 / fp16 HuggingFace cache
+ *              (`torch.tensor(..., dtype=k.dtype)`,
+ *              proveKV/scripts/ppl_validate_multi_agent.py:226-272);
+ *   fanout     every decoded vector is written `fanout` times, copy k at
+ *              element offset + k * fanout_stride: one decode of the shared
+ *              pool feeds the caches of several agents (rehydrate fan-out).
+ * With group = H, stride_outer = D, stride_inner = T * D a segment writes a
+ * layer's [1, H, T, D] K or V tensor at token offset elem_offset / D: the
+ * re-layout of flatten_heads_tokens (proveKV/src/pool.rs:19-33) and the cache
+ * patch fused into the decode.  Offsets, strides and fanout_stride are
+ * multiples of 4 elements; d_out is 16-byte aligned; out_elems counts
+ * elements of out_dtype. */
+int pkv_decode_segments_ex(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec,
+                           const uint8_t* d_wire, uint64_t wire_bytes, const pkv_seg* segs,
+                           uint32_t nseg, void* d_out, int out_dtype, uint64_t out_elems,
+                           uint32_t fanout, uint64_t fanout_stride, uint32_t* d_status,
+                           void* stream);
 
 /* ---------------------------------------------------------------- host-buffer
  * Drop-ins for the adapters' inherent batch methods: host slices in, wire

@@ -35,6 +35,7 @@ RADII_F32 = 0
 RADII_LOG_U8 = 1
 DT_F32 = 0
 DT_BF16 = 1
+DT_F16 = 2
 
 # every symbol include/pkv_codec.h declares
 EXPORTS = (
@@ -42,7 +43,8 @@ EXPORTS = (
     "pkv_turbo_profile_create", "pkv_turbo_profile_create_with_constants", "pkv_fib_profile_create",
     "pkv_fib_profile_create_with_constants", "pkv_profile_destroy", "pkv_turbo_constants",
     "pkv_fib_constants", "pkv_profile_constants", "pkv_payload_len", "pkv_header_len", "pkv_blob_len",
-    "pkv_segments_status", "pkv_encode_segments", "pkv_decode_segments", "pkv_encode_batch_compact",
+    "pkv_segments_status", "pkv_encode_segments", "pkv_decode_segments", "pkv_decode_segments_ex",
+    "pkv_encode_batch_compact",
     "pkv_decode_batch_compact", "pkv_parse_header", "pkv_record_len", "pkv_encode_vectors", "pkv_decode_vectors",
     "pkv_host_angle_bins", "pkv_host_logf", "pkv_host_expf",
 )
@@ -113,6 +115,7 @@ def _declare(L):
         "pkv_segments_status": ([P, P, U32, P], I32),
         "pkv_encode_segments": ([P, P, I32, I32, P, U64, P, U32, P, U64, P, P], I32),
         "pkv_decode_segments": ([P, P, I32, P, U64, P, U32, P, U64, P, P], I32),
+        "pkv_decode_segments_ex": ([P, P, I32, P, U64, P, U32, P, I32, U64, U32, U64, P, P], I32),
         "pkv_encode_batch_compact": ([P, P, I32, P, U64, P, U64, P, P], I32),
         "pkv_decode_batch_compact": ([P, P, P, U64, P, U64, P, P], I32),
         "pkv_parse_header": ([P, P, U64, P, P], I32),

@@ -187,10 +187,16 @@ bool seg_extent(const pkv_seg& s, uint32_t dim, uint64_t* end) {
 
 int validate_segments(const pkv_profile* p, int radii, bool encode, int dtype, const void* d_f32,
                       uint64_t f32_elems, const pkv_seg* segs, uint32_t nseg, const void* d_wire,
-                      uint64_t wire_bytes, std::vector<uint32_t>& tile_start) {
+                      uint64_t wire_bytes, std::vector<uint32_t>& tile_start, uint32_t fanout = 1,
+                      uint64_t fanout_stride = 0) {
     if (!segs || nseg == 0) return PKV_ERR_INVALID_ARG;
     if (!d_f32 || !d_wire) return PKV_ERR_INVALID_ARG;
-    const uint32_t align = dtype == PKV_BF16 ? 8u : 4u;
+    if (fanout == 0 || fanout_stride % 4 != 0) return PKV_ERR_INVALID_ARG;
+    // encode reads 16 B (8 bf16 / 4 f32) per access; decode writes 4 values per access
+    const uint32_t align = encode && dtype == PKV_BF16 ? 8u : 4u;
+    uint64_t fan_extra;
+    if (__builtin_mul_overflow(static_cast<uint64_t>(fanout - 1), fanout_stride, &fan_extra))
+        return PKV_ERR_DIM_MISMATCH;
     if (reinterpret_cast<uintptr_t>(d_f32) % 16 != 0) return PKV_ERR_INVALID_ARG;
     const uint32_t plen = p->kind == PKV_CODEC_TURBO ? turbo_plen(p, radii) : fib_plen(p);
     const uint32_t hdr = hdr_len(p);
@@ -205,7 +211,8 @@ int validate_segments(const pkv_profile* p, int radii, bool encode, int dtype, c
         if (encode && s.n_vectors == 0) return PKV_ERR_EMPTY_BATCH;
         if (s.elem_offset % align || s.stride_outer % align || s.stride_inner % align) return PKV_ERR_INVALID_ARG;
         uint64_t end;
-        if (!seg_extent(s, p->dim, &end) || end > f32_elems) return PKV_ERR_DIM_MISMATCH;
+        if (!seg_extent(s, p->dim, &end) || __builtin_add_overflow(end, fan_extra, &end) || end > f32_elems)
+            return PKV_ERR_DIM_MISMATCH;
         uint64_t blob_end;
         if (!mul_add_ok(s.n_vectors, plen, hdr, &blob_end) ||
             __builtin_add_overflow(blob_end, s.wire_offset, &blob_end) || blob_end > wire_bytes)
@@ -375,15 +382,17 @@ int launch_fib_encode_queued(pkv_ctx* ctx, const LaunchCommon& lc, const pkv_pro
 int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool encode, int dtype,
                         const void* d_f32, uint64_t f32_elems, const pkv_seg* segs, uint32_t nseg,
                         const uint8_t* d_wire, uint64_t wire_bytes, uint32_t* d_status, hipStream_t stream,
-                        bool per_vector = false) {
+                        bool per_vector = false, uint32_t fanout = 1, uint64_t fanout_stride = 0) {
     if (!ctx || !prof) return PKV_ERR_INVALID_ARG;
     if (prof->kind == PKV_CODEC_TURBO && radii != PKV_RADII_F32 && radii != PKV_RADII_LOG_U8)
         return PKV_ERR_INVALID_ARG;
     if (prof->kind == PKV_CODEC_FIB) radii = PKV_RADII_F32;
-    if (dtype != PKV_F32 && dtype != PKV_BF16) return PKV_ERR_INVALID_ARG;
-    if (!encode && dtype != PKV_F32) return PKV_ERR_INVALID_ARG;
+    // dtype: encode input (f32 / bf16) or decode output (f32 / bf16 / f16)
+    if (dtype != PKV_F32 && dtype != PKV_BF16 && (encode || dtype != PKV_F16)) return PKV_ERR_INVALID_ARG;
+    if (encode && fanout != 1) return PKV_ERR_INVALID_ARG;
     std::vector<uint32_t> tiles;
-    int rc = validate_segments(prof, radii, encode, dtype, d_f32, f32_elems, segs, nseg, d_wire, wire_bytes, tiles);
+    int rc = validate_segments(prof, radii, encode, dtype, d_f32, f32_elems, segs, nseg, d_wire, wire_bytes, tiles,
+                               fanout, fanout_stride);
     if (rc) return rc;
     HIP_TRY(hipSetDevice(ctx->device));
     Slot* sl;
@@ -401,18 +410,19 @@ int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool e
     lc.status = status;
     lc.radii = static_cast<uint32_t>(radii);
     lc.plen = prof->kind == PKV_CODEC_TURBO ? turbo_plen(prof, radii) : fib_plen(prof);
-    lc.in_bf16 = dtype == PKV_BF16 ? 1u : 0u;
+    lc.in_bf16 = encode && dtype == PKV_BF16 ? 1u : 0u;
     lc.per_vector = per_vector ? 1u : 0u;
+    lc.out_dtype = encode ? static_cast<uint32_t>(PKV_F32) : static_cast<uint32_t>(dtype);
+    lc.fanout = fanout;
+    lc.fanout_stride = fanout_stride;
     const uint32_t nblocks = tiles[nseg];
     int e;
     if (prof->kind == PKV_CODEC_TURBO) {
         e = encode ? launch_turbo_encode(lc, turbo_dev(prof), d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
-                   : launch_turbo_decode(lc, turbo_dev(prof), d_wire, static_cast<float*>(const_cast<void*>(d_f32)),
-                                         nblocks, stream);
+                   : launch_turbo_decode(lc, turbo_dev(prof), d_wire, const_cast<void*>(d_f32), nblocks, stream);
     } else {
         e = encode ? launch_fib_encode_queued(ctx, lc, prof, d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
-                   : launch_fib_decode(lc, fib_dev(prof), d_wire, static_cast<float*>(const_cast<void*>(d_f32)),
-                                       nblocks, stream);
+                   : launch_fib_decode(lc, fib_dev(prof), d_wire, const_cast<void*>(d_f32), nblocks, stream);
     }
     int rc2 = finish_slot(sl, stream);
     if (e) return hip_status(static_cast<hipError_t>(e));
@@ -965,6 +975,17 @@ int pkv_decode_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, 
                         uint32_t* d_status, void* stream) {
     return run_segments(ctx, prof, radii_codec, false, PKV_F32, d_out, out_elems, segs, nseg, d_wire, wire_bytes,
                         d_status, static_cast<hipStream_t>(stream));
+}
+
+int pkv_decode_segments_ex(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, const uint8_t* d_wire,
+                           uint64_t wire_bytes, const pkv_seg* segs, uint32_t nseg, void* d_out, int out_dtype,
+                           uint64_t out_elems, uint32_t fanout, uint64_t fanout_stride, uint32_t* d_status,
+                           void* stream) {
+    if (!ctx) return PKV_ERR_INVALID_ARG;
+    if (out_dtype != PKV_F32 && out_dtype != PKV_BF16 && out_dtype != PKV_F16) return PKV_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    return run_segments_locked(ctx, prof, radii_codec, false, out_dtype, d_out, out_elems, segs, nseg, d_wire,
+                               wire_bytes, d_status, static_cast<hipStream_t>(stream), false, fanout, fanout_stride);
 }
 
 int pkv_parse_header(const pkv_profile* p, const uint8_t* b, uint64_t len, uint64_t* n_vectors, int* radii_codec) {

@@ -103,6 +103,9 @@ struct LaunchCommon {
     uint32_t plen;                // payload bytes per vector
     uint32_t in_bf16;             // encode input dtype
     uint32_t per_vector;          // fib encode: FibQuantizer::encode semantics for every vector
+    uint32_t out_dtype;           // decode output: PKV_F32, PKV_BF16 or PKV_F16 (RNE from the f32 decode)
+    uint32_t fanout;              // decode: copies of every output vector (>= 1) ...
+    uint64_t fanout_stride;       // ... this many elements apart
 };
 
 // Up to 48 constant header bytes (TQW1 / FB1 record headers, TQB1 / FB2 blob
@@ -122,11 +125,11 @@ int make_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint3
 // Kernel launchers (pkv_kernels.hip).  Return a hipError_t as int.
 int launch_turbo_encode(const LaunchCommon& lc, const TurboDev& td, const void* in, uint8_t* wire,
                         uint32_t nblocks, void* stream);
-int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_t* wire, float* out,
+int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_t* wire, void* out,
                         uint32_t nblocks, void* stream);
 int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire,
                       uint32_t nblocks, const FibRedo& rq, void* stream);
-int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, float* out,
+int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, void* out,
                       uint32_t nblocks, void* stream);
 int launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, void* stream);
 int launch_fib_product_check(const float* rot32, const float* cb, uint32_t* bad, void* stream);

@@ -171,9 +171,49 @@ __device__ void stage_rows_in(float* stage, const void* __restrict__ in, bool bf
     }
 }
 
+// f32 -> bfloat16 bits, round to nearest even (torch's / c10's conversion).
+__device__ __forceinline__ uint32_t bf16_rne(float x) {
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;   // NaN stays a (quiet) NaN
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// f32 -> binary16 bits, round to nearest even (v_cvt_f16_f32 in the default mode).
+__device__ __forceinline__ uint32_t f16_rne(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+
+__device__ __forceinline__ uint32_t pack_out2(float a, float b, uint32_t dt) {
+    return dt == PKV_BF16 ? bf16_rne(a) | (bf16_rne(b) << 16) : f16_rne(a) | (f16_rne(b) << 16);
+}
+
+// Store four consecutive values of one output vector at element offset `off`
+// (a multiple of 4) in the decode's output dtype, in every fan-out copy.
+__device__ __forceinline__ void store_out4(void* __restrict__ out, const LaunchCommon& lc, uint64_t off, float4 v) {
+    if (lc.out_dtype == PKV_F32) {
+        for (uint32_t k = 0; k < lc.fanout; ++k, off += lc.fanout_stride)
+            *reinterpret_cast<float4*>(static_cast<float*>(out) + off) = v;
+    } else {
+        const uint2 w = make_uint2(pack_out2(v.x, v.y, lc.out_dtype), pack_out2(v.z, v.w, lc.out_dtype));
+        for (uint32_t k = 0; k < lc.fanout; ++k, off += lc.fanout_stride)
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + off) = w;
+    }
+}
+
+__device__ __forceinline__ void store_out1(void* __restrict__ out, const LaunchCommon& lc, uint64_t off, float v) {
+    if (lc.out_dtype == PKV_F32) {
+        for (uint32_t k = 0; k < lc.fanout; ++k, off += lc.fanout_stride) static_cast<float*>(out)[off] = v;
+    } else {
+        const uint16_t w = static_cast<uint16_t>(lc.out_dtype == PKV_BF16 ? bf16_rne(v) : f16_rne(v));
+        for (uint32_t k = 0; k < lc.fanout; ++k, off += lc.fanout_stride) static_cast<uint16_t*>(out)[off] = w;
+    }
+}
+
+// LDS rows (pitch DIM + 4) of nv vectors -> their output positions, 16 B per
+// lane per store; rows whose bit is set in the skip masks are not written.
 template <int DIM>
-__device__ void stage_rows_out(float* __restrict__ out, const float* stage, const SegDev& s, uint32_t v0,
-                               uint32_t nv, uint32_t skip_mask_lo, uint32_t skip_mask_hi, int lane) {
+__device__ void stage_rows_out(void* __restrict__ out, const LaunchCommon& lc, const float* stage, const SegDev& s,
+                               uint32_t v0, uint32_t nv, uint32_t skip_mask_lo, uint32_t skip_mask_hi, int lane) {
     constexpr int PITCH = DIM + 4;
     constexpr int Q = DIM / 4;
     for (uint32_t i = lane; i < nv * Q; i += WAVE) {
@@ -181,7 +221,7 @@ __device__ void stage_rows_out(float* __restrict__ out, const float* stage, cons
         uint32_t skip = r < 32 ? (skip_mask_lo >> r) & 1u : (skip_mask_hi >> (r - 32)) & 1u;
         if (skip) continue;
         uint64_t off = vec_elem_offset(s, v0 + r);
-        *reinterpret_cast<float4*>(out + off + 4 * c) = *reinterpret_cast<const float4*>(stage + r * PITCH + 4 * c);
+        store_out4(out, lc, off + 4 * c, *reinterpret_cast<const float4*>(stage + r * PITCH + 4 * c));
     }
 }
 
@@ -808,7 +848,7 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
 // ------------------------------------------------------------ turbo decode
 template <int DIM, int PB>
 __global__ __launch_bounds__(TILE) void turbo_decode_kernel(
-    LaunchCommon lc, const uint8_t* __restrict__ wire, float* __restrict__ out,
+    LaunchCommon lc, const uint8_t* __restrict__ wire, void* __restrict__ out,
     const float* __restrict__ signs, const float* __restrict__ cs_tab, uint64_t seed, uint32_t pbits_rt,
     uint32_t proj, uint32_t mode) {
     constexpr int PITCH = DIM + 4;
@@ -913,7 +953,7 @@ __global__ __launch_bounds__(TILE) void turbo_decode_kernel(
     skip_lo = static_cast<uint32_t>(badmask);
     skip_hi = static_cast<uint32_t>(badmask >> 32);
     wave_sync();
-    stage_rows_out<DIM>(out, stage, seg, v0, nv, skip_lo, skip_hi, lane);
+    stage_rows_out<DIM>(out, lc, stage, seg, v0, nv, skip_lo, skip_hi, lane);
 }
 
 // LDS words per wave of turbo_decode_split_kernel: max(payloads, rows).
@@ -928,7 +968,7 @@ __host__ __device__ constexpr uint32_t turbo_split_wave_words(uint32_t pwd) {
 // stores them straight from registers.
 template <int PB>
 __global__ __launch_bounds__(TILE) void turbo_decode_split_kernel(
-    LaunchCommon lc, const uint8_t* __restrict__ wire, float* __restrict__ out,
+    LaunchCommon lc, const uint8_t* __restrict__ wire, void* __restrict__ out,
     const float* __restrict__ signs, const float* __restrict__ cs_tab, uint64_t seed, uint32_t pbits_rt,
     uint32_t proj, uint32_t mode) {
     constexpr int DIM = 64;
@@ -1034,7 +1074,7 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split_kernel(
     }
     const uint64_t badm = __ballot(active && h == 0 && !vok);
     wave_sync();
-    stage_rows_out<DIM>(out, stage, seg, t0, nv, static_cast<uint32_t>(badm), 0u, lane);
+    stage_rows_out<DIM>(out, lc, stage, seg, t0, nv, static_cast<uint32_t>(badm), 0u, lane);
 }
 
 // ------------------------------------------------------------ fib encode
@@ -1510,7 +1550,7 @@ __global__ __launch_bounds__(TILE) void fib_fixup_kernel(LaunchCommon lc, const 
 // decoded row as one coalesced 256-byte write.
 template <int DIM>
 __global__ __launch_bounds__(TILE) void fib_decode_kernel(LaunchCommon lc, const uint8_t* __restrict__ wire,
-                                                          float* __restrict__ out,
+                                                          void* __restrict__ out,
                                                           const float* __restrict__ rot32t,
                                                           const float* __restrict__ cb) {
     static_assert(DIM == 64, "one lane per column of a 64-wide vector");
@@ -1603,7 +1643,7 @@ __global__ __launch_bounds__(TILE) void fib_decode_kernel(LaunchCommon lc, const
         } else if (!ofinite) {
             if (lane == 0) status_fail(lc.status, sidx, 1, vi, KIND_DECODE_NONFINITE);
         } else {
-            out[off + lane] = o;
+            store_out1(out, lc, off + lane, o);
         }
     }
 }
@@ -1619,18 +1659,20 @@ __global__ __launch_bounds__(TILE) void fib_decode_kernel(LaunchCommon lc, const
 // profile falls back to fib_decode_kernel on any difference.
 typedef float v32f __attribute__((ext_vector_type(32)));
 
-template <int DIM>
+template <int DIM, bool STAGED>
 __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, const uint8_t* __restrict__ wire,
-                                                               float* __restrict__ out,
+                                                               void* __restrict__ out,
                                                                const float* __restrict__ rot32,
                                                                const float* __restrict__ cb) {
     static_assert(DIM == 64, "two 32-column MFMA blocks");
     constexpr int BLOCKS = DIM / 4;
     constexpr uint32_t PLEN = 2 + (BLOCKS * 5 + 7) / 8;   // 12
     constexpr int PAY_WORDS = WAVE * PLEN / 4 + 4;
+    constexpr int HPITCH = 32 + 4;       // one half row (32 columns) per vector, padded
     __shared__ float rot_s[DIM * DIM];   // f32(Pi), row-major
     __shared__ float4 cb_s[32];
     __shared__ uint32_t pay_s[WAVES][PAY_WORDS];
+    __shared__ float half_s[STAGED ? WAVES : 1][STAGED ? 32 * HPITCH : 4];   // output staging: 32 vectors x 32 cols
     {
         const float4* src = reinterpret_cast<const float4*>(rot32);
         float4* dst = reinterpret_cast<float4*>(rot_s);
@@ -1705,16 +1747,44 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
         const bool active = t0 + static_cast<uint32_t>(n) < nv;
         const uint32_t vi = v0 + t0 + static_cast<uint32_t>(n);
         if (active && h == 0 && vbad) status_fail(lc.status, sidx, 1, vi, ok ? KIND_DECODE_NONFINITE : KIND_CORRUPT);
-        if (active && !vbad) {
-            float* orow = out + vec_elem_offset(seg, vi);
+        if constexpr (!STAGED) {
+            if (active && !vbad) {
+                const uint64_t orow = vec_elem_offset(seg, vi);
 #pragma unroll
-            for (int bb = 0; bb < 2; ++bb)
+                for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int q = 16 * bb + 4 * g;   // registers q .. q + 3: columns 32bb + 8g + 4h .. + 3
-                    *reinterpret_cast<float4*>(orow + 32 * bb + 8 * g + 4 * h) =
-                        make_float4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3]);
-                }
+                    for (int g = 0; g < 4; ++g) {   // registers q .. q + 3: columns 32bb + 8g + 4h .. + 3
+                        const int q = 16 * bb + 4 * g;
+                        store_out4(out, lc, orow + 32 * bb + 8 * g + 4 * h,
+                                   make_float4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3]));
+                    }
+            }
+            continue;
+        }
+        // vectors (of the 32) to write: active and good
+        const uint32_t wmask = static_cast<uint32_t>(__ballot(active && !vbad && h == 0));
+        // Fan-out: stores go through LDS half a row at a time, so every store
+        // instruction writes 8 whole 128 B half rows instead of 32 B into each
+        // of 32 rows (at 8 copies that is 1.4 -> 5.3 TB/s of writes); one
+        // copy keeps the direct stores above (the LDS pass costs ~3 %).
+        float* hs = half_s[wave];
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {   // registers q .. q + 3: columns 32bb + 8g + 4h .. + 3
+                const int q = 16 * bb + 4 * g;
+                *reinterpret_cast<float4*>(hs + n * HPITCH + 8 * g + 4 * h) =
+                    make_float4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3]);
+            }
+            wave_sync();
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t r = static_cast<uint32_t>(lane >> 3) + 8u * k, c = lane & 7;
+                if ((wmask >> r) & 1u)
+                    store_out4(out, lc, vec_elem_offset(seg, v0 + t0 + r) + 32 * bb + 4 * c,
+                               *reinterpret_cast<const float4*>(hs + r * HPITCH + 4 * c));
+            }
+            wave_sync();   // the next half row overwrites the staging rows
         }
     }
 }
@@ -1799,7 +1869,7 @@ int launch_turbo_encode(const LaunchCommon& lc, const TurboDev& td, const void* 
                                 td.qjl, td.cs, td.seed, td.pbits, td.proj, td.mode);
 }
 
-int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_t* wire, float* out,
+int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_t* wire, void* out,
                         uint32_t nblocks, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (td.dim == 64 && td.pbits <= 4) {
@@ -1833,11 +1903,14 @@ int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, 
     return hipGetLastError();
 }
 
-int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, float* out, uint32_t nblocks,
+int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, void* out, uint32_t nblocks,
                       void* stream) {
-    if (fd.mfma_decode)
-        hipLaunchKernelGGL(fib_decode_mfma_kernel<64>, dim3(nblocks), dim3(TILE), 0, static_cast<hipStream_t>(stream),
-                           lc, wire, out, fd.rot32, fd.codebook);
+    if (fd.mfma_decode && lc.fanout > 1)
+        hipLaunchKernelGGL((fib_decode_mfma_kernel<64, true>), dim3(nblocks), dim3(TILE), 0,
+                           static_cast<hipStream_t>(stream), lc, wire, out, fd.rot32, fd.codebook);
+    else if (fd.mfma_decode)
+        hipLaunchKernelGGL((fib_decode_mfma_kernel<64, false>), dim3(nblocks), dim3(TILE), 0,
+                           static_cast<hipStream_t>(stream), lc, wire, out, fd.rot32, fd.codebook);
     else
         hipLaunchKernelGGL(fib_decode_kernel<64>, dim3(nblocks), dim3(TILE), 0, static_cast<hipStream_t>(stream), lc,
                            wire, out, fd.rot32t, fd.codebook);

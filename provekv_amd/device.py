@@ -192,18 +192,28 @@ class Profile:
         L.check(rc, "pkv_encode_segments")
 
     def decode_segments(self, wire, segs: np.ndarray, out, radii: int = L.RADII_F32, status=None,
-                        stream=None) -> None:
+                        stream=None, fanout: int = 1, fanout_stride: int = 0) -> None:
+        """Decode into `out` (float32, bfloat16 or float16; the latter two are
+        the f32 decode rounded to nearest even), each vector written `fanout`
+        times `fanout_stride` elements apart."""
         torch = _torch()
         segs = np.ascontiguousarray(segs, dtype=SEG_DTYPE)
-        if out.dtype != torch.float32 or wire.dtype != torch.uint8:
-            raise TypeError("decode writes float32 from a uint8 wire")
+        dts = {torch.float32: L.DT_F32, torch.bfloat16: L.DT_BF16, torch.float16: L.DT_F16}
+        if out.dtype not in dts or wire.dtype != torch.uint8:
+            raise TypeError("decode writes float32 / bfloat16 / float16 from a uint8 wire")
         if not (out.is_contiguous() and wire.is_contiguous()):
             raise ValueError("tensors must be contiguous")
         st = self._status_ptr(status, len(segs))
-        rc = L.lib().pkv_decode_segments(self.ctx.ptr, self._ptr, radii, wire.data_ptr(), wire.numel(),
-                                         segs.ctypes.data, len(segs), out.data_ptr(), out.numel(), st,
-                                         _stream_ptr(stream))
-        L.check(rc, "pkv_decode_segments")
+        if out.dtype == torch.float32 and fanout == 1:
+            rc = L.lib().pkv_decode_segments(self.ctx.ptr, self._ptr, radii, wire.data_ptr(), wire.numel(),
+                                             segs.ctypes.data, len(segs), out.data_ptr(), out.numel(), st,
+                                             _stream_ptr(stream))
+            L.check(rc, "pkv_decode_segments")
+            return
+        rc = L.lib().pkv_decode_segments_ex(self.ctx.ptr, self._ptr, radii, wire.data_ptr(), wire.numel(),
+                                            segs.ctypes.data, len(segs), out.data_ptr(), dts[out.dtype], out.numel(),
+                                            fanout, fanout_stride, st, _stream_ptr(stream))
+        L.check(rc, "pkv_decode_segments_ex")
 
     def status_error(self, status_host: np.ndarray, segs: np.ndarray | None = None):
         """Turn per-segment status words (2 per segment, host copy) into a

@@ -55,6 +55,82 @@ def _tier(owners, layers: int, heads: int, dim: int, corpus_tokens: int, hdr: in
     return TierLayout(np.array(enc, dtype=SEG_DTYPE), np.array(dec, dtype=SEG_DTYPE), wire, out, blobs)
 
 
+class DeviceKVCache:
+    """A KV cache in HuggingFace ``DynamicCache`` layout on the GPU: per layer
+    one K and one V tensor [1, H, T, D] (float32, bfloat16 or float16), all in
+    one allocation [copies][layers][K|V][H][T][D].  ``copies`` independent
+    caches (one per agent served on this GPU) share the allocation so that one
+    decode can fan out to all of them.
+
+    Implements proveKV's ``CacheTarget`` (proveKV/src/pool.rs:646-658):
+    ``num_layers``, ``append_key``, ``append_value``, ``seq_len``; a key or
+    value is one token's [H * D] vector, the [tokens][heads][head_dim] rows of
+    ``decompress_all_layers_with_seed`` (pool.rs:447-469).
+    """
+
+    def __init__(self, layers: int, heads: int, tokens: int, dim: int, dtype=None, copies: int = 1,
+                 device="cuda"):
+        import torch
+        self.layers, self.heads, self.tokens, self.dim, self.copies = layers, heads, tokens, dim, copies
+        self.buf = torch.zeros((copies, layers, 2, heads, tokens, dim), dtype=dtype or torch.float32, device=device)
+        self._seq_len = 0
+
+    # ---- layout
+    @property
+    def copy_stride(self) -> int:
+        return self.layers * 2 * self.heads * self.tokens * self.dim
+
+    def elem_offset(self, layer: int, side: int, token: int) -> int:
+        """Element offset of (layer, K|V, head 0, token) in copy 0."""
+        return ((layer * 2 + side) * self.heads * self.tokens + token) * self.dim
+
+    def keys(self, layer: int, copy: int = 0):
+        return self.buf[copy, layer, 0].unsqueeze(0)
+
+    def values(self, layer: int, copy: int = 0):
+        return self.buf[copy, layer, 1].unsqueeze(0)
+
+    def segments_for(self, tier: "TierLayout", first_tokens: list) -> np.ndarray:
+        """Decode segments writing the blobs of `tier` at the given first token
+        of each owner: vector i = t * H + h goes to [h][t0 + t] of its layer."""
+        rows = []
+        k = 0
+        for t0 in first_tokens:
+            for layer in range(self.layers):
+                for side in (0, 1):
+                    _, _, _, wire_off, _ = tier.blob_offsets[k]
+                    n = int(tier.enc[k]["n_vectors"])
+                    rows.append((self.elem_offset(layer, side, t0), self.dim, self.tokens * self.dim, wire_off, n,
+                                 self.heads))
+                    k += 1
+        assert k == len(tier.blob_offsets)
+        return np.array(rows, dtype=SEG_DTYPE)
+
+    # ---- CacheTarget (proveKV/src/pool.rs:646-658)
+    def num_layers(self) -> int:
+        return self.layers
+
+    def _append(self, side: int, layer: int, position: int, vec) -> None:
+        import torch
+        if not (0 <= layer < self.layers and 0 <= position < self.tokens):
+            raise IndexError(f"layer {layer} / position {position} outside the cache")
+        v = torch.as_tensor(np.asarray(vec, dtype=np.float32)).reshape(self.heads, self.dim)
+        self.buf[:, layer, side, :, position, :] = v.to(self.buf.device, self.buf.dtype)
+        self._seq_len = max(self._seq_len, position + 1)
+
+    def append_key(self, layer: int, position: int, key) -> None:
+        self._append(0, layer, position, key)
+
+    def append_value(self, layer: int, position: int, value) -> None:
+        self._append(1, layer, position, value)
+
+    def seq_len(self) -> int:
+        return self._seq_len
+
+    def mark_filled(self, tokens: int) -> None:
+        self._seq_len = max(self._seq_len, tokens)
+
+
 class TwoTierPlan:
     """Pool over tokens [0, prefix) with fib_k4_n32 (FB2); one turbo (TQB1)
     shell per agent over its own token range.  Decode output per tier is
@@ -109,11 +185,49 @@ class TwoTierPlan:
         self.turbo.decode_segments(bufs["shell_wire"], self.shells.dec, bufs["shell_out"], radii=self.radii,
                                    status=bufs["shell_dstatus"], stream=stream)
 
-    def check(self, bufs):
-        """Raise the first failure recorded by the last encode/decode."""
-        for prof, key, segs in ((self.fib, "pool_status", self.pool.enc), (self.turbo, "shell_status", self.shells.enc),
-                                (self.fib, "pool_dstatus", self.pool.dec),
-                                (self.turbo, "shell_dstatus", self.shells.dec)):
+    def rehydrate(self, bufs, cache: DeviceKVCache, stream=None):
+        """Decode the pool and every shell straight into `cache` -- prefix at
+        tokens [0, prefix), agent a's tokens after the prefix and the agents
+        before it (the cache patch of the reference harness,
+        proveKV/scripts/ppl_validate_multi_agent.py:226-272) -- in the cache's
+        dtype, once per cache copy: two launches.  Status words land in
+        bufs["pool_cstatus"] / bufs["shell_cstatus"]."""
+        import torch
+        key = id(cache)
+        if getattr(self, "_cache_key", None) != key:
+            firsts, t = [], self.prefix
+            for nt in self.agent_tokens:
+                firsts.append(t)
+                t += nt
+            self._cache_segs = (cache.segments_for(self.pool, [0]), cache.segments_for(self.shells, firsts))
+            self._cache_key = key
+        if cache.tokens < self.tokens or cache.layers != self.layers or cache.heads != self.heads:
+            raise ValueError("cache too small for this plan")
+        pseg, sseg = self._cache_segs
+        for name, n in (("pool_cstatus", len(pseg)), ("shell_cstatus", len(sseg))):
+            if name not in bufs:
+                bufs[name] = torch.empty(2 * n, dtype=torch.int32, device=cache.buf.device)
+        out = cache.buf.view(-1)
+        self.fib.decode_segments(bufs["pool_wire"], pseg, out, status=bufs["pool_cstatus"], stream=stream,
+                                 fanout=cache.copies, fanout_stride=cache.copy_stride)
+        self.turbo.decode_segments(bufs["shell_wire"], sseg, out, radii=self.radii, status=bufs["shell_cstatus"],
+                                   stream=stream, fanout=cache.copies, fanout_stride=cache.copy_stride)
+        cache.mark_filled(self.tokens)
+
+    def check_rehydrate(self, bufs):
+        """Raise the first failure recorded by the last rehydrate."""
+        pseg, sseg = self._cache_segs
+        for prof, key, segs in ((self.fib, "pool_cstatus", pseg), (self.turbo, "shell_cstatus", sseg)):
+            err = prof.status_error(bufs[key].cpu().numpy().view(np.uint32), segs)
+            if err is not None:
+                raise err
+
+    def check(self, bufs, decode: bool = True):
+        """Raise the first failure recorded by the last encode (and decode)."""
+        checks = [(self.fib, "pool_status", self.pool.enc), (self.turbo, "shell_status", self.shells.enc)]
+        if decode:
+            checks += [(self.fib, "pool_dstatus", self.pool.dec), (self.turbo, "shell_dstatus", self.shells.dec)]
+        for prof, key, segs in checks:
             st = bufs[key].cpu().numpy().view(np.uint32)
             err = prof.status_error(st, segs)
             if err is not None:

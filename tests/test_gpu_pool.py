@@ -1,11 +1,16 @@
 """GPU parity of the batched two-tier path (all (owner, layer, K|V) blobs in
 one launch per tier) against per-blob oracle calls on the gathered vectors,
 plus the receipt byte math at the N=8 SmolLM2 shape."""
+import ctypes
+import struct
+
 import numpy as np
 import pytest
 
 from oracle import oracle as O
+from provekv_amd import _lib as L
 from provekv_amd import synth
+from provekv_amd.device import SEG_DTYPE, Profile
 from provekv_amd.pool import TwoTierPlan
 
 pytestmark = pytest.mark.gpu
@@ -65,3 +70,106 @@ def test_smollm2_n8_receipt_bytes(ctx):
         assert b["pool"] == 14746512
         assert b["per_agent_shell"] == shell
         assert b["total"] == system
+
+
+def _patched_cache(plan, corpus, layers, heads, dim, prefix, agents, lossy):
+    """Oracle decodes placed like patch_cache_with_multi_agent_kv
+    (proveKV/scripts/ppl_validate_multi_agent.py:226-272): [layer][K|V][H][T][D] f32."""
+    T = prefix + sum(agents)
+    cb, rot = plan.fib.constants()
+    cb, rot = cb.reshape(32, 4), rot.reshape(dim, dim)
+    ref = np.zeros((layers, 2, heads, T, dim), np.float32)
+    owners = [(0, prefix, "fib")]
+    t = prefix
+    for nt in agents:
+        owners.append((t, nt, "turbo"))
+        t += nt
+    for t0, nt, kind in owners:
+        for layer in range(layers):
+            for side in (0, 1):
+                x = gather(corpus, t0, nt, layer, side)
+                if kind == "fib":
+                    dec = O.fib_decode_batch(O.fib_encode_batch(x, cb, rot), cb, rot)
+                else:
+                    dec = O.turbo_decode_batch(O.turbo_encode_batch(x, SEED, radii_codec=int(lossy)), dim, SEED)
+                ref[layer, side, :, t0:t0 + nt, :] = dec.reshape(nt, heads, dim).transpose(1, 0, 2)
+    return ref
+
+
+@pytest.mark.parametrize("dtype,copies,lossy", [("float32", 1, False), ("bfloat16", 2, False),
+                                                ("float16", 3, True)])
+def test_rehydrate_into_cache_layout(ctx, dtype, copies, lossy):
+    """Fused rehydrate: both tiers decoded straight into [1, H, T, D] per
+    layer, in the cache dtype (RNE of the f32 decode), into `copies` caches."""
+    import torch
+    from provekv_amd.pool import DeviceKVCache
+    layers, heads, dim, prefix, agents = 2, 4, 64, 21, [3, 6]
+    corpus = synth.corpus_tokens(5, layers, heads, prefix + sum(agents), dim)
+    plan = TwoTierPlan(ctx, layers, heads, dim, prefix, agents, seed=SEED, lossy=lossy)
+    bufs = plan.alloc()
+    plan.encode(torch.from_numpy(corpus.reshape(-1)).cuda(), bufs)
+    tdt = getattr(torch, dtype)
+    cache = DeviceKVCache(layers, heads, prefix + sum(agents), dim, dtype=tdt, copies=copies)
+    cache.buf.fill_(7.0)
+    plan.rehydrate(bufs, cache)
+    torch.cuda.synchronize()
+    plan.check_rehydrate(bufs)
+    assert cache.seq_len() == prefix + sum(agents) and cache.num_layers() == layers
+    ref = torch.from_numpy(_patched_cache(plan, corpus, layers, heads, dim, prefix, agents, lossy)).to(tdt)
+    got = cache.buf.cpu()
+    for c in range(copies):
+        assert torch.equal(got[c].view(torch.int16 if dtype != "float32" else torch.int32),
+                           ref.view(torch.int16 if dtype != "float32" else torch.int32))
+    assert tuple(cache.keys(1, copies - 1).shape) == (1, heads, prefix + sum(agents), dim)
+
+
+def test_cache_target_append(ctx):
+    """CacheTarget (proveKV/src/pool.rs:646-658): append one token's [H * D]
+    key / value at a position in every copy."""
+    import torch
+    from provekv_amd.pool import DeviceKVCache
+    cache = DeviceKVCache(3, 2, 8, 64, dtype=torch.bfloat16, copies=2)
+    k = np.arange(128, dtype=np.float32) / 7
+    cache.append_key(1, 5, k)
+    cache.append_value(2, 6, -k)
+    assert cache.seq_len() == 7 and cache.num_layers() == 3
+    want = torch.from_numpy(k.reshape(2, 64)).to(torch.bfloat16)
+    assert torch.equal(cache.keys(1, 1)[0, :, 5, :].cpu(), want)
+    assert torch.equal(cache.values(2, 0)[0, :, 6, :].cpu(), -want)
+    with pytest.raises(IndexError):
+        cache.append_key(3, 0, k)
+
+
+def test_decode_output_dtype_rounding_edges(ctx):
+    """With an identity rotation and a unit f16 norm the decode returns the
+    codebook entries exactly, so planted values check the bf16 / f16
+    conversion against torch's own (round to nearest even): ties, f16
+    subnormals, the f16 overflow threshold, zeros."""
+    import torch
+    vals = [1 + 2 ** -8, 1 + 3 * 2 ** -8, -(1 + 2 ** -8), 1 + 2 ** -11, 1 + 3 * 2 ** -11, 65504.0, 65519.0,
+            65520.0, 1e5, -1e5, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 1e-6, -1e-7, 2.0 ** -126, 0.0, -0.0,
+            1 / 3, np.pi, -np.e, 3.4e38, 1.5 * 2 ** -14, 2 ** -14 - 2 ** -25]
+    rng = np.random.RandomState(1)
+    rest = rng.randn(128 - len(vals)) * 10.0 ** rng.randint(-8, 6, 128 - len(vals))
+    cb = np.array(vals + list(rest), np.float32).reshape(32, 4)
+    rot = np.ascontiguousarray(np.eye(64))
+    ptr = ctypes.c_void_p()
+    L.check(L.lib().pkv_fib_profile_create_with_constants(ctx.ptr, 64, 4, 32, cb.ctypes.data, rot.ctypes.data,
+                                                          ctypes.byref(ptr)), "pkv_fib_profile_create_with_constants")
+    prof = Profile(ctx, ptr, L.CODEC_FIB, 64)
+    n = 8
+    blob = bytearray(b"FB2" + bytes([1, 5, 0]) + struct.pack("<II", 16, n) + bytes([0]) + struct.pack("<HH", 2, 10))
+    for v in range(n):
+        idx = sum(((v * 16 + b) % 32) << (5 * b) for b in range(16))
+        blob += struct.pack("<H", 0x3C00) + idx.to_bytes(10, "little")
+    wire = torch.frombuffer(blob, dtype=torch.uint8).cuda()
+    want32 = O.fib_decode_batch(bytes(blob), cb, rot)   # the codebook entries, but -0.0 + 0.0 = +0.0
+    assert np.array_equal(want32[0], np.where(cb[:16].reshape(64) == 0, 0.0, cb[:16].reshape(64)))
+    segs = np.array([(0, 0, 64, 0, n, n)], dtype=SEG_DTYPE)
+    for tdt in (torch.float32, torch.bfloat16, torch.float16):
+        out = torch.empty(n * 64, dtype=tdt, device="cuda")
+        prof.decode_segments(wire, segs, out)
+        torch.cuda.synchronize()
+        want = torch.from_numpy(want32).reshape(-1).to(tdt)
+        bits = torch.int32 if tdt == torch.float32 else torch.int16
+        assert torch.equal(out.cpu().view(bits), want.view(bits)), tdt
