@@ -211,6 +211,114 @@ def bench_legacy(args):
     print(json.dumps(out), flush=True)
 
 
+def bench_config4(args):
+    """BASELINE config 4 at full size: Llama-3-8B KV (32 layers x K|V x 8 KV
+    heads x 32768 tokens x head_dim 128) as bf16, turbo b = 4 with Hadamard
+    dim 128 and BlockLogU8 radii, one TQB1-L blob per (layer, K|V) in one
+    launch, then decode to f32.  The seeded generator produces two layers'
+    values on the host (bf16, RNE); they are tiled over the 32 layers on the
+    device (per-vector cost does not depend on the values' layer).  value =
+    f32-equivalent KV bytes (8,589,934,592) / GPU time of encode + decode.
+    Parity: sampled vectors of several blobs against the oracle on the f32
+    upcast."""
+    import torch
+    from oracle import oracle as O
+    from provekv_amd import _lib as L
+    from provekv_amd import synth
+    from provekv_amd.device import SEG_DTYPE, default_context
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU"}))
+        sys.exit(1)
+    layers, heads, tokens, dim, gen_layers = 32, 8, 32768, 128, 2
+    log(f"[bench] generating {gen_layers} layers of config-4 values (bf16)")
+    K, V = synth.kv_cache(4, gen_layers, heads, tokens, dim, k_sigma=0.7, outliers=4, outlier_mult=10.0,
+                          v_scale=1.0)
+    block = torch.from_numpy(np.ascontiguousarray(np.stack([K, V], axis=1))).to(torch.bfloat16)
+    del K, V
+    n = heads * tokens
+    x = torch.empty((layers // gen_layers, gen_layers * 2 * n * dim), dtype=torch.bfloat16, device="cuda")
+    x[:] = block.reshape(1, -1).cuda()
+    x = x.reshape(-1)
+    ctx = default_context()
+    prof = ctx.turbo_profile(dim, 4, 32, 42)
+    plen = prof.payload_len(L.RADII_LOG_U8)
+    blob = 38 + n * plen
+    nseg = 2 * layers
+    segs = np.array([(b * n * dim, 0, dim, b * blob, n, n) for b in range(nseg)], dtype=SEG_DTYPE)
+    wire = torch.empty(nseg * blob, dtype=torch.uint8, device="cuda")
+    out = torch.empty(nseg * n * dim, dtype=torch.float32, device="cuda")
+    est = torch.empty(2 * nseg, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(est)
+    stream = torch.cuda.current_stream()
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record(stream)
+        prof.encode_segments(x, segs, wire, radii=L.RADII_LOG_U8, status=est)
+        if ev is not None:
+            ev[1].record(stream)
+        prof.decode_segments(wire, segs, out, radii=L.RADII_LOG_U8, status=dst)
+        if ev is not None:
+            ev[2].record(stream)
+
+    log(f"[bench] config 4: {nseg} blobs x {n} vectors, warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    for s_ in (est, dst):
+        err = prof.status_error(s_.cpu().numpy().view(np.uint32), segs)
+        if err is not None:
+            raise err
+    steps = max(1, min(args.steps, 5))
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        step()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    step_ms = t0.elapsed_time(t1) / steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for k in range(steps):
+        step(evs[k])
+    torch.cuda.synchronize()
+    enc_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
+    dec_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    # sampled parity: 512 vectors of four blobs, bytes and decodes vs the oracle
+    rng = np.random.RandomState(4)
+    parity = True
+    for b in (0, 1, nseg - 2, nseg - 1):
+        idx = np.sort(rng.choice(n, 512, replace=False))
+        gb = b % (2 * gen_layers)
+        xs = block.reshape(2 * gen_layers, n, dim)[gb][idx].to(torch.float32).numpy()
+        ref = O.turbo_encode_batch(xs, 42, radii_codec=1)
+        w = wire[b * blob + 38:(b + 1) * blob].cpu().numpy().reshape(n, plen)[idx]
+        parity &= w.tobytes() == ref[38:]
+        got = out[b * n * dim:(b + 1) * n * dim].reshape(n, dim)[idx].cpu().numpy()
+        parity &= np.array_equal(got.view(np.uint32), O.turbo_decode_batch(ref, dim, 42).view(np.uint32))
+    f32_bytes = nseg * n * dim * 4
+    wire_bytes = nseg * blob
+    enc_alg = nseg * n * dim * 2 + wire_bytes
+    dec_alg = wire_bytes + f32_bytes
+    dom, dom_ms, dom_alg = ("encode", enc_ms, enc_alg) if enc_ms >= dec_ms else ("decode", dec_ms, dec_alg)
+    res = {"metric": "KV codec encode+decode GB/s (f32-equivalent KV) and % HBM peak, Llama-3-8B shape",
+           "value": round(f32_bytes / (step_ms * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+           "ms_per_step": round(step_ms, 3), "dtype": "f32 arithmetic on bf16 input",
+           "data": f"synthetic (seeded config-4 distribution, {gen_layers} generated layers tiled over {layers})",
+           "config": {"workload": "config4: 32L x K|V x 8 KV heads x 32768 tokens x d128, bf16 in, turbo b=4 "
+                                  "QJL-32, TQB1-L (BlockLogU8 radii)", "blobs": nseg, "vectors_per_blob": n,
+                      "wire_bytes": wire_bytes},
+           "kernels_ms": {"encode": round(enc_ms, 3), "decode": round(dec_ms, 3)},
+           "kernels_gbs": {"encode": round(enc_alg / (enc_ms * 1e-3) / 1e9, 1),
+                           "decode": round(dec_alg / (dec_ms * 1e-3) / 1e9, 1)},
+           "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(dom_alg / (dom_ms * 1e-3) / 1e9, 1),
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(dom_alg / (dom_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                        "algorithmic_bytes": dom_alg},
+           "parity_sampled_2048": bool(parity)}
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -225,8 +333,9 @@ def main():
     ap.add_argument("--copies", type=int, default=8,
                     help="KV caches filled from one decode: config 3 rehydrates all 8 agents' full 1024-token "
                          "KV (default 8)")
-    ap.add_argument("--workload", choices=("pool", "legacy"), default="pool",
-                    help="pool: the config-3 metric (default); legacy: per-vector TQW1 / FB1 records")
+    ap.add_argument("--workload", choices=("pool", "legacy", "config4"), default="pool",
+                    help="pool: the config-3 metric (default); legacy: per-vector TQW1 / FB1 records; "
+                         "config4: Llama-3-8B shape, bf16, d128, TQB1-L")
     args = ap.parse_args()
     if args.copies == 1:   # one cache: the fib decode stores directly (no LDS staging)
         KERNEL_SYMBOL["fib_decode"] = "fib_decode_mfma_kernel<64, false>"
@@ -236,6 +345,9 @@ def main():
         sys.exit(2)
     if args.workload == "legacy":
         bench_legacy(args)
+        return
+    if args.workload == "config4":
+        bench_config4(args)
         return
 
     import torch

@@ -631,26 +631,42 @@ void pkv_ctx_destroy(pkv_ctx* ctx) {
 }
 
 // Operands of the head_dim-64 QJL MFMA path (layout in TurboDev).
+// Operands of the QJL matrix-core path.  Head_dim 64 (v_mfma_f32_32x32x2_f32,
+// 32-projection tiles): qa[t][c][lane] = G[32t + lane % 32][32 (lane / 32) + c],
+// qb[t][r][lane] = bound of projection 32t + 8 (r / 4) + 4 (lane / 32) + r % 4.
+// Head_dim 128 (v_mfma_f32_16x16x4_f32, 16-projection tiles):
+// qa[t][c][lane] = G[16t + lane % 16][32 (lane / 16) + c],
+// qb[t][r][lane] = bound of projection 16t + 4 (lane / 16) + r.
+// bound_j = k u |g_j| (1 + 2^-10), rounded up, u = 2^-24, k = 200 (64) or
+// 400 (128): the reference's sequential dot is within (d + 2)u sum|g_c res_c|
+// and the matrix core's within (2d + 2)u.
 static void turbo_qjl_mfma_constants(pkv_profile* p) {
-    const uint32_t dim = p->dim, tiles = p->proj / 32;
+    const uint32_t dim = p->dim;
+    const bool wide = dim == 128;
+    const uint32_t tp = wide ? 16 : 32;                 // projections per tile
+    const uint32_t tiles = p->proj / tp, nb = wide ? 4 : 16;
     p->qa.assign(static_cast<size_t>(tiles) * 32 * 64, 0.0f);
-    p->qb.assign(static_cast<size_t>(tiles) * 16 * 64, 0.0f);
+    p->qb.assign(static_cast<size_t>(tiles) * nb * 64, 0.0f);
     const double u = std::ldexp(1.0, -24);
+    const double k = wide ? 400.0 : 200.0;
     for (uint32_t t = 0; t < tiles; ++t)
         for (uint32_t lane = 0; lane < 64; ++lane) {
-            for (uint32_t c = 0; c < 32; ++c)
-                p->qa[(t * 32 + c) * 64 + lane] = p->qjl[static_cast<size_t>(32 * t + lane % 32) * dim + 32 * (lane / 32) + c];
-            for (uint32_t q = 0; q < 16; ++q) {
-                const uint32_t j = 32 * t + 8 * (q / 4) + 4 * (lane / 32) + q % 4;
+            for (uint32_t c = 0; c < 32; ++c) {
+                const uint32_t row = wide ? 16 * t + lane % 16 : 32 * t + lane % 32;
+                const uint32_t col = wide ? 32 * (lane / 16) + c : 32 * (lane / 32) + c;
+                p->qa[(t * 32 + c) * 64 + lane] = p->qjl[static_cast<size_t>(row) * dim + col];
+            }
+            for (uint32_t r = 0; r < nb; ++r) {
+                const uint32_t j = wide ? 16 * t + 4 * (lane / 16) + r : 32 * t + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
                 double g2 = 0.0;
                 for (uint32_t c = 0; c < dim; ++c) {
                     const double g = p->qjl[static_cast<size_t>(j) * dim + c];
                     g2 += g * g;
                 }
-                const double b = 200.0 * u * std::sqrt(g2) * (1.0 + std::ldexp(1.0, -10));
+                const double b = k * u * std::sqrt(g2) * (1.0 + std::ldexp(1.0, -10));
                 float bf = static_cast<float>(b);
                 if (static_cast<double>(bf) < b) bf = std::nextafter(bf, std::numeric_limits<float>::infinity());
-                p->qb[(t * 16 + q) * 64 + lane] = bf;
+                p->qb[(t * nb + r) * 64 + lane] = bf;
             }
         }
 }
@@ -700,7 +716,7 @@ static int turbo_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t bits, uint3
     if (!rc) rc = upload(&p->d_signs, p->signs);
     if (!rc) rc = upload(&p->d_qjl, p->qjl);
     if (!rc) rc = upload(&p->d_cs, p->cs);
-    if (!rc && dim == 64 && qrows) {
+    if (!rc && (dim == 64 || dim == 128) && qrows) {
         turbo_qjl_mfma_constants(p);
         rc = upload(&p->d_qa, p->qa);
         if (!rc) rc = upload(&p->d_qb, p->qb);

@@ -36,6 +36,7 @@ constexpr int WAVES = TILE / WAVE;
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 __constant__ LogfEntry c_logf_tab[16] = {PKV_LOGF_TABLE};
 __constant__ uint64_t c_exp2f_tab[32] = {PKV_EXP2F_TABLE};
@@ -840,6 +841,342 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
         lds_to_global(blob + 38 + static_cast<uint64_t>(t0) * plen, pay, nv * plen, lane);
     } while (false);
     if (tile == 0 && (blockIdx.x & 1u) == 0 && threadIdx.x < 38) {
+        blob[threadIdx.x] = static_cast<uint8_t>(
+            tqb1_byte(threadIdx.x, DIM, pbits, lc.radii, proj, seed, seg.n_vectors, plen));
+    }
+}
+
+// Head_dim 128: four lanes per vector.  Lane (q, n) = (lane / 16, lane % 16)
+// holds elements 32q .. 32q + 31 of vector n of a 16-vector group.  FWHT
+// stages 1..16 run in registers, stage 32 pairs quarters q and q ^ 1 through
+// v_permlane16_swap, stage 64 pairs q and q ^ 2 through v_permlane32_swap
+// (same operands and rounding as fwht_normalized).  The QJL dots come from
+// v_mfma_f32_16x16x4_f32: its B operand takes lane (q, n) as (K slot q,
+// column n), so K-step c covers dimensions 32q + c of the 16 vectors, and
+// a 16-projection tile accumulates in 4 registers per lane (projection
+// 16p + 4q + r of vector n in register r).  A sign is taken when
+// |dot'| > 400 * 2^-24 * |g_j| * |res| * (1 + 2^-10): the reference's 128
+// sequential products and sums stay within 130u sum|g_c res_c| and the
+// matrix core's within 258u (twice the sequential count), with
+// sum|g_c res_c| <= |g_j| |res|; the other dots are recomputed in the
+// reference's order, each quarter continuing the previous quarter's sum.
+constexpr int QA128_PER_TILE = 32 * 64;   // A operand floats of one 16-projection tile
+constexpr int QB128_PER_TILE = 4 * 64;    // bound floats of one 16-projection tile
+
+// Value of lane l ^ 16 (the other quarter of the same half).
+__device__ __forceinline__ uint32_t partner16(uint32_t x, int q) {
+    const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (q & 1) ? p[0] : p[1];
+}
+
+// fwht_normalized stages (turbo-quant/src/rotation.rs:379-398) on a 128-wide
+// vector split over four lanes, 32 elements per lane.
+__device__ __forceinline__ void fwht_quarter(float (&v)[32], int q) {
+#pragma unroll
+    for (int step = 1; step < 32; step *= 2) {
+#pragma unroll
+        for (int start = 0; start < 32; start += 2 * step) {
+#pragma unroll
+            for (int off = 0; off < step; ++off) {
+                const float a = v[start + off], b = v[start + off + step];
+                v[start + off] = a + b;
+                v[start + off + step] = a - b;
+            }
+        }
+    }
+    // step 32: element c of quarter 2k with c of quarter 2k + 1: (a + b, a - b)
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+        const float o = u2f(partner16(f2u(v[c]), q));
+        v[c] = (q & 1) ? o - v[c] : v[c] + o;
+    }
+    // step 64: quarters 0, 1 with 2, 3
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+        const float o = u2f(partner(f2u(v[c]), q >> 1));
+        v[c] = (q & 2) ? o - v[c] : v[c] + o;
+    }
+}
+
+// OR of a value over the four lanes of a vector.
+__device__ __forceinline__ uint32_t or_quarters(uint32_t x, int q) {
+    x |= partner16(x, q);
+    return x | partner(x, q >> 1);
+}
+
+template <int PB>
+__global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
+    LaunchCommon lc, const void* __restrict__ in, uint8_t* __restrict__ wire, const float* __restrict__ signs,
+    const float* __restrict__ qjl, const float* __restrict__ cs_tab, const float* __restrict__ qa,
+    const float* __restrict__ qb, uint64_t seed, uint32_t pbits_rt, uint32_t proj) {
+    constexpr int DIM = 128;
+    constexpr int HP = 16;   // pairs per lane
+    constexpr int GV = 16;   // vectors per wave
+    extern __shared__ uint32_t smem_u[];   // per wave: 16 payloads
+    __shared__ float cs_lds[512];
+    __shared__ LogfEntry logf_lds[16];
+
+    const uint32_t pbits = PB ? static_cast<uint32_t>(PB) : pbits_rt;
+    const uint32_t levels = 1u << pbits;
+    for (uint32_t t = threadIdx.x; t < 2 * levels; t += blockDim.x) cs_lds[t] = cs_tab[t];
+    if (threadIdx.x < 16) logf_lds[threadIdx.x] = c_logf_tab[threadIdx.x];
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int q = lane >> 4, n = lane & 15;
+    // four workgroups per TILE-vector tile, one 16-vector group per wave
+    const uint32_t blk = blockIdx.x >> 2;
+    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const SegDev seg = lc.segs[sidx];
+    const uint32_t tile = blk - lc.tile_start[sidx];
+    const uint32_t plen = lc.plen, pwd = plen >> 2;
+    const bool f32r = lc.radii == PKV_RADII_F32;
+    uint32_t* pay = smem_u + wave * (GV * pwd + 4);
+    uint8_t* blob = wire + seg.wire_offset;
+    const bool bf16 = lc.in_bf16 != 0;
+    const float scale = fwht_scale<DIM>();
+    const uint32_t rwords = f32r ? 64u : 64u / 4 + 2;          // radii words in the payload
+    const uint32_t bwords = (64u * pbits + 31) / 32;            // angle index words
+
+    auto load_signs = [&](float (&sg)[32]) {
+        const float4* sp = reinterpret_cast<const float4*>(signs + 32 * q);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float4 v = sp[k];
+            sg[4 * k] = v.x; sg[4 * k + 1] = v.y; sg[4 * k + 2] = v.z; sg[4 * k + 3] = v.w;
+        }
+    };
+
+    do {
+        const uint32_t t0 = tile * TILE + (blockIdx.x & 3u) * (TILE / 4) + GV * static_cast<uint32_t>(wave);
+        if (t0 >= seg.n_vectors) break;
+        const uint32_t nv = min(static_cast<uint32_t>(GV), seg.n_vectors - t0);
+        const bool active = static_cast<uint32_t>(n) < nv;   // other lanes repeat the last vector
+        const uint64_t off = vec_elem_offset(seg, t0 + min(static_cast<uint32_t>(n), nv - 1)) + 32u * q;
+        uint32_t* pv = pay + n * pwd;   // this vector's payload
+
+        float y[32];
+        auto load_quarter = [&](float (&v)[32]) {
+            if (!bf16) {
+                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(in) + off);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float4 w = src[k];
+                    v[4 * k] = w.x; v[4 * k + 1] = w.y; v[4 * k + 2] = w.z; v[4 * k + 3] = w.w;
+                }
+            } else {
+                const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(in) + off);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint4 w = src[k];
+                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        v[8 * k + 2 * t] = u2f(ww[t] << 16);
+                        v[8 * k + 2 * t + 1] = u2f(ww[t] & 0xffff0000u);
+                    }
+                }
+            }
+        };
+        load_quarter(y);
+        bool finite = true;
+        {
+            float sg[32];
+            load_signs(sg);
+#pragma unroll
+            for (int c = 0; c < 32; ++c) {
+                finite &= isfinite_f(y[c]);
+                y[c] = y[c] * sg[c];
+            }
+        }
+        fwht_quarter(y, q);
+#pragma unroll
+        for (int c = 0; c < 32; ++c) y[c] *= scale;
+
+        // zero this vector's angle index words: all quarters OR into them
+        if (q == 0 && active)
+            for (uint32_t k = 0; k < bwords; ++k) pv[rwords + k] = 0u;
+        wave_sync();
+
+        // radii and angle bins (polar.rs:246-266, 413-421) of pairs 16q + i
+        float r[HP];
+        bool rfinite = true;
+        uint64_t pk = 0;
+        uint32_t slow = 0;
+#pragma unroll
+        for (int i = 0; i < HP; ++i) {
+            const float a = y[2 * i], b = y[2 * i + 1];
+            const float aa = a * a, bb = b * b;
+            r[i] = __builtin_sqrtf(aa + bb);
+            rfinite &= isfinite_f(r[i]);
+            uint32_t safe = 0u;
+            const uint32_t bin = PB == 3 ? octant_bin_u(a, b, safe) : 0u;
+            pk |= static_cast<uint64_t>(bin) << (static_cast<uint32_t>(i) * pbits);
+            slow |= (safe ^ 1u) << i;
+        }
+        if (slow) {   // pairs near an octant line (every pair at other widths): the exact formula
+            float ys[32];
+#pragma unroll
+            for (int c = 0; c < 32; ++c) ys[c] = y[c];
+            for (uint32_t m = slow; m; m &= m - 1u) {
+                const uint32_t i = static_cast<uint32_t>(__ffs(m) - 1);
+                const uint64_t bin = angle_bin_exact(ys[2 * i], ys[2 * i + 1], pbits);
+                pk = (pk & ~(static_cast<uint64_t>(levels - 1u) << (i * pbits))) | (bin << (i * pbits));
+            }
+        }
+        // angle indices, pbits each, LSB-first (bitpack.rs:21-35): this
+        // quarter's 16 * pbits bits start at bit 16 * pbits * q
+        if (active) {
+            const uint32_t bit0 = 16u * pbits * static_cast<uint32_t>(q);
+            const uint32_t nb = 16u * pbits;   // <= 64 bits (pbits <= 4)
+            uint32_t* bwp = pv + rwords + (bit0 >> 5);
+            const uint32_t sh = bit0 & 31u;
+            const uint32_t w0 = static_cast<uint32_t>(pk << sh);
+            const uint32_t w1 = static_cast<uint32_t>((pk << sh) >> 32) | (sh ? static_cast<uint32_t>(pk >> (64 - sh)) : 0u);
+            const uint32_t w2 = sh ? static_cast<uint32_t>(pk >> (96 - sh)) : 0u;
+            atomicOr(bwp, w0);
+            if (sh + nb > 32) atomicOr(bwp + 1, w1);
+            if (sh + nb > 64) atomicOr(bwp + 2, w2);
+        }
+        if (f32r) {
+            if (active)
+#pragma unroll
+                for (int i = 0; i < HP; ++i) pv[16 * q + i] = f2u(r[i]);
+        } else {
+            // CompressedRadiiV1 BlockLogU8 (turbo-quant/src/radius.rs:58-77)
+            float lg[HP];
+            float mn = u2f(0x7f800000u), mx = u2f(0xff800000u);
+#pragma unroll
+            for (int i = 0; i < HP; ++i) {
+                const float v = r[i] < 1.17549435e-38f ? 1.17549435e-38f : r[i];
+                lg[i] = og_logf_normal(v, logf_lds);
+                mn = __builtin_fminf(mn, lg[i]);
+                mx = __builtin_fmaxf(mx, lg[i]);
+            }
+            mn = __builtin_fminf(mn, u2f(partner16(f2u(mn), q)));
+            mx = __builtin_fmaxf(mx, u2f(partner16(f2u(mx), q)));
+            mn = __builtin_fminf(mn, u2f(partner(f2u(mn), q >> 1)));
+            mx = __builtin_fmaxf(mx, u2f(partner(f2u(mx), q >> 1)));
+            const float span = __builtin_fmaxf(mx - mn, 1.1920929e-07f);
+            if (active) {
+#pragma unroll
+                for (int i = 0; i < HP; i += 4) {
+                    uint32_t packed = 0;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        float nrm = (lg[i + t] - mn) / span;
+                        nrm = nrm < 0.0f ? 0.0f : (nrm > 1.0f ? 1.0f : nrm);
+                        const float qv = __builtin_roundf(nrm * 255.0f);
+                        packed |= static_cast<uint32_t>(qv) << (8 * t);
+                    }
+                    pv[4 * q + i / 4] = packed;
+                }
+                if (q == 0) {
+                    pv[16] = f2u(mn);
+                    pv[17] = f2u(mx);
+                }
+            }
+        }
+
+        // polar decode of the code just produced (polar.rs:272-278, 306-316)
+#pragma unroll
+        for (int i = 0; i < HP; ++i) {
+            const uint32_t bin = static_cast<uint32_t>(pk >> (static_cast<uint32_t>(i) * pbits)) & (levels - 1u);
+            y[2 * i] = r[i] * cs_lds[2 * bin];
+            y[2 * i + 1] = r[i] * cs_lds[2 * bin + 1];
+        }
+        fwht_quarter(y, q);
+        // residual against x read again (turbo.rs:269-273)
+        asm volatile("" ::: "memory");
+        {
+            float x[32], sg[32];
+            load_quarter(x);
+            load_signs(sg);
+#pragma unroll
+            for (int c = 0; c < 32; ++c) y[c] = x[c] - (y[c] * scale) * sg[c];
+        }
+        bool resfinite = true;
+        float rn2 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 32; ++c) {
+            resfinite &= isfinite_f(y[c]);
+            rn2 = __builtin_fmaf(y[c], y[c], rn2);
+        }
+        rn2 = rn2 + u2f(partner16(f2u(rn2), q));
+        rn2 = rn2 + u2f(partner(f2u(rn2), q >> 1));
+        const float rn = __builtin_sqrtf(rn2) * 1.0001f;   // |res|, rounded up far past its f32 error
+
+        uint32_t sbits[2] = {0u, 0u}, unc[2] = {0u, 0u};
+        const uint32_t ptiles = proj / 16;
+#pragma unroll
+        for (uint32_t p = 0; p < 4; ++p) {
+            if (p >= ptiles) break;
+            const float* qa_p = qa + p * QA128_PER_TILE;
+            const float* qb_p = qb + p * QB128_PER_TILE;
+            v4f acc = {};
+#pragma unroll
+            for (int c = 0; c < 32; ++c)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa_p[c * 64 + lane], y[c], acc, 0, 0, 0);
+            // register r: projection 16p + 4q + r of vector n
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const uint32_t j = 16u * p + 4u * static_cast<uint32_t>(q) + static_cast<uint32_t>(rr);
+                const float bnd = qb_p[rr * 64 + lane] * rn;
+                sbits[j >> 5] |= (acc[rr] >= 0.0f ? 1u : 0u) << (j & 31u);
+                unc[j >> 5] |= (__builtin_fabsf(acc[rr]) > bnd ? 0u : 1u) << (j & 31u);
+            }
+        }
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            sbits[w] = or_quarters(sbits[w], q);
+            unc[w] = or_quarters(unc[w], q);
+        }
+        // undecided signs: the reference's sequential dot, each quarter
+        // continuing the previous quarter's partial sum
+        if (__ballot(active && (unc[0] | unc[1]) != 0u)) {
+#pragma unroll
+            for (uint32_t w = 0; w < 2; ++w) {
+                if (32u * w >= proj) break;
+                const uint32_t m = active ? unc[w] : 0u;
+                uint32_t any = m;
+                for (int sh2 = 1; sh2 < 64; sh2 <<= 1) any |= __shfl_xor(any, sh2);
+                while (any) {
+                    const uint32_t j = static_cast<uint32_t>(__ffs(any) - 1);
+                    any &= any - 1u;
+                    const float* g = qjl + static_cast<size_t>(32 * w + j) * DIM + 32 * q;
+                    float run = 0.0f;
+                    for (int st = 0; st < 4; ++st) {
+                        if (q == st) {
+                            float d = run;
+#pragma unroll
+                            for (int c = 0; c < 32; ++c) d = d + g[c] * y[c];
+                            run = d;
+                        }
+                        const float prev = __shfl(run, lane >= 16 ? lane - 16 : lane);
+                        if (q == st + 1) run = prev;
+                    }
+                    const float full = __shfl(run, 48 + n);   // quarter 3 holds the whole sum
+                    if ((m >> j) & 1u) sbits[w] = (sbits[w] & ~(1u << j)) | (full >= 0.0f ? 1u << j : 0u);
+                }
+            }
+        }
+
+        // status (per vector, first failure in vector order) and the QJL words
+        const bool fin_v = or_quarters(finite ? 0u : 1u, q) == 0u;
+        const bool rfin_v = or_quarters(rfinite ? 0u : 1u, q) == 0u;
+        const bool resfin_v = or_quarters(resfinite ? 0u : 1u, q) == 0u;
+        if (active && q == 0) {
+            const uint32_t vi = t0 + n;
+            if (!fin_v) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_INPUT);
+            else if (!rfin_v) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RADIUS);
+            else if (!resfin_v) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RESIDUAL);
+            pv[rwords + bwords] = sbits[0];
+            if (proj > 32) pv[rwords + bwords + 1] = sbits[1];
+        }
+        wave_sync();
+        lds_to_global(blob + 38 + static_cast<uint64_t>(t0) * plen, pay, nv * plen, lane);
+    } while (false);
+    if (tile == 0 && (blockIdx.x & 3u) == 0 && threadIdx.x < 38) {
         blob[threadIdx.x] = static_cast<uint8_t>(
             tqb1_byte(threadIdx.x, DIM, pbits, lc.radii, proj, seed, seg.n_vectors, plen));
     }
@@ -1848,6 +2185,7 @@ int launch_turbo_encode(const LaunchCommon& lc, const TurboDev& td, const void* 
                         uint32_t nblocks, void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (td.dim == 64 && td.mode && td.qa && td.pbits <= 4) {
+        if (nblocks > (1u << 30)) return hipErrorInvalidValue;   // 2 workgroups per tile
         const size_t vec_words = (lc.plen >> 2) + (lc.radii == PKV_RADII_F32 ? 0u : 32u);
         const size_t lds = static_cast<size_t>(WAVES) * (32 * vec_words + 4) * sizeof(uint32_t);
         return td.pbits == 3
@@ -1855,6 +2193,15 @@ int launch_turbo_encode(const LaunchCommon& lc, const TurboDev& td, const void* 
                                     td.cs, td.qa, td.qb, td.seed, td.pbits, td.proj)
                    : launch_big_lds(turbo_encode_qjl_kernel<0>, 2 * nblocks, lds, st, lc, in, wire, td.signs, td.qjl,
                                     td.cs, td.qa, td.qb, td.seed, td.pbits, td.proj);
+    }
+    if (td.dim == 128 && td.mode && td.qa && td.pbits <= 4) {
+        if (nblocks > (1u << 29)) return hipErrorInvalidValue;   // 4 workgroups per tile
+        const size_t lds = static_cast<size_t>(WAVES) * (16 * (lc.plen >> 2) + 4) * sizeof(uint32_t);
+        return td.pbits == 3
+                   ? launch_big_lds(turbo_encode_qjl128_kernel<3>, 4 * nblocks, lds, st, lc, in, wire, td.signs,
+                                    td.qjl, td.cs, td.qa, td.qb, td.seed, td.pbits, td.proj)
+                   : launch_big_lds(turbo_encode_qjl128_kernel<0>, 4 * nblocks, lds, st, lc, in, wire, td.signs,
+                                    td.qjl, td.cs, td.qa, td.qb, td.seed, td.pbits, td.proj);
     }
     if (td.dim == 64)
         return td.pbits == 3

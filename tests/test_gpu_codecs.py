@@ -57,6 +57,35 @@ def test_turbo_dim128_bit_exact(ctx):
         assert rel_err(dec, O.turbo_decode_batch(blob, 128, SEED)) <= 1e-6
 
 
+@pytest.mark.parametrize("n", [1, 15, 16, 17, 63, 257, 1000])
+def test_turbo_dim128_group_sizes(ctx, n):
+    """Head_dim 128 encodes 16 vectors per wave (four lanes each): partial
+    groups and tiles, both radii codecs, bit-exact."""
+    x = kv_vectors(900 + n, n, 128)
+    for rc in (0, 1):
+        ad = TurboQuantAdapter(128, 4, 32, RadiiCompression.Lossy if rc else RadiiCompression.Lossless)
+        blob = ad.encode_batch_compact(x, SEED)
+        assert blob == O.turbo_encode_batch(x, SEED, radii_codec=rc)
+        assert np.array_equal(ad.decode_batch_compact(blob, SEED).view(np.uint32),
+                              O.turbo_decode_batch(blob, 128, SEED).view(np.uint32))
+
+
+def test_turbo_dim128_edge_inputs_and_projections(ctx):
+    rng = np.random.RandomState(8)
+    x = rng.randn(80, 128).astype(np.float32)
+    x[0] = 0.0                      # zero residual: every QJL sign takes the exact path
+    x[1] = -0.0
+    x[2, ::2] = 0.0
+    x[3] = 1e-30
+    x[4] = np.float32(1e18)
+    x[5, :] = np.arange(128, dtype=np.float32)
+    x[6] = 1.0                      # a constant vector: one non-zero Hadamard coefficient
+    for proj in (32, 64):
+        prof = ctx.turbo_profile(128, 4, proj, SEED, 1)
+        for rc in (L.RADII_F32, L.RADII_LOG_U8):
+            assert prof.encode_batch_compact(x, rc) == O.turbo_encode_batch(x, SEED, proj=proj, radii_codec=rc)
+
+
 @pytest.mark.parametrize("bits,mode", [(8, 1), (4, 0), (2, 1)])
 def test_turbo_other_bit_widths(ctx, bits, mode):
     x = kv_vectors(7, 200)
