@@ -1414,6 +1414,123 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split_kernel(
     stage_rows_out<DIM>(out, lc, stage, seg, t0, nv, static_cast<uint32_t>(badm), 0u, lane);
 }
 
+// Turbo decode at head_dim 128: four lanes per vector as in
+// turbo_encode_qjl128_kernel, one 16-vector group per wave, four workgroups
+// per tile; rows leave through LDS, 512 B contiguous per row.
+__host__ __device__ constexpr uint32_t turbo_split128_wave_words(uint32_t pwd) {
+    return (16 * pwd + 4 > 16 * (128 + 4) + 4) ? 16 * pwd + 4 : 16 * (128 + 4) + 4;
+}
+
+template <int PB>
+__global__ __launch_bounds__(TILE) void turbo_decode_split128_kernel(
+    LaunchCommon lc, const uint8_t* __restrict__ wire, void* __restrict__ out,
+    const float* __restrict__ signs, const float* __restrict__ cs_tab, uint64_t seed, uint32_t pbits_rt,
+    uint32_t proj) {
+    constexpr int DIM = 128;
+    constexpr int HP = 16;
+    constexpr int GV = 16;
+    extern __shared__ uint32_t smem_u[];   // per wave: 16 payloads, then 16 decoded rows
+    __shared__ float cs_lds[512];
+    __shared__ uint64_t exp_lds[32];
+
+    const uint32_t pbits = PB ? static_cast<uint32_t>(PB) : pbits_rt;
+    const uint32_t levels = 1u << pbits;
+    for (uint32_t t = threadIdx.x; t < 2 * levels; t += blockDim.x) cs_lds[t] = cs_tab[t];
+    if (threadIdx.x < 32) exp_lds[threadIdx.x] = c_exp2f_tab[threadIdx.x];
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int q = lane >> 4, n = lane & 15;
+    const uint32_t blk = blockIdx.x >> 2;
+    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const SegDev seg = lc.segs[sidx];
+    const uint32_t tile = blk - lc.tile_start[sidx];
+    const uint32_t plen = lc.plen, pwd = plen >> 2;
+    const uint8_t* blob = wire + seg.wire_offset;
+
+    // header check (every wave; 38 bytes)
+    const uint32_t hb = lane < 38 ? blob[lane] : 0u;
+    const bool hbad = lane < 38 && tqb1_checked(lane) &&
+                      hb != tqb1_byte(lane, DIM, pbits, lc.radii, proj, seed, seg.n_vectors, plen);
+    if (__ballot(hbad) != 0ull) {
+        if (lane == 0) status_fail(lc.status, sidx, 0, 0u, KIND_HEADER);
+        return;
+    }
+    const uint32_t t0 = tile * TILE + (blockIdx.x & 3u) * (TILE / 4) + GV * static_cast<uint32_t>(wave);
+    if (t0 >= seg.n_vectors) return;
+    const uint32_t nv = min(static_cast<uint32_t>(GV), seg.n_vectors - t0);
+    uint32_t* sw = smem_u + wave * turbo_split128_wave_words(pwd);
+    global_to_lds(sw, blob + 38 + static_cast<uint64_t>(t0) * plen, nv * plen, lane);
+    wave_sync();
+
+    const bool active = static_cast<uint32_t>(n) < nv;
+    const uint32_t* pw = sw + min(static_cast<uint32_t>(n), nv - 1) * pwd;
+    const bool f32r = lc.radii == PKV_RADII_F32;
+    const uint32_t rwords = f32r ? 64u : 64u / 4 + 2;
+    bool ok = true;
+    float r[HP];
+    if (f32r) {
+#pragma unroll
+        for (int i = 0; i < HP; ++i) {
+            r[i] = u2f(pw[16 * q + i]);
+            ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);   // radius.rs:88-104
+        }
+    } else {
+        const float mn = u2f(pw[16]), mx = u2f(pw[17]);
+        ok &= isfinite_f(mn) && isfinite_f(mx) && !(mn > mx);   // radius.rs:171-177
+        const float span = mx - mn;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t w = pw[4 * q + k];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float u = static_cast<float>((w >> (8 * t)) & 0xffu);
+                const int i = 4 * k + t;
+                r[i] = og_expf(mn + span * (u / 255.0f), exp_lds);   // radius.rs:128-145
+                ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);             // polar.rs:127-133
+            }
+        }
+    }
+    // this quarter's 16 angle indices: bits 16 pbits q .. (pbits <= 4: <= 64 bits)
+    const uint32_t bit0 = 16u * pbits * static_cast<uint32_t>(q);
+    const uint32_t* aw = pw + rwords + (bit0 >> 5);
+    const uint32_t sh = bit0 & 31u;
+    const uint64_t lo64 = static_cast<uint64_t>(aw[0]) | static_cast<uint64_t>(aw[1]) << 32;
+    uint64_t pk = lo64 >> sh;
+    if (sh) pk |= static_cast<uint64_t>(aw[2]) << (64 - sh);
+    // the angle field is 64 * pbits bits, a whole number of words: no padding
+    // bits to check (bitpack.rs:88-109); nor in the 32/64-bit QJL field
+
+    float y[32];
+#pragma unroll
+    for (int i = 0; i < HP; ++i) {
+        const uint32_t bin = static_cast<uint32_t>(pk >> (static_cast<uint32_t>(i) * pbits)) & (levels - 1u);
+        y[2 * i] = r[i] * cs_lds[2 * bin];
+        y[2 * i + 1] = r[i] * cs_lds[2 * bin + 1];
+    }
+    fwht_quarter(y, q);
+    const float scale = fwht_scale<DIM>();
+    const bool vok = or_quarters(ok ? 0u : 1u, q) == 0u;
+    if (active && q == 0 && !vok) status_fail(lc.status, sidx, 1, t0 + n, KIND_CORRUPT);
+    // rows through LDS (over the consumed payloads) so they leave coalesced
+    wave_sync();
+    float* stage = reinterpret_cast<float*>(sw);
+    {
+        float* srow = stage + n * (DIM + 4) + 32 * q;
+        const float4* sp = reinterpret_cast<const float4*>(signs + 32 * q);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float4 sg = sp[k];
+            *reinterpret_cast<float4*>(srow + 4 * k) =
+                make_float4((y[4 * k] * scale) * sg.x, (y[4 * k + 1] * scale) * sg.y, (y[4 * k + 2] * scale) * sg.z,
+                            (y[4 * k + 3] * scale) * sg.w);
+        }
+    }
+    const uint64_t badm = __ballot(active && q == 0 && !vok);
+    wave_sync();
+    stage_rows_out<DIM>(out, lc, stage, seg, t0, nv, static_cast<uint32_t>(badm), 0u, lane);
+}
+
 // ------------------------------------------------------------ fib encode
 // FibQuantizer::encode_batch (fib-quant/src/codec.rs:578-729; n < 4 takes
 // FibQuantizer::encode, 471-516) + FibCodeV1::encode_batch (FB2, 225-320).
@@ -2225,6 +2342,14 @@ int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_
                                               td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode)
                              : launch_big_lds(turbo_decode_split_kernel<0>, 2 * nblocks, lds, st, lc, wire, out,
                                               td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode);
+    }
+    if (td.dim == 128 && td.pbits <= 4) {
+        if (nblocks > (1u << 29)) return hipErrorInvalidValue;   // 4 workgroups per tile
+        const size_t lds = static_cast<size_t>(WAVES) * turbo_split128_wave_words(lc.plen >> 2) * sizeof(uint32_t);
+        return td.pbits == 3 ? launch_big_lds(turbo_decode_split128_kernel<3>, 4 * nblocks, lds, st, lc, wire, out,
+                                              td.signs, td.cs, td.seed, td.pbits, td.proj)
+                             : launch_big_lds(turbo_decode_split128_kernel<0>, 4 * nblocks, lds, st, lc, wire, out,
+                                              td.signs, td.cs, td.seed, td.pbits, td.proj);
     }
     if (td.dim == 64)
         return td.pbits == 3
