@@ -41,6 +41,16 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 __constant__ LogfEntry c_logf_tab[16] = {PKV_LOGF_TABLE};
 __constant__ uint64_t c_exp2f_tab[32] = {PKV_EXP2F_TABLE};
 
+// u / 255.0f for every u8 code u (radius.rs:139-143), correctly rounded by the
+// compiler at build time: the decode reads it instead of dividing per radius.
+struct Div255 {
+    float v[256];
+    constexpr Div255() : v() {
+        for (int u = 0; u < 256; ++u) v[u] = static_cast<float>(u) / 255.0f;
+    }
+};
+__constant__ Div255 c_div255 = Div255();
+
 // ------------------------------------------------------------ helpers
 __device__ __forceinline__ uint32_t find_segment(const uint32_t* __restrict__ tile_start, uint32_t nseg,
                                                  uint32_t blk) {
@@ -1194,11 +1204,13 @@ __global__ __launch_bounds__(TILE) void turbo_decode_kernel(
     extern __shared__ float smem[];
     __shared__ float cs_lds[512];
     __shared__ uint64_t exp_lds[32];
+    __shared__ float div255_lds[256];
 
     const uint32_t pbits = PB ? static_cast<uint32_t>(PB) : pbits_rt;
     const uint32_t levels = 1u << pbits;
     for (uint32_t t = threadIdx.x; t < 2 * levels; t += blockDim.x) cs_lds[t] = cs_tab[t];
     if (threadIdx.x < 32) exp_lds[threadIdx.x] = c_exp2f_tab[threadIdx.x];
+    for (uint32_t t = threadIdx.x; t < 256; t += blockDim.x) div255_lds[t] = c_div255.v[t];
     __syncthreads();
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1247,8 +1259,8 @@ __global__ __launch_bounds__(TILE) void turbo_decode_kernel(
             float span = mx - mn;
 #pragma unroll
             for (int i = 0; i < PAIRS; ++i) {
-                float u = static_cast<float>((q[i >> 2] >> (8 * (i & 3))) & 0xffu);
-                r[i] = og_expf(mn + span * (u / 255.0f), exp_lds);   // radius.rs:128-145
+                const uint32_t u = (q[i >> 2] >> (8 * (i & 3))) & 0xffu;
+                r[i] = og_expf(mn + span * div255_lds[u], exp_lds);   // radius.rs:128-145
                 ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);     // polar.rs:127-133
             }
         }
@@ -1313,11 +1325,13 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split_kernel(
     extern __shared__ uint32_t smem_u[];   // per wave: 32 payloads
     __shared__ float cs_lds[512];
     __shared__ uint64_t exp_lds[32];
+    __shared__ float div255_lds[256];
 
     const uint32_t pbits = PB ? static_cast<uint32_t>(PB) : pbits_rt;
     const uint32_t levels = 1u << pbits;
     for (uint32_t t = threadIdx.x; t < 2 * levels; t += blockDim.x) cs_lds[t] = cs_tab[t];
     if (threadIdx.x < 32) exp_lds[threadIdx.x] = c_exp2f_tab[threadIdx.x];
+    for (uint32_t t = threadIdx.x; t < 256; t += blockDim.x) div255_lds[t] = c_div255.v[t];
     __syncthreads();
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1366,9 +1380,9 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split_kernel(
             const uint32_t q = pw[4 * h + k];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const float u = static_cast<float>((q >> (8 * t)) & 0xffu);
+                const uint32_t u = (q >> (8 * t)) & 0xffu;
                 const int i = 4 * k + t;
-                r[i] = og_expf(mn + span * (u / 255.0f), exp_lds);   // radius.rs:128-145
+                r[i] = og_expf(mn + span * div255_lds[u], exp_lds);   // radius.rs:128-145
                 ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);             // polar.rs:127-133
             }
         }
@@ -1432,11 +1446,13 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split128_kernel(
     extern __shared__ uint32_t smem_u[];   // per wave: 16 payloads, then 16 decoded rows
     __shared__ float cs_lds[512];
     __shared__ uint64_t exp_lds[32];
+    __shared__ float div255_lds[256];
 
     const uint32_t pbits = PB ? static_cast<uint32_t>(PB) : pbits_rt;
     const uint32_t levels = 1u << pbits;
     for (uint32_t t = threadIdx.x; t < 2 * levels; t += blockDim.x) cs_lds[t] = cs_tab[t];
     if (threadIdx.x < 32) exp_lds[threadIdx.x] = c_exp2f_tab[threadIdx.x];
+    for (uint32_t t = threadIdx.x; t < 256; t += blockDim.x) div255_lds[t] = c_div255.v[t];
     __syncthreads();
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1484,9 +1500,9 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split128_kernel(
             const uint32_t w = pw[4 * q + k];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const float u = static_cast<float>((w >> (8 * t)) & 0xffu);
+                const uint32_t u = (w >> (8 * t)) & 0xffu;
                 const int i = 4 * k + t;
-                r[i] = og_expf(mn + span * (u / 255.0f), exp_lds);   // radius.rs:128-145
+                r[i] = og_expf(mn + span * div255_lds[u], exp_lds);   // radius.rs:128-145
                 ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);             // polar.rs:127-133
             }
         }
