@@ -37,6 +37,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
 __constant__ LogfEntry c_logf_tab[16] = {PKV_LOGF_TABLE};
 __constant__ uint64_t c_exp2f_tab[32] = {PKV_EXP2F_TABLE};
@@ -200,14 +201,23 @@ __device__ __forceinline__ uint32_t pack_out2(float a, float b, uint32_t dt) {
 
 // Store four consecutive values of one output vector at element offset `off`
 // (a multiple of 4) in the decode's output dtype, in every fan-out copy.
+// NT: non-temporal stores, for callers that write whole rows per instruction
+// (the output is not read back by this launch); partial-row writers keep L2
+// write-combining (non-temporal made them 1.6x slower).
+template <bool NT = false>
 __device__ __forceinline__ void store_out4(void* __restrict__ out, const LaunchCommon& lc, uint64_t off, float4 v) {
     if (lc.out_dtype == PKV_F32) {
-        for (uint32_t k = 0; k < lc.fanout; ++k, off += lc.fanout_stride)
-            *reinterpret_cast<float4*>(static_cast<float*>(out) + off) = v;
+        const v4f q = {v.x, v.y, v.z, v.w};
+        for (uint32_t k = 0; k < lc.fanout; ++k, off += lc.fanout_stride) {
+            v4f* p = reinterpret_cast<v4f*>(static_cast<float*>(out) + off);
+            if (NT) __builtin_nontemporal_store(q, p); else *p = q;
+        }
     } else {
-        const uint2 w = make_uint2(pack_out2(v.x, v.y, lc.out_dtype), pack_out2(v.z, v.w, lc.out_dtype));
-        for (uint32_t k = 0; k < lc.fanout; ++k, off += lc.fanout_stride)
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + off) = w;
+        const v2u w = {pack_out2(v.x, v.y, lc.out_dtype), pack_out2(v.z, v.w, lc.out_dtype)};
+        for (uint32_t k = 0; k < lc.fanout; ++k, off += lc.fanout_stride) {
+            v2u* p = reinterpret_cast<v2u*>(static_cast<uint16_t*>(out) + off);
+            if (NT) __builtin_nontemporal_store(w, p); else *p = w;
+        }
     }
 }
 
@@ -232,7 +242,7 @@ __device__ void stage_rows_out(void* __restrict__ out, const LaunchCommon& lc, c
         uint32_t skip = r < 32 ? (skip_mask_lo >> r) & 1u : (skip_mask_hi >> (r - 32)) & 1u;
         if (skip) continue;
         uint64_t off = vec_elem_offset(s, v0 + r);
-        store_out4(out, lc, off + 4 * c, *reinterpret_cast<const float4*>(stage + r * PITCH + 4 * c));
+        store_out4<true>(out, lc, off + 4 * c, *reinterpret_cast<const float4*>(stage + r * PITCH + 4 * c));
     }
 }
 
