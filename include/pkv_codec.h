@@ -110,6 +110,18 @@ int pkv_fib_constants(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint3
                       uint32_t lloyd_restarts, uint32_t lloyd_iterations, float* codebook,
                       double* rotation, double* init_mse, double* training_mse);
 
+/* Profile-constant service.  The reference rebuilds a quantizer's constants
+ * on every adapter call (FibQuantAdapter::build_quantizer,
+ * proveKV/src/codec.rs:471-499, called 2x per layer in a pool build and per
+ * decompress, pool.rs:225, 265-266, 517-519; TurboQuantizer::new per turbo
+ * call, codec.rs:249, 296).  This library builds each distinct profile's
+ * constants (codebook, rotation, signs, QJL matrix) once per process, keyed
+ * by every parameter they depend on, and shares them across contexts and
+ * the host-only generators.  Stats: lookups served from the cache, builds,
+ * distinct entries; clear() drops them (the next request rebuilds). */
+void pkv_constants_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries);
+void pkv_constants_cache_clear(void);
+
 /* Copies the profile constants out (host memory).  turbo: a = signs[dim],
  * b = float qjl[proj*dim]; fib: a = float codebook[n*k], b = double rot[dim*dim]. */
 int pkv_profile_constants(const pkv_profile* prof, void* a, size_t a_bytes, void* b, size_t b_bytes);

@@ -1236,6 +1236,12 @@ int pkv_fib_constants(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint3
     return PKV_OK;
 }
 
+void pkv_constants_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries) {
+    constants_cache_stats(hits, misses, entries);
+}
+
+void pkv_constants_cache_clear(void) { constants_cache_clear(); }
+
 void pkv_host_angle_bins(const float* a, const float* b, uint64_t n, uint32_t pbits, uint32_t* out) {
     for (uint64_t i = 0; i < n; ++i) out[i] = pbits == 3 ? angle_bin3(a[i], b[i]) : angle_bin_exact(a[i], b[i], pbits);
 }

@@ -121,6 +121,9 @@ int make_fib_rotation(uint32_t dim, uint64_t seed, std::vector<double>& rot);
 int make_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint32_t training,
                       uint32_t restarts, uint32_t iterations, std::vector<float>& codebook,
                       double* init_mse, double* train_mse);
+// The make_* builders above memoise per process (one build per distinct profile).
+void constants_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries);
+void constants_cache_clear();
 
 // Kernel launchers (pkv_kernels.hip).  Return a hipError_t as int.
 int launch_turbo_encode(const LaunchCommon& lc, const TurboDev& td, const void* in, uint8_t* wire,

@@ -26,7 +26,11 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <memory>
 #include <mutex>
+#include <tuple>
+#include <type_traits>
 #include <vector>
 
 namespace pkv {
@@ -394,9 +398,11 @@ struct Lloyd {
 
 }  // namespace
 
-// -------------------------------------------------------------- public helpers
-int make_turbo_constants(uint32_t dim, uint32_t proj, uint64_t seed, std::vector<float>& signs,
-                         std::vector<float>& G) {
+// -------------------------------------------------------------- builders
+namespace {
+
+int build_turbo_constants(uint32_t dim, uint32_t proj, uint64_t seed, std::vector<float>& signs,
+                          std::vector<float>& G) {
     signs.assign(dim, 0.0f);
     ChaCha8 srng(seed + 0xA11CE55ED5A5EED5ull);
     for (uint32_t i = 0; i < dim; ++i) signs[i] = srng.gen_bool() ? 1.0f : -1.0f;
@@ -408,15 +414,15 @@ int make_turbo_constants(uint32_t dim, uint32_t proj, uint64_t seed, std::vector
     return PKV_OK;
 }
 
-int make_fib_rotation(uint32_t dim, uint64_t seed, std::vector<double>& rot) {
+int build_fib_rotation(uint32_t dim, uint64_t seed, std::vector<double>& rot) {
     if (dim == 0 || dim > 4096) return PKV_ERR_INVALID_ARG;
     rot = stored_rotation(static_cast<int>(dim), seed);
     return PKV_OK;
 }
 
-int make_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint32_t training,
-                      uint32_t restarts, uint32_t iterations, std::vector<float>& codebook,
-                      double* init_mse, double* train_mse) {
+int build_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint32_t training,
+                       uint32_t restarts, uint32_t iterations, std::vector<float>& codebook,
+                       double* init_mse, double* train_mse) {
     if (k < 4 || k > 32 || dim % k != 0 || n < 2 || dim <= k) return PKV_ERR_UNSUPPORTED;
     const uint64_t cseed = seed + 0x9e3779b97f4a7c15ull;
     const int K = static_cast<int>(k), N = static_cast<int>(n), D = static_cast<int>(dim);
@@ -497,6 +503,114 @@ int make_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint3
     if (init_mse) *init_mse = imse;
     if (train_mse) *train_mse = best_mse;
     return PKV_OK;
+}
+
+// ---- profile-constant service
+// The reference rebuilds a quantizer's constants on every adapter call: the
+// Lloyd codebook and the QR rotation 2x per layer in a pool build and again
+// per decompress (proveKV/src/codec.rs:471-499, pool.rs:225, 265-266,
+// 517-519), the Hadamard signs and QJL matrix per turbo call (codec.rs:249,
+// 296).  Here every distinct profile is built once per process and shared:
+// the key is the full parameter set the constants (and the reference's
+// profile digest) are a function of.
+struct FibCodebook {
+    std::vector<float> cb;
+    double init_mse, train_mse;
+};
+struct TurboConsts {
+    std::vector<float> signs, G;
+};
+using FibKey = std::tuple<uint32_t, uint32_t, uint32_t, uint64_t, uint32_t, uint32_t, uint32_t>;
+using RotKey = std::tuple<uint32_t, uint64_t>;
+using TurboKey = std::tuple<uint32_t, uint32_t, uint64_t>;
+
+struct ConstCache {
+    std::mutex mu;
+    std::map<FibKey, std::shared_ptr<const FibCodebook>> cb;
+    std::map<RotKey, std::shared_ptr<const std::vector<double>>> rot;
+    std::map<TurboKey, std::shared_ptr<const TurboConsts>> turbo;
+    uint64_t hits = 0, misses = 0;
+};
+ConstCache& cache() {
+    static ConstCache c;
+    return c;
+}
+
+// Look `key` up in `m`; on a miss build outside the lock (two threads may
+// both build a new key; the first insert wins and both results are equal).
+template <typename M, typename K, typename Build>
+int cached(M& m, const K& key, std::shared_ptr<const typename M::mapped_type::element_type>& out, Build build) {
+    ConstCache& c = cache();
+    {
+        std::lock_guard<std::mutex> lock(c.mu);
+        auto it = m.find(key);
+        if (it != m.end()) {
+            ++c.hits;
+            out = it->second;
+            return PKV_OK;
+        }
+        ++c.misses;
+    }
+    auto v = std::make_shared<std::remove_const_t<typename M::mapped_type::element_type>>();
+    int rc = build(*v);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lock(c.mu);
+    out = m.emplace(key, std::move(v)).first->second;
+    return PKV_OK;
+}
+
+}  // namespace
+
+// -------------------------------------------------------------- public helpers
+int make_turbo_constants(uint32_t dim, uint32_t proj, uint64_t seed, std::vector<float>& signs,
+                         std::vector<float>& G) {
+    std::shared_ptr<const TurboConsts> t;
+    int rc = cached(cache().turbo, TurboKey(dim, proj, seed), t,
+                    [&](TurboConsts& v) { return build_turbo_constants(dim, proj, seed, v.signs, v.G); });
+    if (rc) return rc;
+    signs = t->signs;
+    G = t->G;
+    return PKV_OK;
+}
+
+int make_fib_rotation(uint32_t dim, uint64_t seed, std::vector<double>& rot) {
+    std::shared_ptr<const std::vector<double>> r;
+    int rc = cached(cache().rot, RotKey(dim, seed), r,
+                    [&](std::vector<double>& v) { return build_fib_rotation(dim, seed, v); });
+    if (rc) return rc;
+    rot = *r;
+    return PKV_OK;
+}
+
+int make_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint32_t training,
+                      uint32_t restarts, uint32_t iterations, std::vector<float>& codebook,
+                      double* init_mse, double* train_mse) {
+    std::shared_ptr<const FibCodebook> f;
+    int rc = cached(cache().cb, FibKey(dim, k, n, seed, training, restarts, iterations), f, [&](FibCodebook& v) {
+        return build_fib_codebook(dim, k, n, seed, training, restarts, iterations, v.cb, &v.init_mse, &v.train_mse);
+    });
+    if (rc) return rc;
+    codebook = f->cb;
+    if (init_mse) *init_mse = f->init_mse;
+    if (train_mse) *train_mse = f->train_mse;
+    return PKV_OK;
+}
+
+void constants_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries) {
+    ConstCache& c = cache();
+    std::lock_guard<std::mutex> lock(c.mu);
+    if (hits) *hits = c.hits;
+    if (misses) *misses = c.misses;
+    if (entries) *entries = c.cb.size() + c.rot.size() + c.turbo.size();
+}
+
+void constants_cache_clear() {
+    ConstCache& c = cache();
+    std::lock_guard<std::mutex> lock(c.mu);
+    c.cb.clear();
+    c.rot.clear();
+    c.turbo.clear();
+    c.hits = c.misses = 0;
 }
 
 }  // namespace pkv

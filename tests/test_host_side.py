@@ -135,3 +135,37 @@ def test_angle_bins_match_glibc_atan2f_formula():
         f = np.floor(np.float32(u * np.float32(8.0)))
         want[i] = (int(f) if f > 0 else 0) % 8
     assert np.array_equal(got, want)
+
+
+def test_profile_constant_service_builds_each_profile_once():
+    """One build per distinct profile per process (the reference rebuilds on
+    every adapter call, proveKV/src/codec.rs:471-499): a second request is a
+    cache hit with identical constants; another seed is a new build."""
+    import time
+    lib = L.lib()
+    lib.pkv_constants_cache_clear()
+    cb1, cb2 = np.zeros(128, np.float32), np.zeros(128, np.float32)
+    rot1, rot2 = np.zeros(64 * 64), np.zeros(64 * 64)
+    t0 = time.perf_counter()
+    L.check(lib.pkv_fib_constants(64, 4, 32, 42, 2048, 4, 8, cb1.ctypes.data, rot1.ctypes.data, None, None), "fib")
+    t1 = time.perf_counter()
+    L.check(lib.pkv_fib_constants(64, 4, 32, 42, 2048, 4, 8, cb2.ctypes.data, rot2.ctypes.data, None, None), "fib")
+    t2 = time.perf_counter()
+    assert np.array_equal(cb1, cb2) and np.array_equal(rot1, rot2)
+    h, m, e = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+    lib.pkv_constants_cache_stats(ctypes.byref(h), ctypes.byref(m), ctypes.byref(e))
+    assert (h.value, m.value, e.value) == (2, 2, 2)        # codebook + rotation, built once each
+    assert t2 - t1 < (t1 - t0) / 5
+    cb3 = np.zeros(128, np.float32)
+    L.check(lib.pkv_fib_constants(64, 4, 32, 43, 2048, 4, 8, cb3.ctypes.data, None, None, None), "fib")
+    assert not np.array_equal(cb3, cb1)
+    s1, g1 = np.zeros(64, np.float32), np.zeros(32 * 64, np.float32)
+    s2, g2 = np.zeros(64, np.float32), np.zeros(32 * 64, np.float32)
+    L.check(lib.pkv_turbo_constants(64, 32, 42, s1.ctypes.data, g1.ctypes.data), "turbo")
+    L.check(lib.pkv_turbo_constants(64, 32, 42, s2.ctypes.data, g2.ctypes.data), "turbo")
+    assert np.array_equal(s1, s2) and np.array_equal(g1, g2)
+    lib.pkv_constants_cache_stats(ctypes.byref(h), ctypes.byref(m), ctypes.byref(e))
+    assert (h.value, m.value, e.value) == (3, 4, 4)
+    # the cached constants are the oracle's
+    ocb, _, _ = O.fib_codebook()
+    assert np.array_equal(cb1.reshape(32, 4), ocb)
