@@ -17,7 +17,8 @@ duration (HIP events on the launch stream) against 8 TB/s.
 cpu_baseline = the C oracle (a one-thread restatement of the reference Rust
 codecs) timed on a bounded sample of the same workload on the host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--lossy] [--workload pool|legacy]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--lossy]
+                       [--workload pool|legacy|config4|score]
 """
 from __future__ import annotations
 
@@ -319,6 +320,155 @@ def bench_config4(args):
     print(json.dumps(res), flush=True)
 
 
+VALU_PEAK_OPS = 256 * 4 * 16 * 2.4e9   # f32 lane-ops/s without packed FP32 (157.3 TFLOP/s / 4)
+
+
+def bench_score(args):
+    """Scoring on compressed keys (TurboQuantizer::inner_product_estimate_prepared,
+    the attention logits of KvShadowCache::attention_scores, turbo-quant/src/
+    kv.rs:269-320) at the config-4 shape: the K half of Llama-3-8B's KV
+    (32 layers x 8 KV heads x 32768 tokens, head_dim 128) as TQB1-L blobs
+    resident in HBM, one blob per (layer, KV head); each blob scored against
+    its GQA group of 4 query heads (32 query heads / 8 KV heads), scale
+    1/sqrt(128).  One step = prepare the 1024 queries + one scoring launch.
+    value = query-key scores per second.  Parity: sampled codes of several
+    blobs against the C oracle, bit for bit."""
+    import torch
+    from oracle import oracle as O
+    from provekv_amd import _lib as L
+    from provekv_amd import synth
+    from provekv_amd.device import SEG_DTYPE, default_context
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU"}))
+        sys.exit(1)
+    layers, kv_heads, tokens, dim, group, gen_layers = 32, 8, 32768, 128, 4, 2
+    log(f"[bench] generating {gen_layers} layers of config-4 keys")
+    K, _ = synth.kv_cache(4, gen_layers, kv_heads, tokens, dim, k_sigma=0.7, outliers=4, outlier_mult=10.0,
+                          v_scale=1.0)
+    block = torch.from_numpy(np.ascontiguousarray(K)).to(torch.bfloat16)   # [gl, H, T, D]
+    del K
+    nseg = layers * kv_heads
+    x = torch.empty((layers // gen_layers, block.numel()), dtype=torch.bfloat16, device="cuda")
+    x[:] = block.reshape(1, -1).cuda()
+    x = x.reshape(-1)
+    ctx = default_context()
+    prof = ctx.turbo_profile(dim, 4, 32, 42)
+    plen = prof.payload_len(L.RADII_LOG_U8)
+    blob = 38 + tokens * plen
+    segs = np.array([(b * tokens * dim, 0, dim, b * blob, tokens, tokens) for b in range(nseg)], dtype=SEG_DTYPE)
+    wire = torch.empty(nseg * blob, dtype=torch.uint8, device="cuda")
+    est = torch.empty(2 * nseg, dtype=torch.int32, device="cuda")
+    log(f"[bench] encoding {nseg} key blobs x {tokens} tokens (untimed)")
+    prof.encode_segments(x, segs, wire, radii=L.RADII_LOG_U8, status=est)
+    torch.cuda.synchronize()
+    err = prof.status_error(est.cpu().numpy().view(np.uint32), segs)
+    if err is not None:
+        raise err
+    del x
+    nq = nseg * group
+    rng = np.random.RandomState(11)
+    qh = rng.randn(nq, dim).astype(np.float32)
+    q = torch.from_numpy(qh).cuda()
+    W = prof.prepared_len()
+    prep = torch.empty((nq, W), dtype=torch.float32, device="cuda")
+    ld = nseg * tokens
+    scores = torch.empty(group * ld, dtype=torch.float32, device="cuda")
+    ssegs = np.array([(b * tokens, 1, 1, b * blob, tokens, 1) for b in range(nseg)], dtype=SEG_DTYPE)
+    pst = torch.empty(2, dtype=torch.int32, device="cuda")
+    sst = torch.empty(2 * nseg, dtype=torch.int32, device="cuda")
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(dim)))
+    stream = torch.cuda.current_stream()
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record(stream)
+        prof.prepare_queries(q, prep, status=pst)
+        if ev is not None:
+            ev[1].record(stream)
+        prof.score_segments(wire, ssegs, prep, scores, ld, radii=L.RADII_LOG_U8, post_scale=scale, status=sst,
+                            nq=group, query_stride=group)
+        if ev is not None:
+            ev[2].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    perr = prof.status_error(pst.cpu().numpy().view(np.uint32))
+    serr = prof.score_status_error(sst.cpu().numpy().view(np.uint32))
+    if perr is not None or serr is not None:
+        raise perr or serr
+    steps = max(1, args.steps)
+    log(f"[bench] timing {steps} steps")
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        step()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    step_ms = t0.elapsed_time(t1) / steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for k in range(steps):
+        step(evs[k])
+    torch.cuda.synchronize()
+    prep_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
+    score_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    # sampled parity: 256 codes of four blobs, every query of the group, bit for bit
+    pref = O.turbo_prepare_queries(qh, 42)
+    parity = np.array_equal(prep.cpu().numpy().view(np.uint32), pref.view(np.uint32))
+    got_all = scores.reshape(group, ld)
+    samp = np.random.RandomState(5)
+    for b in (0, 1, nseg // 2, nseg - 1):
+        idx = np.sort(samp.choice(tokens, 256, replace=False))
+        w = wire[b * blob:(b + 1) * blob].cpu().numpy()
+        sub = w[:38].copy()
+        sub[30:34] = np.frombuffer(np.uint32(len(idx)).tobytes(), np.uint8)
+        sub = sub.tobytes() + w[38:].reshape(tokens, plen)[idx].tobytes()
+        ref = O.turbo_score(sub, pref[b * group:(b + 1) * group], dim, 42) * np.float32(scale)
+        got = got_all[:, b * tokens:(b + 1) * tokens][:, idx].cpu().numpy()
+        parity &= np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    pairs = nseg * tokens * group
+    wire_bytes = nseg * blob
+    alg = wire_bytes + pairs * 4 + nq * W * 4
+    lane_ops = pairs * ((dim // 2) * 6 + 32)   # per pair: LDS offset + 2 mul + add + mul + add; 32 QJL FMAs
+    # CPU baseline: the oracle (one thread) scoring a bounded sample
+    cpu = None
+    if not args.no_cpu_baseline:
+        n_s = 20000
+        w0 = wire[:blob].cpu().numpy()
+        sub = w0[:38].copy()
+        sub[30:34] = np.frombuffer(np.uint32(n_s).tobytes(), np.uint8)
+        sub = sub.tobytes() + w0[38:38 + n_s * plen].tobytes()
+        reps, t_cpu = 0, 0.0
+        while t_cpu < 10.0:
+            c0 = time.perf_counter()
+            O.turbo_score(sub, pref[:group], dim, 42)
+            t_cpu += time.perf_counter() - c0
+            reps += 1
+        cpu = {"value": round(reps * n_s * group / t_cpu, 1), "unit": "scores/s", "cores": 1, "kind": "port",
+               "sample": f"{reps} x ({n_s} codes of blob 0 x {group} queries) through the C oracle's "
+                         "ora_turbo_score (validation + sequential estimator)"}
+    res = {"metric": "compressed-domain attention scores per second (TQB1-L keys, GQA 4)",
+           "value": round(pairs / (step_ms * 1e-3), 1), "unit": "scores/s", "n_gpus": 1, "steps": steps,
+           "warmup": args.warmup, "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "f32",
+           "data": f"synthetic (seeded config-4 keys, {gen_layers} generated layers tiled over {layers}; "
+                   "Gaussian queries)",
+           "config": {"workload": "score: config-4 keys (32L x 8 KV heads x 32768 tokens x d128, turbo b=4 QJL-32, "
+                                  "TQB1-L) x GQA groups of 4 query heads, scale 1/sqrt(128)",
+                      "blobs": nseg, "codes_per_blob": tokens, "queries": nq, "wire_bytes": wire_bytes},
+           "kernels_ms": {"prepare": round(prep_ms, 4), "score": round(score_ms, 4)},
+           "roofline": {"bound": "valu", "kernel": "turbo_score_kernel<128, 32>",
+                        "achieved": round(lane_ops / (score_ms * 1e-3) / 1e12, 2),
+                        "peak": round(VALU_PEAK_OPS / 1e12, 2), "unit": "T lane-ops/s",
+                        "frac": round(lane_ops / (score_ms * 1e-3) / VALU_PEAK_OPS, 4),
+                        "hbm_gbs": round(alg / (score_ms * 1e-3) / 1e9, 1),
+                        "hbm_frac": round(alg / (score_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                        "algorithmic_bytes": alg, "lane_ops": lane_ops},
+           "cpu_baseline": cpu, "parity_sampled": bool(parity)}
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -333,9 +483,10 @@ def main():
     ap.add_argument("--copies", type=int, default=8,
                     help="KV caches filled from one decode: config 3 rehydrates all 8 agents' full 1024-token "
                          "KV (default 8)")
-    ap.add_argument("--workload", choices=("pool", "legacy", "config4"), default="pool",
+    ap.add_argument("--workload", choices=("pool", "legacy", "config4", "score"), default="pool",
                     help="pool: the config-3 metric (default); legacy: per-vector TQW1 / FB1 records; "
-                         "config4: Llama-3-8B shape, bf16, d128, TQB1-L")
+                         "config4: Llama-3-8B shape, bf16, d128, TQB1-L; score: attention scores on "
+                         "config-4 compressed keys")
     args = ap.parse_args()
     if args.copies == 1:   # one cache: the fib decode stores directly (no LDS staging)
         KERNEL_SYMBOL["fib_decode"] = "fib_decode_mfma_kernel<64, false>"
@@ -348,6 +499,9 @@ def main():
         return
     if args.workload == "config4":
         bench_config4(args)
+        return
+    if args.workload == "score":
+        bench_score(args)
         return
 
     import torch

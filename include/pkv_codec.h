@@ -253,6 +253,57 @@ int pkv_decode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const ui
 int pkv_parse_header(const pkv_profile* prof, const uint8_t* blob, uint64_t len,
                      uint64_t* n_vectors, int* radii_codec);
 
+/* ---------------------------------------------------------------- scoring
+ * Inner-product scores straight from TQB1 codes, without decoding them:
+ * TurboQuantizer::prepare_query / inner_product_estimate_prepared /
+ * score_batch_prepared (turbo-quant/src/turbo.rs:316-381), the scorer under
+ * TurboIndex::search_prepared (index.rs:98-140) and
+ * KvShadowCache::attention_scores_with_options (kv.rs:269-320).  Turbo
+ * profiles only (head_dim 64 or 128). */
+
+/* Floats per prepared query: dim (+ proj with QJL): [R q][G q]. */
+uint32_t pkv_prepared_len(const pkv_profile* prof);
+
+/* prepare_query (turbo.rs:322-338; PolarQuantizer::project_query, polar.rs:
+ * 336-343; QjlQuantizer::project_query, qjl.rs:266-282) for nq device queries
+ * d_queries[nq][dim] (f32) into d_prepared[nq][pkv_prepared_len].  d_status:
+ * 2 device words (may be NULL); word 0 = (q << 4) | 0 for the first query
+ * with a non-finite input, rotated or projected value (NonFiniteInput). */
+int pkv_turbo_prepare_queries(pkv_ctx* ctx, const pkv_profile* prof, const float* d_queries, uint32_t nq,
+                              float* d_prepared, uint32_t* d_status, void* stream);
+
+/* inner_product_estimate_prepared of every code of every segment against
+ * nq prepared queries, times post_scale (1.0f for the plain score; the
+ * AttentionScale factor of attention_scores_with_options, applied after the
+ * score's finiteness check, kv.rs:305-318):
+ *     d_scores[q * ld + col(i)]  = score(code i of segment s, prepared row s * query_stride + q),
+ *     col(i) = elem_offset + (i / group) * stride_outer + (i % group) * stride_inner
+ * (the segment addressing of pkv_decode_segments, in score units; a
+ * contiguous layout is group = 1, stride_outer = 1).  query_stride = 0: all
+ * segments score the same nq queries; query_stride = nq: each (layer, KV
+ * head) segment scores its own group of query heads (GQA).  d_prepared holds
+ * prepared_rows rows of pkv_prepared_len floats.  Each blob's header is
+ * checked as pkv_decode_segments does.  d_status: 2*nseg device words (may be
+ * NULL): word 0 = a rejected header / code (no score written for it), word 1
+ * = a non-finite score (turbo.rs:362-367); pkv_score_status resolves them. */
+int pkv_turbo_score_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, const uint8_t* d_wire,
+                             uint64_t wire_bytes, const pkv_seg* segs, uint32_t nseg, const float* d_prepared,
+                             uint64_t prepared_rows, uint32_t nq, uint64_t query_stride, float post_scale,
+                             float* d_scores, uint64_t score_elems, uint64_t ld, uint32_t* d_status, void* stream);
+
+/* Status words of pkv_turbo_score_segments -> pkv_error: per segment in
+ * order, a rejected code (the blob is validated before any score) precedes a
+ * non-finite score; both are PKV_ERR_CORRUPT_PAYLOAD (MalformedCode). */
+int pkv_score_status(const uint32_t* host_status, uint32_t nseg, pkv_error* err);
+
+/* Host-buffer form: one TQB1 blob and nq host queries -> scores[nq][n]
+ * (row q = score_batch_prepared(prepare_query(queries[q]), codes)).  Errors:
+ * a non-finite query (PKV_ERR_NONFINITE_INPUT, index = query) before any
+ * rejected code or non-finite score (PKV_ERR_CORRUPT_PAYLOAD, index = code). */
+int pkv_turbo_score_batch(pkv_ctx* ctx, const pkv_profile* prof, const uint8_t* payload, uint64_t len,
+                          const float* queries, uint32_t nq, float post_scale, float* scores, uint64_t scores_cap,
+                          uint64_t* n_out, pkv_error* err);
+
 /* ---------------------------------------------------------------- host math
  * Host builds of the exact scalar routines the kernels use (test hooks):
  * angle bins of (a[i], b[i]) for pbits, and logf / expf over arrays. */

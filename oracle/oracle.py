@@ -119,6 +119,10 @@ def _declare(L):
     L.ora_fib_encode_fb1.restype = I32
     L.ora_fib_decode_fb1.argtypes = [U32, U32, U32, P, P, P, P, U64, I32, P, P]
     L.ora_fib_decode_fb1.restype = I32
+    L.ora_turbo_prepare_query.argtypes = [U32, U32, I32, P, P, P, P]
+    L.ora_turbo_prepare_query.restype = I32
+    L.ora_turbo_score.argtypes = [U32, U32, U32, U64, I32, P, P, U64, P, U32, P, P, P]
+    L.ora_turbo_score.restype = I32
     L.ora_pack_bits.argtypes = [P, U64, I32, P]
     L.ora_unpack_bits.argtypes = [P, U64, I32, P]
     L.ora_unpack_bits.restype = I32
@@ -429,6 +433,42 @@ def fib_decode_fb1(records: list, codebook: np.ndarray, rotation: np.ndarray, ea
     if rc:
         raise OracleError(rc, int(fail[0]))
     return out[:len(records)]
+
+
+# ---------------------------------------------------------------- scoring on codes
+def turbo_prepare_queries(q: np.ndarray, seed: int, proj=32, mode=1) -> np.ndarray:
+    """TurboQuantizer::prepare_query per row: [nq, dim + proj] (rotated, projected)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    nq, dim = q.shape
+    signs, G = turbo_constants(dim, proj if mode else 0, seed)
+    if G.size == 0:
+        G = np.zeros((1, dim), dtype=np.float32)
+    w = dim + (proj if mode else 0)
+    out = np.zeros((nq, w), dtype=np.float32)
+    for i in range(nq):
+        rc = lib().ora_turbo_prepare_query(dim, proj, mode, _p(signs), _p(np.ascontiguousarray(G, np.float32)),
+                                           _p(q[i]), out[i].ctypes.data_as(C.c_void_p))
+        if rc:
+            raise OracleError(rc, i)
+    return out
+
+
+def turbo_score(blob: bytes, prepared: np.ndarray, dim: int, seed: int, bits=4, proj=32, mode=1) -> np.ndarray:
+    """inner_product_estimate_prepared of every code of a TQB1 blob against
+    every prepared query: [nq, n]."""
+    signs, _ = turbo_constants(dim, 0, seed)
+    prepared = np.ascontiguousarray(prepared, dtype=np.float32)
+    nq = prepared.shape[0]
+    buf = np.frombuffer(blob, dtype=np.uint8).copy()
+    n_out = np.zeros(1, dtype=np.uint64)
+    fail = np.zeros(1, dtype=np.uint64)
+    n = (len(blob) - 38) // max(1, turbo_payload_len(dim, bits, proj, mode, blob[15] if len(blob) > 15 else 0))
+    scores = np.zeros((max(nq, 1), max(n, 1)), dtype=np.float32)
+    rc = lib().ora_turbo_score(dim, bits, proj, seed, mode, _p(signs), _p(buf), len(blob), _p(prepared), nq,
+                               _p(scores), _p(n_out), _p(fail))
+    if rc:
+        raise OracleError(rc, int(fail[0]))
+    return scores[:nq, :int(n_out[0])]
 
 
 def pack_bits(values, bits: int) -> bytes:

@@ -992,6 +992,7 @@ int ora_turbo_decode_batch(uint32_t dim, uint32_t bits, uint32_t proj, uint64_t 
         for (uint32_t i = 0; i < pairs; ++i)
             if (!isfinite(radii[i]) || radii[i] < 0.0f) { if (fail_index) *fail_index = v; return ORA_ERR_MALFORMED; }
     }
+    if (!out) return ORA_OK;   /* validation only */
     for (uint64_t v = 0; v < n; ++v) {
         const uint8_t* p = in + 38 + v * plen;
         if (rc_byte) {
@@ -1467,6 +1468,106 @@ int ora_fib_decode_fb1(uint32_t d, uint32_t k, uint32_t N, const float* cb, cons
     }
     free(m32);
     return rc;
+}
+
+/* ======================================================================
+ * 10. Scoring on compressed codes: TurboQuantizer::prepare_query and
+ *     inner_product_estimate_prepared (turbo-quant/src/turbo.rs:316-381),
+ *     PolarQuantizer::project_query / inner_product_estimate_with_projected_query
+ *     (polar.rs:330-370), QjlQuantizer::project_query /
+ *     inner_product_estimate_with_projected_query(_and_source_norm)
+ *     (qjl.rs:265-330).  Parity: pinned by the estimator's own identities
+ *     (tests/test_oracle_score.py): unbiasedness against the exact inner
+ *     product, the l2 identity, and exact reconstruction cases.
+ * ====================================================================== */
+
+/* prepared = [R q (dim)][G q (proj, QJL only)]; R q is the forward
+ * FastHadamard rotation (sign, FWHT, scale), G q sequential f32 dots. */
+int ora_turbo_prepare_query(uint32_t dim, uint32_t proj, int mode, const float* signs, const float* G,
+                            const float* q, float* out) {
+    for (uint32_t c = 0; c < dim; ++c)
+        if (!isfinite(q[c])) return ORA_ERR_NONFINITE_INPUT;           /* prepare_query, turbo.rs:330 */
+    ora_turbo_rotate(dim, signs, q, out);
+    for (uint32_t c = 0; c < dim; ++c)
+        if (!isfinite(out[c])) return ORA_ERR_NONFINITE_INPUT;         /* polar.rs:341 */
+    if (mode) {
+        for (uint32_t j = 0; j < proj; ++j) {
+            float s = -0.0f;   /* Rust's f32 Sum folds from -0.0 */
+            for (uint32_t c = 0; c < dim; ++c) s += G[(size_t)j * dim + c] * q[c];
+            out[dim + j] = s;
+            if (!isfinite(s)) return ORA_ERR_NONFINITE_INPUT;          /* qjl.rs:279 */
+        }
+    }
+    return ORA_OK;
+}
+
+/* Scores of every code of a TQB1 blob against nq prepared queries:
+ * scores[q * n + i] = polar(i, q) + qjl(i, q), with
+ *   polar = sum_pairs r * (qa * cos(theta) + qb * sin(theta))   (sequential f32)
+ *   qjl   = (sqrt(PI / 2) * 1 / m) * sum_j sign_j * (G q)_j       (unit source norm)
+ * The blob is validated as decode_batch does (wire.rs:401-568) before any
+ * score; a non-finite polar / qjl / total score fails (polar.rs:362-366,
+ * qjl.rs:322-327, turbo.rs:362-367).  fail_index: the lowest failing code. */
+int ora_turbo_score(uint32_t dim, uint32_t bits, uint32_t proj, uint64_t seed, int mode, const float* signs,
+                    const uint8_t* in, uint64_t len, const float* prepared, uint32_t nq, float* scores,
+                    uint64_t* n_out, uint64_t* fail_index) {
+    uint64_t n = 0;
+    /* the batch decoder's header and payload validation, nothing decoded */
+    int rc = ora_turbo_decode_batch(dim, bits, proj, seed, mode, signs, in, len, NULL, UINT64_MAX, &n, fail_index);
+    if (rc != ORA_OK) return rc;
+    if (n_out) *n_out = n;
+    if (n == 0) return ORA_OK;
+    int pbits = mode ? (int)bits - 1 : (int)bits;
+    uint32_t pairs = dim / 2;
+    int rcodec = in[15];
+    uint32_t plen = turbo_payload_len(dim, pbits, proj, mode, rcodec);
+    uint32_t angle_bytes = (pairs * (uint32_t)pbits + 7) / 8;
+    const float scale = sqrtf(3.14159274101257324f / 2.0f) * 1.0f / (float)proj;
+    float radii[128];
+    uint16_t idx[128];
+    uint64_t first_bad = UINT64_MAX;
+    for (uint64_t v = 0; v < n; ++v) {
+        const uint8_t* p = in + 38 + v * plen;
+        if (rcodec) {
+            float mn = get_f32(p + pairs), mx = get_f32(p + pairs + 4);
+            float span = mx - mn;
+            for (uint32_t i = 0; i < pairs; ++i) radii[i] = expf(mn + span * ((float)p[i] / 255.0f));
+            p += pairs + 8;
+        } else {
+            for (uint32_t i = 0; i < pairs; ++i) radii[i] = get_f32(p + 4 * i);
+            p += 4 * pairs;
+        }
+        for (uint32_t i = 0; i < pairs; ++i) idx[i] = (uint16_t)read_bits(p, (size_t)i * pbits, pbits);
+        p += angle_bytes;
+        for (uint32_t qi = 0; qi < nq; ++qi) {
+            const float* pq = prepared + (size_t)qi * (dim + (mode ? proj : 0));
+            float est = 0.0f;
+            for (uint32_t i = 0; i < pairs; ++i) {
+                float th = dequant_angle(idx[i], pbits);
+                est += radii[i] * (pq[2 * i] * cosf(th) + pq[2 * i + 1] * sinf(th));
+            }
+            int bad = !isfinite(est);
+            float total = est;
+            if (mode) {
+                float e2 = -0.0f;
+                for (uint32_t j = 0; j < proj; ++j) {
+                    int bit = (p[j >> 3] >> (j & 7)) & 1;
+                    e2 += (bit ? 1.0f : -1.0f) * pq[dim + j];
+                }
+                float qj = scale * e2;
+                bad |= !isfinite(qj);
+                total = est + qj;
+            }
+            bad |= !isfinite(total);
+            scores[(size_t)qi * n + v] = total;
+            if (bad && v < first_bad) first_bad = v;
+        }
+    }
+    if (first_bad != UINT64_MAX) {
+        if (fail_index) *fail_index = first_bad;
+        return ORA_ERR_MALFORMED;
+    }
+    return ORA_OK;
 }
 
 /* ======================================================================

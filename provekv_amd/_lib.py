@@ -46,7 +46,8 @@ EXPORTS = (
     "pkv_segments_status", "pkv_encode_segments", "pkv_decode_segments", "pkv_decode_segments_ex",
     "pkv_encode_batch_compact",
     "pkv_decode_batch_compact", "pkv_parse_header", "pkv_record_len", "pkv_encode_vectors", "pkv_decode_vectors",
-    "pkv_constants_cache_stats", "pkv_constants_cache_clear", "pkv_host_angle_bins", "pkv_host_logf",
+    "pkv_constants_cache_stats", "pkv_constants_cache_clear", "pkv_prepared_len", "pkv_turbo_prepare_queries",
+    "pkv_turbo_score_segments", "pkv_score_status", "pkv_turbo_score_batch", "pkv_host_angle_bins", "pkv_host_logf",
     "pkv_host_expf",
 )
 
@@ -125,6 +126,12 @@ def _declare(L):
         "pkv_decode_vectors": ([P, P, I32, P, P, U64, P, U64, P], I32),
         "pkv_constants_cache_stats": ([P, P, P], None),
         "pkv_constants_cache_clear": ([], None),
+        "pkv_prepared_len": ([P], U32),
+        "pkv_turbo_prepare_queries": ([P, P, P, U32, P, P, P], I32),
+        "pkv_turbo_score_segments": ([P, P, I32, P, U64, P, U32, P, U64, U32, U64, C.c_float, P, U64, U64, P, P],
+                                     I32),
+        "pkv_score_status": ([P, U32, P], I32),
+        "pkv_turbo_score_batch": ([P, P, P, U64, P, U32, C.c_float, P, U64, P, P], I32),
         "pkv_host_angle_bins": ([P, P, U64, U32, P], None),
         "pkv_host_logf": ([P, U64, P], None),
         "pkv_host_expf": ([P, U64, P], None),

@@ -1105,6 +1105,225 @@ int pkv_decode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, const uint8_
     return resolve_status(prof, hs, 1, &seg, err);
 }
 
+// ---- scoring on compressed codes (turbo-quant/src/turbo.rs:322-381)
+namespace {
+
+// QJL estimator scale with unit source norm: (PI / 2).sqrt() * 1.0 / m in f32
+// (qjl.rs:312-313; PI = std::f32::consts::PI).
+float qjl_score_scale(uint32_t proj) {
+    const float pi = 3.14159265358979323846f;
+    return std::sqrt(pi / 2.0f) * 1.0f / static_cast<float>(proj);
+}
+
+// The segment table against a score matrix: segment i's codes land in
+// columns col(i) < ld of every query row; blobs lie inside the wire buffer.
+int validate_score_segments(const pkv_profile* p, int radii, const pkv_seg* segs, uint32_t nseg, uint32_t nq,
+                            uint64_t prepared_rows, uint64_t query_stride, uint64_t ld, uint64_t score_elems,
+                            uint64_t wire_bytes, std::vector<uint32_t>& tile_start) {
+    if (!segs || nseg == 0) return PKV_ERR_INVALID_ARG;
+    uint64_t rows_needed;   // (nseg - 1) * query_stride + nq prepared rows
+    if (nq && (!mul_add_ok(nseg - 1, query_stride, nq, &rows_needed) || rows_needed > prepared_rows))
+        return PKV_ERR_DIM_MISMATCH;
+    const uint32_t plen = turbo_plen(p, radii);
+    const uint32_t hdr = hdr_len(p);
+    uint64_t rows_end = 0;
+    if (nq && !mul_add_ok(nq - 1, ld, 0, &rows_end)) return PKV_ERR_DIM_MISMATCH;
+    tile_start.assign(nseg + 1, 0);
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < nseg; ++i) {
+        const pkv_seg& s = segs[i];
+        if (s.group == 0 || s.n_vectors > MAX_SEG_VECTORS) return PKV_ERR_INVALID_ARG;
+        uint64_t end;   // one past the largest column
+        if (!seg_extent(s, 1, &end)) return PKV_ERR_DIM_MISMATCH;
+        if (s.n_vectors && nq) {
+            uint64_t last;
+            if (end > ld || __builtin_add_overflow(rows_end, end, &last) || last > score_elems)
+                return PKV_ERR_DIM_MISMATCH;
+        }
+        uint64_t blob_end;
+        if (!mul_add_ok(s.n_vectors, plen, hdr, &blob_end) ||
+            __builtin_add_overflow(blob_end, s.wire_offset, &blob_end) || blob_end > wire_bytes)
+            return PKV_ERR_CAPACITY;
+        uint64_t tiles = (static_cast<uint64_t>(s.n_vectors) + TILE - 1) / TILE;
+        if (tiles == 0) tiles = 1;
+        tile_start[i] = static_cast<uint32_t>(total);
+        total += tiles;
+        if (total > 0x7fffffffull) return PKV_ERR_INVALID_ARG;
+    }
+    tile_start[nseg] = static_cast<uint32_t>(total);
+    return PKV_OK;
+}
+
+// Status of a scoring launch: per segment, a rejected code (word 0: the blob
+// is validated as a whole before any score, wire.rs:401-568) precedes a
+// non-finite score (word 1); segments in order.
+int resolve_score_status(const uint32_t* st, uint32_t nseg, pkv_error* err) {
+    for (uint32_t s = 0; s < nseg; ++s) {
+        const uint32_t w0 = st[2 * s], w1 = st[2 * s + 1];
+        if (w0 == STATUS_NONE && w1 == STATUS_NONE) continue;
+        const uint32_t pick = w0 != STATUS_NONE ? w0 : w1;
+        if (err) {
+            err->status = PKV_ERR_CORRUPT_PAYLOAD;
+            err->segment = static_cast<int32_t>(s);
+            err->index = pick >> 4;
+        }
+        return PKV_ERR_CORRUPT_PAYLOAD;
+    }
+    if (err) { err->status = PKV_OK; err->segment = -1; err->index = 0; }
+    return PKV_OK;
+}
+
+int prepare_locked(pkv_ctx* ctx, const pkv_profile* prof, const float* d_q, uint32_t nq, float* d_prepared,
+                   uint32_t* d_status, hipStream_t stream) {
+    if (d_status) {
+        int rc = launch_fill_u32(d_status, STATUS_NONE, 2, stream);
+        if (rc) return hip_status(static_cast<hipError_t>(rc));
+    }
+    if (nq == 0) return PKV_OK;
+    const float rscale = 1.0f / std::sqrt(static_cast<float>(prof->dim));   // rotation.rs:393-397
+    int e = launch_turbo_prepare(turbo_dev(prof), d_q, nq, d_prepared, rscale, d_status, stream);
+    return e ? hip_status(static_cast<hipError_t>(e)) : PKV_OK;
+}
+
+int score_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, const uint8_t* d_wire, uint64_t wire_bytes,
+                 const pkv_seg* segs, uint32_t nseg, const float* d_prepared, uint64_t prepared_rows, uint32_t nq,
+                 uint64_t query_stride, float post, float* d_scores, uint64_t score_elems, uint64_t ld,
+                 uint32_t* d_status, hipStream_t stream) {
+    std::vector<uint32_t> tiles;
+    int rc = validate_score_segments(prof, radii, segs, nseg, nq, prepared_rows, query_stride, ld, score_elems,
+                                     wire_bytes, tiles);
+    if (rc) return rc;
+    Slot* sl;
+    SegDev* dsegs;
+    uint32_t *dtiles, *dstat;
+    rc = stage_table(ctx, segs, nseg, tiles, d_status == nullptr, stream, &sl, &dsegs, &dtiles, &dstat);
+    if (rc) return rc;
+    uint32_t* status = d_status ? d_status : dstat;
+    rc = launch_fill_u32(status, STATUS_NONE, 2ull * nseg, stream);
+    if (rc) { finish_slot(sl, stream); return hip_status(static_cast<hipError_t>(rc)); }
+    LaunchCommon lc;
+    lc.segs = dsegs;
+    lc.tile_start = dtiles;
+    lc.nseg = nseg;
+    lc.status = status;
+    lc.radii = static_cast<uint32_t>(radii);
+    lc.plen = turbo_plen(prof, radii);
+    lc.in_bf16 = 0;
+    lc.per_vector = 0;
+    lc.out_dtype = PKV_F32;
+    lc.fanout = 1;
+    lc.fanout_stride = 0;
+    const float qscale = prof->mode ? qjl_score_scale(prof->proj) : 0.0f;
+    int e = launch_turbo_score(lc, turbo_dev(prof), d_wire, d_prepared, nq, query_stride, d_scores, ld, qscale, post,
+                               tiles[nseg], stream);
+    int rc2 = finish_slot(sl, stream);
+    if (e) return hip_status(static_cast<hipError_t>(e));
+    return rc2;
+}
+
+bool score_profile_ok(const pkv_profile* p) {
+    return p && p->kind == PKV_CODEC_TURBO && (p->dim == 64 || p->dim == 128) && p->pbits >= 1 && p->pbits <= 8 &&
+           (!p->mode || p->proj == 32 || p->proj == 64);
+}
+
+}  // namespace
+
+uint32_t pkv_prepared_len(const pkv_profile* p) {
+    if (!p || p->kind != PKV_CODEC_TURBO) return 0;
+    return p->dim + (p->mode ? p->proj : 0);
+}
+
+int pkv_turbo_prepare_queries(pkv_ctx* ctx, const pkv_profile* prof, const float* d_queries, uint32_t nq,
+                              float* d_prepared, uint32_t* d_status, void* stream) {
+    if (!ctx || !prof) return PKV_ERR_INVALID_ARG;
+    if (prof->kind != PKV_CODEC_TURBO) return PKV_ERR_INVALID_ARG;
+    if (!score_profile_ok(prof)) return PKV_ERR_UNSUPPORTED;
+    if (nq && (!d_queries || !d_prepared)) return PKV_ERR_INVALID_ARG;
+    if (reinterpret_cast<uintptr_t>(d_queries) % 4 || reinterpret_cast<uintptr_t>(d_prepared) % 4)
+        return PKV_ERR_INVALID_ARG;
+    if (nq > 0x7fffffffu) return PKV_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    return prepare_locked(ctx, prof, d_queries, nq, d_prepared, d_status, static_cast<hipStream_t>(stream));
+}
+
+int pkv_turbo_score_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, const uint8_t* d_wire,
+                             uint64_t wire_bytes, const pkv_seg* segs, uint32_t nseg, const float* d_prepared,
+                             uint64_t prepared_rows, uint32_t nq, uint64_t query_stride, float post_scale,
+                             float* d_scores, uint64_t score_elems, uint64_t ld, uint32_t* d_status, void* stream) {
+    if (!ctx || !prof) return PKV_ERR_INVALID_ARG;
+    if (prof->kind != PKV_CODEC_TURBO) return PKV_ERR_INVALID_ARG;
+    if (!score_profile_ok(prof)) return PKV_ERR_UNSUPPORTED;
+    if (radii_codec != PKV_RADII_F32 && radii_codec != PKV_RADII_LOG_U8) return PKV_ERR_INVALID_ARG;
+    if (!std::isfinite(post_scale)) return PKV_ERR_INVALID_ARG;   // kv.rs:309-313
+    if (!d_wire || (nq && (!d_prepared || !d_scores))) return PKV_ERR_INVALID_ARG;
+    if (reinterpret_cast<uintptr_t>(d_scores) % 4 || reinterpret_cast<uintptr_t>(d_prepared) % 4)
+        return PKV_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    return score_locked(ctx, prof, radii_codec, d_wire, wire_bytes, segs, nseg, d_prepared, prepared_rows, nq,
+                        query_stride, post_scale, d_scores, score_elems, ld, d_status,
+                        static_cast<hipStream_t>(stream));
+}
+
+int pkv_score_status(const uint32_t* host_status, uint32_t nseg, pkv_error* err) {
+    if (!host_status && nseg) return PKV_ERR_INVALID_ARG;
+    return resolve_score_status(host_status, nseg, err);
+}
+
+int pkv_turbo_score_batch(pkv_ctx* ctx, const pkv_profile* prof, const uint8_t* payload, uint64_t len,
+                          const float* queries, uint32_t nq, float post_scale, float* scores, uint64_t scores_cap,
+                          uint64_t* n_out, pkv_error* err) {
+    if (err) { err->status = PKV_OK; err->segment = -1; err->index = 0; }
+    if (!ctx || !prof || !payload || (nq && !queries)) return PKV_ERR_INVALID_ARG;
+    if (prof->kind != PKV_CODEC_TURBO) return PKV_ERR_INVALID_ARG;
+    if (!score_profile_ok(prof)) return PKV_ERR_UNSUPPORTED;
+    if (!std::isfinite(post_scale)) return PKV_ERR_INVALID_ARG;
+    uint64_t n = 0;
+    int radii = 0;
+    int rc = pkv_parse_header(prof, payload, len, &n, &radii);
+    if (rc) { if (err) err->status = rc; return rc; }
+    if (n_out) *n_out = n;
+    if (n > MAX_SEG_VECTORS || nq > (1u << 24)) return PKV_ERR_INVALID_ARG;
+    uint64_t need;
+    if (__builtin_mul_overflow(n, static_cast<uint64_t>(nq), &need)) return PKV_ERR_INVALID_ARG;
+    if (need && (!scores || scores_cap < need)) return PKV_ERR_CAPACITY;
+    const uint64_t blob = pkv_blob_len(prof, radii, n);
+    const uint32_t W = pkv_prepared_len(prof);
+    auto pad = [](uint64_t b) { return (b + 255) & ~static_cast<uint64_t>(255); };
+    const uint64_t q_bytes = static_cast<uint64_t>(nq) * prof->dim * sizeof(float);
+    const uint64_t p_bytes = static_cast<uint64_t>(nq) * W * sizeof(float);
+    const uint64_t s_bytes = need * sizeof(float);
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    rc = ensure_scratch(ctx, pad(blob) + pad(q_bytes) + pad(p_bytes) + pad(s_bytes) + 256);
+    if (rc) return rc;
+    auto* base = static_cast<uint8_t*>(ctx->scratch);
+    uint8_t* d_wire = base;
+    auto* d_q = reinterpret_cast<float*>(base + pad(blob));
+    auto* d_p = reinterpret_cast<float*>(base + pad(blob) + pad(q_bytes));
+    auto* d_s = reinterpret_cast<float*>(base + pad(blob) + pad(q_bytes) + pad(p_bytes));
+    auto* d_st = reinterpret_cast<uint32_t*>(base + pad(blob) + pad(q_bytes) + pad(p_bytes) + pad(s_bytes));
+    hipStream_t st = ctx->own_stream;
+    HIP_TRY(hipMemcpyAsync(d_wire, payload, blob, hipMemcpyHostToDevice, st));
+    if (q_bytes) HIP_TRY(hipMemcpyAsync(d_q, queries, q_bytes, hipMemcpyHostToDevice, st));
+    rc = prepare_locked(ctx, prof, d_q, nq, d_p, d_st, st);
+    pkv_seg seg{0, 1, 1, 0, static_cast<uint32_t>(n), 1};
+    if (!rc)
+        rc = score_locked(ctx, prof, radii, d_wire, blob, &seg, 1, d_p, nq, nq, 0, post_scale, d_s, need ? need : 1,
+                          n ? n : 1, d_st + 2, st);
+    if (rc) { (void)hipStreamSynchronize(st); return rc; }
+    uint32_t hs[4];
+    HIP_TRY(hipMemcpyAsync(hs, d_st, sizeof hs, hipMemcpyDeviceToHost, st));
+    if (s_bytes) HIP_TRY(hipMemcpyAsync(scores, d_s, s_bytes, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    if (hs[0] != STATUS_NONE) {   // prepare_query runs before any score (turbo.rs:316-319)
+        if (err) { err->status = PKV_ERR_NONFINITE_INPUT; err->segment = -1; err->index = hs[0] >> 4; }
+        return PKV_ERR_NONFINITE_INPUT;
+    }
+    return resolve_score_status(hs + 2, 1, err);
+}
+
 uint32_t pkv_record_len(const pkv_profile* prof) { return prof ? record_hdr_len(prof) + record_plen(prof) : 0; }
 
 int pkv_encode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const float* vectors, uint64_t n,

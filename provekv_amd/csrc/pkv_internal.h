@@ -19,6 +19,7 @@ enum Kind : uint32_t {
     KIND_CORRUPT = 5,
     KIND_HEADER = 6,
     KIND_DECODE_NONFINITE = 7,
+    KIND_SCORE_NONFINITE = 8,
 };
 constexpr uint32_t STATUS_NONE = 0xFFFFFFFFu;
 constexpr uint32_t MAX_SEG_VECTORS = (1u << 28) - 1;
@@ -130,6 +131,11 @@ int launch_turbo_encode(const LaunchCommon& lc, const TurboDev& td, const void* 
                         uint32_t nblocks, void* stream);
 int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_t* wire, void* out,
                         uint32_t nblocks, void* stream);
+int launch_turbo_prepare(const TurboDev& td, const float* q, uint32_t nq, float* out, float rscale,
+                         uint32_t* status, void* stream);
+int launch_turbo_score(const LaunchCommon& lc, const TurboDev& td, const uint8_t* wire, const float* prepared,
+                       uint32_t nq, uint64_t qstride, float* scores, uint64_t ld, float qscale, float post,
+                       uint32_t nblocks, void* stream);
 int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire,
                       uint32_t nblocks, const FibRedo& rq, void* stream);
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, void* out,

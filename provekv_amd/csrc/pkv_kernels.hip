@@ -1557,6 +1557,230 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split128_kernel(
     stage_rows_out<DIM>(out, lc, stage, seg, t0, nv, static_cast<uint32_t>(badm), 0u, lane);
 }
 
+// ------------------------------------------------------------ scoring on codes
+// TurboQuantizer::prepare_query (turbo-quant/src/turbo.rs:322-338) for nq
+// queries, one wave per query: [R q (DIM)][G q (proj, QJL only)], with
+//   R q = FastHadamardRotation::apply (rotation.rs:202-211): q * signs, the
+//         in-place butterflies of fwht_normalized (rotation.rs:379-398) in
+//         stage order, then * (1 / sqrt(DIM)); each butterfly is one f32 add
+//         or subtract of the same two operands as the sequential loop, so
+//         spreading a stage across lanes changes no bit;
+//   G q = QjlQuantizer::project_query (qjl.rs:266-282): per projection j a
+//         sequential f32 fold of G[j][c] * q[c] from -0.0, the neutral element
+//         of Rust's f32 Sum (an all-zero sum keeps the sign of its terms).
+// A query with a non-finite input, rotated or projected value marks status
+// word 0 of segment 0 with its index (turbo.rs:330, polar.rs:341, qjl.rs:280).
+template <int DIM>
+__global__ __launch_bounds__(WAVE) void turbo_prepare_kernel(const float* __restrict__ q, uint32_t nq,
+                                                             float* __restrict__ out, const float* __restrict__ signs,
+                                                             const float* __restrict__ G, uint32_t proj,
+                                                             uint32_t mode, float rscale, uint32_t* status) {
+    __shared__ float v[DIM];
+    __shared__ float raw[DIM];
+    const uint32_t qi = blockIdx.x, lane = threadIdx.x;
+    if (qi >= nq) return;
+    const float* src = q + static_cast<uint64_t>(qi) * DIM;
+    const uint32_t W = DIM + (mode ? proj : 0u);
+    float* dst = out + static_cast<uint64_t>(qi) * W;
+    bool bad = false;
+#pragma unroll
+    for (int c = lane; c < DIM; c += WAVE) {
+        const float x = src[c];
+        raw[c] = x;
+        v[c] = x * signs[c];
+        bad |= !isfinite_f(x);
+    }
+    wave_sync();
+#pragma unroll
+    for (int step = 1; step < DIM; step *= 2) {
+#pragma unroll
+        for (int bf = lane; bf < DIM / 2; bf += WAVE) {
+            const int i = (bf / step) * 2 * step + bf % step, j = i + step;
+            const float a = v[i], b = v[j];
+            v[i] = a + b;
+            v[j] = a - b;
+        }
+        wave_sync();
+    }
+#pragma unroll
+    for (int c = lane; c < DIM; c += WAVE) {
+        const float y = v[c] * rscale;
+        dst[c] = y;
+        bad |= !isfinite_f(y);
+    }
+    if (mode) {
+        for (uint32_t j = lane; j < proj; j += WAVE) {
+            const float* g = G + static_cast<uint64_t>(j) * DIM;
+            float acc = -0.0f;
+#pragma unroll 16
+            for (int c = 0; c < DIM; ++c) acc = acc + g[c] * raw[c];
+            dst[DIM + j] = acc;
+            bad |= !isfinite_f(acc);
+        }
+    }
+    if (__ballot(bad) != 0ull && lane == 0 && status) status_fail(status, 0, 0, qi, KIND_NONFINITE_INPUT);
+}
+
+// TurboQuantizer::inner_product_estimate_prepared (turbo.rs:341-369) of every
+// code of every segment against nq prepared queries:
+//   polar = sum over pairs i of r_i * (qa_i * cos(theta_i) + qb_i * sin(theta_i))
+//           (PolarQuantizer::inner_product_estimate_with_projected_query,
+//           polar.rs:346-370: a sequential f32 loop from +0.0)
+//   qjl   = scale * sum_j s_j * (G q)_j, s_j = +1 for a set sign bit, -1
+//           otherwise, a fold from -0.0, scale = sqrt(PI / 2) * 1 / m
+//           (qjl.rs:294-330 with unit source norm)
+//   score = polar + qjl, then * post (AttentionScale of
+//           KvShadowCache::attention_scores_with_options, kv.rs:277-320:
+//           applied after the finiteness check; post = 1 leaves it unchanged).
+// One lane per code: its radii, its sign factors (+-1.0, folded in with an
+// FMA whose product is exact, so each step rounds like the reference's add)
+// and, at head_dim 64, the (cos, sin) of its angle bins stay in registers
+// (head_dim 128 keeps the bins as LDS byte offsets into the (cos, sin) table)
+// while the wave walks the queries, whose values are uniform across lanes
+// and arrive as scalar loads.  A code the decoder rejects (header, radius
+// checks, as decode_batch at wire.rs:401-568) marks status word 0 and gets no
+// score; a non-finite score marks word 1 (polar.rs:364, qjl.rs:324,
+// turbo.rs:362).  scores[q * ld + col], col = the segment's strided position
+// of the code (elem_offset + (i / group) * stride_outer + (i % group) *
+// stride_inner, in score units).  Segment s reads prepared rows
+// s * qstride .. s * qstride + nq - 1 (qstride 0: every segment scores the
+// same queries).  PROJ: 0 (PolarOnly), 32 or 64.
+template <int DIM, int PROJ>
+__global__ __launch_bounds__(TILE) void turbo_score_kernel(
+    LaunchCommon lc, const uint8_t* __restrict__ wire, const float* __restrict__ prepared, uint32_t nq,
+    uint64_t qstride, float* __restrict__ scores, uint64_t ld, const float* __restrict__ cs_tab, uint64_t seed,
+    uint32_t pbits, uint32_t hproj, float qscale, float post) {
+    constexpr int PAIRS = DIM / 2;
+    constexpr bool HOIST = DIM == 64;     // (cos, sin) per pair in registers
+    constexpr int W = DIM + PROJ;
+    extern __shared__ uint32_t smem_u[];  // per wave: 64 payloads
+    __shared__ float2 cs_lds[256];
+    __shared__ uint64_t exp_lds[32];
+    __shared__ float div255_lds[256];
+
+    const uint32_t levels = 1u << pbits;
+    for (uint32_t t = threadIdx.x; t < levels; t += blockDim.x)
+        cs_lds[t] = make_float2(cs_tab[2 * t], cs_tab[2 * t + 1]);
+    if (threadIdx.x < 32) exp_lds[threadIdx.x] = c_exp2f_tab[threadIdx.x];
+    for (uint32_t t = threadIdx.x; t < 256; t += blockDim.x) div255_lds[t] = c_div255.v[t];
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t blk = blockIdx.x;
+    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const SegDev seg = lc.segs[sidx];
+    const uint32_t tile = blk - lc.tile_start[sidx];
+    const uint32_t plen = lc.plen, pwd = plen >> 2;
+    const uint8_t* blob = wire + seg.wire_offset;
+    const uint32_t hb = lane < 38 ? blob[lane] : 0u;
+    const bool hbad = lane < 38 && tqb1_checked(lane) &&
+                      hb != tqb1_byte(lane, DIM, pbits, lc.radii, hproj, seed, seg.n_vectors, plen);
+    if (__ballot(hbad) != 0ull) {
+        if (lane == 0) status_fail(lc.status, sidx, 0, 0u, KIND_HEADER);
+        return;
+    }
+    const uint32_t v0 = tile * TILE + static_cast<uint32_t>(wave) * WAVE;
+    if (v0 >= seg.n_vectors) return;
+    const uint32_t nv = min(static_cast<uint32_t>(WAVE), seg.n_vectors - v0);
+    uint32_t* sw = smem_u + wave * (WAVE * pwd + 4);
+    global_to_lds(sw, blob + 38 + static_cast<uint64_t>(v0) * plen, nv * plen, lane);
+    wave_sync();
+    const bool active = static_cast<uint32_t>(lane) < nv;
+    const uint32_t* pw = sw + min(static_cast<uint32_t>(lane), nv - 1) * pwd;
+
+    // radii: f32 or BlockLogU8 through expf, with the decoder's checks
+    // (radius.rs:88-104, 128-145, 171-177; polar.rs:127-133)
+    float r[PAIRS];
+    bool ok = true;
+    uint32_t w = 0;
+    if (lc.radii == PKV_RADII_F32) {
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+            r[i] = u2f(pw[w++]);
+            ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);
+        }
+    } else {
+        constexpr int QW = PAIRS / 4;
+        const float mn = u2f(pw[QW]), mx = u2f(pw[QW + 1]);
+        ok &= isfinite_f(mn) && isfinite_f(mx) && !(mn > mx);
+        const float span = mx - mn;
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+            const uint32_t u = (pw[i >> 2] >> (8 * (i & 3))) & 0xffu;
+            r[i] = og_expf(mn + span * div255_lds[u], exp_lds);
+            ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);
+        }
+        w = QW + 2;
+    }
+    // angle bins, pbits each, LSB-first; PAIRS * pbits is a whole number of
+    // words for every accepted profile, so there is no padding to check
+    const uint32_t* aw = pw + w;
+    float cs[HOIST ? DIM : 1];
+    uint32_t boff[HOIST ? 1 : PAIRS / 2];   // byte offsets into cs_lds, 16 bits each
+    {
+        uint64_t acc = 0;
+        uint32_t nb = 0, k = 0;
+#pragma unroll
+        for (int i = 0; i < (HOIST ? 1 : PAIRS / 2); ++i) boff[i] = 0u;
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+            if (nb < pbits) { acc |= static_cast<uint64_t>(aw[k++]) << nb; nb += 32; }
+            const uint32_t b = static_cast<uint32_t>(acc) & (levels - 1u);
+            acc >>= pbits;
+            nb -= pbits;
+            if constexpr (HOIST) {
+                const float2 c = cs_lds[b];
+                cs[2 * i] = c.x;
+                cs[2 * i + 1] = c.y;
+            } else {
+                boff[i >> 1] |= (b * 8u) << (16 * (i & 1));
+            }
+        }
+    }
+    const uint32_t* sgw = aw + (PAIRS * pbits + 31) / 32;
+    float sg[PROJ ? PROJ : 1];
+#pragma unroll
+    for (int j = 0; j < PROJ; ++j) sg[j] = ((sgw[j >> 5] >> (j & 31)) & 1u) ? 1.0f : -1.0f;
+    if (active && !ok) status_fail(lc.status, sidx, 0, v0 + lane, KIND_CORRUPT);
+    const uint64_t col = vec_elem_offset(seg, v0 + min(static_cast<uint32_t>(lane), nv - 1));
+    const bool store = active && ok;
+    const char* csb = reinterpret_cast<const char*>(cs_lds);
+    bool fin = true;
+    const float* pseg = prepared + static_cast<uint64_t>(sidx) * qstride * W;
+    for (uint32_t q = 0; q < nq; ++q) {
+        const float* pq = pseg + static_cast<uint64_t>(q) * W;
+        float est = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+            float c, sn;
+            if constexpr (HOIST) {
+                c = cs[2 * i];
+                sn = cs[2 * i + 1];
+            } else {
+                const float2 t =
+                    *reinterpret_cast<const float2*>(csb + ((boff[i >> 1] >> (16 * (i & 1))) & 0xffffu));
+                c = t.x;
+                sn = t.y;
+            }
+            est = est + r[i] * (pq[2 * i] * c + pq[2 * i + 1] * sn);
+        }
+        bool f = isfinite_f(est);
+        float total = est;
+        if constexpr (PROJ != 0) {
+            float e2 = -0.0f;
+#pragma unroll
+            for (int j = 0; j < PROJ; ++j) e2 = __builtin_fmaf(sg[j], pq[DIM + j], e2);
+            const float qj = qscale * e2;
+            f &= isfinite_f(qj);
+            total = est + qj;
+        }
+        f &= isfinite_f(total);
+        fin &= f;
+        if (store) scores[static_cast<uint64_t>(q) * ld + col] = total * post;
+    }
+    if (store && !fin) status_fail(lc.status, sidx, 1, v0 + lane, KIND_SCORE_NONFINITE);
+}
+
 // ------------------------------------------------------------ fib encode
 // FibQuantizer::encode_batch (fib-quant/src/codec.rs:578-729; n < 4 takes
 // FibQuantizer::encode, 471-516) + FibCodeV1::encode_batch (FB2, 225-320).
@@ -2388,6 +2612,44 @@ int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_
                                 td.cs, td.seed, td.pbits, td.proj, td.mode)
                : launch_big_lds(turbo_decode_kernel<128, 0>, nblocks, stage_bytes<128>(), st, lc, wire, out, td.signs,
                                 td.cs, td.seed, td.pbits, td.proj, td.mode);
+}
+
+int launch_turbo_prepare(const TurboDev& td, const float* q, uint32_t nq, float* out, float rscale,
+                         uint32_t* status, void* stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (nq == 0) return hipSuccess;
+    if (td.dim == 64)
+        hipLaunchKernelGGL(turbo_prepare_kernel<64>, dim3(nq), dim3(WAVE), 0, st, q, nq, out, td.signs, td.qjl,
+                           td.proj, td.mode, rscale, status);
+    else if (td.dim == 128)
+        hipLaunchKernelGGL(turbo_prepare_kernel<128>, dim3(nq), dim3(WAVE), 0, st, q, nq, out, td.signs, td.qjl,
+                           td.proj, td.mode, rscale, status);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+int launch_turbo_score(const LaunchCommon& lc, const TurboDev& td, const uint8_t* wire, const float* prepared,
+                       uint32_t nq, uint64_t qstride, float* scores, uint64_t ld, float qscale, float post,
+                       uint32_t nblocks, void* stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const size_t lds = static_cast<size_t>(WAVES) * (WAVE * (lc.plen >> 2) + 4) * sizeof(uint32_t);
+    if (td.pbits < 1 || td.pbits > 8) return hipErrorInvalidValue;
+    const uint32_t proj = td.mode ? td.proj : 0u;
+#define PKV_SCORE(D, P)                                                                                        \
+    launch_big_lds(turbo_score_kernel<D, P>, nblocks, lds, st, lc, wire, prepared, nq, qstride, scores, ld,   \
+                   td.cs, td.seed, td.pbits, td.proj, qscale, post)
+    if (td.dim == 64) {
+        if (proj == 0) return PKV_SCORE(64, 0);
+        if (proj == 32) return PKV_SCORE(64, 32);
+        if (proj == 64) return PKV_SCORE(64, 64);
+    } else if (td.dim == 128) {
+        if (proj == 0) return PKV_SCORE(128, 0);
+        if (proj == 32) return PKV_SCORE(128, 32);
+        if (proj == 64) return PKV_SCORE(128, 64);
+    }
+#undef PKV_SCORE
+    return hipErrorInvalidValue;
 }
 
 int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire, uint32_t nblocks,

@@ -234,6 +234,78 @@ class Profile:
             return L.PkvError(code, "segment status", s, pick >> 4)
         return None
 
+    # ------------------------------------------------------------ scoring
+    def prepared_len(self) -> int:
+        return int(L.lib().pkv_prepared_len(self._ptr))
+
+    def prepare_queries(self, queries, prepared=None, status=None, stream=None):
+        """TurboQuantizer::prepare_query (turbo-quant/src/turbo.rs:322-338) for
+        every row of a float32 device tensor [nq, dim]: [nq, prepared_len]."""
+        torch = _torch()
+        if queries.dtype != torch.float32 or not queries.is_contiguous():
+            raise TypeError("queries must be a contiguous float32 tensor")
+        nq = queries.numel() // self.dim
+        if queries.numel() != nq * self.dim:
+            raise ValueError("queries must hold whole dim-sized rows")
+        if prepared is None:
+            prepared = torch.empty((nq, self.prepared_len()), dtype=torch.float32, device=queries.device)
+        elif prepared.dtype != torch.float32 or prepared.numel() < nq * self.prepared_len():
+            raise ValueError("prepared buffer too small")
+        st = None if status is None else status.data_ptr()
+        rc = L.lib().pkv_turbo_prepare_queries(self.ctx.ptr, self._ptr, queries.data_ptr(), nq, prepared.data_ptr(),
+                                               st, _stream_ptr(stream))
+        L.check(rc, "pkv_turbo_prepare_queries")
+        return prepared
+
+    def score_segments(self, wire, segs: np.ndarray, prepared, scores, ld: int, radii: int = L.RADII_F32,
+                       post_scale: float = 1.0, status=None, stream=None, nq: int | None = None,
+                       query_stride: int = 0) -> None:
+        """inner_product_estimate_prepared (turbo.rs:341-369) of every code of
+        every segment against nq prepared queries (segment s: rows
+        s * query_stride + q; nq defaults to every row), times post_scale,
+        into scores[q * ld + col(i)] (col: the segment addressing in score
+        units)."""
+        torch = _torch()
+        segs = np.ascontiguousarray(segs, dtype=SEG_DTYPE)
+        if wire.dtype != torch.uint8 or scores.dtype != torch.float32 or prepared.dtype != torch.float32:
+            raise TypeError("score reads a uint8 wire and float32 prepared queries, writes float32")
+        if not (wire.is_contiguous() and scores.is_contiguous() and prepared.is_contiguous()):
+            raise ValueError("tensors must be contiguous")
+        rows = prepared.numel() // self.prepared_len()
+        nq = rows if nq is None else nq
+        st = self._status_ptr(status, len(segs))
+        rc = L.lib().pkv_turbo_score_segments(self.ctx.ptr, self._ptr, radii, wire.data_ptr(), wire.numel(),
+                                              segs.ctypes.data, len(segs), prepared.data_ptr(), rows, nq,
+                                              query_stride, float(post_scale), scores.data_ptr(), scores.numel(),
+                                              ld, st, _stream_ptr(stream))
+        L.check(rc, "pkv_turbo_score_segments")
+
+    @staticmethod
+    def score_status_error(status_host: np.ndarray):
+        """Scoring status words -> PkvError (or None): a rejected code precedes
+        a non-finite score within a segment; segments in order."""
+        st = np.ascontiguousarray(status_host, dtype=np.uint32)
+        err = L.Error()
+        rc = L.lib().pkv_score_status(st.ctypes.data, len(st) // 2, C.byref(err))
+        return None if rc == 0 else L.PkvError(rc, "score status", err.segment, err.index)
+
+    def score_batch(self, payload: bytes, queries: np.ndarray, post_scale: float = 1.0) -> np.ndarray:
+        """Host buffers: scores[nq, n] of one TQB1 blob against host queries
+        (prepare_query + score_batch_prepared per query row)."""
+        q = np.ascontiguousarray(queries, dtype=np.float32).reshape(-1, self.dim)
+        buf = np.frombuffer(payload, dtype=np.uint8)
+        n = C.c_uint64(0)
+        err = L.Error()
+        rc = L.lib().pkv_parse_header(self._ptr, buf.ctypes.data, len(buf), C.byref(n), None)
+        if rc:
+            raise L.PkvError(rc, "pkv_parse_header")
+        out = np.zeros((len(q), max(int(n.value), 1)), dtype=np.float32)
+        rc = L.lib().pkv_turbo_score_batch(self.ctx.ptr, self._ptr, buf.ctypes.data, len(buf), q.ctypes.data, len(q),
+                                           float(post_scale), out.ctypes.data, out.size, C.byref(n), C.byref(err))
+        if rc:
+            raise L.PkvError(rc, "pkv_turbo_score_batch", err.segment, err.index)
+        return out[:, :int(n.value)]
+
     # ------------------------------------------------------------ host buffers
     def encode_batch_compact(self, vectors: np.ndarray, radii: int = L.RADII_F32) -> bytes:
         x = np.ascontiguousarray(vectors, dtype=np.float32)
