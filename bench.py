@@ -354,18 +354,23 @@ def bench_score(args):
     x = x.reshape(-1)
     ctx = default_context()
     prof = ctx.turbo_profile(dim, 4, 32, 42)
-    plen = prof.payload_len(L.RADII_LOG_U8)
-    blob = 38 + tokens * plen
-    segs = np.array([(b * tokens * dim, 0, dim, b * blob, tokens, tokens) for b in range(nseg)], dtype=SEG_DTYPE)
-    wire = torch.empty(nseg * blob, dtype=torch.uint8, device="cuda")
     est = torch.empty(2 * nseg, dtype=torch.int32, device="cuda")
-    log(f"[bench] encoding {nseg} key blobs x {tokens} tokens (untimed)")
-    prof.encode_segments(x, segs, wire, radii=L.RADII_LOG_U8, status=est)
-    torch.cuda.synchronize()
-    err = prof.status_error(est.cpu().numpy().view(np.uint32), segs)
-    if err is not None:
-        raise err
+    wires = {}
+    for radii in (L.RADII_LOG_U8, L.RADII_F32):
+        plen_r = prof.payload_len(radii)
+        blob_r = 38 + tokens * plen_r
+        segs = np.array([(b * tokens * dim, 0, dim, b * blob_r, tokens, tokens) for b in range(nseg)],
+                        dtype=SEG_DTYPE)
+        w = torch.empty(nseg * blob_r, dtype=torch.uint8, device="cuda")
+        log(f"[bench] encoding {nseg} key blobs x {tokens} tokens, radii codec {radii} (untimed)")
+        prof.encode_segments(x, segs, w, radii=radii, status=est)
+        torch.cuda.synchronize()
+        err = prof.status_error(est.cpu().numpy().view(np.uint32), segs)
+        if err is not None:
+            raise err
+        wires[radii] = (w, plen_r, blob_r)
     del x
+    wire, plen, blob = wires[L.RADII_LOG_U8]
     nq = nseg * group
     rng = np.random.RandomState(11)
     qh = rng.randn(nq, dim).astype(np.float32)
@@ -380,13 +385,16 @@ def bench_score(args):
     scale = float(np.float32(1.0) / np.sqrt(np.float32(dim)))
     stream = torch.cuda.current_stream()
 
-    def step(ev=None):
+    def step(ev=None, radii=L.RADII_LOG_U8):
+        w, _, blob_r = wires[radii]
+        sg = ssegs if radii == L.RADII_LOG_U8 else np.array(
+            [(b * tokens, 1, 1, b * blob_r, tokens, 1) for b in range(nseg)], dtype=SEG_DTYPE)
         if ev is not None:
             ev[0].record(stream)
         prof.prepare_queries(q, prep, status=pst)
         if ev is not None:
             ev[1].record(stream)
-        prof.score_segments(wire, ssegs, prep, scores, ld, radii=L.RADII_LOG_U8, post_scale=scale, status=sst,
+        prof.score_segments(w, sg, prep, scores, ld, radii=radii, post_scale=scale, status=sst,
                             nq=group, query_stride=group)
         if ev is not None:
             ev[2].record(stream)
@@ -413,6 +421,22 @@ def bench_score(args):
     torch.cuda.synchronize()
     prep_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
     score_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    # the same keys with f32 radii (TQB1 lossless: the in-memory TurboCode form)
+    for k in range(max(1, args.warmup)):
+        step(radii=L.RADII_F32)
+    evs32 = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for k in range(steps):
+        step(evs32[k], radii=L.RADII_F32)
+    torch.cuda.synchronize()
+    serr = prof.score_status_error(sst.cpu().numpy().view(np.uint32))
+    if serr is not None:
+        raise serr
+    score32_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs32]))
+    w32, plen32, blob32 = wires[L.RADII_F32]
+    alg32 = nseg * blob32 + nseg * tokens * group * 4 + nq * prof.prepared_len() * 4
+    # the timed region above left TQB1-L scores in `scores`: rerun one TQB1-L step for the parity sample
+    step()
+    torch.cuda.synchronize()
     # sampled parity: 256 codes of four blobs, every query of the group, bit for bit
     pref = O.turbo_prepare_queries(qh, 42)
     parity = np.array_equal(prep.cpu().numpy().view(np.uint32), pref.view(np.uint32))
@@ -430,7 +454,7 @@ def bench_score(args):
     pairs = nseg * tokens * group
     wire_bytes = nseg * blob
     alg = wire_bytes + pairs * 4 + nq * W * 4
-    lane_ops = pairs * ((dim // 2) * 6 + 32)   # per pair: LDS offset + 2 mul + add + mul + add; 32 QJL FMAs
+    lane_ops = pairs * ((dim // 2) * 3 + 32)   # per pair: table offset, mul, add (+ LDS read); 32 QJL FMAs
     # CPU baseline: the oracle (one thread) scoring a bounded sample
     cpu = None
     if not args.no_cpu_baseline:
@@ -457,8 +481,13 @@ def bench_score(args):
            "config": {"workload": "score: config-4 keys (32L x 8 KV heads x 32768 tokens x d128, turbo b=4 QJL-32, "
                                   "TQB1-L) x GQA groups of 4 query heads, scale 1/sqrt(128)",
                       "blobs": nseg, "codes_per_blob": tokens, "queries": nq, "wire_bytes": wire_bytes},
-           "kernels_ms": {"prepare": round(prep_ms, 4), "score": round(score_ms, 4)},
-           "roofline": {"bound": "valu", "kernel": "turbo_score_kernel<128, 32>",
+           "kernels_ms": {"prepare": round(prep_ms, 4), "score": round(score_ms, 4),
+                          "score_f32_radii": round(score32_ms, 4)},
+           "f32_radii": {"scores_per_s": round(pairs / (score32_ms * 1e-3), 1),
+                         "hbm_gbs": round(alg32 / (score32_ms * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(alg32 / (score32_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         "algorithmic_bytes": alg32},
+           "roofline": {"bound": "valu", "kernel": "turbo_score_lut_kernel<128, 32, true, 3>",
                         "achieved": round(lane_ops / (score_ms * 1e-3) / 1e12, 2),
                         "peak": round(VALU_PEAK_OPS / 1e12, 2), "unit": "T lane-ops/s",
                         "frac": round(lane_ops / (score_ms * 1e-3) / VALU_PEAK_OPS, 4),
@@ -466,6 +495,12 @@ def bench_score(args):
                         "hbm_frac": round(alg / (score_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                         "algorithmic_bytes": alg, "lane_ops": lane_ops},
            "cpu_baseline": cpu, "parity_sampled": bool(parity)}
+    if args.copy_calib:   # the reference kernel for rocprofv3 --pmc byte counters
+        src = torch.empty(1 << 28, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     print(json.dumps(res), flush=True)
 
 

@@ -99,9 +99,9 @@ __device__ void lds_to_global(uint8_t* __restrict__ dst, const uint32_t* lds, ui
 
 // Move nbytes from global memory at any byte alignment into LDS (LDS byte 0 ==
 // src byte 0).  Only aligned dwords holding at least one source byte are read;
-// each lane issues up to 8 loads before it waits on any of them.
+// each lane issues up to BATCH loads before it waits on any of them.
+template <uint32_t BATCH = 8>
 __device__ void global_to_lds(uint32_t* lds, const uint8_t* __restrict__ src, uint32_t nbytes, int lane) {
-    constexpr uint32_t BATCH = 8;
     const uintptr_t a = reinterpret_cast<uintptr_t>(src);
     const uint32_t* s32 = reinterpret_cast<const uint32_t*>(a & ~static_cast<uintptr_t>(3));
     const uint32_t sh = static_cast<uint32_t>(a & 3u);
@@ -1645,13 +1645,15 @@ __global__ __launch_bounds__(WAVE) void turbo_prepare_kernel(const float* __rest
 // stride_inner, in score units).  Segment s reads prepared rows
 // s * qstride .. s * qstride + nq - 1 (qstride 0: every segment scores the
 // same queries).  PROJ: 0 (PolarOnly), 32 or 64.
-template <int DIM, int PROJ>
+template <int DIM, int PROJ, bool LOSSY, bool NARROW>
 __global__ __launch_bounds__(TILE) void turbo_score_kernel(
     LaunchCommon lc, const uint8_t* __restrict__ wire, const float* __restrict__ prepared, uint32_t nq,
     uint64_t qstride, float* __restrict__ scores, uint64_t ld, const float* __restrict__ cs_tab, uint64_t seed,
     uint32_t pbits, uint32_t hproj, float qscale, float post) {
     constexpr int PAIRS = DIM / 2;
     constexpr bool HOIST = DIM == 64;     // (cos, sin) per pair in registers
+    constexpr int OB = NARROW ? 8 : 16;   // bits per LDS byte offset (8 when 8 * (levels - 1) < 256)
+    constexpr int OPW = 32 / OB;
     constexpr int W = DIM + PROJ;
     extern __shared__ uint32_t smem_u[];  // per wave: 64 payloads
     __shared__ float2 cs_lds[256];
@@ -1693,7 +1695,7 @@ __global__ __launch_bounds__(TILE) void turbo_score_kernel(
     float r[PAIRS];
     bool ok = true;
     uint32_t w = 0;
-    if (lc.radii == PKV_RADII_F32) {
+    if constexpr (!LOSSY) {
 #pragma unroll
         for (int i = 0; i < PAIRS; ++i) {
             r[i] = u2f(pw[w++]);
@@ -1716,12 +1718,12 @@ __global__ __launch_bounds__(TILE) void turbo_score_kernel(
     // words for every accepted profile, so there is no padding to check
     const uint32_t* aw = pw + w;
     float cs[HOIST ? DIM : 1];
-    uint32_t boff[HOIST ? 1 : PAIRS / 2];   // byte offsets into cs_lds, 16 bits each
+    uint32_t boff[HOIST ? 1 : PAIRS / OPW];   // byte offsets into cs_lds, OB bits each
     {
         uint64_t acc = 0;
         uint32_t nb = 0, k = 0;
 #pragma unroll
-        for (int i = 0; i < (HOIST ? 1 : PAIRS / 2); ++i) boff[i] = 0u;
+        for (int i = 0; i < (HOIST ? 1 : PAIRS / OPW); ++i) boff[i] = 0u;
 #pragma unroll
         for (int i = 0; i < PAIRS; ++i) {
             if (nb < pbits) { acc |= static_cast<uint64_t>(aw[k++]) << nb; nb += 32; }
@@ -1733,7 +1735,7 @@ __global__ __launch_bounds__(TILE) void turbo_score_kernel(
                 cs[2 * i] = c.x;
                 cs[2 * i + 1] = c.y;
             } else {
-                boff[i >> 1] |= (b * 8u) << (16 * (i & 1));
+                boff[i / OPW] |= (b * 8u) << (OB * (i % OPW));
             }
         }
     }
@@ -1758,7 +1760,7 @@ __global__ __launch_bounds__(TILE) void turbo_score_kernel(
                 sn = cs[2 * i + 1];
             } else {
                 const float2 t =
-                    *reinterpret_cast<const float2*>(csb + ((boff[i >> 1] >> (16 * (i & 1))) & 0xffffu));
+                    *reinterpret_cast<const float2*>(csb + ((boff[i / OPW] >> (OB * (i % OPW))) & ((1u << OB) - 1u)));
                 c = t.x;
                 sn = t.y;
             }
@@ -1770,6 +1772,196 @@ __global__ __launch_bounds__(TILE) void turbo_score_kernel(
             float e2 = -0.0f;
 #pragma unroll
             for (int j = 0; j < PROJ; ++j) e2 = __builtin_fmaf(sg[j], pq[DIM + j], e2);
+            const float qj = qscale * e2;
+            f &= isfinite_f(qj);
+            total = est + qj;
+        }
+        f &= isfinite_f(total);
+        fin &= f;
+        if (store) scores[static_cast<uint64_t>(q) * ld + col] = total * post;
+    }
+    if (store && !fin) status_fail(lc.status, sidx, 1, v0 + lane, KIND_SCORE_NONFINITE);
+}
+
+// The same scores for profiles with at most 16 angle bins (pbits <= 4), with
+// the per-pair term looked up instead of recomputed: for a chunk of up to
+// four queries the block first tabulates, in LDS,
+//   T[q][i][b] = qa_i * cos(theta_b) + qb_i * sin(theta_b)
+// -- the parenthesised sum of polar.rs:361, the same two products and add --
+// so each (code, query, pair) costs one LDS read, a multiply by r_i and the
+// sequential add: est = est + r_i * T[q][i][bin_i], bit for bit the
+// reference's expression.  Payloads are staged through LDS 32 lanes at a
+// time (raw words into registers), and the staging space is then reused for
+// the table, which keeps four workgroups per CU at head_dim 128.
+template <int DIM, int PROJ, bool LOSSY, int PB>
+__global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(DIM == 128 && PROJ ? 3 : 4))) void
+turbo_score_lut_kernel(
+    LaunchCommon lc, const uint8_t* __restrict__ wire, const float* __restrict__ prepared, uint32_t nq,
+    uint64_t qstride, float* __restrict__ scores, uint64_t ld, const float* __restrict__ cs_tab, uint64_t seed,
+    uint32_t hproj, float qscale, float post) {
+    constexpr uint32_t pbits = PB;
+    constexpr int PAIRS = DIM / 2;
+    constexpr int LUTQ = PAIRS * 16;             // floats per query: [pair][bin]
+    constexpr int W = DIM + PROJ;
+    constexpr int RW = LOSSY ? PAIRS / 4 + 2 : PAIRS;   // radii words
+    constexpr int AWMAX = (PAIRS * PB + 31) / 32;       // angle words
+    constexpr int SW = PROJ / 32;                       // sign words
+    extern __shared__ uint32_t smem_u[];
+    __shared__ float2 cs_lds[16];
+    __shared__ uint64_t exp_lds[32];
+    __shared__ float div255_lds[256];
+
+    constexpr uint32_t levels = 1u << pbits;
+    if (threadIdx.x < 16)
+        cs_lds[threadIdx.x] = threadIdx.x < levels ? make_float2(cs_tab[2 * threadIdx.x], cs_tab[2 * threadIdx.x + 1])
+                                                   : make_float2(0.0f, 0.0f);
+    if (threadIdx.x < 32) exp_lds[threadIdx.x] = c_exp2f_tab[threadIdx.x];
+    if (LOSSY)
+        for (uint32_t t = threadIdx.x; t < 256; t += blockDim.x) div255_lds[t] = c_div255.v[t];
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t blk = blockIdx.x;
+    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const SegDev seg = lc.segs[sidx];
+    const uint32_t tile = blk - lc.tile_start[sidx];
+    const uint32_t plen = lc.plen, pwd = plen >> 2;
+    const uint8_t* blob = wire + seg.wire_offset;
+    const uint32_t hb = lane < 38 ? blob[lane] : 0u;   // checked once the payloads are staged
+    const uint32_t v0 = tile * TILE + static_cast<uint32_t>(wave) * WAVE;
+    const uint32_t nv = v0 < seg.n_vectors ? min(static_cast<uint32_t>(WAVE), seg.n_vectors - v0) : 0u;
+    const bool active = static_cast<uint32_t>(lane) < nv;
+
+    // raw payload words, 32 lanes per round through this wave's staging area
+    uint32_t rw[RW], aw[AWMAX], sgw[SW ? SW : 1];
+    {
+        uint32_t* sw = smem_u + wave * (32 * pwd + 4);
+        constexpr uint32_t nwa = AWMAX;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const uint32_t h0 = 32u * half;
+            const uint32_t hn = nv > h0 ? min(32u, nv - h0) : 0u;
+            if (hn) global_to_lds<16>(sw, blob + 38 + static_cast<uint64_t>(v0 + h0) * plen, hn * plen, lane);
+            wave_sync();
+            if ((lane >> 5) == half) {
+                const uint32_t* pw = sw + min(static_cast<uint32_t>(lane & 31), hn ? hn - 1 : 0u) * pwd;
+#pragma unroll
+                for (int k = 0; k < RW; ++k) rw[k] = pw[k];
+#pragma unroll
+                for (int k = 0; k < AWMAX; ++k) aw[k] = pw[RW + k];
+#pragma unroll
+                for (int k = 0; k < SW; ++k) sgw[k] = pw[RW + nwa + k];
+            }
+            wave_sync();
+        }
+    }
+    const bool hbad = lane < 38 && tqb1_checked(lane) &&
+                      hb != tqb1_byte(lane, DIM, pbits, lc.radii, hproj, seed, seg.n_vectors, plen);
+    if (__ballot(hbad) != 0ull) {   // the same header for every wave of the block: all leave
+        if (lane == 0 && wave == 0) status_fail(lc.status, sidx, 0, 0u, KIND_HEADER);
+        return;
+    }
+    // radii with the decoder's checks (radius.rs:88-104, 128-145, 171-177; polar.rs:127-133)
+    float r[PAIRS];
+    bool ok = true;
+    if constexpr (!LOSSY) {
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+            r[i] = u2f(rw[i]);
+            ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);
+        }
+    } else {
+        const float mn = u2f(rw[PAIRS / 4]), mx = u2f(rw[PAIRS / 4 + 1]);
+        ok &= isfinite_f(mn) && isfinite_f(mx) && !(mn > mx);
+        const float span = mx - mn;
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+            const uint32_t u = (rw[i >> 2] >> (8 * (i & 3))) & 0xffu;
+            r[i] = og_expf(mn + span * div255_lds[u], exp_lds);
+            ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);
+        }
+    }
+    // byte offsets bin * 4 of every pair, four per word
+    uint32_t boff[PAIRS / 4];
+#pragma unroll
+    for (int i = 0; i < PAIRS / 4; ++i) boff[i] = 0u;
+#pragma unroll
+    for (int i = 0; i < PAIRS; ++i) {
+        constexpr uint32_t M = levels - 1u;
+        const int bit = i * PB, wd = bit >> 5, sh = bit & 31;
+        uint32_t b = aw[wd] >> sh;
+        if (sh + PB > 32) b |= aw[wd + 1] << (32 - sh);
+        boff[i >> 2] |= ((b & M) * 4u) << (8 * (i & 3));
+    }
+    // sketch signs as f16 +-1.0, two per register, folded in by a mixed FMA
+    // whose product (+-1 times p) is exact: e2 + s_j * p_j rounds once, as the
+    // reference's add of sign as f32 * p (qjl.rs:316-321)
+    uint32_t sgh[PROJ ? PROJ / 2 : 1];
+#pragma unroll
+    for (int j2 = 0; j2 < PROJ / 2; ++j2) {
+        const uint32_t w = sgw[(2 * j2) >> 5] >> ((2 * j2) & 31);
+        sgh[j2] = ((w & 1u) ? 0x3c00u : 0xbc00u) | (((w & 2u) ? 0x3c00u : 0xbc00u) << 16);
+    }
+    if (active && !ok) status_fail(lc.status, sidx, 0, v0 + lane, KIND_CORRUPT);
+    const uint64_t col = vec_elem_offset(seg, v0 + min(static_cast<uint32_t>(lane), nv ? nv - 1 : 0u));
+    const bool store = active && ok;
+    const float* pseg = prepared + static_cast<uint64_t>(sidx) * qstride * W;
+    float* lut = reinterpret_cast<float*>(smem_u);
+    constexpr int PER = LUTQ / TILE;   // table entries per thread and query
+    static_assert(LUTQ % TILE == 0, "table fill");
+    float qa[PER], qb[PER];           // the next query's rotated pairs this thread tabulates
+    auto fetch = [&](uint32_t q) {
+        const float* pq = pseg + static_cast<uint64_t>(q) * W;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const uint32_t i = (threadIdx.x + k * TILE) / 16;
+            qa[k] = pq[2 * i];
+            qb[k] = pq[2 * i + 1];
+        }
+    };
+    if (nq) fetch(0);
+    bool fin = true;
+    for (uint32_t q = 0; q < nq; ++q) {
+        __syncthreads();   // staging / the previous query's table is no longer read
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const uint32_t e = threadIdx.x + k * TILE;
+            const float2 c = cs_lds[e % 16];
+            lut[e] = qa[k] * c.x + qb[k] * c.y;
+        }
+        __syncthreads();
+        if (q + 1 < nq) fetch(q + 1);   // in flight while this query is scored
+        // keep the per-pair offsets and the signs packed: unpacked per query, not hoisted
+        // out of the loop into one register each
+#pragma unroll
+        for (int k = 0; k < PAIRS / 4; ++k) asm volatile("" : "+v"(boff[k]));
+#pragma unroll
+        for (int k = 0; k < (PROJ ? PROJ / 2 : 1); ++k) asm volatile("" : "+v"(sgh[k]));
+        const char* lb = reinterpret_cast<const char*>(lut);
+        auto tab = [&](int i) {
+            const uint32_t off = (boff[i >> 2] >> (8 * (i & 3))) & 0xffu;
+            return *reinterpret_cast<const float*>(lb + off + 4 * (i * 16));
+        };
+        constexpr int DEPTH = 4;   // table reads in flight ahead of the sequential sum
+        float ring[DEPTH];
+#pragma unroll
+        for (int k = 0; k < DEPTH; ++k) ring[k] = tab(k);
+        float est = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+            const float t = ring[i % DEPTH];
+            if (i + DEPTH < PAIRS) ring[i % DEPTH] = tab(i + DEPTH);
+            est = est + r[i] * t;
+        }
+        bool f = isfinite_f(est);
+        float total = est;
+        if constexpr (PROJ != 0) {
+            const float* pq = pseg + static_cast<uint64_t>(q) * W;
+            float e2 = -0.0f;
+#pragma unroll
+            for (int j = 0; j < PROJ; ++j) {
+                const _Float16 h = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sgh[j >> 1] >> (16 * (j & 1))));
+                e2 = __builtin_fmaf(static_cast<float>(h), pq[DIM + j], e2);
+            }
             const float qj = qscale * e2;
             f &= isfinite_f(qj);
             total = est + qj;
@@ -2636,18 +2828,42 @@ int launch_turbo_score(const LaunchCommon& lc, const TurboDev& td, const uint8_t
     const size_t lds = static_cast<size_t>(WAVES) * (WAVE * (lc.plen >> 2) + 4) * sizeof(uint32_t);
     if (td.pbits < 1 || td.pbits > 8) return hipErrorInvalidValue;
     const uint32_t proj = td.mode ? td.proj : 0u;
-#define PKV_SCORE(D, P)                                                                                        \
-    launch_big_lds(turbo_score_kernel<D, P>, nblocks, lds, st, lc, wire, prepared, nq, qstride, scores, ld,   \
-                   td.cs, td.seed, td.pbits, td.proj, qscale, post)
-    if (td.dim == 64) {
-        if (proj == 0) return PKV_SCORE(64, 0);
-        if (proj == 32) return PKV_SCORE(64, 32);
-        if (proj == 64) return PKV_SCORE(64, 64);
-    } else if (td.dim == 128) {
-        if (proj == 0) return PKV_SCORE(128, 0);
-        if (proj == 32) return PKV_SCORE(128, 32);
-        if (proj == 64) return PKV_SCORE(128, 64);
+#define PKV_SCORE(D, P, LO, NA)                                                                                \
+    launch_big_lds(turbo_score_kernel<D, P, LO, NA>, nblocks, lds, st, lc, wire, prepared, nq, qstride, scores, \
+                   ld, td.cs, td.seed, td.pbits, td.proj, qscale, post)
+#define PKV_SCORE_R(D, P)                                                                                      \
+    (lc.radii == PKV_RADII_F32 ? (narrow ? PKV_SCORE(D, P, false, true) : PKV_SCORE(D, P, false, false))        \
+                               : (narrow ? PKV_SCORE(D, P, true, true) : PKV_SCORE(D, P, true, false)))
+    if ((td.pbits == 3 || td.pbits == 4) && proj <= 32) {   // table path: [pair][bin] terms in LDS
+        const size_t stage = static_cast<size_t>(WAVES) * (32 * (lc.plen >> 2) + 4) * sizeof(uint32_t);
+        const size_t table = static_cast<size_t>(td.dim / 2) * 16 * sizeof(float);
+        const size_t llds = std::max(stage, table);
+#define PKV_LUT(D, P, PB)                                                                                      \
+    (lc.radii == PKV_RADII_F32                                                                                 \
+         ? launch_big_lds(turbo_score_lut_kernel<D, P, false, PB>, nblocks, llds, st, lc, wire, prepared, nq,   \
+                          qstride, scores, ld, td.cs, td.seed, td.proj, qscale, post)                           \
+         : launch_big_lds(turbo_score_lut_kernel<D, P, true, PB>, nblocks, llds, st, lc, wire, prepared, nq,    \
+                          qstride, scores, ld, td.cs, td.seed, td.proj, qscale, post))
+        if (td.dim == 64)
+            return td.pbits == 3 ? (proj ? PKV_LUT(64, 32, 3) : PKV_LUT(64, 0, 3))
+                                 : (proj ? PKV_LUT(64, 32, 4) : PKV_LUT(64, 0, 4));
+        if (td.dim == 128)
+            return td.pbits == 3 ? (proj ? PKV_LUT(128, 32, 3) : PKV_LUT(128, 0, 3))
+                                 : (proj ? PKV_LUT(128, 32, 4) : PKV_LUT(128, 0, 4));
+#undef PKV_LUT
+        return hipErrorInvalidValue;
     }
+    const bool narrow = td.dim == 128 && td.pbits <= 5;
+    if (td.dim == 64) {
+        if (proj == 0) return lc.radii == PKV_RADII_F32 ? PKV_SCORE(64, 0, false, false) : PKV_SCORE(64, 0, true, false);
+        if (proj == 32) return lc.radii == PKV_RADII_F32 ? PKV_SCORE(64, 32, false, false) : PKV_SCORE(64, 32, true, false);
+        if (proj == 64) return lc.radii == PKV_RADII_F32 ? PKV_SCORE(64, 64, false, false) : PKV_SCORE(64, 64, true, false);
+    } else if (td.dim == 128) {
+        if (proj == 0) return PKV_SCORE_R(128, 0);
+        if (proj == 32) return PKV_SCORE_R(128, 32);
+        if (proj == 64) return PKV_SCORE_R(128, 64);
+    }
+#undef PKV_SCORE_R
 #undef PKV_SCORE
     return hipErrorInvalidValue;
 }
