@@ -2564,11 +2564,11 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
     constexpr int BLOCKS = DIM / 4;
     constexpr uint32_t PLEN = 2 + (BLOCKS * 5 + 7) / 8;   // 12
     constexpr int PAY_WORDS = WAVE * PLEN / 4 + 4;
-    constexpr int HPITCH = 32 + 4;       // one half row (32 columns) per vector, padded
+    constexpr int RPITCH = DIM + 4;      // one staged row per vector, padded
     __shared__ float rot_s[DIM * DIM];   // f32(Pi), row-major
     __shared__ float4 cb_s[32];
     __shared__ uint32_t pay_s[WAVES][PAY_WORDS];
-    __shared__ float half_s[STAGED ? WAVES : 1][STAGED ? 32 * HPITCH : 4];   // output staging: 32 vectors x 32 cols
+    __shared__ float half_s[STAGED ? WAVES : 1][STAGED ? 16 * RPITCH : 4];   // output staging: 16 rows
     {
         const float4* src = reinterpret_cast<const float4*>(rot32);
         float4* dst = reinterpret_cast<float4*>(rot_s);
@@ -2604,10 +2604,14 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
     global_to_lds(sw, blob + 19 + static_cast<uint64_t>(v0) * PLEN, nv * PLEN, lane);
     wave_sync();
 
+    // Sub-tile s, lane n: wave vector w = (n % 16) + 16 s + 32 (n / 16) -- vectors
+    // w and w + 32 are the same head at consecutive tokens when a blob holds
+    // 32 heads (vector = token * H + head), so the staged stores below write
+    // two adjacent rows per run.  Any other layout is just another order.
     for (uint32_t sub = 0; sub < 2; ++sub) {
-        const uint32_t t0 = 32 * sub;   // first vector of this tile within the wave
-        if (t0 >= nv) break;
-        const uint32_t my = min(t0 + static_cast<uint32_t>(n), nv - 1);   // lanes past the end repeat the last
+        if (sub == 1 && nv <= 16) break;
+        const uint32_t w = (static_cast<uint32_t>(n) & 15u) + 16u * sub + 32u * (static_cast<uint32_t>(n) >> 4);
+        const uint32_t my = min(w, nv - 1);   // lanes past the end repeat the last
         const uint32_t q0 = sw[3 * my], q1 = sw[3 * my + 1], q2 = sw[3 * my + 2];
         const uint64_t lo = (static_cast<uint64_t>(q0) >> 16) | (static_cast<uint64_t>(q1) << 16) |
                             (static_cast<uint64_t>(q2) << 48);
@@ -2640,8 +2644,8 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
         // a vector is bad if either half-wave saw a bad value
         const uint64_t badm = __ballot(!(ok && fin));
         const bool vbad = ((badm >> n) | (badm >> (n + 32))) & 1ull;
-        const bool active = t0 + static_cast<uint32_t>(n) < nv;
-        const uint32_t vi = v0 + t0 + static_cast<uint32_t>(n);
+        const bool active = w < nv;
+        const uint32_t vi = v0 + w;
         if (active && h == 0 && vbad) status_fail(lc.status, sidx, 1, vi, ok ? KIND_DECODE_NONFINITE : KIND_CORRUPT);
         if constexpr (!STAGED) {
             if (active && !vbad) {
@@ -2659,28 +2663,39 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
         }
         // vectors (of the 32) to write: active and good
         const uint32_t wmask = static_cast<uint32_t>(__ballot(active && !vbad && h == 0));
-        // Fan-out: stores go through LDS half a row at a time, so every store
-        // instruction writes 8 whole 128 B half rows instead of 32 B into each
-        // of 32 rows (at 8 copies that is 1.4 -> 5.3 TB/s of writes); one
-        // copy keeps the direct stores above (the LDS pass costs ~3 %).
+        // Fan-out: rows go through LDS, 16 whole rows (8 heads x 2 tokens) per
+        // pass, so each store instruction writes 4 whole 256 B rows -- two
+        // runs of two adjacent rows -- instead of 32 B into each of 32 rows
+        // (direct stores: 1.4 TB/s at 8 copies).  Row p of a pass holds lane
+        // n = (p % 8) + 8 pass + 16 (p / 8); one copy keeps the direct stores.
         float* hs = half_s[wave];
 #pragma unroll
-        for (int bb = 0; bb < 2; ++bb) {
+        for (uint32_t pass = 0; pass < 2; ++pass) {
+            if (((static_cast<uint32_t>(n) >> 3) & 1u) == pass) {
+                const uint32_t row = (static_cast<uint32_t>(n) & 7u) + 8u * (static_cast<uint32_t>(n) >> 4);
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {   // registers q .. q + 3: columns 32bb + 8g + 4h .. + 3
-                const int q = 16 * bb + 4 * g;
-                *reinterpret_cast<float4*>(hs + n * HPITCH + 8 * g + 4 * h) =
-                    make_float4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3]);
+                for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {   // registers q .. q + 3: columns 32bb + 8g + 4h .. + 3
+                        const int q = 16 * bb + 4 * g;
+                        *reinterpret_cast<float4*>(hs + row * RPITCH + 32 * bb + 8 * g + 4 * h) =
+                            make_float4(acc[q], acc[q + 1], acc[q + 2], acc[q + 3]);
+                    }
             }
             wave_sync();
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t r = static_cast<uint32_t>(lane >> 3) + 8u * k, c = lane & 7;
-                if ((wmask >> r) & 1u)
-                    store_out4(out, lc, vec_elem_offset(seg, v0 + t0 + r) + 32 * bb + 4 * c,
-                               *reinterpret_cast<const float4*>(hs + r * HPITCH + 4 * c));
+            for (int kk = 0; kk < 4; ++kk) {
+                // lanes 0-15: row 2kk (token t), 16-31: row 2kk + 8 (token t + 1), then the next head
+                const uint32_t sel = static_cast<uint32_t>(lane) >> 4, c = lane & 15;
+                const uint32_t row = 2u * kk + (sel >> 1) + 8u * (sel & 1u);
+                const uint32_t ln = (row & 7u) + 8u * pass + 16u * (row >> 3);
+                if ((wmask >> ln) & 1u) {
+                    const uint32_t wv = (ln & 15u) + 16u * sub + 32u * (ln >> 4);
+                    store_out4(out, lc, vec_elem_offset(seg, v0 + wv) + 4 * c,
+                               *reinterpret_cast<const float4*>(hs + row * RPITCH + 4 * c));
+                }
             }
-            wave_sync();   // the next half row overwrites the staging rows
+            wave_sync();   // the next pass overwrites the staging rows
         }
     }
 }
