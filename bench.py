@@ -7,7 +7,10 @@ hot tier (TQB1, lossless radii).  One step = build the pool + all 8 shells
 (encode: 2 launches) and rehydrate all 8 agents' full 1024-token KV -- pool
 and every shell, decoded once and written to each agent's cache -- straight
 into HuggingFace-layout KV caches ([1, H, T, D] per layer and K|V, f32;
-decode: 2 launches; 3,221,225,472 B written), inputs resident in HBM.
+decode: 2 launches; 3,221,225,472 B written), inputs resident in HBM.  The
+shell encode runs first, then the shell rehydrate on a second stream (on at
+most --side-workgroups workgroups) beside the pool encode, then the pool
+rehydrate (`--serial-tiers`: the four launches in order on one stream).
 
 value = f32 KV bytes of the context (402,653,184 B, the metric's "f32 in") /
 the GPU time of one step (events at the two ends of K back-to-back steps).  kernels_ms: a second pass
@@ -518,6 +521,11 @@ def main():
     ap.add_argument("--copies", type=int, default=8,
                     help="KV caches filled from one decode: config 3 rehydrates all 8 agents' full 1024-token "
                          "KV (default 8)")
+    ap.add_argument("--serial-tiers", action="store_true",
+                    help="run the pool tier and the shell tier one after the other on one stream (default: the "
+                         "shell tier on a second stream, concurrent with the pool tier)")
+    ap.add_argument("--side-workgroups", type=int, default=256,
+                    help="workgroups of the shell-tier rehydrate while it overlaps the pool encode")
     ap.add_argument("--workload", choices=("pool", "legacy", "config4", "score"), default="pool",
                     help="pool: the config-3 metric (default); legacy: per-vector TQW1 / FB1 records; "
                          "config4: Llama-3-8B shape, bf16, d128, TQB1-L; score: attention scores on "
@@ -558,11 +566,12 @@ def main():
     cache = DeviceKVCache(layers, heads, plan.tokens, dim, dtype=cache_dtype, copies=args.copies)
     dev = torch.from_numpy(corpus.reshape(-1)).cuda()
     stream = torch.cuda.current_stream()
+    side = None if args.serial_tiers else torch.cuda.Stream()   # default priority
 
     def step(evs=None):
         if evs is None:
-            plan.encode(dev, bufs)
-            plan.rehydrate(bufs, cache)
+            plan.build_and_rehydrate(dev, bufs, cache, stream=stream, side=side,
+                                     side_workgroups=args.side_workgroups)
             return
         e = evs
         pseg, sseg = plan._cache_segs
@@ -646,7 +655,9 @@ def main():
                                f", rehydrated into {args.copies} x [1,H,T,D] {args.cache_dtype} KV cache(s)",
                    "layers": layers, "kv_heads": heads, "head_dim": dim, "prefix_tokens": prefix,
                    "agents": len(agents), "agent_tokens": agents[0], "seed": 42,
-                   "cache_dtype": args.cache_dtype, "cache_copies": args.copies},
+                   "cache_dtype": args.cache_dtype, "cache_copies": args.copies,
+                   "tier_streams": 1 if args.serial_tiers else 2,
+                   "side_workgroups": None if args.serial_tiers else args.side_workgroups},
         "hbm_fraction_codec": round(total_alg / (step_gpu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "kernels_ms": {n: round(per[n], 4) for n in names},
         "kernels_gbs": {n: round(kern_gbs[n], 1) for n in names},

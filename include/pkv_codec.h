@@ -201,6 +201,19 @@ int pkv_decode_segments_ex(pkv_ctx* ctx, const pkv_profile* prof, int radii_code
                            uint32_t fanout, uint64_t fanout_stride, uint32_t* d_status,
                            void* stream);
 
+/* pkv_decode_segments_ex on a bounded share of the GPU: the head_dim-64
+ * turbo decode runs on at most max_workgroups workgroups (0: no bound), each
+ * looping over the blob tiles, so a kernel queued on another stream (the
+ * other tier's encode) gets the remaining compute units instead of waiting
+ * behind a full grid.  Other profiles decode as pkv_decode_segments_ex.  No
+ * counterpart in the reference (its tiers run one after the other); for
+ * callers that overlap the pool and shell tiers of one rehydrate. */
+int pkv_decode_segments_bounded(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec,
+                                const uint8_t* d_wire, uint64_t wire_bytes, const pkv_seg* segs,
+                                uint32_t nseg, void* d_out, int out_dtype, uint64_t out_elems,
+                                uint32_t fanout, uint64_t fanout_stride, uint32_t max_workgroups,
+                                uint32_t* d_status, void* stream);
+
 /* ---------------------------------------------------------------- host-buffer
  * Drop-ins for the adapters' inherent batch methods: host slices in, wire
  * bytes out (and back), with the H2D / launch / D2H / sync inside, exactly the

@@ -382,7 +382,8 @@ int launch_fib_encode_queued(pkv_ctx* ctx, const LaunchCommon& lc, const pkv_pro
 int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool encode, int dtype,
                         const void* d_f32, uint64_t f32_elems, const pkv_seg* segs, uint32_t nseg,
                         const uint8_t* d_wire, uint64_t wire_bytes, uint32_t* d_status, hipStream_t stream,
-                        bool per_vector = false, uint32_t fanout = 1, uint64_t fanout_stride = 0) {
+                        bool per_vector = false, uint32_t fanout = 1, uint64_t fanout_stride = 0,
+                        uint32_t grid_cap = 0) {
     if (!ctx || !prof) return PKV_ERR_INVALID_ARG;
     if (prof->kind == PKV_CODEC_TURBO && radii != PKV_RADII_F32 && radii != PKV_RADII_LOG_U8)
         return PKV_ERR_INVALID_ARG;
@@ -415,6 +416,7 @@ int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool e
     lc.out_dtype = encode ? static_cast<uint32_t>(PKV_F32) : static_cast<uint32_t>(dtype);
     lc.fanout = fanout;
     lc.fanout_stride = fanout_stride;
+    lc.grid_cap = grid_cap;
     const uint32_t nblocks = tiles[nseg];
     int e;
     if (prof->kind == PKV_CODEC_TURBO) {
@@ -1002,6 +1004,18 @@ int pkv_decode_segments_ex(pkv_ctx* ctx, const pkv_profile* prof, int radii_code
     std::lock_guard<std::mutex> lock(ctx->mu);
     return run_segments_locked(ctx, prof, radii_codec, false, out_dtype, d_out, out_elems, segs, nseg, d_wire,
                                wire_bytes, d_status, static_cast<hipStream_t>(stream), false, fanout, fanout_stride);
+}
+
+int pkv_decode_segments_bounded(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, const uint8_t* d_wire,
+                                uint64_t wire_bytes, const pkv_seg* segs, uint32_t nseg, void* d_out, int out_dtype,
+                                uint64_t out_elems, uint32_t fanout, uint64_t fanout_stride, uint32_t max_workgroups,
+                                uint32_t* d_status, void* stream) {
+    if (!ctx) return PKV_ERR_INVALID_ARG;
+    if (out_dtype != PKV_F32 && out_dtype != PKV_BF16 && out_dtype != PKV_F16) return PKV_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    return run_segments_locked(ctx, prof, radii_codec, false, out_dtype, d_out, out_elems, segs, nseg, d_wire,
+                               wire_bytes, d_status, static_cast<hipStream_t>(stream), false, fanout, fanout_stride,
+                               max_workgroups);
 }
 
 int pkv_parse_header(const pkv_profile* p, const uint8_t* b, uint64_t len, uint64_t* n_vectors, int* radii_codec) {

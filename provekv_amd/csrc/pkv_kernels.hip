@@ -1346,7 +1346,12 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split_kernel(
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int h = lane >> 5, n = lane & 31;
-    const uint32_t blk = blockIdx.x >> 1;
+    // half-tiles vb = 2 * tile + half; a grid smaller than the count loops
+    // (a bounded share of the GPU, so another kernel can run beside it)
+    const uint32_t nvb = 2u * lc.tile_start[lc.nseg];
+    for (uint32_t vb = blockIdx.x; vb < nvb; vb += gridDim.x) {
+    wave_sync();   // the previous half-tile's rows are out of LDS
+    const uint32_t blk = vb >> 1;
     const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
     const SegDev seg = lc.segs[sidx];
     const uint32_t tile = blk - lc.tile_start[sidx];
@@ -1359,10 +1364,10 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split_kernel(
                       hb != tqb1_byte(lane, DIM, pbits, lc.radii, proj, seed, seg.n_vectors, plen);
     if (__ballot(hbad) != 0ull) {
         if (lane == 0) status_fail(lc.status, sidx, 0, 0u, KIND_HEADER);
-        return;
+        continue;
     }
-    const uint32_t t0 = tile * TILE + (blockIdx.x & 1u) * (TILE / 2) + 32u * static_cast<uint32_t>(wave);
-    if (t0 >= seg.n_vectors) return;
+    const uint32_t t0 = tile * TILE + (vb & 1u) * (TILE / 2) + 32u * static_cast<uint32_t>(wave);
+    if (t0 >= seg.n_vectors) continue;
     const uint32_t nv = min(32u, seg.n_vectors - t0);
     // per wave: the 32 payloads, later the 32 decoded rows (pitch DIM + 4)
     uint32_t* sw = smem_u + wave * turbo_split_wave_words(pwd);
@@ -1436,6 +1441,7 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split_kernel(
     const uint64_t badm = __ballot(active && h == 0 && !vok);
     wave_sync();
     stage_rows_out<DIM>(out, lc, stage, seg, t0, nv, static_cast<uint32_t>(badm), 0u, lane);
+    }
 }
 
 // Turbo decode at head_dim 128: four lanes per vector as in
@@ -2795,9 +2801,11 @@ int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (td.dim == 64 && td.pbits <= 4) {
         const size_t lds = static_cast<size_t>(WAVES) * turbo_split_wave_words(lc.plen >> 2) * sizeof(uint32_t);
-        return td.pbits == 3 ? launch_big_lds(turbo_decode_split_kernel<3>, 2 * nblocks, lds, st, lc, wire, out,
+        if (nblocks > (1u << 30)) return hipErrorInvalidValue;   // 2 workgroups per tile
+        const uint32_t grid = lc.grid_cap ? std::min(2 * nblocks, lc.grid_cap) : 2 * nblocks;
+        return td.pbits == 3 ? launch_big_lds(turbo_decode_split_kernel<3>, grid, lds, st, lc, wire, out,
                                               td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode)
-                             : launch_big_lds(turbo_decode_split_kernel<0>, 2 * nblocks, lds, st, lc, wire, out,
+                             : launch_big_lds(turbo_decode_split_kernel<0>, grid, lds, st, lc, wire, out,
                                               td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode);
     }
     if (td.dim == 128 && td.pbits <= 4) {

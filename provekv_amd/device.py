@@ -192,10 +192,11 @@ class Profile:
         L.check(rc, "pkv_encode_segments")
 
     def decode_segments(self, wire, segs: np.ndarray, out, radii: int = L.RADII_F32, status=None,
-                        stream=None, fanout: int = 1, fanout_stride: int = 0) -> None:
+                        stream=None, fanout: int = 1, fanout_stride: int = 0, max_workgroups: int = 0) -> None:
         """Decode into `out` (float32, bfloat16 or float16; the latter two are
         the f32 decode rounded to nearest even), each vector written `fanout`
-        times `fanout_stride` elements apart."""
+        times `fanout_stride` elements apart.  max_workgroups > 0 bounds the
+        head_dim-64 turbo decode's grid (it then loops over the tiles)."""
         torch = _torch()
         segs = np.ascontiguousarray(segs, dtype=SEG_DTYPE)
         dts = {torch.float32: L.DT_F32, torch.bfloat16: L.DT_BF16, torch.float16: L.DT_F16}
@@ -204,6 +205,13 @@ class Profile:
         if not (out.is_contiguous() and wire.is_contiguous()):
             raise ValueError("tensors must be contiguous")
         st = self._status_ptr(status, len(segs))
+        if max_workgroups:
+            rc = L.lib().pkv_decode_segments_bounded(self.ctx.ptr, self._ptr, radii, wire.data_ptr(), wire.numel(),
+                                                     segs.ctypes.data, len(segs), out.data_ptr(), dts[out.dtype],
+                                                     out.numel(), fanout, fanout_stride, max_workgroups, st,
+                                                     _stream_ptr(stream))
+            L.check(rc, "pkv_decode_segments_bounded")
+            return
         if out.dtype == torch.float32 and fanout == 1:
             rc = L.lib().pkv_decode_segments(self.ctx.ptr, self._ptr, radii, wire.data_ptr(), wire.numel(),
                                              segs.ctypes.data, len(segs), out.data_ptr(), out.numel(), st,

@@ -192,6 +192,40 @@ class TwoTierPlan:
         proveKV/scripts/ppl_validate_multi_agent.py:226-272) -- in the cache's
         dtype, once per cache copy: two launches.  Status words land in
         bufs["pool_cstatus"] / bufs["shell_cstatus"]."""
+        self._rehydrate_tier("pool", bufs, cache, stream)
+        self._rehydrate_tier("shells", bufs, cache, stream)
+
+    def build_and_rehydrate(self, corpus, bufs, cache: DeviceKVCache, stream=None, side=None,
+                            side_workgroups: int = 256):
+        """One whole step: each tier's encode followed by its rehydrate into
+        `cache`.  The tiers share nothing but the read-only corpus (disjoint
+        wires, status words and cache token ranges), so with a `side` stream
+        they overlap: the shell encode runs first on `stream`; then the shell
+        rehydrate (HBM writes) runs on `side` on at most `side_workgroups`
+        workgroups while the pool encode (VALU and matrix cores) takes the rest
+        of the GPU on `stream`; then the pool rehydrate.  `stream` waits for
+        `side` at the end, so work queued after this call sees both tiers
+        done.  Without `side` the four launches run in order on `stream`."""
+        import torch
+        main = stream if stream is not None else torch.cuda.current_stream()
+        if side is None:
+            self.encode(corpus, bufs, stream=main)
+            self.rehydrate(bufs, cache, stream=main)
+            return
+        shells_encoded, join = torch.cuda.Event(), torch.cuda.Event()
+        self.turbo.encode_segments(corpus, self.shells.enc, bufs["shell_wire"], radii=self.radii,
+                                   status=bufs["shell_status"], stream=main)
+        shells_encoded.record(main)
+        side.wait_event(shells_encoded)
+        self._rehydrate_tier("shells", bufs, cache, side, max_workgroups=side_workgroups)
+        self.fib.encode_segments(corpus, self.pool.enc, bufs["pool_wire"], status=bufs["pool_status"], stream=main)
+        self._rehydrate_tier("pool", bufs, cache, main)
+        join.record(side)
+        main.wait_event(join)
+
+    def _cache_tables(self, bufs, cache: DeviceKVCache):
+        """Decode segment tables for `cache` (built once per cache) and the
+        rehydrate status buffers."""
         import torch
         key = id(cache)
         if getattr(self, "_cache_key", None) != key:
@@ -207,12 +241,19 @@ class TwoTierPlan:
         for name, n in (("pool_cstatus", len(pseg)), ("shell_cstatus", len(sseg))):
             if name not in bufs:
                 bufs[name] = torch.empty(2 * n, dtype=torch.int32, device=cache.buf.device)
+
+    def _rehydrate_tier(self, tier: str, bufs, cache: DeviceKVCache, stream, max_workgroups: int = 0):
+        self._cache_tables(bufs, cache)
+        pseg, sseg = self._cache_segs
         out = cache.buf.view(-1)
-        self.fib.decode_segments(bufs["pool_wire"], pseg, out, status=bufs["pool_cstatus"], stream=stream,
-                                 fanout=cache.copies, fanout_stride=cache.copy_stride)
-        self.turbo.decode_segments(bufs["shell_wire"], sseg, out, radii=self.radii, status=bufs["shell_cstatus"],
-                                   stream=stream, fanout=cache.copies, fanout_stride=cache.copy_stride)
-        cache.mark_filled(self.tokens)
+        if tier == "pool":
+            self.fib.decode_segments(bufs["pool_wire"], pseg, out, status=bufs["pool_cstatus"], stream=stream,
+                                     fanout=cache.copies, fanout_stride=cache.copy_stride)
+        else:
+            self.turbo.decode_segments(bufs["shell_wire"], sseg, out, radii=self.radii,
+                                       status=bufs["shell_cstatus"], stream=stream, fanout=cache.copies,
+                                       fanout_stride=cache.copy_stride, max_workgroups=max_workgroups)
+            cache.mark_filled(self.tokens)
 
     def check_rehydrate(self, bufs):
         """Raise the first failure recorded by the last rehydrate."""

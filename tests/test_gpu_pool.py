@@ -123,6 +123,74 @@ def test_rehydrate_into_cache_layout(ctx, dtype, copies, lossy):
     assert tuple(cache.keys(1, copies - 1).shape) == (1, heads, prefix + sum(agents), dim)
 
 
+@pytest.mark.parametrize("lossy", [False, True])
+def test_build_and_rehydrate_two_streams(ctx, lossy):
+    """The whole step with the shell tier on a second stream: encode bytes and
+    the rehydrated caches equal the one-stream step bit for bit, and work
+    queued on the main stream afterwards sees both tiers (the join)."""
+    import torch
+    from provekv_amd.pool import DeviceKVCache
+    layers, heads, dim, prefix, agents = 3, 8, 64, 150, [20, 33, 7]
+    corpus = synth.corpus_tokens(9, layers, heads, prefix + sum(agents), dim)
+    dev = torch.from_numpy(corpus.reshape(-1)).cuda()
+    plan = TwoTierPlan(ctx, layers, heads, dim, prefix, agents, seed=SEED, lossy=lossy)
+    caches, wires = [], []
+    side = torch.cuda.Stream()
+    for use_side in (False, True):
+        bufs = plan.alloc()
+        cache = DeviceKVCache(layers, heads, prefix + sum(agents), dim, copies=3)
+        cache.buf.fill_(7.0)
+        main = torch.cuda.Stream()
+        with torch.cuda.stream(main):
+            for _ in range(2):   # back to back: the second step reuses every buffer
+                plan.build_and_rehydrate(dev, bufs, cache, stream=main, side=side if use_side else None)
+            snap = cache.buf.clone()   # queued on main after the join
+        torch.cuda.synchronize()
+        plan.check(bufs, decode=False)
+        plan.check_rehydrate(bufs)
+        caches.append(snap.cpu())
+        wires.append((bufs["pool_wire"].cpu(), bufs["shell_wire"].cpu()))
+    assert torch.equal(caches[0].view(torch.int32), caches[1].view(torch.int32))
+    assert torch.equal(wires[0][0], wires[1][0]) and torch.equal(wires[0][1], wires[1][1])
+    ref = torch.from_numpy(_patched_cache(plan, corpus, layers, heads, dim, prefix, agents, lossy))
+    assert torch.equal(caches[1][0].view(torch.int32), ref.view(torch.int32))
+
+
+@pytest.mark.parametrize("max_workgroups", [1, 3, 64])
+def test_bounded_turbo_decode_matches_full_grid(ctx, max_workgroups):
+    """pkv_decode_segments_bounded: a grid of a few workgroups looping over
+    every half-tile writes the same cache as one workgroup per half-tile,
+    and reports a corrupt vector the same way."""
+    import torch
+    from provekv_amd.pool import DeviceKVCache
+    layers, heads, dim, prefix, agents = 2, 8, 64, 10, [40, 17, 300]
+    corpus = synth.corpus_tokens(11, layers, heads, prefix + sum(agents), dim)
+    plan = TwoTierPlan(ctx, layers, heads, dim, prefix, agents, seed=SEED)
+    bufs = plan.alloc()
+    plan.encode(torch.from_numpy(corpus.reshape(-1)).cuda(), bufs)
+    plen = plan.turbo.payload_len()
+    # corrupt one radius of vector 123 of blob 5 (a negative radius)
+    _, _, _, off, _ = plan.shells.blob_offsets[5]
+    pos = off + 38 + 123 * plen + 4 * 7
+    bufs["shell_wire"][pos:pos + 4] = torch.from_numpy(np.frombuffer(np.float32(-2.0).tobytes(), np.uint8).copy()).cuda()
+    outs, stats = [], []
+    for bound in (0, max_workgroups):
+        cache = DeviceKVCache(layers, heads, prefix + sum(agents), dim, copies=2)
+        cache.buf.fill_(3.0)
+        plan._cache_tables(bufs, cache)
+        _, sseg = plan._cache_segs
+        st = torch.zeros(2 * len(sseg), dtype=torch.int32, device="cuda")
+        plan.turbo.decode_segments(bufs["shell_wire"], sseg, cache.buf.view(-1), status=st, fanout=2,
+                                   fanout_stride=cache.copy_stride, max_workgroups=bound)
+        torch.cuda.synchronize()
+        outs.append(cache.buf.cpu())
+        stats.append(st.cpu().numpy().view(np.uint32).copy())
+    assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32))
+    assert np.array_equal(stats[0], stats[1])
+    err = plan.turbo.status_error(stats[1], sseg)
+    assert err is not None and err.segment == 5 and err.index == 123
+
+
 def test_cache_target_append(ctx):
     """CacheTarget (proveKV/src/pool.rs:646-658): append one token's [H * D]
     key / value at a position in every copy."""
