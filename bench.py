@@ -54,10 +54,14 @@ def cpu_baseline(corpus: np.ndarray, plan, budget_s: float = 16.0) -> dict:
     x_pool = np.ascontiguousarray(corpus[:plan.prefix, 0, :, 0, :].reshape(-1, dim))[:25600]
     x_shell = np.ascontiguousarray(corpus[plan.prefix:plan.prefix + plan.agent_tokens[0], 0, :, 0, :]
                                    .reshape(-1, dim))
+    freps = 0
     t0 = time.perf_counter()
-    blob = O.fib_encode_batch(x_pool, cb, rot)
-    t1 = time.perf_counter()
-    O.fib_decode_batch(blob, cb, rot)
+    while True:
+        blob = O.fib_encode_batch(x_pool, cb, rot)
+        O.fib_decode_batch(blob, cb, rot)
+        freps += 1
+        if time.perf_counter() - t0 > budget_s / 2:
+            break
     t2 = time.perf_counter()
     reps = 0
     t3 = time.perf_counter()
@@ -68,15 +72,15 @@ def cpu_baseline(corpus: np.ndarray, plan, budget_s: float = 16.0) -> dict:
         if time.perf_counter() - t3 > budget_s / 2:
             break
     t4 = time.perf_counter()
-    fib_s_per_vec = ((t1 - t0) + (t2 - t1)) / x_pool.shape[0]
+    fib_s_per_vec = (t2 - t0) / (freps * x_pool.shape[0])
     turbo_s_per_vec = (t4 - t3) / (reps * x_shell.shape[0])
     n_pool = plan.prefix * plan.heads * layers * 2
     n_shell = sum(plan.agent_tokens) * plan.heads * layers * 2
     total_s = n_pool * fib_s_per_vec + n_shell * turbo_s_per_vec
     f32_bytes = (n_pool + n_shell) * dim * 4
     return {"value": round(f32_bytes / total_s / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": (f"oracle/pkv_oracle.c, 1 thread: fib FB2 encode+decode of {x_pool.shape[0]} pool vectors "
-                       f"({(t2 - t0):.2f} s) and turbo TQB1 encode+decode of {x_shell.shape[0]} shell vectors x "
+            "sample": (f"oracle/pkv_oracle.c, 1 thread: fib FB2 encode+decode of {x_pool.shape[0]} pool vectors x "
+                       f"{freps} reps ({(t2 - t0):.2f} s) and turbo TQB1 encode+decode of {x_shell.shape[0]} shell vectors x "
                        f"{reps} reps ({(t4 - t3):.2f} s), scaled to the {n_pool}+{n_shell}-vector workload"),
             "encode_decode_s_projected": round(total_s, 2)}
 
