@@ -1824,6 +1824,7 @@ turbo_score_lut_kernel(
     if (threadIdx.x < 32) exp_lds[threadIdx.x] = c_exp2f_tab[threadIdx.x];
     if (LOSSY)
         for (uint32_t t = threadIdx.x; t < 256; t += blockDim.x) div255_lds[t] = c_div255.v[t];
+    __syncthreads();   // the tables are read by every wave (radii below, the (cos, sin) terms later)
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint32_t blk = blockIdx.x;
