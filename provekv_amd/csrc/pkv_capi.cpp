@@ -89,14 +89,6 @@ struct Slot {
     uint64_t hash = 0;
 };
 
-// fib encode redo queues, a ring of their own (the kernels write them)
-struct RedoSlot {
-    void* dev = nullptr;
-    size_t cap = 0;
-    hipEvent_t ev = nullptr;
-    Users users;
-};
-
 }  // namespace
 
 struct pkv_ctx {
@@ -104,8 +96,6 @@ struct pkv_ctx {
     std::mutex mu;
     Slot slots[kSlots];
     int next = 0;
-    RedoSlot redo[kSlots];
-    int redo_next = 0;
     hipStream_t own_stream = nullptr;   // for the host-buffer entry points
     void* scratch = nullptr;            // host-buffer entry points: in + out
     size_t scratch_cap = 0;
@@ -336,48 +326,6 @@ FibDev fib_dev(const pkv_profile* p) {
     return f;
 }
 
-// fib encode: the next redo-queue buffer of the ring (a 4-word head and TILE
-// entries per workgroup), then the MFMA kernel and the exact fixup.
-int launch_fib_encode_queued(pkv_ctx* ctx, const LaunchCommon& lc, const pkv_profile* prof, const void* d_in,
-                             uint8_t* d_wire, uint32_t nblocks, hipStream_t stream) {
-    // a redo buffer last used by this stream alone needs no wait (stream order)
-    RedoSlot* pick = nullptr;
-    for (RedoSlot& r : ctx->redo)
-        if (r.dev && r.users.only(stream)) { pick = &r; break; }
-    if (!pick) {
-        pick = &ctx->redo[ctx->redo_next];
-        ctx->redo_next = (ctx->redo_next + 1) % kSlots;
-    }
-    RedoSlot& rs = *pick;
-    hipError_t e = hipSuccess;
-    if (!rs.ev && (e = hipEventCreateWithFlags(&rs.ev, hipEventDisableTiming)) != hipSuccess) return e;
-    if (!rs.users.only(stream)) {
-        int rc = rs.users.drain_stream(rs.ev, stream);
-        if (rc) return hipErrorUnknown;
-    }
-    const size_t counts_bytes = (16 * static_cast<size_t>(nblocks) + 255) & ~static_cast<size_t>(255);
-    const size_t need = counts_bytes + 4 * static_cast<size_t>(TILE) * nblocks;
-    if (rs.cap < need) {
-        if (rs.users.n || rs.users.overflow) {
-            int rc = rs.users.drain_host(rs.ev);
-            if (rc) return hipErrorUnknown;
-        }
-        if (rs.dev && (e = hipFree(rs.dev)) != hipSuccess) return e;
-        rs.dev = nullptr;
-        rs.cap = 0;
-        const size_t cap = std::max<size_t>(need + need / 4, 1 << 16);
-        if ((e = hipMalloc(&rs.dev, cap)) != hipSuccess) return e;
-        rs.cap = cap;
-    }
-    FibRedo rq;
-    rq.heads = static_cast<uint32_t*>(rs.dev);
-    rq.entries = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(rs.dev) + counts_bytes);
-    int rc = launch_fib_encode(lc, fib_dev(prof), d_in, d_wire, nblocks, rq, stream);
-    if (rc) return rc;
-    rs.users.add(stream);
-    return hipSuccess;
-}
-
 // Caller holds ctx->mu.
 int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool encode, int dtype,
                         const void* d_f32, uint64_t f32_elems, const pkv_seg* segs, uint32_t nseg,
@@ -423,7 +371,7 @@ int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool e
         e = encode ? launch_turbo_encode(lc, turbo_dev(prof), d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
                    : launch_turbo_decode(lc, turbo_dev(prof), d_wire, const_cast<void*>(d_f32), nblocks, stream);
     } else {
-        e = encode ? launch_fib_encode_queued(ctx, lc, prof, d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
+        e = encode ? launch_fib_encode(lc, fib_dev(prof), d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
                    : launch_fib_decode(lc, fib_dev(prof), d_wire, const_cast<void*>(d_f32), nblocks, stream);
     }
     int rc2 = finish_slot(sl, stream);
@@ -618,11 +566,6 @@ void pkv_ctx_destroy(pkv_ctx* ctx) {
         if (s.ev) (void)hipEventDestroy(s.ev);
         if (s.dev) (void)hipFree(s.dev);
         if (s.host) (void)hipHostFree(s.host);
-    }
-    for (RedoSlot& r : ctx->redo) {
-        if (r.users.n || r.users.overflow) (void)r.users.drain_host(r.ev);
-        if (r.ev) (void)hipEventDestroy(r.ev);
-        if (r.dev) (void)hipFree(r.dev);
     }
     if (ctx->own_stream) {
         (void)hipStreamSynchronize(ctx->own_stream);

@@ -85,16 +85,6 @@ struct FibDev {
     uint32_t dim, k, n, bits;
 };
 
-// Per-workgroup queues of vectors whose approximate argmin was not proven,
-// filled by fib_encode_kernel and drained by fib_fixup_kernel.  Workgroup b
-// (TILE vectors of one segment) writes heads[4b ..] = {entry count, segment,
-// first vector index, 0} and owns entries[b * TILE ..]; an entry is (vector
-// index within the workgroup) | (mask of undecided blocks) << 8.
-struct FibRedo {
-    uint32_t* heads;        // 4 words per workgroup
-    uint32_t* entries;      // TILE per workgroup
-};
-
 struct LaunchCommon {
     const SegDev* segs;
     const uint32_t* tile_start;   // nseg + 1 prefix of workgroups per segment
@@ -137,8 +127,8 @@ int launch_turbo_prepare(const TurboDev& td, const float* q, uint32_t nq, float*
 int launch_turbo_score(const LaunchCommon& lc, const TurboDev& td, const uint8_t* wire, const float* prepared,
                        uint32_t nq, uint64_t qstride, float* scores, uint64_t ld, float qscale, float post,
                        uint32_t nblocks, void* stream);
-int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire,
-                      uint32_t nblocks, const FibRedo& rq, void* stream);
+int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire, uint32_t nblocks,
+                      void* stream);
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, void* out,
                       uint32_t nblocks, void* stream);
 int launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, void* stream);

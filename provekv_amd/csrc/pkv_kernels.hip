@@ -2002,8 +2002,9 @@ turbo_score_lut_kernel(
 // If the second smallest key exceeds the smallest by more than `thr` (2.5x
 // the host-derived worst-case error of a key against the reference's f32
 // distance), the smallest key's codeword is the reference's strict argmin.
-// Otherwise the vector is queued with the mask of its undecided blocks (a
-// few % of vectors) and fib_fixup_kernel redoes those blocks exactly: f64
+// Otherwise the vector is queued (in the workgroup's LDS queue) with the mask
+// of its undecided blocks (a few % of vectors), and once every wave has
+// queued, the workgroup redoes those blocks exactly (fib_fixup_wave): f64
 // sequential rows of the exact x_hat and the AVX2-order f32 distances.
 // Segments of fewer than 4 vectors (the reference's single-vector path with
 // an f64 x_hat) queue all 16 blocks.
@@ -2213,24 +2214,168 @@ __device__ __forceinline__ void fib_encode_score(const LaunchCommon& lc, const S
             q_entries[slot] = (vi - tile_v0) | (small ? 0xFFFFu : redo) << 8;
         }
     }
-    // payload [f16 norm][16 x 5-bit indices] = 12 bytes via LDS, so the
-    // wave's 32 payloads leave as one byte range
+    // payload [f16 norm][16 x 5-bit indices] = 12 bytes, kept in LDS: the
+    // exact redo patches it there and the wave's 64 payloads then leave as
+    // one byte range
     if (owner) {
         pay[3 * n + 0] = static_cast<uint32_t>(h16) | (iw[0] << 16);
         pay[3 * n + 1] = (iw[0] >> 16) | (iw[1] << 16);
         pay[3 * n + 2] = (iw[1] >> 16) | (iw[2] << 16);
     }
-    wave_sync();
-    lds_to_global(blob + 19 + static_cast<uint64_t>(v0) * PLEN, pay, nv * PLEN, lane);
-    wave_sync();
+    (void)blob;
+    (void)nv;
 }
 
-constexpr int FIB_PAY_WORDS = 32 * 3 + 4;
+// Exact redo of the queued (vector, block) decisions of fib_encode_kernel,
+// run by the encoding workgroup itself once every wave has queued: wave w
+// takes the queue's groups of 16 entries w, w + 4, ...  4 lanes per vector
+// load it, one lane takes the sequential f64 norm and the 4 lanes form
+// x_hat = f32(x / norm) (segments of fewer than 4 vectors keep x / norm in
+// f64, codec.rs:481 vs 608); then 16 undecided blocks at a time get one lane
+// per rho row (sequential f64 dot, rotation.rs:107-113) and a quarter of the
+// codewords per lane in the AVX2 distance order with strict <
+// (simd_nearest.rs:44-104); the entry's owner lane patches the 5-bit fields
+// of the payload in LDS (pay_of(local vector) -> its 3 payload words).
+struct FibFixupLds {
+    float x[WAVES][16][64 + 4];   // x, then x_hat (segments of >= 4 vectors); padded rows
+    double nrm[WAVES][16];
+    float part[WAVES][16][4][2];
+    float rho[WAVES][16][4];
+    uint32_t mask[WAVES][16];
+    uint8_t res[WAVES][16][16];
+};
+
+template <int DIM, typename PayOf>
+__device__ void fib_fixup_wave(const LaunchCommon& lc, const void* __restrict__ in, const double* __restrict__ rot_t,
+                               const float* __restrict__ cb, const SegDev& seg, uint32_t tile_v0,
+                               const uint32_t* ents, uint32_t count, FibFixupLds& f, PayOf pay_of, int wave,
+                               int lane) {
+    static_assert(DIM == 64, "four lanes of 16 elements per vector");
+    constexpr int G = 16;
+    const int e = lane >> 2, t = lane & 3;
+    const bool small = seg.n_vectors < 4 || lc.per_vector != 0;
+    for (uint32_t g0 = G * static_cast<uint32_t>(wave); g0 < count; g0 += G * WAVES) {
+        const uint32_t ne = min(static_cast<uint32_t>(G), count - g0);
+        const bool has = static_cast<uint32_t>(e) < ne;
+        uint32_t li = 0, mask = 0;
+        if (has) {
+            const uint32_t ent = ents[g0 + e];
+            li = ent & 0xFFu;
+            mask = ent >> 8;
+            const uint64_t off = vec_elem_offset(seg, tile_v0 + li) + 16u * static_cast<uint32_t>(t);
+            float4* dst = reinterpret_cast<float4*>(&f.x[wave][e][16 * t]);
+            if (!lc.in_bf16) {
+                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(in) + off);
+                const float4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
+                dst[0] = v0; dst[1] = v1; dst[2] = v2; dst[3] = v3;
+            } else {
+                const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(in) + off);
+                const uint4 w0 = src[0], w1 = src[1];
+                const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    dst[k] = make_float4(u2f(w[2 * k] << 16), u2f(w[2 * k] & 0xffff0000u), u2f(w[2 * k + 1] << 16),
+                                         u2f(w[2 * k + 1] & 0xffff0000u));
+            }
+            if (t == 0) f.mask[wave][e] = mask;
+        }
+        wave_sync();
+        if (has && t == 0) {   // l2_norm: sequential f64; a square of an f32 is exact, so fma == s + d * d
+            double s2 = 0.0;
+#pragma unroll 16
+            for (int c = 0; c < DIM; ++c) {
+                const double d = static_cast<double>(f.x[wave][e][c]);
+                s2 = __builtin_fma(d, d, s2);
+            }
+            f.nrm[wave][e] = __builtin_sqrt(s2);
+        }
+        wave_sync();
+        if (has && !small) {
+            const double nrm = f.nrm[wave][e];
+#pragma unroll
+            for (int c = 16 * t; c < 16 * t + 16; ++c)
+                f.x[wave][e][c] = static_cast<float>(static_cast<double>(f.x[wave][e][c]) / nrm);
+        }
+        wave_sync();
+        uint32_t total = 0;
+        for (uint32_t j = 0; j < ne; ++j) total += __popc(f.mask[wave][j]);
+        for (uint32_t p0 = 0; p0 < total; p0 += G) {
+            const uint32_t qi = p0 + static_cast<uint32_t>(e);
+            int pe = -1, pb = 0;
+            if (qi < total) {
+                uint32_t acc = 0;
+                for (uint32_t j = 0; j < ne; ++j) {
+                    uint32_t m = f.mask[wave][j];
+                    const uint32_t c = __popc(m);
+                    if (qi < acc + c) {
+                        for (uint32_t k = qi - acc; k > 0; --k) m &= m - 1u;
+                        pe = static_cast<int>(j);
+                        pb = __ffs(m) - 1;
+                        break;
+                    }
+                    acc += c;
+                }
+            }
+            if (pe >= 0) {   // Pi^T: at step c all lanes read within one 512 B row
+                const double* col = rot_t + (4 * pb + t);
+                const float* xr = f.x[wave][pe];
+                double a = 0.0;
+                if (!small) {
+#pragma unroll 16
+                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * static_cast<double>(xr[c]);
+                } else {
+                    const double nrm = f.nrm[wave][pe];
+                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * (static_cast<double>(xr[c]) / nrm);
+                }
+                f.rho[wave][e][t] = static_cast<float>(a);
+            }
+            wave_sync();
+            if (pe >= 0) {
+                const float s0 = f.rho[wave][e][0], s1 = f.rho[wave][e][1];
+                const float s2 = f.rho[wave][e][2], s3 = f.rho[wave][e][3];
+                float bd = u2f(0x7f800000u);
+                uint32_t bw = 0;
+#pragma unroll
+                for (int w = 8 * t; w < 8 * t + 8; ++w) {
+                    const float* c = cb + 4 * w;
+                    const float e0 = c[0] - s0, e1 = c[1] - s1, e2 = c[2] - s2, e3 = c[3] - s3;
+                    const float dd = (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
+                    if (dd < bd) { bd = dd; bw = static_cast<uint32_t>(w); }
+                }
+                f.part[wave][e][t][0] = bd;
+                f.part[wave][e][t][1] = u2f(bw);
+            }
+            wave_sync();
+            if (pe >= 0 && t == 0) {
+                float bd = f.part[wave][e][0][0];
+                uint32_t bw = f2u(f.part[wave][e][0][1]);
+                for (int u = 1; u < 4; ++u)
+                    if (f.part[wave][e][u][0] < bd) { bd = f.part[wave][e][u][0]; bw = f2u(f.part[wave][e][u][1]); }
+                f.res[wave][pe][pb] = static_cast<uint8_t>(bw);
+            }
+            wave_sync();
+        }
+        if (has && t == 0) {   // index b at payload bits 16 + 5b (after the f16 norm), LSB-first
+            uint32_t* pw = pay_of(li);
+            for (int b = 0; b < DIM / 4; ++b) {
+                if (!((mask >> b) & 1u)) continue;
+                const uint32_t w = f.res[wave][e][b];
+                const int bit = 16 + 5 * b, wd = bit >> 5, sh = bit & 31;
+                pw[wd] = (pw[wd] & ~(31u << sh)) | (w << sh);
+                if (sh > 27) pw[wd + 1] = (pw[wd + 1] & ~(31u >> (32 - sh))) | (w >> (32 - sh));
+            }
+        }
+        wave_sync();
+    }
+}
+
+constexpr int FIB_PAY_WORDS = 64 * 3 + 4;   // per wave: both 32-vector sub-tiles
 
 template <int DIM>
 __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const void* __restrict__ in,
                                                           uint8_t* __restrict__ wire, const uint32_t* __restrict__ mf,
-                                                          float thr, FibRedo rq) {
+                                                          float thr, const double* __restrict__ rot_t,
+                                                          const float* __restrict__ cb) {
     static_assert(DIM == 64, "the MFMA layout is built for head_dim 64");
     extern __shared__ uint32_t smem_u[];
     uint32_t* rot_lds = smem_u;   // MF_ROT block (MF_SCA words)
@@ -2263,8 +2408,8 @@ __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const
     const uint4 sa4 = reinterpret_cast<const uint4*>(mf + MF_SCA)[lane];
     const v4u sa = {sa4.x, sa4.y, sa4.z, sa4.w};
     __shared__ uint32_t q_count;
+    __shared__ uint32_t q_entries[TILE];   // (local vector) | (blocks to redo) << 8
     if (threadIdx.x == 0) q_count = 0;
-    uint32_t* q_entries = rq.entries + static_cast<uint64_t>(blk) * TILE;
     const uint32_t tile_v0 = tile * TILE;
     __syncthreads();
 
@@ -2280,163 +2425,23 @@ __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const
     if (v0 + 32 < seg.n_vectors) {
         FibTileRot t;
         fib_encode_rotate(t, xb, rot_lds, lane);
-        fib_encode_score<DIM>(lc, seg, sidx, blob, v0 + 32, t, pay, sa, thr, &q_count, q_entries, tile_v0, lane);
+        fib_encode_score<DIM>(lc, seg, sidx, blob, v0 + 32, t, pay + 96, sa, thr, &q_count, q_entries, tile_v0,
+                              lane);
     }
     if (tile == 0 && threadIdx.x < 19)
         blob[threadIdx.x] = static_cast<uint8_t>(fb2_byte(threadIdx.x, 5u, DIM / 4, seg.n_vectors, 10u));
-    __syncthreads();
-    if (threadIdx.x == 0)
-        *reinterpret_cast<uint4*>(rq.heads + 4ull * blk) = make_uint4(q_count, sidx, tile_v0, 0u);
-}
-
-// Exact redo of the queued (vector, block) decisions of fib_encode_kernel.
-// Wave w of workgroup b drains the queue of encode workgroup 4b + w, 16
-// entries at a time: 4 lanes per vector load it, one lane takes the
-// sequential f64 norm and the 4 lanes form x_hat = f32(x / norm) (segments of
-// fewer than 4 vectors keep x / norm in f64, codec.rs:481 vs 608); then 16
-// undecided blocks at a time get one lane per rho row (sequential f64 dot,
-// rotation.rs:107-113) and a quarter of the codewords per lane in the AVX2
-// distance order with strict < (simd_nearest.rs:44-104); the entry's owner
-// lane patches the 5-bit fields.
-template <int DIM>
-__global__ __launch_bounds__(TILE) void fib_fixup_kernel(LaunchCommon lc, const void* __restrict__ in,
-                                                         uint8_t* __restrict__ wire, const double* __restrict__ rot_t,
-                                                         const float* __restrict__ cb, FibRedo rq, uint32_t ntiles) {
-    static_assert(DIM == 64, "four lanes of 16 elements per vector");
-    constexpr int G = 16;
-    __shared__ float x_s[WAVES][G][DIM + 4];   // x, then x_hat (segments of >= 4 vectors); padded rows
-    __shared__ double nrm_s[WAVES][G];
-    __shared__ float part_s[WAVES][G][4][2];
-    __shared__ float rho_s[WAVES][G][4];
-    __shared__ uint32_t mask_s[WAVES][G];
-    __shared__ uint8_t res_s[WAVES][G][DIM / 4];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int e = lane >> 2, t = lane & 3;
-    const uint32_t tb = blockIdx.x * WAVES + wave;
-    if (tb >= ntiles) return;
-    const uint4 head = *reinterpret_cast<const uint4*>(rq.heads + 4ull * tb);
-    const uint32_t count = min(head.x, TILE);
-    if (count == 0) return;
-    const SegDev seg = lc.segs[head.y];
-    const bool small = seg.n_vectors < 4 || lc.per_vector != 0;
-    const uint32_t tile_v0 = head.z;
-    const uint32_t* ents = rq.entries + static_cast<uint64_t>(tb) * TILE;
-    for (uint32_t g0 = 0; g0 < count; g0 += G) {
-        const uint32_t ne = min(static_cast<uint32_t>(G), count - g0);
-        const bool has = static_cast<uint32_t>(e) < ne;
-        uint32_t vi = 0, mask = 0;
-        if (has) {
-            const uint32_t ent = ents[g0 + e];
-            vi = tile_v0 + (ent & 0xFFu);
-            mask = ent >> 8;
-            const uint64_t off = vec_elem_offset(seg, vi) + 16u * static_cast<uint32_t>(t);
-            float4* dst = reinterpret_cast<float4*>(&x_s[wave][e][16 * t]);
-            if (!lc.in_bf16) {
-                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(in) + off);
-                const float4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
-                dst[0] = v0; dst[1] = v1; dst[2] = v2; dst[3] = v3;
-            } else {
-                const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(in) + off);
-                const uint4 w0 = src[0], w1 = src[1];
-                const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    dst[k] = make_float4(u2f(w[2 * k] << 16), u2f(w[2 * k] & 0xffff0000u), u2f(w[2 * k + 1] << 16),
-                                         u2f(w[2 * k + 1] & 0xffff0000u));
-            }
-            if (t == 0) mask_s[wave][e] = mask;
-        }
-        wave_sync();
-        if (has && t == 0) {   // l2_norm: sequential f64; a square of an f32 is exact, so fma == s + d * d
-            double s2 = 0.0;
-#pragma unroll 16
-            for (int c = 0; c < DIM; ++c) {
-                const double d = static_cast<double>(x_s[wave][e][c]);
-                s2 = __builtin_fma(d, d, s2);
-            }
-            nrm_s[wave][e] = __builtin_sqrt(s2);
-        }
-        wave_sync();
-        if (has && !small) {
-            const double nrm = nrm_s[wave][e];
-#pragma unroll
-            for (int c = 16 * t; c < 16 * t + 16; ++c)
-                x_s[wave][e][c] = static_cast<float>(static_cast<double>(x_s[wave][e][c]) / nrm);
-        }
-        wave_sync();
-        uint32_t total = 0;
-        for (uint32_t j = 0; j < ne; ++j) total += __popc(mask_s[wave][j]);
-        for (uint32_t p0 = 0; p0 < total; p0 += G) {
-            const uint32_t qi = p0 + static_cast<uint32_t>(e);
-            int pe = -1, pb = 0;
-            if (qi < total) {
-                uint32_t acc = 0;
-                for (uint32_t j = 0; j < ne; ++j) {
-                    uint32_t m = mask_s[wave][j];
-                    const uint32_t c = __popc(m);
-                    if (qi < acc + c) {
-                        for (uint32_t k = qi - acc; k > 0; --k) m &= m - 1u;
-                        pe = static_cast<int>(j);
-                        pb = __ffs(m) - 1;
-                        break;
-                    }
-                    acc += c;
-                }
-            }
-            if (pe >= 0) {   // Pi^T: at step c all lanes read within one 512 B row
-                const double* col = rot_t + (4 * pb + t);
-                const float* xr = x_s[wave][pe];
-                double a = 0.0;
-                if (!small) {
-#pragma unroll 16
-                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * static_cast<double>(xr[c]);
-                } else {
-                    const double nrm = nrm_s[wave][pe];
-                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * (static_cast<double>(xr[c]) / nrm);
-                }
-                rho_s[wave][e][t] = static_cast<float>(a);
-            }
-            wave_sync();
-            if (pe >= 0) {
-                const float s0 = rho_s[wave][e][0], s1 = rho_s[wave][e][1];
-                const float s2 = rho_s[wave][e][2], s3 = rho_s[wave][e][3];
-                float bd = u2f(0x7f800000u);
-                uint32_t bw = 0;
-#pragma unroll
-                for (int w = 8 * t; w < 8 * t + 8; ++w) {
-                    const float* c = cb + 4 * w;
-                    const float e0 = c[0] - s0, e1 = c[1] - s1, e2 = c[2] - s2, e3 = c[3] - s3;
-                    const float dd = (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
-                    if (dd < bd) { bd = dd; bw = static_cast<uint32_t>(w); }
-                }
-                part_s[wave][e][t][0] = bd;
-                part_s[wave][e][t][1] = u2f(bw);
-            }
-            wave_sync();
-            if (pe >= 0 && t == 0) {
-                float bd = part_s[wave][e][0][0];
-                uint32_t bw = f2u(part_s[wave][e][0][1]);
-                for (int u = 1; u < 4; ++u)
-                    if (part_s[wave][e][u][0] < bd) { bd = part_s[wave][e][u][0]; bw = f2u(part_s[wave][e][u][1]); }
-                res_s[wave][pe][pb] = static_cast<uint8_t>(bw);
-            }
-            wave_sync();
-        }
-        if (has && t == 0) {
-            uint8_t* p = wire + seg.wire_offset + 19 + static_cast<uint64_t>(vi) * 12 + 2;
-            uint32_t iw[3] = {0u, 0u, 0u};
-            for (int i = 0; i < 10; ++i) iw[i >> 2] |= static_cast<uint32_t>(p[i]) << (8 * (i & 3));
-            for (int b = 0; b < DIM / 4; ++b) {
-                if (!((mask >> b) & 1u)) continue;
-                const uint32_t w = res_s[wave][e][b];
-                const int bit = 5 * b, wd = bit >> 5, sh = bit & 31;
-                iw[wd] = (iw[wd] & ~(31u << sh)) | (w << sh);
-                if (sh > 27) iw[wd + 1] = (iw[wd + 1] & ~(31u >> (32 - sh))) | (w >> (32 - sh));
-            }
-            for (int i = 0; i < 10; ++i) p[i] = static_cast<uint8_t>(iw[i >> 2] >> (8 * (i & 3)));
-        }
-        wave_sync();
+    __syncthreads();   // the queue is complete and every payload is in LDS
+    {
+        __shared__ FibFixupLds fx;
+        uint32_t* pay0 = smem_u + MF_SCA;
+        auto pay_of = [pay0](uint32_t li) {   // local vector -> its payload words
+            return pay0 + (li >> 6) * FIB_PAY_WORDS + 3u * (li & 63u);
+        };
+        fib_fixup_wave<DIM>(lc, in, rot_t, cb, seg, tile_v0, q_entries, q_count, fx, pay_of, wave, lane);
     }
+    __syncthreads();   // patched payloads
+    if (v0 < seg.n_vectors)
+        lds_to_global(blob + 19 + static_cast<uint64_t>(v0) * 12u, pay, min(64u, seg.n_vectors - v0) * 12u, lane);
 }
 
 // ------------------------------------------------------------ fib decode
@@ -2893,14 +2898,11 @@ int launch_turbo_score(const LaunchCommon& lc, const TurboDev& td, const uint8_t
 }
 
 int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire, uint32_t nblocks,
-                      const FibRedo& rq, void* stream) {
+                      void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     constexpr size_t lds = (MF_SCA + WAVES * FIB_PAY_WORDS) * sizeof(uint32_t);
-    hipError_t e = launch_big_lds(fib_encode_kernel<64>, nblocks, lds, st, lc, in, wire, fd.mf, fd.thr, rq);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(fib_fixup_kernel<64>, dim3((nblocks + WAVES - 1) / WAVES), dim3(TILE), 0, st, lc, in, wire,
-                       fd.rot_t, fd.codebook, rq, nblocks);
-    return hipGetLastError();
+    return launch_big_lds(fib_encode_kernel<64>, nblocks, lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot_t,
+                          fd.codebook);
 }
 
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, void* out, uint32_t nblocks,
