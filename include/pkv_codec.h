@@ -202,10 +202,12 @@ int pkv_decode_segments_ex(pkv_ctx* ctx, const pkv_profile* prof, int radii_code
                            void* stream);
 
 /* pkv_decode_segments_ex on a bounded share of the GPU: the head_dim-64
- * turbo decode runs on at most max_workgroups workgroups (0: no bound), each
- * looping over the blob tiles, so a kernel queued on another stream (the
- * other tier's encode) gets the remaining compute units instead of waiting
- * behind a full grid.  Other profiles decode as pkv_decode_segments_ex.  No
+ * turbo decode and the fib matrix-core decode run on at most max_workgroups
+ * workgroups (0: no bound), each looping over the blob tiles, so a kernel
+ * queued on another stream (the other tier's encode) gets the remaining
+ * compute units instead of waiting behind a full grid.  Other profiles (and
+ * the fib VALU decode, used only when a profile's matrix-core products fail
+ * their check) decode as pkv_decode_segments_ex.  No
  * counterpart in the reference (its tiers run one after the other); for
  * callers that overlap the pool and shell tiers of one rehydrate. */
 int pkv_decode_segments_bounded(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec,

@@ -97,7 +97,8 @@ struct LaunchCommon {
     uint32_t out_dtype;           // decode output: PKV_F32, PKV_BF16 or PKV_F16 (RNE from the f32 decode)
     uint32_t fanout;              // decode: copies of every output vector (>= 1) ...
     uint64_t fanout_stride;       // ... this many elements apart
-    uint32_t grid_cap = 0;        // d64 turbo decode: at most this many workgroups (0: one per half-tile)
+    uint32_t grid_cap = 0;        // at most this many workgroups, each walking tiles (0: one per tile);
+                                  // d64 turbo decode and the fib MFMA decode
 };
 
 // Up to 48 constant header bytes (TQW1 / FB1 record headers, TQB1 / FB2 blob

@@ -2593,9 +2593,17 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
     }
     __syncthreads();
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    // one tile per workgroup, or (grid capped) a workgroup walks the tiles
+    // blockIdx.x, blockIdx.x + gridDim.x, ... with the tables loaded once
+    const uint32_t nblk = lc.tile_start[lc.nseg];
+    for (uint32_t blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
+    wave_sync();   // the previous tile's LDS reads are done
+    // opaque per tile: the loop must not keep lane-derived addresses or table
+    // reads live across tiles (register pressure)
+    int zoff = 0, lane = threadIdx.x & 63;
+    asm volatile("" : "+s"(zoff), "+v"(lane));
     const int h = lane >> 5, n = lane & 31;
-    const uint32_t blk = blockIdx.x;
     const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
     const SegDev seg = lc.segs[sidx];
     const uint32_t tile = blk - lc.tile_start[sidx];
@@ -2608,9 +2616,9 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
     if (lane == 14 && hb != 0u) bad = true;   // norm format must be Fp16Paper
     if (__ballot(bad) != 0ull) {
         if (lane == 0) status_fail(lc.status, sidx, 0, 0u, KIND_HEADER);
-        return;
+        continue;
     }
-    if (v0 >= seg.n_vectors) return;
+    if (v0 >= seg.n_vectors) continue;
     const uint32_t nv = min(static_cast<uint32_t>(WAVE), seg.n_vectors - v0);
     uint32_t* sw = pay_s[wave];
     global_to_lds(sw, blob + 19 + static_cast<uint64_t>(v0) * PLEN, nv * PLEN, lane);
@@ -2640,7 +2648,7 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
             const float cr[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(rot_s[(4 * b + t) * DIM + lane], cr[t], zero, 0, 0, 0);
+                const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(rot_s[(4 * b + t) * DIM + lane + zoff], cr[t], zero, 0, 0, 0);
 #pragma unroll
                 for (int q = 0; q < 32; ++q) acc[q] = acc[q] + p[q];
             }
@@ -2709,6 +2717,7 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
             }
             wave_sync();   // the next pass overwrites the staging rows
         }
+    }
     }
 }
 
@@ -2907,11 +2916,12 @@ int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, 
 
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, void* out, uint32_t nblocks,
                       void* stream) {
+    const uint32_t grid = lc.grid_cap ? std::min(nblocks, lc.grid_cap) : nblocks;
     if (fd.mfma_decode && lc.fanout > 1)
-        hipLaunchKernelGGL((fib_decode_mfma_kernel<64, true>), dim3(nblocks), dim3(TILE), 0,
+        hipLaunchKernelGGL((fib_decode_mfma_kernel<64, true>), dim3(grid), dim3(TILE), 0,
                            static_cast<hipStream_t>(stream), lc, wire, out, fd.rot32, fd.codebook);
     else if (fd.mfma_decode)
-        hipLaunchKernelGGL((fib_decode_mfma_kernel<64, false>), dim3(nblocks), dim3(TILE), 0,
+        hipLaunchKernelGGL((fib_decode_mfma_kernel<64, false>), dim3(grid), dim3(TILE), 0,
                            static_cast<hipStream_t>(stream), lc, wire, out, fd.rot32, fd.codebook);
     else
         hipLaunchKernelGGL(fib_decode_kernel<64>, dim3(nblocks), dim3(TILE), 0, static_cast<hipStream_t>(stream), lc,

@@ -191,6 +191,47 @@ def test_bounded_turbo_decode_matches_full_grid(ctx, max_workgroups):
     assert err is not None and err.segment == 5 and err.index == 123
 
 
+@pytest.mark.parametrize("max_workgroups,copies", [(1, 2), (3, 1), (7, 2), (5, 8)])
+def test_bounded_fib_decode_matches_full_grid(ctx, max_workgroups, copies):
+    """The fib matrix-core decode on a bounded grid (workgroups looping over
+    the tiles of every segment, staged fan-out stores or direct ones) writes
+    the same cache as one workgroup per tile, and reports a corrupt norm the
+    same way."""
+    import torch
+    from provekv_amd.pool import DeviceKVCache
+    layers, heads, dim, prefix, agents = 2, 8, 64, 300, [5]
+    corpus = synth.corpus_tokens(12, layers, heads, prefix + sum(agents), dim)
+    plan = TwoTierPlan(ctx, layers, heads, dim, prefix, agents, seed=SEED)
+    bufs = plan.alloc()
+    plan.encode(torch.from_numpy(corpus.reshape(-1)).cuda(), bufs)
+    plen = plan.fib.payload_len()
+    # an infinite f16 norm for vector 1000 of blob 2 (FB2 header: 19 bytes)
+    _, _, _, off, _ = plan.pool.blob_offsets[2]
+    pos = off + 19 + 1000 * plen
+    bufs["pool_wire"][pos:pos + 2] = torch.tensor([0x00, 0x7C], dtype=torch.uint8, device="cuda")
+    outs, stats = [], []
+    for bound in (0, max_workgroups):
+        cache = DeviceKVCache(layers, heads, prefix + sum(agents), dim, copies=copies)
+        cache.buf.fill_(3.0)
+        plan._cache_tables(bufs, cache)
+        pseg, _ = plan._cache_segs
+        st = torch.zeros(2 * len(pseg), dtype=torch.int32, device="cuda")
+        plan.fib.decode_segments(bufs["pool_wire"], pseg, cache.buf.view(-1), status=st, fanout=copies,
+                                 fanout_stride=cache.copy_stride, max_workgroups=bound)
+        torch.cuda.synchronize()
+        outs.append(cache.buf.cpu())
+        stats.append(st.cpu().numpy().view(np.uint32).copy())
+    assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32))
+    assert np.array_equal(stats[0], stats[1])
+    err = plan.fib.status_error(stats[1], pseg)
+    assert err is not None and err.segment == 2 and err.index == 1000
+    # every other vector is the oracle's decode
+    cb, rot = plan.fib.constants()
+    want = O.fib_decode_batch(plan.blob(bufs, "pool", 0), cb.reshape(32, 4), rot.reshape(64, 64)).reshape(prefix, heads, dim)
+    got = outs[1][0, 0, 0, :, :prefix, :].permute(1, 0, 2).numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def test_cache_target_append(ctx):
     """CacheTarget (proveKV/src/pool.rs:646-658): append one token's [H * D]
     key / value at a position in every copy."""
