@@ -571,11 +571,16 @@ __device__ __forceinline__ void fwht_split(float (&v)[32], int h) {
             }
         }
     }
-    // step 32: element c (half 0) with c + 32 (half 1): (a + b, a - b)
+    // step 32: element c (half 0) with c + 32 (half 1): (a + b, a - b).  One
+    // v_permlane32_swap of two copies of v[c] leaves a in the first and b in
+    // the second in every lane; each half then takes fma(b, +-1, a), whose
+    // product is exact, so its single rounding is that of a + b or a - b
+    // (signed zeros included).
+    const float sgn = h ? -1.0f : 1.0f;
 #pragma unroll
     for (int c = 0; c < 32; ++c) {
-        const float o = u2f(partner(f2u(v[c]), h));
-        v[c] = h ? o - v[c] : v[c] + o;
+        const auto p = __builtin_amdgcn_permlane32_swap(f2u(v[c]), f2u(v[c]), false, false);
+        v[c] = __builtin_fmaf(u2f(p[1]), sgn, u2f(p[0]));
     }
 }
 
@@ -614,15 +619,23 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
     const uint32_t rwords = f32r ? 32u : 32u / 4 + 2;          // radii words in the payload
     const uint32_t bwords = (32u * pbits + 31) / 32;            // angle index words
 
-    // signs of this lane's half, read where they are used
-    auto load_signs = [&](float (&sg)[32]) {
+    // signs of this lane's half as a bit mask (bit c: element 32h + c is
+    // negated).  The signs are +-1.0, and multiplying by +-1.0 is exact, so
+    // flipping the sign bit is the same product bit for bit, NaN and
+    // subnormals included.
+    uint32_t smask = 0;
+    {
         const float4* sp = reinterpret_cast<const float4*>(signs + 32 * h);
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const float4 v = sp[k];
-            sg[4 * k] = v.x; sg[4 * k + 1] = v.y; sg[4 * k + 2] = v.z; sg[4 * k + 3] = v.w;
+            smask |= (f2u(v.x) >> 31) << (4 * k) | (f2u(v.y) >> 31) << (4 * k + 1) |
+                     (f2u(v.z) >> 31) << (4 * k + 2) | (f2u(v.w) >> 31) << (4 * k + 3);
         }
-    };
+    }
+    // (m is smask; each use passes its own opaque copy so the 32 shifted
+    // masks are not kept live between the two uses)
+    auto flip = [](float v, uint32_t m, int c) { return u2f(f2u(v) ^ ((m << (31 - c)) & 0x80000000u)); };
 
     do {
         const uint32_t t0 = tile * TILE + (blockIdx.x & 1u) * (TILE / 2) + 32u * static_cast<uint32_t>(wave);
@@ -659,12 +672,12 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
         load_half(y);
         bool finite = true;
         {
-            float sg[32];
-            load_signs(sg);
+            uint32_t m = smask;
+            asm volatile("" : "+v"(m));
 #pragma unroll
             for (int c = 0; c < 32; ++c) {
                 finite &= isfinite_f(y[c]);
-                y[c] = y[c] * sg[c];
+                y[c] = flip(y[c], m, c);
             }
         }
         fwht_split(y, h);
@@ -768,11 +781,12 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
         // residual against x read again (turbo.rs:269-273)
         asm volatile("" ::: "memory");
         {
-            float x[32], sg[32];
+            float x[32];
             load_half(x);
-            load_signs(sg);
+            uint32_t m = smask;
+            asm volatile("" : "+v"(m));
 #pragma unroll
-            for (int c = 0; c < 32; ++c) y[c] = x[c] - (y[c] * scale) * sg[c];
+            for (int c = 0; c < 32; ++c) y[c] = x[c] - flip(y[c] * scale, m, c);
         }
         bool resfinite = true;
         float rn2 = 0.0f;
@@ -904,17 +918,20 @@ __device__ __forceinline__ void fwht_quarter(float (&v)[32], int q) {
             }
         }
     }
-    // step 32: element c of quarter 2k with c of quarter 2k + 1: (a + b, a - b)
+    // step 32: element c of quarter 2k with c of quarter 2k + 1: (a + b, a - b);
+    // step 64: quarters 0, 1 with 2, 3.  As in fwht_split, one swap of two
+    // copies of v[c] leaves a and b in every lane, and fma(b, +-1, a) rounds
+    // exactly like a + b or a - b.
+    const float s32 = (q & 1) ? -1.0f : 1.0f, s64 = (q & 2) ? -1.0f : 1.0f;
 #pragma unroll
     for (int c = 0; c < 32; ++c) {
-        const float o = u2f(partner16(f2u(v[c]), q));
-        v[c] = (q & 1) ? o - v[c] : v[c] + o;
+        const auto p = __builtin_amdgcn_permlane16_swap(f2u(v[c]), f2u(v[c]), false, false);
+        v[c] = __builtin_fmaf(u2f(p[1]), s32, u2f(p[0]));
     }
-    // step 64: quarters 0, 1 with 2, 3
 #pragma unroll
     for (int c = 0; c < 32; ++c) {
-        const float o = u2f(partner(f2u(v[c]), q >> 1));
-        v[c] = (q & 2) ? o - v[c] : v[c] + o;
+        const auto p = __builtin_amdgcn_permlane32_swap(f2u(v[c]), f2u(v[c]), false, false);
+        v[c] = __builtin_fmaf(u2f(p[1]), s64, u2f(p[0]));
     }
 }
 
