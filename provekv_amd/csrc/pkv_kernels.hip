@@ -706,12 +706,16 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
             slow |= (safe ^ 1u) << i;
         }
         if (slow) {   // pairs near an octant line (every pair at other widths): the exact formula
-            float ys[32];
-#pragma unroll
-            for (int c = 0; c < 32; ++c) ys[c] = y[c];
             for (uint32_t m = slow; m; m &= m - 1u) {
                 const uint32_t i = static_cast<uint32_t>(__ffs(m) - 1);
-                const uint64_t bin = angle_bin_exact(ys[2 * i], ys[2 * i + 1], pbits);
+                // pair i by selects (a dynamic index into y would go through scratch)
+                float a = y[0], b = y[1];
+#pragma unroll
+                for (int j = 1; j < HP; ++j) {
+                    a = static_cast<uint32_t>(j) == i ? y[2 * j] : a;
+                    b = static_cast<uint32_t>(j) == i ? y[2 * j + 1] : b;
+                }
+                const uint64_t bin = angle_bin_exact(a, b, pbits);
                 pk = (pk & ~(static_cast<uint64_t>(levels - 1u) << (i * pbits))) | (bin << (i * pbits));
             }
         }
@@ -863,13 +867,19 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
         }
         wave_sync();
         if (!f32r) {   // close the gaps left by the f32 radii words
-            uint32_t tmp[(32 / 4 + 2) + 8 + 2];
+            // each half moves at most TMAX words: fixed trip count, predicated,
+            // so tmp stays in registers
+            constexpr uint32_t TMAX = (32 / 4 + 2) + 8 + 2;
+            uint32_t tmp[TMAX];
             const uint32_t k0 = static_cast<uint32_t>(h) * (pwd / 2 + 1);
             const uint32_t k1 = h ? pwd : pwd / 2 + 1;
-            for (uint32_t k = k0; k < k1; ++k) tmp[k - k0] = active ? pv[k] : 0u;
+#pragma unroll
+            for (uint32_t j = 0; j < TMAX; ++j) tmp[j] = (active && k0 + j < k1) ? pv[k0 + j] : 0u;
             wave_sync();
             if (active)
-                for (uint32_t k = k0; k < k1; ++k) pay[n * pwd + k] = tmp[k - k0];
+#pragma unroll
+                for (uint32_t j = 0; j < TMAX; ++j)
+                    if (k0 + j < k1) pay[n * pwd + k0 + j] = tmp[j];
             wave_sync();
         }
         lds_to_global(blob + 38 + static_cast<uint64_t>(t0) * plen, pay, nv * plen, lane);
@@ -1052,12 +1062,16 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
             slow |= (safe ^ 1u) << i;
         }
         if (slow) {   // pairs near an octant line (every pair at other widths): the exact formula
-            float ys[32];
-#pragma unroll
-            for (int c = 0; c < 32; ++c) ys[c] = y[c];
             for (uint32_t m = slow; m; m &= m - 1u) {
                 const uint32_t i = static_cast<uint32_t>(__ffs(m) - 1);
-                const uint64_t bin = angle_bin_exact(ys[2 * i], ys[2 * i + 1], pbits);
+                // pair i by selects (a dynamic index into y would go through scratch)
+                float a = y[0], b = y[1];
+#pragma unroll
+                for (int j = 1; j < HP; ++j) {
+                    a = static_cast<uint32_t>(j) == i ? y[2 * j] : a;
+                    b = static_cast<uint32_t>(j) == i ? y[2 * j + 1] : b;
+                }
+                const uint64_t bin = angle_bin_exact(a, b, pbits);
                 pk = (pk & ~(static_cast<uint64_t>(levels - 1u) << (i * pbits))) | (bin << (i * pbits));
             }
         }
