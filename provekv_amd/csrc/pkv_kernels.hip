@@ -2170,7 +2170,7 @@ template <int DIM>
 __device__ __forceinline__ void fib_encode_score(const LaunchCommon& lc, const SegDev& seg, uint32_t sidx,
                                                  uint8_t* __restrict__ blob, uint32_t v0, const FibTileRot& t,
                                                  uint32_t* pay, const v4u& sa, float thr, uint32_t* q_count,
-                                                 uint32_t* q_entries, uint32_t tile_v0, int lane) {
+                                                 uint32_t* q_entries, double* q_nrm, uint32_t tile_v0, int lane) {
     constexpr uint32_t PLEN = 12;   // f16 norm + 16 x 5 bits
     const int h = lane >> 5, n = lane & 31;
     const uint32_t nv = min(32u, seg.n_vectors - v0);
@@ -2243,6 +2243,7 @@ __device__ __forceinline__ void fib_encode_score(const LaunchCommon& lc, const S
         if (queue) {
             const uint32_t slot = base + static_cast<uint32_t>(__popcll(qmask & ((1ull << lane) - 1ull)));
             q_entries[slot] = (vi - tile_v0) | (small ? 0xFFFFu : redo) << 8;
+            q_nrm[slot] = nrm;
         }
     }
     // payload [f16 norm][16 x 5-bit indices] = 12 bytes, kept in LDS: the
@@ -2258,15 +2259,19 @@ __device__ __forceinline__ void fib_encode_score(const LaunchCommon& lc, const S
 }
 
 // Exact redo of the queued (vector, block) decisions of fib_encode_kernel,
-// run by the encoding workgroup itself once every wave has queued: wave w
-// takes the queue's groups of 16 entries w, w + 4, ...  4 lanes per vector
-// load it, one lane takes the sequential f64 norm and the 4 lanes form
+// run by the encoding workgroup itself once every wave has queued.  The
+// queue is cut into groups of up to 16 entries, a short queue spread over
+// all four waves (wave w takes groups w, w + 4, ...).  4 lanes per vector
+// load it; its sequential f64 norm comes from the queue (fib_encode_rotate
+// computed it in the reference's order) and the 4 lanes form
 // x_hat = f32(x / norm) (segments of fewer than 4 vectors keep x / norm in
 // f64, codec.rs:481 vs 608); then 16 undecided blocks at a time get one lane
-// per rho row (sequential f64 dot, rotation.rs:107-113) and a quarter of the
-// codewords per lane in the AVX2 distance order with strict <
-// (simd_nearest.rs:44-104); the entry's owner lane patches the 5-bit fields
-// of the payload in LDS (pay_of(local vector) -> its 3 payload words).
+// per rho row -- the sequential f64 dot of row 4b + t of Pi with x_hat
+// (rotation.rs:107-113), Pi row-major so each lane reads its row as 16-byte
+// loads -- and a quarter of the codewords per lane in the AVX2 distance
+// order with strict < (simd_nearest.rs:44-104); the entry's owner lane
+// patches the 5-bit fields of the payload in LDS (pay_of(local vector) ->
+// its 3 payload words).
 struct FibFixupLds {
     float x[WAVES][16][64 + 4];   // x, then x_hat (segments of >= 4 vectors); padded rows
     double nrm[WAVES][16];
@@ -2277,16 +2282,17 @@ struct FibFixupLds {
 };
 
 template <int DIM, typename PayOf>
-__device__ void fib_fixup_wave(const LaunchCommon& lc, const void* __restrict__ in, const double* __restrict__ rot_t,
+__device__ void fib_fixup_wave(const LaunchCommon& lc, const void* __restrict__ in, const double* __restrict__ rot,
                                const float* __restrict__ cb, const SegDev& seg, uint32_t tile_v0,
-                               const uint32_t* ents, uint32_t count, FibFixupLds& f, PayOf pay_of, int wave,
-                               int lane) {
+                               const uint32_t* ents, const double* ent_nrm, uint32_t count, FibFixupLds& f,
+                               PayOf pay_of, int wave, int lane) {
     static_assert(DIM == 64, "four lanes of 16 elements per vector");
     constexpr int G = 16;
     const int e = lane >> 2, t = lane & 3;
     const bool small = seg.n_vectors < 4 || lc.per_vector != 0;
-    for (uint32_t g0 = G * static_cast<uint32_t>(wave); g0 < count; g0 += G * WAVES) {
-        const uint32_t ne = min(static_cast<uint32_t>(G), count - g0);
+    const uint32_t gsz = min(static_cast<uint32_t>(G), max(1u, (count + WAVES - 1) / WAVES));
+    for (uint32_t g0 = gsz * static_cast<uint32_t>(wave); g0 < count; g0 += gsz * WAVES) {
+        const uint32_t ne = min(gsz, count - g0);
         const bool has = static_cast<uint32_t>(e) < ne;
         uint32_t li = 0, mask = 0;
         if (has) {
@@ -2308,17 +2314,10 @@ __device__ void fib_fixup_wave(const LaunchCommon& lc, const void* __restrict__ 
                     dst[k] = make_float4(u2f(w[2 * k] << 16), u2f(w[2 * k] & 0xffff0000u), u2f(w[2 * k + 1] << 16),
                                          u2f(w[2 * k + 1] & 0xffff0000u));
             }
-            if (t == 0) f.mask[wave][e] = mask;
-        }
-        wave_sync();
-        if (has && t == 0) {   // l2_norm: sequential f64; a square of an f32 is exact, so fma == s + d * d
-            double s2 = 0.0;
-#pragma unroll 16
-            for (int c = 0; c < DIM; ++c) {
-                const double d = static_cast<double>(f.x[wave][e][c]);
-                s2 = __builtin_fma(d, d, s2);
+            if (t == 0) {
+                f.mask[wave][e] = mask;
+                f.nrm[wave][e] = ent_nrm[g0 + e];
             }
-            f.nrm[wave][e] = __builtin_sqrt(s2);
         }
         wave_sync();
         if (has && !small) {
@@ -2347,16 +2346,30 @@ __device__ void fib_fixup_wave(const LaunchCommon& lc, const void* __restrict__ 
                     acc += c;
                 }
             }
-            if (pe >= 0) {   // Pi^T: at step c all lanes read within one 512 B row
-                const double* col = rot_t + (4 * pb + t);
+            if (pe >= 0) {   // row 4 pb + t of Pi, two batches of 16 loads in flight
+                const double2* row = reinterpret_cast<const double2*>(rot + static_cast<uint32_t>(4 * pb + t) * DIM);
                 const float* xr = f.x[wave][pe];
+                const double nrm = f.nrm[wave][pe];
                 double a = 0.0;
-                if (!small) {
-#pragma unroll 16
-                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * static_cast<double>(xr[c]);
-                } else {
-                    const double nrm = f.nrm[wave][pe];
-                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * (static_cast<double>(xr[c]) / nrm);
+#pragma unroll 1
+                for (int hh = 0; hh < 2; ++hh) {
+                    double2 r[16];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) r[k] = row[16 * hh + k];
+                    const float* xh = xr + 32 * hh;
+                    if (!small) {
+#pragma unroll
+                        for (int k = 0; k < 16; ++k) {
+                            a = a + r[k].x * static_cast<double>(xh[2 * k]);
+                            a = a + r[k].y * static_cast<double>(xh[2 * k + 1]);
+                        }
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < 16; ++k) {
+                            a = a + r[k].x * (static_cast<double>(xh[2 * k]) / nrm);
+                            a = a + r[k].y * (static_cast<double>(xh[2 * k + 1]) / nrm);
+                        }
+                    }
                 }
                 f.rho[wave][e][t] = static_cast<float>(a);
             }
@@ -2367,11 +2380,11 @@ __device__ void fib_fixup_wave(const LaunchCommon& lc, const void* __restrict__ 
                 float bd = u2f(0x7f800000u);
                 uint32_t bw = 0;
 #pragma unroll
-                for (int w = 8 * t; w < 8 * t + 8; ++w) {
-                    const float* c = cb + 4 * w;
-                    const float e0 = c[0] - s0, e1 = c[1] - s1, e2 = c[2] - s2, e3 = c[3] - s3;
+                for (int w = 0; w < 8; ++w) {
+                    const float4 cw = reinterpret_cast<const float4*>(cb)[8 * t + w];
+                    const float e0 = cw.x - s0, e1 = cw.y - s1, e2 = cw.z - s2, e3 = cw.w - s3;
                     const float dd = (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
-                    if (dd < bd) { bd = dd; bw = static_cast<uint32_t>(w); }
+                    if (dd < bd) { bd = dd; bw = static_cast<uint32_t>(8 * t + w); }
                 }
                 f.part[wave][e][t][0] = bd;
                 f.part[wave][e][t][1] = u2f(bw);
@@ -2405,7 +2418,7 @@ constexpr int FIB_PAY_WORDS = 64 * 3 + 4;   // per wave: both 32-vector sub-tile
 template <int DIM>
 __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const void* __restrict__ in,
                                                           uint8_t* __restrict__ wire, const uint32_t* __restrict__ mf,
-                                                          float thr, const double* __restrict__ rot_t,
+                                                          float thr, const double* __restrict__ rot,
                                                           const float* __restrict__ cb) {
     static_assert(DIM == 64, "the MFMA layout is built for head_dim 64");
     extern __shared__ uint32_t smem_u[];
@@ -2440,6 +2453,7 @@ __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const
     const v4u sa = {sa4.x, sa4.y, sa4.z, sa4.w};
     __shared__ uint32_t q_count;
     __shared__ uint32_t q_entries[TILE];   // (local vector) | (blocks to redo) << 8
+    __shared__ double q_nrm[TILE];         // each entry's sequential f64 norm
     if (threadIdx.x == 0) q_count = 0;
     const uint32_t tile_v0 = tile * TILE;
     __syncthreads();
@@ -2451,13 +2465,14 @@ __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const
         fib_encode_rotate(t, xa, rot_lds, lane);
         __builtin_amdgcn_sched_barrier(0);
         if (v0 + 32 < seg.n_vectors) load_half_row(xb, in, bf16, seg, min(v0 + 32 + n, last), h);
-        fib_encode_score<DIM>(lc, seg, sidx, blob, v0, t, pay, sa, thr, &q_count, q_entries, tile_v0, lane);
+        fib_encode_score<DIM>(lc, seg, sidx, blob, v0, t, pay, sa, thr, &q_count, q_entries, q_nrm, tile_v0,
+                              lane);
     }
     if (v0 + 32 < seg.n_vectors) {
         FibTileRot t;
         fib_encode_rotate(t, xb, rot_lds, lane);
-        fib_encode_score<DIM>(lc, seg, sidx, blob, v0 + 32, t, pay + 96, sa, thr, &q_count, q_entries, tile_v0,
-                              lane);
+        fib_encode_score<DIM>(lc, seg, sidx, blob, v0 + 32, t, pay + 96, sa, thr, &q_count, q_entries, q_nrm,
+                              tile_v0, lane);
     }
     if (tile == 0 && threadIdx.x < 19)
         blob[threadIdx.x] = static_cast<uint8_t>(fb2_byte(threadIdx.x, 5u, DIM / 4, seg.n_vectors, 10u));
@@ -2468,7 +2483,7 @@ __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const
         auto pay_of = [pay0](uint32_t li) {   // local vector -> its payload words
             return pay0 + (li >> 6) * FIB_PAY_WORDS + 3u * (li & 63u);
         };
-        fib_fixup_wave<DIM>(lc, in, rot_t, cb, seg, tile_v0, q_entries, q_count, fx, pay_of, wave, lane);
+        fib_fixup_wave<DIM>(lc, in, rot, cb, seg, tile_v0, q_entries, q_nrm, q_count, fx, pay_of, wave, lane);
     }
     __syncthreads();   // patched payloads
     if (v0 < seg.n_vectors)
@@ -2941,7 +2956,7 @@ int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, 
                       void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     constexpr size_t lds = (MF_SCA + WAVES * FIB_PAY_WORDS) * sizeof(uint32_t);
-    return launch_big_lds(fib_encode_kernel<64>, nblocks, lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot_t,
+    return launch_big_lds(fib_encode_kernel<64>, nblocks, lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot64,
                           fd.codebook);
 }
 
