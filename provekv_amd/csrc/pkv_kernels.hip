@@ -2267,11 +2267,11 @@ __device__ __forceinline__ void fib_encode_score(const LaunchCommon& lc, const S
 // x_hat = f32(x / norm) (segments of fewer than 4 vectors keep x / norm in
 // f64, codec.rs:481 vs 608); then 16 undecided blocks at a time get one lane
 // per rho row -- the sequential f64 dot of row 4b + t of Pi with x_hat
-// (rotation.rs:107-113), Pi row-major so each lane reads its row as 16-byte
-// loads -- and a quarter of the codewords per lane in the AVX2 distance
-// order with strict < (simd_nearest.rs:44-104); the entry's owner lane
-// patches the 5-bit fields of the payload in LDS (pay_of(local vector) ->
-// its 3 payload words).
+// (rotation.rs:107-113), read from Pi^T so that each step's loads of the
+// wave share one 512-byte row -- and a quarter of the codewords per lane in
+// the AVX2 distance order with strict < (simd_nearest.rs:44-104); the
+// entry's owner lane patches the 5-bit fields of the payload in LDS
+// (pay_of(local vector) -> its 3 payload words).
 struct FibFixupLds {
     float x[WAVES][16][64 + 4];   // x, then x_hat (segments of >= 4 vectors); padded rows
     double nrm[WAVES][16];
@@ -2282,7 +2282,7 @@ struct FibFixupLds {
 };
 
 template <int DIM, typename PayOf>
-__device__ void fib_fixup_wave(const LaunchCommon& lc, const void* __restrict__ in, const double* __restrict__ rot,
+__device__ void fib_fixup_wave(const LaunchCommon& lc, const void* __restrict__ in, const double* __restrict__ rot_t,
                                const float* __restrict__ cb, const SegDev& seg, uint32_t tile_v0,
                                const uint32_t* ents, const double* ent_nrm, uint32_t count, FibFixupLds& f,
                                PayOf pay_of, int wave, int lane) {
@@ -2346,30 +2346,16 @@ __device__ void fib_fixup_wave(const LaunchCommon& lc, const void* __restrict__ 
                     acc += c;
                 }
             }
-            if (pe >= 0) {   // row 4 pb + t of Pi, two batches of 16 loads in flight
-                const double2* row = reinterpret_cast<const double2*>(rot + static_cast<uint32_t>(4 * pb + t) * DIM);
+            if (pe >= 0) {   // Pi^T: at step c all lanes read within one 512 B row
+                const double* col = rot_t + (4 * pb + t);
                 const float* xr = f.x[wave][pe];
-                const double nrm = f.nrm[wave][pe];
                 double a = 0.0;
-#pragma unroll 1
-                for (int hh = 0; hh < 2; ++hh) {
-                    double2 r[16];
-#pragma unroll
-                    for (int k = 0; k < 16; ++k) r[k] = row[16 * hh + k];
-                    const float* xh = xr + 32 * hh;
-                    if (!small) {
-#pragma unroll
-                        for (int k = 0; k < 16; ++k) {
-                            a = a + r[k].x * static_cast<double>(xh[2 * k]);
-                            a = a + r[k].y * static_cast<double>(xh[2 * k + 1]);
-                        }
-                    } else {
-#pragma unroll
-                        for (int k = 0; k < 16; ++k) {
-                            a = a + r[k].x * (static_cast<double>(xh[2 * k]) / nrm);
-                            a = a + r[k].y * (static_cast<double>(xh[2 * k + 1]) / nrm);
-                        }
-                    }
+                if (!small) {
+#pragma unroll 16
+                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * static_cast<double>(xr[c]);
+                } else {
+                    const double nrm = f.nrm[wave][pe];
+                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * (static_cast<double>(xr[c]) / nrm);
                 }
                 f.rho[wave][e][t] = static_cast<float>(a);
             }
@@ -2418,7 +2404,7 @@ constexpr int FIB_PAY_WORDS = 64 * 3 + 4;   // per wave: both 32-vector sub-tile
 template <int DIM>
 __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const void* __restrict__ in,
                                                           uint8_t* __restrict__ wire, const uint32_t* __restrict__ mf,
-                                                          float thr, const double* __restrict__ rot,
+                                                          float thr, const double* __restrict__ rot_t,
                                                           const float* __restrict__ cb) {
     static_assert(DIM == 64, "the MFMA layout is built for head_dim 64");
     extern __shared__ uint32_t smem_u[];
@@ -2483,7 +2469,7 @@ __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const
         auto pay_of = [pay0](uint32_t li) {   // local vector -> its payload words
             return pay0 + (li >> 6) * FIB_PAY_WORDS + 3u * (li & 63u);
         };
-        fib_fixup_wave<DIM>(lc, in, rot, cb, seg, tile_v0, q_entries, q_nrm, q_count, fx, pay_of, wave, lane);
+        fib_fixup_wave<DIM>(lc, in, rot_t, cb, seg, tile_v0, q_entries, q_nrm, q_count, fx, pay_of, wave, lane);
     }
     __syncthreads();   // patched payloads
     if (v0 < seg.n_vectors)
@@ -2956,7 +2942,7 @@ int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, 
                       void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     constexpr size_t lds = (MF_SCA + WAVES * FIB_PAY_WORDS) * sizeof(uint32_t);
-    return launch_big_lds(fib_encode_kernel<64>, nblocks, lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot64,
+    return launch_big_lds(fib_encode_kernel<64>, nblocks, lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot_t,
                           fd.codebook);
 }
 
