@@ -2274,6 +2274,7 @@ __device__ __forceinline__ void fib_encode_score(const LaunchCommon& lc, const S
 // (pay_of(local vector) -> its 3 payload words).
 struct FibFixupLds {
     float x[WAVES][16][64 + 4];   // x, then x_hat (segments of >= 4 vectors); padded rows
+    double xh[WAVES][64];         // f64 x / norm of one entry (segments of < 4 vectors)
     double nrm[WAVES][16];
     float part[WAVES][16][4][2];
     float rho[WAVES][16][4];
@@ -2330,9 +2331,19 @@ __device__ void fib_fixup_wave(const LaunchCommon& lc, const void* __restrict__ 
         uint32_t total = 0;
         for (uint32_t j = 0; j < ne; ++j) total += __popc(f.mask[wave][j]);
         for (uint32_t p0 = 0; p0 < total; p0 += G) {
+            if (small) {   // every entry queues all 16 blocks, so this pass is entry p0 / 16: its f64 x_hat once
+                const uint32_t pe0 = p0 / G;
+                f.xh[wave][lane] = static_cast<double>(f.x[wave][pe0][lane]) / f.nrm[wave][pe0];
+                wave_sync();
+            }
             const uint32_t qi = p0 + static_cast<uint32_t>(e);
             int pe = -1, pb = 0;
-            if (qi < total) {
+            if (small) {   // entry qi / 16, block qi % 16
+                if (qi < total) {
+                    pe = static_cast<int>(qi >> 4);
+                    pb = static_cast<int>(qi & 15u);
+                }
+            } else if (qi < total) {
                 uint32_t acc = 0;
                 for (uint32_t j = 0; j < ne; ++j) {
                     uint32_t m = f.mask[wave][j];
@@ -2354,8 +2365,9 @@ __device__ void fib_fixup_wave(const LaunchCommon& lc, const void* __restrict__ 
 #pragma unroll 16
                     for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * static_cast<double>(xr[c]);
                 } else {
-                    const double nrm = f.nrm[wave][pe];
-                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * (static_cast<double>(xr[c]) / nrm);
+                    const double* xh = f.xh[wave];
+#pragma unroll 16
+                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * xh[c];
                 }
                 f.rho[wave][e][t] = static_cast<float>(a);
             }
