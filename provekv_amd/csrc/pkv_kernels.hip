@@ -2037,8 +2037,8 @@ turbo_score_lut_kernel(
 // of its undecided blocks (a few % of vectors), and once every wave has
 // queued, the workgroup redoes those blocks exactly (fib_fixup_wave): f64
 // sequential rows of the exact x_hat and the AVX2-order f32 distances.
-// Segments of fewer than 4 vectors (the reference's single-vector path with
-// an f64 x_hat) queue all 16 blocks.
+// Segments of fewer than 4 vectors and per-vector encodes (the reference's
+// single-vector path with an f64 x_hat) queue all 16 blocks.
 
 
 // f16 halves of a, b by round-toward-zero: hi = (a_hi, b_hi), lo = the
