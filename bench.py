@@ -528,7 +528,7 @@ def main():
     ap.add_argument("--serial-tiers", action="store_true",
                     help="run the pool tier and the shell tier one after the other on one stream (default: the "
                          "shell tier on a second stream, concurrent with the pool tier)")
-    ap.add_argument("--side-workgroups", type=int, default=256,
+    ap.add_argument("--side-workgroups", type=int, default=192,
                     help="workgroups of the shell-tier rehydrate while it overlaps the pool encode")
     ap.add_argument("--workload", choices=("pool", "legacy", "config4", "score"), default="pool",
                     help="pool: the config-3 metric (default); legacy: per-vector TQW1 / FB1 records; "
