@@ -169,3 +169,17 @@ def test_profile_constant_service_builds_each_profile_once():
     # the cached constants are the oracle's
     ocb, _, _ = O.fib_codebook()
     assert np.array_equal(cb1.reshape(32, 4), ocb)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 prints a JSON error line and
+    exits with status 2 before touching any device."""
+    import json
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120, cwd=root)
+    assert r.returncode == 2
+    line = json.loads(r.stdout.strip().splitlines()[-1])
+    assert line["n_gpus"] == 2 and "one GPU" in line["error"]
