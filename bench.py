@@ -324,6 +324,12 @@ def bench_config4(args):
                         "frac": round(dom_alg / (dom_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                         "algorithmic_bytes": dom_alg},
            "parity_sampled_2048": bool(parity)}
+    if args.copy_calib:   # the reference kernel for rocprofv3 --pmc byte counters
+        src = torch.empty(1 << 28, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     print(json.dumps(res), flush=True)
 
 
