@@ -153,7 +153,11 @@ typedef struct pkv_seg {
 /* Per-segment status words written by the kernels (2 per segment): word 0 =
  * first input-validation failure, word 1 = first later failure, each packed
  * as (vector_index << 4) | kind; 0xFFFFFFFF = none.  pkv_segments_status()
- * turns them into a pkv_error following the reference's precedence. */
+ * turns them into a pkv_error following the reference's precedence: segments
+ * in order; within a fib segment an input-validation failure precedes a norm
+ * failure (FibQuantizer::encode_batch, fib-quant/src/codec.rs:592-610 before
+ * 694-704: every segment is taken as a batch of >= 4 vectors, the pool and
+ * shell case); within a turbo segment the first failing vector wins. */
 int pkv_segments_status(const pkv_profile* prof, const uint32_t* host_status, uint32_t nseg,
                         pkv_error* err);
 
@@ -264,7 +268,12 @@ int pkv_decode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const ui
 
 /* Parses a TQB1 / FB2 header against the profile (host memory) and reports
  * the number of vectors and the radii codec; PKV_ERR_CORRUPT_PAYLOAD on any
- * mismatch the reference decoder rejects. */
+ * header mismatch the reference decoder rejects before reading a vector,
+ * including a buffer shorter than the header's vectors.  Bytes after the last
+ * TQB1 payload are not a header fault: the reference rejects them only after
+ * every vector (cursor.finish(), turbo-quant/src/wire.rs:566), and so do
+ * pkv_decode_batch_compact and pkv_turbo_score_batch; FB2 accepts them
+ * (fib-quant/src/codec.rs:380-386). */
 int pkv_parse_header(const pkv_profile* prof, const uint8_t* blob, uint64_t len,
                      uint64_t* n_vectors, int* radii_codec);
 

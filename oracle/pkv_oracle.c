@@ -961,8 +961,7 @@ int ora_turbo_decode_batch(uint32_t dim, uint32_t bits, uint32_t proj, uint64_t 
     if (pbits_w != pbits) return ORA_ERR_MALFORMED;
     uint32_t pairs = dim / 2;
     if (plen != turbo_payload_len(dim, pbits, proj, mode, rc_byte)) return ORA_ERR_MALFORMED;
-    if (len < 38 + n * (uint64_t)plen) return ORA_ERR_MALFORMED;
-    if (len != 38 + n * (uint64_t)plen) return ORA_ERR_MALFORMED;   /* cursor.finish() */
+    if (len < 38 + n * (uint64_t)plen) return ORA_ERR_MALFORMED;   /* wire.rs:489-498 */
     if (n_out) *n_out = n;
     if (cap_vectors < n) return ORA_ERR_CAPACITY;
     uint32_t angle_bytes = (pairs * (uint32_t)pbits + 7) / 8;
@@ -992,6 +991,9 @@ int ora_turbo_decode_batch(uint32_t dim, uint32_t bits, uint32_t proj, uint64_t 
         for (uint32_t i = 0; i < pairs; ++i)
             if (!isfinite(radii[i]) || radii[i] < 0.0f) { if (fail_index) *fail_index = v; return ORA_ERR_MALFORMED; }
     }
+    /* cursor.finish() (wire.rs:566): trailing bytes are rejected only after
+     * every vector has been read and validated */
+    if (len != 38 + n * (uint64_t)plen) return ORA_ERR_MALFORMED;
     if (!out) return ORA_OK;   /* validation only */
     for (uint64_t v = 0; v < n; ++v) {
         const uint8_t* p = in + 38 + v * plen;

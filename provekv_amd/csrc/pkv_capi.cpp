@@ -36,10 +36,10 @@ int hip_status(hipError_t e) {
 
 
 // Streams that have launched work on a buffer since it was last known idle.
-// No event is recorded per launch: when the buffer must be reused or rewritten
-// the library records an event on each of these streams at that moment (it
-// follows all their earlier work) and waits on it.  Past kMaxUsers streams
-// the device is synchronised instead.
+// No event is recorded per launch: when the buffer must be rewritten the
+// library records an event on each of these streams at that moment (it
+// follows all their earlier work) and the host waits on it.  Past kMaxUsers
+// streams the device is synchronised instead.
 constexpr int kMaxUsers = 4;
 struct Users {
     hipStream_t s[kMaxUsers] = {};
@@ -50,7 +50,6 @@ struct Users {
             if (s[i] == st) return;
         if (n < kMaxUsers) s[n++] = st; else overflow = true;
     }
-    bool only(hipStream_t st) const { return !overflow && (n == 0 || (n == 1 && s[0] == st)); }
     // host waits until every recorded user is done
     int drain_host(hipEvent_t ev) {
         if (overflow) HIP_TRY(hipDeviceSynchronize());
@@ -63,26 +62,16 @@ struct Users {
         overflow = false;
         return PKV_OK;
     }
-    // `st` waits (on the device) until every other recorded user is done
-    int drain_stream(hipEvent_t ev, hipStream_t st) {
-        if (overflow) HIP_TRY(hipDeviceSynchronize());
-        else
-            for (int i = 0; i < n; ++i)
-                if (s[i] != st) {
-                    HIP_TRY(hipEventRecord(ev, s[i]));
-                    HIP_TRY(hipStreamWaitEvent(st, ev, 0));
-                }
-        n = 0;
-        overflow = false;
-        return PKV_OK;
-    }
 };
 
 struct Slot {
     void* dev = nullptr;         // segs | tile_start | status
     void* host = nullptr;        // pinned staging (keeps the uploaded table)
     size_t cap = 0;
-    hipEvent_t ev = nullptr;
+    hipEvent_t ev = nullptr;     // drain helper
+    hipEvent_t up_ev = nullptr;  // recorded on the uploading stream right after the table copy
+    hipStream_t up_stream = nullptr;
+    bool up_done = true;         // the host has seen up_ev complete
     Users users;                 // streams that read (or wrote status into) the slot
     bool shared = false;         // table only (no status words): reusable by equal tables
     uint32_t nseg = 0;
@@ -175,9 +164,11 @@ bool seg_extent(const pkv_seg& s, uint32_t dim, uint64_t* end) {
     return true;
 }
 
+// Checks a segment table against the tensor and wire extents and writes the
+// prefix of workgroup tiles per segment into tile_start[0 .. nseg].
 int validate_segments(const pkv_profile* p, int radii, bool encode, int dtype, const void* d_f32,
                       uint64_t f32_elems, const pkv_seg* segs, uint32_t nseg, const void* d_wire,
-                      uint64_t wire_bytes, std::vector<uint32_t>& tile_start, uint32_t fanout = 1,
+                      uint64_t wire_bytes, uint32_t* tile_start, uint32_t fanout = 1,
                       uint64_t fanout_stride = 0) {
     if (!segs || nseg == 0) return PKV_ERR_INVALID_ARG;
     if (!d_f32 || !d_wire) return PKV_ERR_INVALID_ARG;
@@ -190,9 +181,8 @@ int validate_segments(const pkv_profile* p, int radii, bool encode, int dtype, c
     if (reinterpret_cast<uintptr_t>(d_f32) % 16 != 0) return PKV_ERR_INVALID_ARG;
     const uint32_t plen = p->kind == PKV_CODEC_TURBO ? turbo_plen(p, radii) : fib_plen(p);
     const uint32_t hdr = hdr_len(p);
-    tile_start.assign(nseg + 1, 0);
-    std::vector<std::pair<uint64_t, uint64_t>> blobs;
-    blobs.reserve(nseg);
+    std::vector<std::pair<uint64_t, uint64_t>> blobs;   // encode only
+    if (encode) blobs.reserve(nseg);
     uint64_t total = 0;
     for (uint32_t i = 0; i < nseg; ++i) {
         const pkv_seg& s = segs[i];
@@ -207,7 +197,7 @@ int validate_segments(const pkv_profile* p, int radii, bool encode, int dtype, c
         if (!mul_add_ok(s.n_vectors, plen, hdr, &blob_end) ||
             __builtin_add_overflow(blob_end, s.wire_offset, &blob_end) || blob_end > wire_bytes)
             return PKV_ERR_CAPACITY;
-        blobs.emplace_back(s.wire_offset, blob_end);
+        if (encode) blobs.emplace_back(s.wire_offset, blob_end);
         uint64_t tiles = (static_cast<uint64_t>(s.n_vectors) + TILE - 1) / TILE;
         if (tiles == 0) tiles = 1;   // an empty blob still gets its header checked
         tile_start[i] = static_cast<uint32_t>(total);
@@ -234,7 +224,9 @@ uint64_t fnv1a(const void* p, size_t n) {
 // none) into a ring slot and copy it to the device on `stream`.  A table the
 // device already holds in a table-only slot is reused as is: the kernels only
 // read it, so a launch in flight on it does not matter, and repeated calls
-// over the same segments (every step of a serving loop) upload nothing.
+// over the same segments (every step of a serving loop) upload nothing.  A
+// caller on another stream than the one that uploaded the table waits (on the
+// device) for that upload unless the host has already seen it complete.
 int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vector<uint32_t>& tiles,
                 bool need_status, hipStream_t stream, Slot** out_slot, SegDev** d_segs, uint32_t** d_tiles,
                 uint32_t** d_status) {
@@ -247,6 +239,12 @@ int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vec
     if (!need_status) {
         for (Slot& c : ctx->slots) {
             if (c.shared && c.nseg == nseg && c.hash == hash && std::memcmp(c.host, segs, seg_bytes) == 0) {
+                if (!c.up_done && c.up_stream != stream) {
+                    const hipError_t q = hipEventQuery(c.up_ev);
+                    if (q == hipSuccess) c.up_done = true;
+                    else if (q == hipErrorNotReady) HIP_TRY(hipStreamWaitEvent(stream, c.up_ev, 0));
+                    else return hip_status(q);
+                }
                 auto* d = static_cast<uint8_t*>(c.dev);
                 *d_segs = reinterpret_cast<SegDev*>(d);
                 *d_tiles = reinterpret_cast<uint32_t*>(d + tile_off);
@@ -259,6 +257,7 @@ int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vec
     Slot& sl = ctx->slots[ctx->next];
     ctx->next = (ctx->next + 1) % kSlots;
     if (!sl.ev) HIP_TRY(hipEventCreateWithFlags(&sl.ev, hipEventDisableTiming));
+    if (!sl.up_ev) HIP_TRY(hipEventCreateWithFlags(&sl.up_ev, hipEventDisableTiming));
     // the pinned copy and the device table are about to be rewritten
     if (sl.users.n || sl.users.overflow) {
         int rc = sl.users.drain_host(sl.ev);
@@ -278,6 +277,9 @@ int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vec
     std::memcpy(h, segs, seg_bytes);
     std::memcpy(h + tile_off, tiles.data(), tile_bytes);
     HIP_TRY(hipMemcpyAsync(sl.dev, sl.host, stat_off, hipMemcpyHostToDevice, stream));
+    HIP_TRY(hipEventRecord(sl.up_ev, stream));
+    sl.up_stream = stream;
+    sl.up_done = false;
     sl.shared = !need_status;
     sl.nseg = nseg;
     sl.hash = hash;
@@ -326,32 +328,15 @@ FibDev fib_dev(const pkv_profile* p) {
     return f;
 }
 
-// Caller holds ctx->mu.
-int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool encode, int dtype,
-                        const void* d_f32, uint64_t f32_elems, const pkv_seg* segs, uint32_t nseg,
-                        const uint8_t* d_wire, uint64_t wire_bytes, uint32_t* d_status, hipStream_t stream,
-                        bool per_vector = false, uint32_t fanout = 1, uint64_t fanout_stride = 0,
-                        uint32_t grid_cap = 0) {
-    if (!ctx || !prof) return PKV_ERR_INVALID_ARG;
-    if (prof->kind == PKV_CODEC_TURBO && radii != PKV_RADII_F32 && radii != PKV_RADII_LOG_U8)
-        return PKV_ERR_INVALID_ARG;
-    if (prof->kind == PKV_CODEC_FIB) radii = PKV_RADII_F32;
-    // dtype: encode input (f32 / bf16) or decode output (f32 / bf16 / f16)
-    if (dtype != PKV_F32 && dtype != PKV_BF16 && (encode || dtype != PKV_F16)) return PKV_ERR_INVALID_ARG;
-    if (encode && fanout != 1) return PKV_ERR_INVALID_ARG;
-    std::vector<uint32_t> tiles;
-    int rc = validate_segments(prof, radii, encode, dtype, d_f32, f32_elems, segs, nseg, d_wire, wire_bytes, tiles,
-                               fanout, fanout_stride);
-    if (rc) return rc;
-    HIP_TRY(hipSetDevice(ctx->device));
-    Slot* sl;
-    SegDev* dsegs;
-    uint32_t *dtiles, *dstat;
-    rc = stage_table(ctx, segs, nseg, tiles, d_status == nullptr, stream, &sl, &dsegs, &dtiles, &dstat);
-    if (rc) return rc;
-    uint32_t* status = d_status ? d_status : dstat;
-    rc = launch_fill_u32(status, STATUS_NONE, 2ull * nseg, stream);
-    if (rc) { finish_slot(sl, stream); return hip_status(static_cast<hipError_t>(rc)); }
+// Clears the status words and launches the encode or decode kernel of the
+// profile over a device-resident segment table (dsegs, dtiles: nseg + 1 tile
+// prefix, nblocks tiles in all).  Returns a hipError_t as int.
+int launch_segments(const pkv_profile* prof, int radii, bool encode, int dtype, const void* d_f32,
+                    const uint8_t* d_wire, const SegDev* dsegs, const uint32_t* dtiles, uint32_t nseg,
+                    uint32_t nblocks, uint32_t* status, bool per_vector, uint32_t fanout, uint64_t fanout_stride,
+                    uint32_t grid_cap, hipStream_t stream) {
+    int e = launch_fill_u32(status, STATUS_NONE, 2ull * nseg, stream);
+    if (e) return e;
     LaunchCommon lc;
     lc.segs = dsegs;
     lc.tile_start = dtiles;
@@ -365,15 +350,39 @@ int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool e
     lc.fanout = fanout;
     lc.fanout_stride = fanout_stride;
     lc.grid_cap = grid_cap;
-    const uint32_t nblocks = tiles[nseg];
-    int e;
-    if (prof->kind == PKV_CODEC_TURBO) {
-        e = encode ? launch_turbo_encode(lc, turbo_dev(prof), d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
-                   : launch_turbo_decode(lc, turbo_dev(prof), d_wire, const_cast<void*>(d_f32), nblocks, stream);
-    } else {
-        e = encode ? launch_fib_encode(lc, fib_dev(prof), d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
-                   : launch_fib_decode(lc, fib_dev(prof), d_wire, const_cast<void*>(d_f32), nblocks, stream);
-    }
+    if (prof->kind == PKV_CODEC_TURBO)
+        return encode ? launch_turbo_encode(lc, turbo_dev(prof), d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
+                      : launch_turbo_decode(lc, turbo_dev(prof), d_wire, const_cast<void*>(d_f32), nblocks, stream);
+    return encode ? launch_fib_encode(lc, fib_dev(prof), d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
+                  : launch_fib_decode(lc, fib_dev(prof), d_wire, const_cast<void*>(d_f32), nblocks, stream);
+}
+
+// Caller holds ctx->mu.
+int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool encode, int dtype,
+                        const void* d_f32, uint64_t f32_elems, const pkv_seg* segs, uint32_t nseg,
+                        const uint8_t* d_wire, uint64_t wire_bytes, uint32_t* d_status, hipStream_t stream,
+                        bool per_vector = false, uint32_t fanout = 1, uint64_t fanout_stride = 0,
+                        uint32_t grid_cap = 0) {
+    if (!ctx || !prof) return PKV_ERR_INVALID_ARG;
+    if (prof->kind == PKV_CODEC_TURBO && radii != PKV_RADII_F32 && radii != PKV_RADII_LOG_U8)
+        return PKV_ERR_INVALID_ARG;
+    if (prof->kind == PKV_CODEC_FIB) radii = PKV_RADII_F32;
+    // dtype: encode input (f32 / bf16) or decode output (f32 / bf16 / f16)
+    if (dtype != PKV_F32 && dtype != PKV_BF16 && (encode || dtype != PKV_F16)) return PKV_ERR_INVALID_ARG;
+    if (encode && fanout != 1) return PKV_ERR_INVALID_ARG;
+    std::vector<uint32_t> tiles(static_cast<size_t>(nseg) + 1);
+    int rc = validate_segments(prof, radii, encode, dtype, d_f32, f32_elems, segs, nseg, d_wire, wire_bytes, tiles.data(),
+                               fanout, fanout_stride);
+    if (rc) return rc;
+    HIP_TRY(hipSetDevice(ctx->device));
+    Slot* sl;
+    SegDev* dsegs;
+    uint32_t *dtiles, *dstat;
+    rc = stage_table(ctx, segs, nseg, tiles, d_status == nullptr, stream, &sl, &dsegs, &dtiles, &dstat);
+    if (rc) return rc;
+    uint32_t* status = d_status ? d_status : dstat;
+    const int e = launch_segments(prof, radii, encode, dtype, d_f32, d_wire, dsegs, dtiles, nseg, tiles[nseg], status,
+                                  per_vector, fanout, fanout_stride, grid_cap, stream);
     int rc2 = finish_slot(sl, stream);
     if (e) return hip_status(static_cast<hipError_t>(e));
     return rc2;
@@ -404,8 +413,12 @@ int resolve_status(const pkv_profile* p, const uint32_t* st, uint32_t nseg, cons
     for (uint32_t s = 0; s < nseg; ++s) {
         uint32_t w0 = st[2 * s], w1 = st[2 * s + 1];
         if (w0 == STATUS_NONE && w1 == STATUS_NONE) continue;
+        // Fib batches of >= 4 vectors validate every input before encoding any
+        // norm (codec.rs:592-610 precede 694-704); smaller ones and per-vector
+        // calls fail at the first failing vector.  Without a segment table
+        // (pkv_segments_status) a fib segment counts as a batch of >= 4.
         uint32_t pick;
-        if (p->kind == PKV_CODEC_FIB && segs && segs[s].n_vectors >= 4 && !per_vector)
+        if (p->kind == PKV_CODEC_FIB && !per_vector && (!segs || segs[s].n_vectors >= 4))
             pick = w0 != STATUS_NONE ? w0 : w1;   // batch validation precedes norm encoding
         else
             pick = std::min(w0, w1);              // per-vector order
@@ -564,6 +577,7 @@ void pkv_ctx_destroy(pkv_ctx* ctx) {
     for (Slot& s : ctx->slots) {
         if (s.users.n || s.users.overflow) (void)s.users.drain_host(s.ev);
         if (s.ev) (void)hipEventDestroy(s.ev);
+        if (s.up_ev) (void)hipEventDestroy(s.up_ev);
         if (s.dev) (void)hipFree(s.dev);
         if (s.host) (void)hipHostFree(s.host);
     }
@@ -974,7 +988,10 @@ int pkv_parse_header(const pkv_profile* p, const uint8_t* b, uint64_t len, uint6
         if (b[14] != p->pbits) return PKV_ERR_CORRUPT_PAYLOAD;
         const uint64_t n = rd32(b + 30);
         if (rd32(b + 34) != turbo_plen(p, rc)) return PKV_ERR_CORRUPT_PAYLOAD;
-        if (len != 38 + n * turbo_plen(p, rc)) return PKV_ERR_CORRUPT_PAYLOAD;   // short, or trailing bytes
+        // a short buffer is rejected before any vector (wire.rs:489-498); trailing
+        // bytes only after every vector (cursor.finish(), wire.rs:566): the
+        // host-buffer decode checks them once the kernel has validated the vectors
+        if (len < 38 + n * turbo_plen(p, rc)) return PKV_ERR_CORRUPT_PAYLOAD;
         if (n_vectors) *n_vectors = n;
         if (radii_codec) *radii_codec = rc;
         return PKV_OK;
@@ -1036,10 +1053,16 @@ int pkv_decode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, const uint8_
     int rc = pkv_parse_header(prof, payload, len, &n, &radii);
     if (rc) { if (err) err->status = rc; return rc; }
     if (n_out) *n_out = n;
-    if (n == 0) return PKV_OK;
+    const uint64_t blob = pkv_blob_len(prof, radii, n);
+    if (n == 0) {
+        if (prof->kind == PKV_CODEC_TURBO && len != blob) {   // cursor.finish(), wire.rs:566
+            if (err) err->status = PKV_ERR_CORRUPT_PAYLOAD;
+            return PKV_ERR_CORRUPT_PAYLOAD;
+        }
+        return PKV_OK;
+    }
     if (n > MAX_SEG_VECTORS) return PKV_ERR_INVALID_ARG;
     if (!out || out_cap_vectors < n) return PKV_ERR_CAPACITY;
-    const uint64_t blob = pkv_blob_len(prof, radii, n);
     const uint64_t out_bytes = n * prof->dim * sizeof(float);
     const uint64_t out_pad = (out_bytes + 255) & ~static_cast<uint64_t>(255);
     std::lock_guard<std::mutex> lock(ctx->mu);
@@ -1059,7 +1082,12 @@ int pkv_decode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, const uint8_
     HIP_TRY(hipMemcpyAsync(hs, d_stat, sizeof hs, hipMemcpyDeviceToHost, st));
     HIP_TRY(hipMemcpyAsync(out, d_out, out_bytes, hipMemcpyDeviceToHost, st));
     HIP_TRY(hipStreamSynchronize(st));
-    return resolve_status(prof, hs, 1, &seg, err);
+    rc = resolve_status(prof, hs, 1, &seg, err);
+    if (rc == PKV_OK && prof->kind == PKV_CODEC_TURBO && len != blob) {   // cursor.finish(), wire.rs:566
+        if (err) { err->status = PKV_ERR_CORRUPT_PAYLOAD; err->segment = -1; err->index = 0; }
+        return PKV_ERR_CORRUPT_PAYLOAD;
+    }
+    return rc;
 }
 
 // ---- scoring on compressed codes (turbo-quant/src/turbo.rs:322-381)
@@ -1277,6 +1305,12 @@ int pkv_turbo_score_batch(pkv_ctx* ctx, const pkv_profile* prof, const uint8_t* 
     if (hs[0] != STATUS_NONE) {   // prepare_query runs before any score (turbo.rs:316-319)
         if (err) { err->status = PKV_ERR_NONFINITE_INPUT; err->segment = -1; err->index = hs[0] >> 4; }
         return PKV_ERR_NONFINITE_INPUT;
+    }
+    // the blob is decoded (every code validated, then cursor.finish() rejects
+    // trailing bytes, wire.rs:566) before any score is computed
+    if (hs[2] == STATUS_NONE && len != blob) {
+        if (err) { err->status = PKV_ERR_CORRUPT_PAYLOAD; err->segment = -1; err->index = 0; }
+        return PKV_ERR_CORRUPT_PAYLOAD;
     }
     return resolve_score_status(hs + 2, 1, err);
 }

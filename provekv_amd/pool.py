@@ -224,10 +224,14 @@ class TwoTierPlan:
         main.wait_event(join)
 
     def _cache_tables(self, bufs, cache: DeviceKVCache):
-        """Decode segment tables for `cache` (built once per cache) and the
-        rehydrate status buffers."""
+        """Decode segment tables for `cache` (built once per cache shape: the
+        table depends on nothing else) and the rehydrate status buffers."""
         import torch
-        key = id(cache)
+        if cache.dim != self.dim:
+            raise ValueError(f"cache head_dim {cache.dim} != plan head_dim {self.dim}")
+        if cache.tokens < self.tokens or cache.layers != self.layers or cache.heads != self.heads:
+            raise ValueError("cache too small for this plan")
+        key = (cache.layers, cache.heads, cache.tokens, cache.dim)
         if getattr(self, "_cache_key", None) != key:
             firsts, t = [], self.prefix
             for nt in self.agent_tokens:
@@ -235,8 +239,6 @@ class TwoTierPlan:
                 t += nt
             self._cache_segs = (cache.segments_for(self.pool, [0]), cache.segments_for(self.shells, firsts))
             self._cache_key = key
-        if cache.tokens < self.tokens or cache.layers != self.layers or cache.heads != self.heads:
-            raise ValueError("cache too small for this plan")
         pseg, sseg = self._cache_segs
         for name, n in (("pool_cstatus", len(pseg)), ("shell_cstatus", len(sseg))):
             if name not in bufs:

@@ -54,7 +54,9 @@ def test_turbo_dim128_bit_exact(ctx):
         blob = ad.encode_batch_compact(x, SEED)
         assert blob == O.turbo_encode_batch(x, SEED, radii_codec=int(lossy))
         dec = ad.decode_batch_compact(blob, SEED)
-        assert rel_err(dec, O.turbo_decode_batch(blob, 128, SEED)) <= 1e-6
+        dref = O.turbo_decode_batch(blob, 128, SEED)
+        assert rel_err(dec, dref) <= 1e-6
+        assert np.array_equal(dec.view(np.uint32), dref.view(np.uint32))
 
 
 @pytest.mark.parametrize("n", [1, 15, 16, 17, 63, 257, 1000])
@@ -86,14 +88,20 @@ def test_turbo_dim128_edge_inputs_and_projections(ctx):
             assert prof.encode_batch_compact(x, rc) == O.turbo_encode_batch(x, SEED, proj=proj, radii_codec=rc)
 
 
-@pytest.mark.parametrize("bits,mode", [(8, 1), (4, 0), (2, 1)])
-def test_turbo_other_bit_widths(ctx, bits, mode):
-    x = kv_vectors(7, 200)
-    prof = ctx.turbo_profile(64, bits, 32, SEED, mode)
-    blob = prof.encode_batch_compact(x)
-    assert blob == O.turbo_encode_batch(x, SEED, bits=bits, mode=mode)
-    dec = prof.decode_batch_compact(blob)
-    assert rel_err(dec, O.turbo_decode_batch(blob, 64, SEED, bits=bits, mode=mode)) <= 1e-6
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("bits,mode", [(8, 1), (9, 1), (6, 0), (4, 0), (2, 1), (1, 0)])
+def test_turbo_other_bit_widths(ctx, dim, bits, mode):
+    """Generic polar bit widths (the kernels specialise pbits 3): bytes and
+    decodes bit for bit, both radii codecs."""
+    x = kv_vectors(7 + bits, 200, dim)
+    prof = ctx.turbo_profile(dim, bits, 32, SEED, mode)
+    for rc in (L.RADII_F32, L.RADII_LOG_U8):
+        blob = prof.encode_batch_compact(x, rc)
+        assert blob == O.turbo_encode_batch(x, SEED, bits=bits, mode=mode, radii_codec=rc)
+        dec = prof.decode_batch_compact(blob)
+        dref = O.turbo_decode_batch(blob, dim, SEED, bits=bits, mode=mode)
+        assert rel_err(dec, dref) <= 1e-6
+        assert np.array_equal(dec.view(np.uint32), dref.view(np.uint32))
 
 
 def test_turbo_edge_inputs(ctx):
@@ -134,6 +142,15 @@ def test_turbo_errors(ctx):
         ad.decode_batch_compact(bytes(neg), SEED)
     with pytest.raises(DecompressionFailed):
         ad.decode_batch_compact(bytes(blob) + b"\0", SEED)     # trailing bytes
+    with pytest.raises(DecompressionFailed):
+        ad.decode_batch_compact(bytes(blob[:-1]), SEED)         # short buffer
+    # a corrupt vector and trailing bytes: the vector is reported, as the
+    # reference validates every vector before cursor.finish() (wire.rs:566)
+    with pytest.raises(DecompressionFailed, match="vector 9"):
+        ad.decode_batch_compact(bytes(neg) + b"\0\0", SEED)
+    with pytest.raises(O.OracleError) as e:
+        O.turbo_decode_batch(bytes(neg) + b"\0\0", 64, SEED)
+    assert e.value.index == 9
     with pytest.raises(DecompressionFailed):
         ad.decode_batch_compact(bytes(blob), SEED + 1)          # seed mismatch
 

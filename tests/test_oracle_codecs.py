@@ -185,6 +185,25 @@ def test_turbo_decode_rejects():
             O.turbo_decode_batch(bytes(bad), 64, SEED)
 
 
+def test_turbo_decode_trailing_bytes_checked_after_vectors():
+    """wire.rs:489-498 rejects a short buffer before any vector, cursor.finish()
+    (wire.rs:566) rejects trailing bytes only after every vector: a blob with a
+    corrupt vector AND trailing bytes reports the vector."""
+    x = np.random.RandomState(2).randn(6, 64).astype(np.float32)
+    blob = bytearray(O.turbo_encode_batch(x, SEED))
+    both = bytearray(blob)
+    struct.pack_into("<f", both, 38 + 144 * 4 + 8, -1.0)   # vector 4: negative radius
+    both.extend(b"\0\0")
+    with pytest.raises(O.OracleError) as e:
+        O.turbo_decode_batch(bytes(both), 64, SEED)
+    assert e.value.kind == "malformed" and e.value.index == 4
+    with pytest.raises(O.OracleError) as e:                 # trailing bytes alone
+        O.turbo_decode_batch(bytes(blob) + b"\0", 64, SEED)
+    assert e.value.kind == "malformed"
+    with pytest.raises(O.OracleError):                      # short by one byte
+        O.turbo_decode_batch(bytes(blob[:-1]), 64, SEED)
+
+
 def test_turbo_lossy_equal_radii_span_clamp():
     # BlockLogU8: equal radii -> span clamps to EPSILON on encode, 0 on decode
     x = np.zeros((4, 64), np.float32)
