@@ -42,7 +42,8 @@ enum pkv_status {
     PKV_ERR_NORM_UNREPRESENTABLE = 9, /* encode_norm: not a finite positive f16 */
     PKV_ERR_EMPTY_BATCH = 10,       /* "empty batch" (wire encode_batch)        */
     PKV_ERR_CAPACITY = 11,          /* caller buffer too small                  */
-    PKV_ERR_NONFINITE_CODE = 12     /* turbo encode: radius / residual not finite */
+    PKV_ERR_NONFINITE_CODE = 12,    /* turbo encode: radius / residual not finite */
+    PKV_ERR_SCRATCH_LIMIT = 13      /* beyond the fixed scratch of pkv_decode_segments_noalloc */
 };
 
 /* Returns a static, human-readable name for a status code. */
@@ -219,6 +220,27 @@ int pkv_decode_segments_bounded(pkv_ctx* ctx, const pkv_profile* prof, int radii
                                 uint32_t nseg, void* d_out, int out_dtype, uint64_t out_elems,
                                 uint32_t fanout, uint64_t fanout_stride, uint32_t max_workgroups,
                                 uint32_t* d_status, void* stream);
+
+/* pkv_decode_segments_ex without any allocation: no hipMalloc, hipFree or
+ * other allocating call, here or in the kernels.  No counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, checks, kernels and results as pkv_decode_segments_ex.  The
+ * segment table, its workgroup prefix and (when d_status is NULL) the status
+ * words live in one fixed device array of the library per GPU (about 208 KiB,
+ * held until the process ends), so nseg <= PKV_NOALLOC_MAX_SEGMENTS; a larger
+ * table returns PKV_ERR_SCRATCH_LIMIT before any work.  Every call on a GPU
+ * shares that array and leaves its contents behind (each call rewrites what it
+ * uses): calls on one stream are ordered, but calls that overlap on one GPU
+ * (other streams, other contexts on the same device) race on it and must be
+ * serialised by the caller.  The table is copied from the caller's host memory
+ * with hipMemcpyAsync on `stream`; segs may be released when the call returns. */
+#define PKV_NOALLOC_MAX_SEGMENTS 4096u
+int pkv_decode_segments_noalloc(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec,
+                                const uint8_t* d_wire, uint64_t wire_bytes, const pkv_seg* segs,
+                                uint32_t nseg, void* d_out, int out_dtype, uint64_t out_elems,
+                                uint32_t fanout, uint64_t fanout_stride, uint32_t* d_status,
+                                void* stream);
 
 /* ---------------------------------------------------------------- host-buffer
  * Drop-ins for the adapters' inherent batch methods: host slices in, wire

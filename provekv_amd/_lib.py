@@ -26,6 +26,8 @@ ERR_NORM_UNREPRESENTABLE = 9
 ERR_EMPTY_BATCH = 10
 ERR_CAPACITY = 11
 ERR_NONFINITE_CODE = 12
+ERR_SCRATCH_LIMIT = 13
+NOALLOC_MAX_SEGMENTS = 4096
 
 CODEC_TURBO = 1
 CODEC_FIB = 2
@@ -44,7 +46,7 @@ EXPORTS = (
     "pkv_fib_profile_create_with_constants", "pkv_profile_destroy", "pkv_turbo_constants",
     "pkv_fib_constants", "pkv_profile_constants", "pkv_payload_len", "pkv_header_len", "pkv_blob_len",
     "pkv_segments_status", "pkv_encode_segments", "pkv_decode_segments", "pkv_decode_segments_ex",
-    "pkv_decode_segments_bounded",
+    "pkv_decode_segments_bounded", "pkv_decode_segments_noalloc",
     "pkv_encode_batch_compact",
     "pkv_decode_batch_compact", "pkv_parse_header", "pkv_record_len", "pkv_encode_vectors", "pkv_decode_vectors",
     "pkv_constants_cache_stats", "pkv_constants_cache_clear", "pkv_prepared_len", "pkv_turbo_prepare_queries",
@@ -120,6 +122,7 @@ def _declare(L):
         "pkv_decode_segments": ([P, P, I32, P, U64, P, U32, P, U64, P, P], I32),
         "pkv_decode_segments_ex": ([P, P, I32, P, U64, P, U32, P, I32, U64, U32, U64, P, P], I32),
         "pkv_decode_segments_bounded": ([P, P, I32, P, U64, P, U32, P, I32, U64, U32, U64, U32, P, P], I32),
+        "pkv_decode_segments_noalloc": ([P, P, I32, P, U64, P, U32, P, I32, U64, U32, U64, P, P], I32),
         "pkv_encode_batch_compact": ([P, P, I32, P, U64, P, U64, P, P], I32),
         "pkv_decode_batch_compact": ([P, P, P, U64, P, U64, P, P], I32),
         "pkv_parse_header": ([P, P, U64, P, P], I32),

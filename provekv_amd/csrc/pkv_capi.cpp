@@ -86,8 +86,9 @@ struct pkv_ctx {
     Slot slots[kSlots];
     int next = 0;
     hipStream_t own_stream = nullptr;   // for the host-buffer entry points
-    void* scratch = nullptr;            // host-buffer entry points: in + out
-    size_t scratch_cap = 0;
+    void* io_buf = nullptr;             // host-buffer entry points: in + out (device memory)
+    size_t io_buf_cap = 0;
+    uint8_t* noalloc = nullptr;         // this device's copy of `scratch` (pkv_decode_segments_noalloc)
 };
 
 struct pkv_profile {
@@ -118,9 +119,43 @@ struct pkv_profile {
     float thr = 0.0f;
 };
 
+// ---- fixed scratch of pkv_decode_segments_noalloc: [segment table | tile
+// prefix | status words] of one call, for at most PKV_NOALLOC_MAX_SEGMENTS
+// segments.  A file-scope device array: every GPU the library runs on holds
+// its own copy, at its own address, from module load to process end.  In host
+// code `scratch` names a host-side stand-in, never the device memory: host code
+// uses only the address hipGetSymbolAddress returns for the current device.
+namespace {
+constexpr size_t pad256c(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+constexpr size_t kNaTileOff = pad256c(sizeof(pkv_seg) * PKV_NOALLOC_MAX_SEGMENTS);
+constexpr size_t kNaStatusOff = kNaTileOff + pad256c(sizeof(uint32_t) * (PKV_NOALLOC_MAX_SEGMENTS + 1));
+constexpr size_t kNaBytes = kNaStatusOff + sizeof(uint32_t) * 2 * PKV_NOALLOC_MAX_SEGMENTS;
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kNaBytes];
+
 namespace {
 
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[kMaxDevices] = {};
 
+// Device address of `scratch` on `device`, looked up once per device with that
+// device current (the caller has made it current).
+int noalloc_scratch(int device, uint8_t** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device >= 0 && device < kMaxDevices && g_scratch_ptr[device]) {
+        *out = g_scratch_ptr[device];
+        return PKV_OK;
+    }
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e);
+    if (!p) return PKV_ERR_DEVICE;
+    if (device >= 0 && device < kMaxDevices) g_scratch_ptr[device] = static_cast<uint8_t*>(p);
+    *out = static_cast<uint8_t*>(p);
+    return PKV_OK;
+}
 
 template <typename T>
 int upload(T** dptr, const std::vector<T>& v) {
@@ -397,14 +432,14 @@ int run_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool encode, 
                                d_status, stream);
 }
 
-int ensure_scratch(pkv_ctx* ctx, size_t bytes) {
-    if (ctx->scratch_cap >= bytes) return PKV_OK;
-    if (ctx->scratch) HIP_TRY(hipFree(ctx->scratch));
-    ctx->scratch = nullptr;
-    ctx->scratch_cap = 0;
+int ensure_io_buf(pkv_ctx* ctx, size_t bytes) {
+    if (ctx->io_buf_cap >= bytes) return PKV_OK;
+    if (ctx->io_buf) HIP_TRY(hipFree(ctx->io_buf));
+    ctx->io_buf = nullptr;
+    ctx->io_buf_cap = 0;
     size_t cap = std::max<size_t>(bytes, 1 << 20);
-    HIP_TRY(hipMalloc(&ctx->scratch, cap));
-    ctx->scratch_cap = cap;
+    HIP_TRY(hipMalloc(&ctx->io_buf, cap));
+    ctx->io_buf_cap = cap;
     return PKV_OK;
 }
 
@@ -541,6 +576,7 @@ const char* pkv_status_string(int status) {
         case PKV_ERR_EMPTY_BATCH: return "empty batch";
         case PKV_ERR_CAPACITY: return "buffer too small";
         case PKV_ERR_NONFINITE_CODE: return "non-finite radius or residual";
+        case PKV_ERR_SCRATCH_LIMIT: return "more segments than the no-allocation scratch holds";
         default: return "unknown status";
     }
 }
@@ -567,6 +603,8 @@ int pkv_ctx_create(int device, pkv_ctx** out) {
     c->device = device;
     hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
     if (e != hipSuccess) { delete c; return hip_status(e); }
+    const int rc = noalloc_scratch(device, &c->noalloc);   // device is current
+    if (rc) { (void)hipStreamDestroy(c->own_stream); delete c; return rc; }
     *out = c;
     return PKV_OK;
 }
@@ -585,7 +623,7 @@ void pkv_ctx_destroy(pkv_ctx* ctx) {
         (void)hipStreamSynchronize(ctx->own_stream);
         (void)hipStreamDestroy(ctx->own_stream);
     }
-    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->io_buf) (void)hipFree(ctx->io_buf);
     delete ctx;
 }
 
@@ -975,6 +1013,38 @@ int pkv_decode_segments_bounded(pkv_ctx* ctx, const pkv_profile* prof, int radii
                                max_workgroups);
 }
 
+// pkv_decode_segments_ex with the table, its tile prefix and the status words
+// in this device's `scratch` (address from set-up): no allocating call.
+int pkv_decode_segments_noalloc(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, const uint8_t* d_wire,
+                                uint64_t wire_bytes, const pkv_seg* segs, uint32_t nseg, void* d_out, int out_dtype,
+                                uint64_t out_elems, uint32_t fanout, uint64_t fanout_stride, uint32_t* d_status,
+                                void* stream) {
+    if (!ctx || !prof) return PKV_ERR_INVALID_ARG;
+    if (nseg > PKV_NOALLOC_MAX_SEGMENTS) return PKV_ERR_SCRATCH_LIMIT;
+    if (!ctx->noalloc) return PKV_ERR_DEVICE;
+    if (out_dtype != PKV_F32 && out_dtype != PKV_BF16 && out_dtype != PKV_F16) return PKV_ERR_INVALID_ARG;
+    int radii = radii_codec;
+    if (prof->kind == PKV_CODEC_TURBO && radii != PKV_RADII_F32 && radii != PKV_RADII_LOG_U8)
+        return PKV_ERR_INVALID_ARG;
+    if (prof->kind == PKV_CODEC_FIB) radii = PKV_RADII_F32;
+    uint32_t tiles[PKV_NOALLOC_MAX_SEGMENTS + 1];   // host stack, no heap
+    int rc = validate_segments(prof, radii, false, out_dtype, d_out, out_elems, segs, nseg, d_wire, wire_bytes, tiles,
+                               fanout, fanout_stride);
+    if (rc) return rc;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    uint8_t* base = ctx->noalloc;
+    // pageable host sources: the runtime stages them before returning
+    HIP_TRY(hipMemcpyAsync(base, segs, sizeof(pkv_seg) * nseg, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(base + kNaTileOff, tiles, sizeof(uint32_t) * (nseg + 1), hipMemcpyHostToDevice, st));
+    uint32_t* status = d_status ? d_status : reinterpret_cast<uint32_t*>(base + kNaStatusOff);
+    const int e = launch_segments(prof, radii, false, out_dtype, d_out, d_wire, reinterpret_cast<const SegDev*>(base),
+                                  reinterpret_cast<const uint32_t*>(base + kNaTileOff), nseg, tiles[nseg], status,
+                                  false, fanout, fanout_stride, 0, st);
+    return e ? hip_status(static_cast<hipError_t>(e)) : PKV_OK;
+}
+
 int pkv_parse_header(const pkv_profile* p, const uint8_t* b, uint64_t len, uint64_t* n_vectors, int* radii_codec) {
     if (!p || !b) return PKV_ERR_INVALID_ARG;
     if (p->kind == PKV_CODEC_TURBO) {
@@ -1024,11 +1094,11 @@ int pkv_encode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, int radii_co
     if (!out || out_cap < blob) return PKV_ERR_CAPACITY;
     const uint64_t in_bytes = n * prof->dim * sizeof(float);
     const uint64_t in_pad = (in_bytes + 255) & ~static_cast<uint64_t>(255);
-    std::lock_guard<std::mutex> lock(ctx->mu);   // serialises use of ctx->scratch
+    std::lock_guard<std::mutex> lock(ctx->mu);   // serialises use of ctx->io_buf
     HIP_TRY(hipSetDevice(ctx->device));
-    int rc = ensure_scratch(ctx, in_pad + blob + 256 + 64);
+    int rc = ensure_io_buf(ctx, in_pad + blob + 256 + 64);
     if (rc) return rc;
-    auto* d_in = static_cast<uint8_t*>(ctx->scratch);
+    auto* d_in = static_cast<uint8_t*>(ctx->io_buf);
     uint8_t* d_wire = d_in + in_pad;
     uint32_t* d_stat = reinterpret_cast<uint32_t*>(d_wire + ((blob + 255) & ~static_cast<uint64_t>(255)));
     hipStream_t st = ctx->own_stream;
@@ -1067,9 +1137,9 @@ int pkv_decode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, const uint8_
     const uint64_t out_pad = (out_bytes + 255) & ~static_cast<uint64_t>(255);
     std::lock_guard<std::mutex> lock(ctx->mu);
     HIP_TRY(hipSetDevice(ctx->device));
-    rc = ensure_scratch(ctx, out_pad + blob + 256 + 64);
+    rc = ensure_io_buf(ctx, out_pad + blob + 256 + 64);
     if (rc) return rc;
-    auto* d_out = static_cast<uint8_t*>(ctx->scratch);
+    auto* d_out = static_cast<uint8_t*>(ctx->io_buf);
     uint8_t* d_wire = d_out + out_pad;
     uint32_t* d_stat = reinterpret_cast<uint32_t*>(d_wire + ((blob + 255) & ~static_cast<uint64_t>(255)));
     hipStream_t st = ctx->own_stream;
@@ -1281,9 +1351,9 @@ int pkv_turbo_score_batch(pkv_ctx* ctx, const pkv_profile* prof, const uint8_t* 
     const uint64_t s_bytes = need * sizeof(float);
     std::lock_guard<std::mutex> lock(ctx->mu);
     HIP_TRY(hipSetDevice(ctx->device));
-    rc = ensure_scratch(ctx, pad(blob) + pad(q_bytes) + pad(p_bytes) + pad(s_bytes) + 256);
+    rc = ensure_io_buf(ctx, pad(blob) + pad(q_bytes) + pad(p_bytes) + pad(s_bytes) + 256);
     if (rc) return rc;
-    auto* base = static_cast<uint8_t*>(ctx->scratch);
+    auto* base = static_cast<uint8_t*>(ctx->io_buf);
     uint8_t* d_wire = base;
     auto* d_q = reinterpret_cast<float*>(base + pad(blob));
     auto* d_p = reinterpret_cast<float*>(base + pad(blob) + pad(q_bytes));
@@ -1333,9 +1403,9 @@ int pkv_encode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const fl
     const uint64_t o_st = o_rec + pad256(rec_bytes + 4);
     std::lock_guard<std::mutex> lock(ctx->mu);
     HIP_TRY(hipSetDevice(ctx->device));
-    int rc = ensure_scratch(ctx, o_st + 256);
+    int rc = ensure_io_buf(ctx, o_st + 256);
     if (rc) return rc;
-    auto* base = static_cast<uint8_t*>(ctx->scratch);
+    auto* base = static_cast<uint8_t*>(ctx->io_buf);
     uint8_t* d_blob = base + o_blob;
     uint32_t* d_stat = reinterpret_cast<uint32_t*>(base + o_st);
     hipStream_t st = ctx->own_stream;
@@ -1375,9 +1445,9 @@ int pkv_decode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const ui
     const uint64_t o_blob = o_off + pad256(8 * (n + 1)), o_st = o_blob + pad256(blob + 4);
     std::lock_guard<std::mutex> lock(ctx->mu);
     HIP_TRY(hipSetDevice(ctx->device));
-    int rc = ensure_scratch(ctx, o_st + 256);
+    int rc = ensure_io_buf(ctx, o_st + 256);
     if (rc) return rc;
-    auto* base = static_cast<uint8_t*>(ctx->scratch);
+    auto* base = static_cast<uint8_t*>(ctx->io_buf);
     const uint8_t* d_rec = base + o_rec;
     const uint64_t* d_off = reinterpret_cast<const uint64_t*>(base + o_off);
     uint8_t* d_blob = base + o_blob;
