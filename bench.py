@@ -46,7 +46,7 @@ def cpu_baseline(corpus: np.ndarray, plan, budget_s: float = 16.0) -> dict:
     """Oracle (one thread) encode + decode of sampled (layer, K|V) blobs of
     both tiers, scaled to the f32-KV GB/s of the whole workload."""
     from oracle import oracle as O
-    cb, rot = plan.fib.constants()
+    cb, rot = O.fib_constants(plan.fib.params["seed"])   # the oracle's own constants
     cb = cb.reshape(32, 4)
     rot = rot.reshape(plan.dim, plan.dim)
     layers, dim = plan.layers, plan.dim
@@ -91,7 +91,7 @@ def spot_check_cache(plan, bufs, cache, corpus):
     oracle decode (rounded to the cache dtype) in every copy."""
     import torch
     from oracle import oracle as O
-    cb, rot = plan.fib.constants()
+    cb, rot = O.fib_constants(plan.fib.params["seed"])   # the oracle's own constants
     cb, rot = cb.reshape(32, 4), rot.reshape(plan.dim, plan.dim)
     heads, dim = plan.heads, plan.dim
     checks = [(0, plan.prefix, O.fib_decode_batch(plan.blob(bufs, "pool", 0), cb, rot))]
@@ -195,7 +195,7 @@ def bench_legacy(args):
     ops["turbo_tqw1_decode"] = (x2.shape[0], t)
     # parity spot check against the oracle on the first records
     m = 2000
-    cb, rot = fib.constants()
+    cb, rot = O.fib_constants(42)
     cb, rot = cb.reshape(32, 4), rot.reshape(64, 64)
     rec1 = fib.record_len()
     ref = O.fib_encode_fb1(x1[:m], cb, rot, each=False)

@@ -102,6 +102,14 @@ int pkv_fib_profile_create_with_constants(pkv_ctx* ctx, uint32_t dim, uint32_t k
                                           pkv_profile** out);
 void pkv_profile_destroy(pkv_profile* prof);
 
+/* Which kernel decodes a fib profile: 1 = the matrix-core decode (every
+ * product f32(Pi)[r][col] * c[w][r % 4] it can form was checked equal to f32
+ * multiplication when the profile was created), 0 = the VALU decode (some
+ * product differed, e.g. a -0.0 product that the matrix core returns as +0.0),
+ * -1 = not a fib profile.  Both produce the bytes of decode_batch_fast
+ * (fib-quant/src/codec.rs:797-844); this only reports which one runs. */
+int pkv_fib_decode_path(const pkv_profile* prof);
+
 /* Host-only constant generators (no device needed): the exact constants
  * pkv_turbo_profile_create / pkv_fib_profile_create derive from a seed.
  * turbo: signs[dim], qjl[projections*dim] (NULL skips);

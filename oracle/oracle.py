@@ -191,6 +191,26 @@ def fib_codebook(d=64, k=4, n=32, seed=42, training=2048, restarts=4, iterations
     return out.reshape(n, k), float(i_mse[0]), float(t_mse[0])
 
 
+_FIB_CONSTANTS = {}
+
+
+def fib_constants(seed: int = 42, d: int = 64, k: int = 4, n: int = 32, training: int = 2048, restarts: int = 4,
+                  iterations: int = 8):
+    """The oracle's own fib profile constants (FibQuantAdapter::build_quantizer,
+    proveKV/src/codec.rs:471-499): codebook [n, k] f32 (codebook.rs:40-60) and
+    rotation [d, d] f64 row-major (rotation.rs:24-58), built once per process
+    and per parameters.  Parity tests feed THESE to the oracle, never the
+    product's constants."""
+    key = (seed, d, k, n, training, restarts, iterations)
+    if key not in _FIB_CONSTANTS:
+        cb, _, _ = fib_codebook(d, k, n, seed, training, restarts, iterations)
+        rot, _ = stored_rotation(d, seed)
+        cb.setflags(write=False)
+        rot.setflags(write=False)
+        _FIB_CONSTANTS[key] = (cb, rot)
+    return _FIB_CONSTANTS[key]
+
+
 def inv_norm_cdf(p: float) -> float:
     return lib().ora_inv_norm_cdf(p)
 

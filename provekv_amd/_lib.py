@@ -43,7 +43,7 @@ DT_F16 = 2
 EXPORTS = (
     "pkv_status_string", "pkv_ctx_create", "pkv_ctx_destroy", "pkv_device_available",
     "pkv_turbo_profile_create", "pkv_turbo_profile_create_with_constants", "pkv_fib_profile_create",
-    "pkv_fib_profile_create_with_constants", "pkv_profile_destroy", "pkv_turbo_constants",
+    "pkv_fib_profile_create_with_constants", "pkv_profile_destroy", "pkv_fib_decode_path", "pkv_turbo_constants",
     "pkv_fib_constants", "pkv_profile_constants", "pkv_payload_len", "pkv_header_len", "pkv_blob_len",
     "pkv_segments_status", "pkv_encode_segments", "pkv_decode_segments", "pkv_decode_segments_ex",
     "pkv_decode_segments_bounded", "pkv_decode_segments_noalloc",
@@ -111,6 +111,7 @@ def _declare(L):
         "pkv_fib_profile_create": ([P, U32, U32, U32, U64, U32, U32, U32, P], I32),
         "pkv_fib_profile_create_with_constants": ([P, U32, U32, U32, P, P, P], I32),
         "pkv_profile_destroy": ([P], None),
+        "pkv_fib_decode_path": ([P], I32),
         "pkv_turbo_constants": ([U32, U32, U64, P, P], I32),
         "pkv_fib_constants": ([U32, U32, U32, U64, U32, U32, U32, P, P, P, P], I32),
         "pkv_profile_constants": ([P, P, C.c_size_t, P, C.c_size_t], I32),

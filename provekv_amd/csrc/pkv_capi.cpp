@@ -943,6 +943,11 @@ void pkv_profile_destroy(pkv_profile* p) {
     delete p;
 }
 
+int pkv_fib_decode_path(const pkv_profile* p) {
+    if (!p || p->kind != PKV_CODEC_FIB) return -1;
+    return p->mfma_decode ? 1 : 0;
+}
+
 int pkv_profile_constants(const pkv_profile* p, void* a, size_t a_bytes, void* b, size_t b_bytes) {
     if (!p) return PKV_ERR_INVALID_ARG;
     if (p->kind == PKV_CODEC_TURBO) {

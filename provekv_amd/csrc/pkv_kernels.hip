@@ -847,7 +847,11 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
                     float d2 = first;
 #pragma unroll
                     for (int c = 0; c < 32; ++c) d2 = d2 + g[c] * y[c];     // half 1: continues over 32..63
-                    const float full = u2f(h ? f2u(d2) : partner(f2u(d2), h));
+                    // every lane takes part in the swap (a cross-lane read under a
+                    // lane-dependent condition would see the inactive half's
+                    // lanes unchanged); half 0 then takes half 1's full sum
+                    const uint32_t other = partner(f2u(d2), h);
+                    const float full = u2f(h ? f2u(d2) : other);
                     if ((m >> j) & 1u) sbits[p] = (sbits[p] & ~(1u << j)) | (full >= 0.0f ? 1u << j : 0u);
                 }
             }

@@ -95,6 +95,21 @@ class Context:
                                                    lloyd_iterations)
             return self._profiles[key]
 
+    def fib_profile_with_constants(self, codebook: np.ndarray, rotation: np.ndarray) -> "Profile":
+        """fib_k4_n32 profile from a caller's FibCodebookV1::codewords [32, 4]
+        f32 and StoredRotation::matrix [64, 64] f64 (not cached: the caller
+        owns the profile)."""
+        cb = np.ascontiguousarray(codebook, dtype=np.float32).reshape(-1)
+        rot = np.ascontiguousarray(rotation, dtype=np.float64).reshape(-1)
+        n, k = 32, 4
+        dim = int(round(np.sqrt(rot.size)))
+        if cb.size != n * k or dim * dim != rot.size:
+            raise ValueError("codebook must be [32, 4] and rotation [dim, dim]")
+        ptr = C.c_void_p()
+        L.check(L.lib().pkv_fib_profile_create_with_constants(self.ptr, dim, k, n, cb.ctypes.data, rot.ctypes.data,
+                                                              C.byref(ptr)), "pkv_fib_profile_create_with_constants")
+        return Profile(self, ptr, L.CODEC_FIB, dim, k=k, n=n, seed=None)
+
 
 _default_ctx = None
 _default_lock = threading.Lock()
@@ -140,6 +155,11 @@ class Profile:
         if self._ptr:
             L.lib().pkv_profile_destroy(self._ptr)
             self._ptr = C.c_void_p()
+
+    def fib_decode_path(self) -> str:
+        """'matrix' (products verified bit-exact at creation) or 'valu'."""
+        p = int(L.lib().pkv_fib_decode_path(self._ptr))
+        return {1: "matrix", 0: "valu"}.get(p, "none")
 
     def payload_len(self, radii: int = L.RADII_F32) -> int:
         return int(L.lib().pkv_payload_len(self._ptr, radii))

@@ -14,29 +14,53 @@ _M2 = np.uint64(0x94D049BB133111EB)
 _GOLD = np.uint64(0x9E3779B97F4A7C15)
 
 
-def splitmix64(seed: int, n: int, start: int = 0) -> np.ndarray:
+_CHUNK = 1 << 16   # elements per pass: the temporaries stay in cache
+
+
+def _splitmix64_into(out: np.ndarray, seed: int, start: int) -> None:
+    """out[i] = splitmix64 output number start + i + 1 of `seed`."""
+    s30, s27, s31 = np.uint64(30), np.uint64(27), np.uint64(31)
     with np.errstate(over="ignore"):
-        idx = np.arange(start + 1, start + n + 1, dtype=np.uint64)
-        z = np.uint64(seed) + idx * _GOLD
-        z = (z ^ (z >> np.uint64(30))) * _M1
-        z = (z ^ (z >> np.uint64(27))) * _M2
-        return z ^ (z >> np.uint64(31))
+        z = np.arange(start + 1, start + out.size + 1, dtype=np.uint64)
+        z *= _GOLD
+        z += np.uint64(seed)
+        z ^= z >> s30
+        z *= _M1
+        z ^= z >> s27
+        z *= _M2
+        z ^= z >> s31
+    out[...] = z
+
+
+def splitmix64(seed: int, n: int, start: int = 0) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint64)
+    for c0 in range(0, n, _CHUNK):
+        _splitmix64_into(out[c0:c0 + _CHUNK], seed, start + c0)
+    return out
 
 
 def normals(seed: int, n: int, stream: int = 0) -> np.ndarray:
-    """n f32 N(0,1) draws; `stream` separates independent sequences."""
+    """n f32 N(0,1) draws; `stream` separates independent sequences.  Pair j
+    takes uniforms u1 (0, 1] and u2 [0, 1) from splitmix64 outputs j and m + j
+    (m = ceil(n / 2)) and yields r cos(2 pi u2), r sin(2 pi u2), r =
+    sqrt(-2 ln u1), in f64, rounded to f32."""
     m = (n + 1) // 2
     base = stream * (1 << 40)
-    a = splitmix64(seed, m, base)
-    b = splitmix64(seed, m, base + m)
-    u1 = ((a >> np.uint64(11)).astype(np.float64) + 1.0) * (1.0 / 9007199254740992.0)   # (0, 1]
-    u2 = (b >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
-    r = np.sqrt(-2.0 * np.log(u1))
-    t = 2.0 * np.pi * u2
-    out = np.empty(2 * m, dtype=np.float64)
-    out[0::2] = r * np.cos(t)
-    out[1::2] = r * np.sin(t)
-    return out[:n].astype(np.float32)
+    out = np.empty(2 * m, dtype=np.float32)
+    a = np.empty(_CHUNK, dtype=np.uint64)
+    b = np.empty(_CHUNK, dtype=np.uint64)
+    inv53 = 1.0 / 9007199254740992.0
+    for c0 in range(0, m, _CHUNK):
+        k = min(_CHUNK, m - c0)
+        _splitmix64_into(a[:k], seed, base + c0)
+        _splitmix64_into(b[:k], seed, base + m + c0)
+        u1 = ((a[:k] >> np.uint64(11)).astype(np.float64) + 1.0) * inv53
+        u2 = (b[:k] >> np.uint64(11)).astype(np.float64) * inv53
+        r = np.sqrt(-2.0 * np.log(u1))
+        t = 2.0 * np.pi * u2
+        out[2 * c0:2 * (c0 + k):2] = r * np.cos(t)
+        out[2 * c0 + 1:2 * (c0 + k):2] = r * np.sin(t)
+    return out[:n]
 
 
 def kv_cache(seed: int, layers: int, heads: int, tokens: int, dim: int, k_sigma: float = 0.5,
@@ -54,6 +78,34 @@ def kv_cache(seed: int, layers: int, heads: int, tokens: int, dim: int, k_sigma:
     K = (zk.astype(np.float64) * (scale * mult[:, :, None, :])).astype(np.float32)
     V = (zv.astype(np.float64) * v_scale).astype(np.float32)
     return K, V
+
+
+def device_kv_bf16(seed: int, layers: int, heads: int, tokens: int, dim: int, k_sigma: float = 0.7,
+                   outliers: int = 4, outlier_mult: float = 10.0, v_scale: float = 1.0, device="cuda"):
+    """The same value distribution generated on the GPU (for shapes too large
+    to generate on the host, e.g. the Llama-3-8B KV of 4.3 GB): K[l, h, t, c]
+    = s[l, h, c] z with s = exp(k_sigma z') and `outliers` channels per head
+    (a seeded permutation) scaled by `outlier_mult`, V = v_scale z; computed in
+    f32, then rounded to bf16 (nearest even).  Returns one bf16 tensor
+    [layers, 2 (K|V), heads, tokens, dim].  Seeded by torch's Philox generator
+    on `device`: reproducible for a given torch build, not equal to the host
+    generator's draws."""
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed(int(seed))
+    out = torch.empty((layers, 2, heads, tokens, dim), dtype=torch.bfloat16, device=device)
+    zs = torch.randn((layers, heads, 1, dim), generator=g, device=device, dtype=torch.float32)
+    mult = torch.ones((layers, heads, 1, dim), device=device, dtype=torch.float32)
+    for li in range(layers):
+        for h in range(heads):
+            perm = torch.randperm(dim, generator=g, device=device)[:outliers]
+            mult[li, h, 0, perm] = outlier_mult
+    scale = torch.exp(k_sigma * zs) * mult
+    for li in range(layers):   # one layer at a time: bounded f32 scratch
+        z = torch.randn((2, heads, tokens, dim), generator=g, device=device, dtype=torch.float32)
+        out[li, 0] = (z[0] * scale[li]).to(torch.bfloat16)
+        out[li, 1] = (z[1] * v_scale).to(torch.bfloat16)
+    return out
 
 
 def corpus_tokens(seed: int, layers: int, heads: int, tokens: int, dim: int, **kw) -> np.ndarray:

@@ -11,6 +11,7 @@ import pytest
 
 from oracle import oracle as O
 from provekv_amd import _lib as L
+from provekv_amd import device as D
 from provekv_amd import synth
 from provekv_amd.codec import (CompressionFailed, DecompressionFailed, FibQuantAdapter, RadiiCompression,
                                TurboQuantAdapter)
@@ -89,6 +90,28 @@ def test_turbo_dim128_edge_inputs_and_projections(ctx):
 
 
 @pytest.mark.parametrize("dim", [64, 128])
+def test_qjl_sign_follows_reference_sum_order(ctx, dim):
+    """Vectors whose QJL dot for one projection is so close to zero that its
+    sign depends on the summation order (tests/golden/qjl_sum_order.npz, built
+    by the oracle): the kernels must reproduce the reference's one sequential
+    sum (qjl.rs:203-220) -- alone, batched, and at every lane position of a
+    32-vector (d64) / 16-vector (d128) group, both radii codecs."""
+    import os
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "qjl_sum_order.npz"))
+    x = f[f"x{dim}"]
+    rng = np.random.RandomState(dim)
+    filler = rng.randn(40, dim).astype(np.float32)
+    batches = [x[i:i + 1] for i in range(len(x))] + [x]
+    for pos in range(0, 32 if dim == 64 else 16, 5):   # the tricky vectors at lane position pos
+        batches.append(np.concatenate([filler[:pos], x, filler[:7]]))
+    prof = ctx.turbo_profile(dim, 4, 32, SEED, 1)
+    for rc in (L.RADII_F32, L.RADII_LOG_U8):
+        for b in batches:
+            b = np.ascontiguousarray(b)
+            assert prof.encode_batch_compact(b, rc) == O.turbo_encode_batch(b, SEED, radii_codec=rc)
+
+
+@pytest.mark.parametrize("dim", [64, 128])
 @pytest.mark.parametrize("bits,mode", [(8, 1), (9, 1), (6, 0), (4, 0), (2, 1), (1, 0)])
 def test_turbo_other_bit_widths(ctx, dim, bits, mode):
     """Generic polar bit widths (the kernels specialise pbits 3): bytes and
@@ -160,14 +183,50 @@ def test_fib_encode_decode_bit_exact(ctx, n):
     x = kv_vectors(100 + n, n)
     ad = FibQuantAdapter(64, 4, 32, 2048, 4, 8)
     blob = ad.encode_batch_compact(x, SEED)
-    prof = ad.build_quantizer(SEED)
-    cb, rot = prof.constants()
+    cb, rot = O.fib_constants(SEED)   # the oracle's own codebook and rotation
     ref = O.fib_encode_batch(x, cb.reshape(32, 4), rot.reshape(64, 64))
     assert blob == ref
     dec = ad.decode_batch_compact(blob, SEED)
     dref = O.fib_decode_batch(ref, cb.reshape(32, 4), rot.reshape(64, 64))
     assert rel_err(dec, dref) <= 1e-6
     assert np.array_equal(dec.view(np.uint32), dref.view(np.uint32))
+
+
+def test_fib_valu_decode_fallback(ctx):
+    """A codebook with exact 0.0 components (and a subnormal one): the matrix
+    core returns a product 0 x (negative) as +0.0 where f32 multiplication
+    gives -0.0, so the profile's product check sends its decode to the VALU
+    kernel.  Bytes and decodes (f32, and bf16 fanned out to two caches) must
+    still be the oracle's, run on the same codebook."""
+    import torch
+    cb, rot = O.fib_constants(SEED)
+    cb = cb.copy()
+    cb[3, 1] = 0.0
+    cb[20, 2] = 0.0
+    cb[7, 0] = np.float32(1e-39)
+    prof = ctx.fib_profile_with_constants(cb, rot)
+    try:
+        assert prof.fib_decode_path() == "valu"
+        x = kv_vectors(31, 1000)
+        blob = prof.encode_batch_compact(x)
+        assert blob == O.fib_encode_batch(x, cb, rot)
+        dref = O.fib_decode_batch(blob, cb, rot)
+        assert np.array_equal(prof.decode_batch_compact(blob).view(np.uint32), dref.view(np.uint32))
+        n = x.shape[0]
+        wire = torch.from_numpy(np.frombuffer(blob, np.uint8).copy()).cuda()
+        segs = D.segments([D.contiguous_segment(0, n, 64, 0)])
+        out = torch.empty(2 * n * 64, dtype=torch.bfloat16, device="cuda")
+        st = torch.empty(2, dtype=torch.int32, device="cuda")
+        prof.decode_segments(wire, segs, out, status=st, fanout=2, fanout_stride=n * 64)
+        torch.cuda.synchronize()
+        assert prof.status_error(st.cpu().numpy().view(np.uint32), segs) is None
+        want = torch.from_numpy(dref.reshape(-1)).to(torch.bfloat16)
+        for c in range(2):
+            assert torch.equal(out[c * n * 64:(c + 1) * n * 64].cpu().view(torch.int16), want.view(torch.int16))
+    finally:
+        prof.close()
+    # the seed-42 profile itself decodes on the matrix cores
+    assert ctx.fib_profile(64, 4, 32, SEED).fib_decode_path() == "matrix"
 
 
 def test_fib_errors(ctx):
@@ -206,8 +265,7 @@ def test_fib_encode_near_ties_take_exact_path(ctx):
     approximate argmin cannot decide them, the exact path must, and the bytes
     must still equal the reference's."""
     ad = FibQuantAdapter(64, 4, 32, 2048, 4, 8)
-    prof = ad.build_quantizer(SEED)
-    cb, rot = prof.constants()
+    cb, rot = O.fib_constants(SEED)
     cb = cb.reshape(32, 4).astype(np.float64)
     rot = rot.reshape(64, 64)
     rng = np.random.RandomState(17)

@@ -39,7 +39,7 @@ def _role_rows(flat, shape, layer, role):
 def _codecs(ctx):
     tur = ctx.turbo_profile(64, 4, 32, SEED)
     fib = ctx.fib_profile(64, 4, 32, SEED)
-    cb, rot = fib.constants()
+    cb, rot = O.fib_constants(SEED)
     return [
         (DeviceKvCodec(tur, "turbo_8bit_batched"), lambda x: O.turbo_encode_batch(x, SEED),
          lambda b: O.turbo_decode_batch(b, 64, SEED)),
@@ -97,7 +97,7 @@ def test_vector_codec_blocks_are_records(ctx):
     x = _tensors(9, KvTensorShape.gqa(1, 1, 1, 5, 64, KvLayout.layers_heads_tokens_dim(), DType.F32))[:64]
     tur = ctx.turbo_profile(64, 4, 32, SEED)
     fib = ctx.fib_profile(64, 4, 32, SEED)
-    cb, rot = fib.constants()
+    cb, rot = O.fib_constants(SEED)
     tc, fc = DeviceKvCodec(tur, "turbo_8bit"), DeviceKvCodec(fib, "fib_k4_n32")
     tb, fb = tc.encode_block(x), fc.encode_block(x)
     assert tb == O.turbo_encode_tqw1(x[None], SEED)[0]

@@ -34,7 +34,7 @@ def test_two_tier_small_bit_exact(ctx, lossy):
     plan.decode(bufs)
     torch.cuda.synchronize()
     plan.check(bufs)
-    cb, rot = plan.fib.constants()
+    cb, rot = O.fib_constants(SEED)
     cb = cb.reshape(32, 4)
     rot = rot.reshape(dim, dim)
     pool_out = bufs["pool_out"].cpu().numpy()
@@ -76,7 +76,7 @@ def _patched_cache(plan, corpus, layers, heads, dim, prefix, agents, lossy):
     """Oracle decodes placed like patch_cache_with_multi_agent_kv
     (proveKV/scripts/ppl_validate_multi_agent.py:226-272): [layer][K|V][H][T][D] f32."""
     T = prefix + sum(agents)
-    cb, rot = plan.fib.constants()
+    cb, rot = O.fib_constants(SEED)
     cb, rot = cb.reshape(32, 4), rot.reshape(dim, dim)
     ref = np.zeros((layers, 2, heads, T, dim), np.float32)
     owners = [(0, prefix, "fib")]
@@ -226,7 +226,7 @@ def test_bounded_fib_decode_matches_full_grid(ctx, max_workgroups, copies):
     err = plan.fib.status_error(stats[1], pseg)
     assert err is not None and err.segment == 2 and err.index == 1000
     # every other vector is the oracle's decode
-    cb, rot = plan.fib.constants()
+    cb, rot = O.fib_constants(SEED)
     want = O.fib_decode_batch(plan.blob(bufs, "pool", 0), cb.reshape(32, 4), rot.reshape(64, 64)).reshape(prefix, heads, dim)
     got = outs[1][0, 0, 0, :, :prefix, :].permute(1, 0, 2).numpy()
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

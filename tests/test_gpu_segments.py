@@ -43,7 +43,7 @@ def _positions(row, dim):
 def _codec(ctx, kind, dim, lossy):
     if kind == "fib":
         prof = ctx.fib_profile(dim, 4, 32, SEED)
-        cb, rot = prof.constants()
+        cb, rot = O.fib_constants(SEED)
         cb, rot = cb.reshape(32, 4), rot.reshape(dim, dim)
         return prof, L.RADII_F32, (lambda x: O.fib_encode_batch(x, cb, rot)), (lambda b: O.fib_decode_batch(b, cb, rot))
     prof = ctx.turbo_profile(dim, 4, 32, SEED)

@@ -204,6 +204,35 @@ def test_turbo_decode_trailing_bytes_checked_after_vectors():
         O.turbo_decode_batch(bytes(blob[:-1]), 64, SEED)
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+def test_qjl_sum_order_fixture(dim):
+    """tests/golden/qjl_sum_order.npz: for each vector the oracle's sign bit of
+    the stored projection is the sign of the reference's sequential sum, and
+    summing the lane groups in rotated order gives the other sign -- so a
+    kernel that hands partial sums on in any other order fails on them."""
+    import os
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "qjl_sum_order.npz"))
+    x, proj, refdot = f[f"x{dim}"], f[f"proj{dim}"], f[f"refdot{dim}"]
+    signs, G = O.turbo_constants(dim, 32, SEED)
+    plen = O.turbo_payload_len(dim)
+    blob = O.turbo_encode_batch(x, SEED, signs=signs, G=G)
+    rec = O.turbo_decode_batch(blob, dim, SEED, signs=signs)
+    groups = 2 if dim == 64 else 4
+    for i in range(len(x)):
+        j = int(proj[i])
+        p = (G[j] * (x[i] - rec[i]).astype(np.float32)).astype(np.float32)
+        seq = np.float32(0)
+        for v in p:
+            seq = np.float32(seq + v)
+        w = dim // groups
+        alt = np.float32(0)
+        for v in np.concatenate([p[w:], p[:w]]):
+            alt = np.float32(alt + v)
+        assert seq == refdot[i] and (seq >= 0) != (alt >= 0)
+        sb = blob[38 + i * plen + plen - 4:38 + (i + 1) * plen]
+        assert bool((sb[j // 8] >> (j % 8)) & 1) == bool(seq >= 0)
+
+
 def test_turbo_lossy_equal_radii_span_clamp():
     # BlockLogU8: equal radii -> span clamps to EPSILON on encode, 0 on decode
     x = np.zeros((4, 64), np.float32)
