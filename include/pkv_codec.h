@@ -358,6 +358,27 @@ int pkv_turbo_score_batch(pkv_ctx* ctx, const pkv_profile* prof, const uint8_t* 
                           const float* queries, uint32_t nq, float post_scale, float* scores, uint64_t scores_cap,
                           uint64_t* n_out, pkv_error* err);
 
+/* ---------------------------------------------------------------- diagnostics
+ * Validation hook, no counterpart in the reference: the encode kernels take
+ * their fast decisions from matrix-core approximations and keep them only
+ * under a proven error bound (the rest is redone in the reference's exact
+ * arithmetic).  This encodes n contiguous f32 device vectors into one blob
+ * (the bytes pkv_encode_segments writes) and also writes the approximations
+ * and bounds, so tests can measure how far inside the bound real data stays:
+ *   fib:   d_diag[(v * 16 + b) * 32 + w] = approximate key of codeword w for
+ *          block b of vector v, f32(|c_w|^2 + 1.25 - 2 c_w . rho'); a block's
+ *          approximate argmin stands only when its two smallest keys (low 5
+ *          bits replaced by the codeword index) differ by more than
+ *          *threshold; n * 512 floats;
+ *   turbo: (QJL profiles with polar bits <= 4, head_dim 64 / 128)
+ *          d_diag[(v * proj + j) * 2 + 0] = matrix-core dot of projection j,
+ *          [.. + 1] = its acceptance bound: the sign stands only when
+ *          |dot| > bound; n * proj * 2 floats; *threshold = 0.
+ * d_status: 2 words as in pkv_encode_segments (may be NULL). */
+int pkv_encode_diagnostics(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, const float* d_in,
+                           uint64_t n, uint8_t* d_wire, uint64_t wire_bytes, float* d_diag,
+                           uint64_t diag_elems, float* threshold, uint32_t* d_status, void* stream);
+
 /* ---------------------------------------------------------------- host math
  * Host builds of the exact scalar routines the kernels use (test hooks):
  * angle bins of (a[i], b[i]) for pbits, and logf / expf over arrays. */

@@ -50,7 +50,8 @@ EXPORTS = (
     "pkv_encode_batch_compact",
     "pkv_decode_batch_compact", "pkv_parse_header", "pkv_record_len", "pkv_encode_vectors", "pkv_decode_vectors",
     "pkv_constants_cache_stats", "pkv_constants_cache_clear", "pkv_prepared_len", "pkv_turbo_prepare_queries",
-    "pkv_turbo_score_segments", "pkv_score_status", "pkv_turbo_score_batch", "pkv_host_angle_bins", "pkv_host_logf",
+    "pkv_turbo_score_segments", "pkv_score_status", "pkv_turbo_score_batch", "pkv_encode_diagnostics",
+    "pkv_host_angle_bins", "pkv_host_logf",
     "pkv_host_expf",
 )
 
@@ -138,6 +139,7 @@ def _declare(L):
                                      I32),
         "pkv_score_status": ([P, U32, P], I32),
         "pkv_turbo_score_batch": ([P, P, P, U64, P, U32, C.c_float, P, U64, P, P], I32),
+        "pkv_encode_diagnostics": ([P, P, I32, P, U64, P, U64, P, U64, P, P, P], I32),
         "pkv_host_angle_bins": ([P, P, U64, U32, P], None),
         "pkv_host_logf": ([P, U64, P], None),
         "pkv_host_expf": ([P, U64, P], None),

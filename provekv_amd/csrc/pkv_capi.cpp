@@ -369,7 +369,7 @@ FibDev fib_dev(const pkv_profile* p) {
 int launch_segments(const pkv_profile* prof, int radii, bool encode, int dtype, const void* d_f32,
                     const uint8_t* d_wire, const SegDev* dsegs, const uint32_t* dtiles, uint32_t nseg,
                     uint32_t nblocks, uint32_t* status, bool per_vector, uint32_t fanout, uint64_t fanout_stride,
-                    uint32_t grid_cap, hipStream_t stream) {
+                    uint32_t grid_cap, hipStream_t stream, float* diag = nullptr) {
     int e = launch_fill_u32(status, STATUS_NONE, 2ull * nseg, stream);
     if (e) return e;
     LaunchCommon lc;
@@ -385,6 +385,7 @@ int launch_segments(const pkv_profile* prof, int radii, bool encode, int dtype, 
     lc.fanout = fanout;
     lc.fanout_stride = fanout_stride;
     lc.grid_cap = grid_cap;
+    lc.diag = diag;
     if (prof->kind == PKV_CODEC_TURBO)
         return encode ? launch_turbo_encode(lc, turbo_dev(prof), d_f32, const_cast<uint8_t*>(d_wire), nblocks, stream)
                       : launch_turbo_decode(lc, turbo_dev(prof), d_wire, const_cast<void*>(d_f32), nblocks, stream);
@@ -397,7 +398,7 @@ int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool e
                         const void* d_f32, uint64_t f32_elems, const pkv_seg* segs, uint32_t nseg,
                         const uint8_t* d_wire, uint64_t wire_bytes, uint32_t* d_status, hipStream_t stream,
                         bool per_vector = false, uint32_t fanout = 1, uint64_t fanout_stride = 0,
-                        uint32_t grid_cap = 0) {
+                        uint32_t grid_cap = 0, float* diag = nullptr) {
     if (!ctx || !prof) return PKV_ERR_INVALID_ARG;
     if (prof->kind == PKV_CODEC_TURBO && radii != PKV_RADII_F32 && radii != PKV_RADII_LOG_U8)
         return PKV_ERR_INVALID_ARG;
@@ -417,7 +418,7 @@ int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool e
     if (rc) return rc;
     uint32_t* status = d_status ? d_status : dstat;
     const int e = launch_segments(prof, radii, encode, dtype, d_f32, d_wire, dsegs, dtiles, nseg, tiles[nseg], status,
-                                  per_vector, fanout, fanout_stride, grid_cap, stream);
+                                  per_vector, fanout, fanout_stride, grid_cap, stream, diag);
     int rc2 = finish_slot(sl, stream);
     if (e) return hip_status(static_cast<hipError_t>(e));
     return rc2;
@@ -1048,6 +1049,28 @@ int pkv_decode_segments_noalloc(pkv_ctx* ctx, const pkv_profile* prof, int radii
                                   reinterpret_cast<const uint32_t*>(base + kNaTileOff), nseg, tiles[nseg], status,
                                   false, fanout, fanout_stride, 0, st);
     return e ? hip_status(static_cast<hipError_t>(e)) : PKV_OK;
+}
+
+int pkv_encode_diagnostics(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, const float* d_in, uint64_t n,
+                           uint8_t* d_wire, uint64_t wire_bytes, float* d_diag, uint64_t diag_elems, float* threshold,
+                           uint32_t* d_status, void* stream) {
+    if (!ctx || !prof || !d_diag || n == 0 || n > MAX_SEG_VECTORS) return PKV_ERR_INVALID_ARG;
+    uint64_t need;
+    if (prof->kind == PKV_CODEC_FIB) {
+        need = n * 16u * 32u;
+        if (threshold) *threshold = prof->thr;
+    } else {
+        if (!prof->mode || !prof->d_qa || prof->pbits > 4) return PKV_ERR_UNSUPPORTED;   // no matrix-core path
+        need = n * prof->proj * 2u;
+        if (threshold) *threshold = 0.0f;
+    }
+    if (diag_elems < need) return PKV_ERR_CAPACITY;
+    if (reinterpret_cast<uintptr_t>(d_diag) % 4) return PKV_ERR_INVALID_ARG;
+    const pkv_seg seg{0, 0, prof->dim, 0, static_cast<uint32_t>(n), static_cast<uint32_t>(n)};
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    return run_segments_locked(ctx, prof, radii_codec, true, PKV_F32, d_in, n * prof->dim, &seg, 1, d_wire,
+                               wire_bytes, d_status, static_cast<hipStream_t>(stream), false, 1, 0, 0, d_diag);
 }
 
 int pkv_parse_header(const pkv_profile* p, const uint8_t* b, uint64_t len, uint64_t* n_vectors, int* radii_codec) {

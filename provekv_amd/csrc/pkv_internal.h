@@ -99,6 +99,9 @@ struct LaunchCommon {
     uint64_t fanout_stride;       // ... this many elements apart
     uint32_t grid_cap = 0;        // at most this many workgroups, each walking tiles (0: one per tile);
                                   // d64 turbo decode and the fib MFMA decode
+    float* diag = nullptr;        // encode diagnostics (pkv_encode_diagnostics): the matrix-core values
+                                  // the kernel decided from, per vector of the (single) segment;
+                                  // non-null selects the kernels' diagnostic instantiations
 };
 
 // Up to 48 constant header bytes (TQW1 / FB1 record headers, TQB1 / FB2 blob

@@ -584,7 +584,9 @@ __device__ __forceinline__ void fwht_split(float (&v)[32], int h) {
     }
 }
 
-template <int PB>
+// DIAG: also write every projection's matrix-core dot and acceptance bound to
+// lc.diag[((vector * proj) + j) * 2 + {0, 1}].
+template <int PB, bool DIAG>
 __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
     LaunchCommon lc, const void* __restrict__ in, uint8_t* __restrict__ wire, const float* __restrict__ signs,
     const float* __restrict__ qjl, const float* __restrict__ cs_tab, const float* __restrict__ qa,
@@ -821,6 +823,13 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
                 const float bnd = qb_p[q * 64 + lane] * rn;
                 sb |= (acc[q] >= 0.0f ? 1u : 0u) << j;
                 un |= (__builtin_fabsf(acc[q]) > bnd ? 0u : 1u) << j;
+                if constexpr (DIAG) {
+                    if (active) {
+                        float* dv = lc.diag + (static_cast<uint64_t>(t0 + static_cast<uint32_t>(n)) * proj + 32u * p + j) * 2u;
+                        dv[0] = acc[q];
+                        dv[1] = bnd;
+                    }
+                }
             }
             sbits[p] = sb | partner(sb, h);
             unc[p] = un | partner(un, h);
@@ -955,7 +964,7 @@ __device__ __forceinline__ uint32_t or_quarters(uint32_t x, int q) {
     return x | partner(x, q >> 1);
 }
 
-template <int PB>
+template <int PB, bool DIAG>
 __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
     LaunchCommon lc, const void* __restrict__ in, uint8_t* __restrict__ wire, const float* __restrict__ signs,
     const float* __restrict__ qjl, const float* __restrict__ cs_tab, const float* __restrict__ qa,
@@ -1179,6 +1188,13 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
                 const float bnd = qb_p[rr * 64 + lane] * rn;
                 sbits[j >> 5] |= (acc[rr] >= 0.0f ? 1u : 0u) << (j & 31u);
                 unc[j >> 5] |= (__builtin_fabsf(acc[rr]) > bnd ? 0u : 1u) << (j & 31u);
+                if constexpr (DIAG) {
+                    if (active) {
+                        float* dv = lc.diag + (static_cast<uint64_t>(t0 + static_cast<uint32_t>(n)) * proj + j) * 2u;
+                        dv[0] = acc[rr];
+                        dv[1] = bnd;
+                    }
+                }
             }
         }
 #pragma unroll
@@ -2170,7 +2186,9 @@ __device__ __forceinline__ void fib_encode_rotate(FibTileRot& t, const float4 (&
 }
 
 // Phase 2: approximate argmin per block, status, redo queue, payload out.
-template <int DIM>
+// DIAG: also write every block's 32 approximate keys (before the index bits
+// replace their low 5 bits) to lc.diag[(vector * 16 + block) * 32 + w].
+template <int DIM, bool DIAG>
 __device__ __forceinline__ void fib_encode_score(const LaunchCommon& lc, const SegDev& seg, uint32_t sidx,
                                                  uint8_t* __restrict__ blob, uint32_t v0, const FibTileRot& t,
                                                  uint32_t* pay, const v4u& sa, float thr, uint32_t* q_count,
@@ -2196,6 +2214,17 @@ __device__ __forceinline__ void fib_encode_score(const LaunchCommon& lc, const S
         const v4u ba = {qa.x, qa.y, qa.x, 0x3C003C00u}, bb = {qb.x, qb.y, qb.x, 0x3C003C00u};
         const v16f d0 = mfma16(sa, ba, zero16);
         const v16f d1 = mfma16(sa, bb, zero16);
+        if constexpr (DIAG) {
+            if (active) {
+                float* dv = lc.diag + static_cast<uint64_t>(v0 + static_cast<uint32_t>(n)) * 512u;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int w = 8 * (r >> 2) + 4 * h + (r & 3);
+                    dv[32 * i + w] = d0[r];
+                    dv[32 * (i + 8) + w] = d1[r];
+                }
+            }
+        }
         // keys of accumulator rows w = 8(r/4) + 4h + r%4; two smallest per
         // half-wave, two keys per step: m2 = min(m2, med3(m1, k, k')),
         // m1 = min3(m1, k, k') (m1 <= m2 throughout)
@@ -2417,7 +2446,7 @@ __device__ void fib_fixup_wave(const LaunchCommon& lc, const void* __restrict__ 
 
 constexpr int FIB_PAY_WORDS = 64 * 3 + 4;   // per wave: both 32-vector sub-tiles
 
-template <int DIM>
+template <int DIM, bool DIAG>
 __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const void* __restrict__ in,
                                                           uint8_t* __restrict__ wire, const uint32_t* __restrict__ mf,
                                                           float thr, const double* __restrict__ rot_t,
@@ -2467,13 +2496,13 @@ __global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const
         fib_encode_rotate(t, xa, rot_lds, lane);
         __builtin_amdgcn_sched_barrier(0);
         if (v0 + 32 < seg.n_vectors) load_half_row(xb, in, bf16, seg, min(v0 + 32 + n, last), h);
-        fib_encode_score<DIM>(lc, seg, sidx, blob, v0, t, pay, sa, thr, &q_count, q_entries, q_nrm, tile_v0,
+        fib_encode_score<DIM, DIAG>(lc, seg, sidx, blob, v0, t, pay, sa, thr, &q_count, q_entries, q_nrm, tile_v0,
                               lane);
     }
     if (v0 + 32 < seg.n_vectors) {
         FibTileRot t;
         fib_encode_rotate(t, xb, rot_lds, lane);
-        fib_encode_score<DIM>(lc, seg, sidx, blob, v0 + 32, t, pay + 96, sa, thr, &q_count, q_entries, q_nrm,
+        fib_encode_score<DIM, DIAG>(lc, seg, sidx, blob, v0 + 32, t, pay + 96, sa, thr, &q_count, q_entries, q_nrm,
                               tile_v0, lane);
     }
     if (tile == 0 && threadIdx.x < 19)
@@ -2831,21 +2860,24 @@ int launch_turbo_encode(const LaunchCommon& lc, const TurboDev& td, const void* 
         if (nblocks > (1u << 30)) return hipErrorInvalidValue;   // 2 workgroups per tile
         const size_t vec_words = (lc.plen >> 2) + (lc.radii == PKV_RADII_F32 ? 0u : 32u);
         const size_t lds = static_cast<size_t>(WAVES) * (32 * vec_words + 4) * sizeof(uint32_t);
-        return td.pbits == 3
-                   ? launch_big_lds(turbo_encode_qjl_kernel<3>, 2 * nblocks, lds, st, lc, in, wire, td.signs, td.qjl,
-                                    td.cs, td.qa, td.qb, td.seed, td.pbits, td.proj)
-                   : launch_big_lds(turbo_encode_qjl_kernel<0>, 2 * nblocks, lds, st, lc, in, wire, td.signs, td.qjl,
-                                    td.cs, td.qa, td.qb, td.seed, td.pbits, td.proj);
+#define PKV_QJL64(PB, DG)                                                                                      \
+    launch_big_lds(turbo_encode_qjl_kernel<PB, DG>, 2 * nblocks, lds, st, lc, in, wire, td.signs, td.qjl, td.cs, \
+                   td.qa, td.qb, td.seed, td.pbits, td.proj)
+        if (lc.diag) return td.pbits == 3 ? PKV_QJL64(3, true) : PKV_QJL64(0, true);
+        return td.pbits == 3 ? PKV_QJL64(3, false) : PKV_QJL64(0, false);
+#undef PKV_QJL64
     }
     if (td.dim == 128 && td.mode && td.qa && td.pbits <= 4) {
         if (nblocks > (1u << 29)) return hipErrorInvalidValue;   // 4 workgroups per tile
         const size_t lds = static_cast<size_t>(WAVES) * (16 * (lc.plen >> 2) + 4) * sizeof(uint32_t);
-        return td.pbits == 3
-                   ? launch_big_lds(turbo_encode_qjl128_kernel<3>, 4 * nblocks, lds, st, lc, in, wire, td.signs,
-                                    td.qjl, td.cs, td.qa, td.qb, td.seed, td.pbits, td.proj)
-                   : launch_big_lds(turbo_encode_qjl128_kernel<0>, 4 * nblocks, lds, st, lc, in, wire, td.signs,
-                                    td.qjl, td.cs, td.qa, td.qb, td.seed, td.pbits, td.proj);
+#define PKV_QJL128(PB, DG)                                                                                      \
+    launch_big_lds(turbo_encode_qjl128_kernel<PB, DG>, 4 * nblocks, lds, st, lc, in, wire, td.signs, td.qjl,   \
+                   td.cs, td.qa, td.qb, td.seed, td.pbits, td.proj)
+        if (lc.diag) return td.pbits == 3 ? PKV_QJL128(3, true) : PKV_QJL128(0, true);
+        return td.pbits == 3 ? PKV_QJL128(3, false) : PKV_QJL128(0, false);
+#undef PKV_QJL128
     }
+    if (lc.diag) return hipErrorInvalidValue;   // diagnostics exist for the matrix-core paths only
     if (td.dim == 64)
         return td.pbits == 3
                    ? launch_big_lds(turbo_encode_kernel<64, 3>, nblocks, stage_bytes<64>(), st, lc, in, wire, td.signs,
@@ -2958,7 +2990,10 @@ int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, 
                       void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     constexpr size_t lds = (MF_SCA + WAVES * FIB_PAY_WORDS) * sizeof(uint32_t);
-    return launch_big_lds(fib_encode_kernel<64>, nblocks, lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot_t,
+    if (lc.diag)
+        return launch_big_lds(fib_encode_kernel<64, true>, nblocks, lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot_t,
+                              fd.codebook);
+    return launch_big_lds(fib_encode_kernel<64, false>, nblocks, lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot_t,
                           fd.codebook);
 }
 

@@ -243,6 +243,24 @@ class Profile:
                                             fanout, fanout_stride, st, _stream_ptr(stream))
         L.check(rc, "pkv_decode_segments_ex")
 
+    def encode_diagnostics(self, inp, wire, diag, radii: int = L.RADII_F32, status=None, stream=None) -> float:
+        """pkv_encode_diagnostics: encode the contiguous float32 device vectors
+        `inp` [n, dim] into one blob in `wire` and write the matrix-core values
+        the kernel decided from into float32 `diag` (fib: n x 16 x 32 keys;
+        turbo: n x proj x (dot, bound)).  Returns the fib key threshold (0 for
+        turbo)."""
+        torch = _torch()
+        if inp.dtype != torch.float32 or diag.dtype != torch.float32 or wire.dtype != torch.uint8:
+            raise TypeError("float32 input and diag, uint8 wire")
+        n = inp.numel() // self.dim
+        thr = C.c_float()
+        st = self._status_ptr(status, 1)
+        rc = L.lib().pkv_encode_diagnostics(self.ctx.ptr, self._ptr, radii, inp.data_ptr(), n, wire.data_ptr(),
+                                            wire.numel(), diag.data_ptr(), diag.numel(), C.byref(thr), st,
+                                            _stream_ptr(stream))
+        L.check(rc, "pkv_encode_diagnostics")
+        return float(thr.value)
+
     def status_error(self, status_host: np.ndarray, segs: np.ndarray | None = None):
         """Turn per-segment status words (2 per segment, host copy) into a
         PkvError (or None).  The fib batch path reports input-validation
