@@ -101,6 +101,8 @@ def _declare(L):
     L.ora_f16_to_f32.restype = C.c_float
     L.ora_nearest_codeword_k4.argtypes = [P, P, I32]
     L.ora_nearest_codeword_k4.restype = I32
+    L.ora_nearest_codeword_k4_avx2.argtypes = [P, P, I32]
+    L.ora_nearest_codeword_k4_avx2.restype = I32
     L.ora_nearest_codeword_scalar.argtypes = [P, P, I32, I32]
     L.ora_nearest_codeword_scalar.restype = I32
     L.ora_fib_encode_batch.argtypes = [U32, U32, U32, P, P, P, U64, P, U64, P, P]
@@ -331,6 +333,12 @@ def nearest_codeword_k4(s, cb) -> int:
     s = np.ascontiguousarray(s, dtype=np.float32)
     cb = np.ascontiguousarray(cb, dtype=np.float32)
     return int(lib().ora_nearest_codeword_k4(_p(s), _p(cb), cb.size // 4))
+
+
+def nearest_codeword_k4_avx2(s, cb) -> int:
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    cb = np.ascontiguousarray(cb, dtype=np.float32)
+    return int(lib().ora_nearest_codeword_k4_avx2(_p(s), _p(cb), cb.size // 4))
 
 
 def nearest_codeword_scalar(s, cb, k) -> int:

@@ -1102,8 +1102,55 @@ int ora_nearest_codeword_scalar(const float* s, const float* cb, int k, int n) {
     return best;
 }
 
+/* nearest_codeword_f32_avx2_k4 (simd_nearest.rs:44-92) with the same vector
+ * instructions: two codewords per _mm256_sub_ps / _mm256_mul_ps against the
+ * broadcast sample, each half summed by two _mm_hadd_ps, i.e. (q0 + q1) +
+ * (q2 + q3); strict < in codeword order; scalar sequential tail.  Results
+ * equal ora_nearest_codeword_k4 (the same IEEE operations); this is the CPU
+ * baseline's hot loop, as the reference runs it on an AVX2 host. */
+#if defined(__x86_64__)
+#include <immintrin.h>
+__attribute__((target("avx2,fma"))) int ora_nearest_codeword_k4_avx2(const float* s, const float* cb, int n) {
+    const __m256 sv = _mm256_setr_ps(s[0], s[1], s[2], s[3], s[0], s[1], s[2], s[3]);
+    int best = 0, i = 0;
+    float bd = INFINITY;
+    for (; i + 2 <= n; i += 2) {
+        const __m256 cw = _mm256_loadu_ps(cb + (size_t)i * 4);
+        const __m256 dl = _mm256_sub_ps(cw, sv);
+        const __m256 sq = _mm256_mul_ps(dl, dl);
+        __m128 lo = _mm256_castps256_ps128(sq), hi = _mm256_extractf128_ps(sq, 1);
+        lo = _mm_hadd_ps(lo, lo);
+        hi = _mm_hadd_ps(hi, hi);
+        const float d0 = _mm_cvtss_f32(_mm_hadd_ps(lo, lo)), d1 = _mm_cvtss_f32(_mm_hadd_ps(hi, hi));
+        if (d0 < bd) { bd = d0; best = i; }
+        if (d1 < bd) { bd = d1; best = i + 1; }
+    }
+    if (i < n) {
+        float dist = 0.0f;
+        for (int j = 0; j < 4; ++j) { float dl = s[j] - cb[(size_t)i * 4 + j]; dist += dl * dl; }
+        if (dist < bd) best = i;
+    }
+    return best;
+}
+static int have_avx2(void) {
+    static int cached = -1;   /* benign race: every thread stores the same value */
+    if (cached < 0) cached = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+    return cached;
+}
+#else
+int ora_nearest_codeword_k4_avx2(const float* s, const float* cb, int n) { return ora_nearest_codeword_k4(s, cb, n); }
+static int have_avx2(void) { return 0; }
+#endif
+
+/* nearest_codeword_f32 (simd_nearest.rs:13-21) on an AVX2 + FMA host: the
+ * AVX2 routine for k = 4 (its pairwise order also without AVX2 here, through
+ * the scalar restatement, so results never depend on the host running the
+ * oracle).  The reference itself, on a host without AVX2, would take the
+ * sequential sum of nearest_codeword_f32_scalar (simd_nearest.rs:24-38);
+ * this build, like the reference on every AVX2 server, uses the pairwise one. */
 static int nearest_dispatch(const float* s, const float* cb, int k, int n) {
-    return k == 4 ? ora_nearest_codeword_k4(s, cb, n) : ora_nearest_codeword_scalar(s, cb, k, n);
+    if (k == 4) return have_avx2() ? ora_nearest_codeword_k4_avx2(s, cb, n) : ora_nearest_codeword_k4(s, cb, n);
+    return ora_nearest_codeword_scalar(s, cb, k, n);
 }
 
 /* l2_norm (codec.rs:1049-1057) */

@@ -65,6 +65,21 @@ def test_avx2_order_matches_scalar_on_lcg_data_simd_nearest_rs():
             assert O.nearest_codeword_k4(s, cb) == O.nearest_codeword_scalar(s, cb, 4)
 
 
+def test_avx2_intrinsics_equal_pairwise_restatement():
+    """The oracle's AVX2 argmin (the instructions of simd_nearest.rs:44-92,
+    used by the CPU baseline) returns the pairwise scalar restatement's index
+    on random samples and on near-ties built on codeword bisectors."""
+    cb = O.fib_constants(SEED)[0]
+    rng = np.random.RandomState(11)
+    S = (rng.randn(20000, 4) * 0.2).astype(np.float32)
+    for i in range(4000):
+        a, b = rng.choice(32, 2, replace=False)
+        t = 0.5 + rng.choice([0.0, 1e-8, -1e-8, 1e-7])
+        S[i] = (t * cb[a] + (1 - t) * cb[b]).astype(np.float32)
+    for s in S:
+        assert O.nearest_codeword_k4_avx2(s, cb) == O.nearest_codeword_k4(s, cb)
+
+
 def test_argmin_brute_force_small():
     rng = np.random.RandomState(3)
     for _ in range(2000):
