@@ -112,6 +112,7 @@ struct pkv_profile {
     float* d_cb = nullptr;
     double* d_cb64 = nullptr;
     double* d_rot_t = nullptr;
+    double* d_rot64 = nullptr;   // row-major f64 rotation (encode's exact redo)
     float* d_rot32t = nullptr;
     float* d_rot32 = nullptr;
     int mfma_decode = 0;
@@ -351,6 +352,7 @@ FibDev fib_dev(const pkv_profile* p) {
     f.codebook = p->d_cb;
     f.codebook64 = p->d_cb64;
     f.rot_t = p->d_rot_t;
+    f.rot64 = p->d_rot64;
     f.rot32t = p->d_rot32t;
     f.rot32 = p->d_rot32;
     f.mfma_decode = p->mfma_decode;
@@ -883,6 +885,7 @@ static int fib_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n
     if (!rc) rc = upload(&p->d_cb, p->codebook);
     if (!rc) rc = upload(&p->d_cb64, p->cb64);
     if (!rc) rc = upload(&p->d_rot_t, p->rot_t);
+    if (!rc) rc = upload(&p->d_rot64, p->rot);
     if (!rc) rc = upload(&p->d_rot32t, p->rot32t);
     if (!rc) rc = upload(&p->d_mf, p->mf);
     if (!rc) rc = upload(&p->d_rot32, p->rot32);
@@ -938,7 +941,8 @@ void pkv_profile_destroy(pkv_profile* p) {
     (void)hipDeviceSynchronize();
     for (void* d : {static_cast<void*>(p->d_signs), static_cast<void*>(p->d_qjl), static_cast<void*>(p->d_cs),
                     static_cast<void*>(p->d_qa), static_cast<void*>(p->d_qb),
-                    static_cast<void*>(p->d_cb), static_cast<void*>(p->d_rot_t), static_cast<void*>(p->d_rot32t),
+                    static_cast<void*>(p->d_cb), static_cast<void*>(p->d_rot_t), static_cast<void*>(p->d_rot64),
+                    static_cast<void*>(p->d_rot32t),
                     static_cast<void*>(p->d_mf), static_cast<void*>(p->d_rot32), static_cast<void*>(p->d_cb64)})
         if (d) (void)hipFree(d);
     delete p;

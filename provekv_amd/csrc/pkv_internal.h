@@ -76,7 +76,8 @@ constexpr uint32_t fib_mfma_row(uint32_t t, uint32_t m) {
 struct FibDev {
     const float* codebook;  // n * k
     const double* codebook64;  // n * k, the same values widened (per-vector f64 decode)
-    const double* rot_t;    // dim * dim, transposed: [col][row] (exact encode fixup)
+    const double* rot_t;    // dim * dim, transposed: [col][row] (per-vector f64 decode)
+    const double* rot64;    // dim * dim, row-major (the encode's exact redo)
     const float* rot32t;    // dim * dim, f32(rot) transposed: [col][row] (VALU decode)
     const float* rot32;     // dim * dim, f32(rot) row-major (MFMA decode)
     int mfma_decode;        // matrix-core products verified bit-exact for this profile

@@ -23,6 +23,10 @@
 // rotation of decode_batch_fast (rotation.rs:136-149).  Host-libm
 // transcendentals come from pkv_math.h.
 #include <hip/hip_runtime.h>
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "pkv_internal.h"
 #include "pkv_math.h"
@@ -2185,15 +2189,17 @@ __device__ __forceinline__ void fib_encode_rotate(FibTileRot& t, const float4 (&
     t.acc1 = acc1;
 }
 
-// Phase 2: approximate argmin per block, status, redo queue, payload out.
+// Phase 2 of a 32-vector tile: approximate argmin per block, norm status and
+// the payload words (into LDS).  Returns the blocks of this lane's vector that
+// the exact redo must decide -- every block under FibQuantizer::encode
+// semantics (segments of fewer than 4 vectors, per-vector calls) -- or 0 for
+// an inactive lane or a rejected input.
 // DIAG: also write every block's 32 approximate keys (before the index bits
 // replace their low 5 bits) to lc.diag[(vector * 16 + block) * 32 + w].
 template <int DIM, bool DIAG>
-__device__ __forceinline__ void fib_encode_score(const LaunchCommon& lc, const SegDev& seg, uint32_t sidx,
-                                                 uint8_t* __restrict__ blob, uint32_t v0, const FibTileRot& t,
-                                                 uint32_t* pay, const v4u& sa, float thr, uint32_t* q_count,
-                                                 uint32_t* q_entries, double* q_nrm, uint32_t tile_v0, int lane) {
-    constexpr uint32_t PLEN = 12;   // f16 norm + 16 x 5 bits
+__device__ __forceinline__ uint32_t fib_encode_score(const LaunchCommon& lc, const SegDev& seg, uint32_t sidx,
+                                                     uint32_t v0, const FibTileRot& t, uint32_t* pay, const v4u& sa,
+                                                     float thr, int lane) {
     const int h = lane >> 5, n = lane & 31;
     const uint32_t nv = min(32u, seg.n_vectors - v0);
     const bool active = static_cast<uint32_t>(n) < nv;   // other lanes repeat the last vector
@@ -2251,6 +2257,10 @@ __device__ __forceinline__ void fib_encode_score(const LaunchCommon& lc, const S
         if (!(u2f(kb2 & ~31u) - u2f(kb1 & ~31u) > thr)) redo |= 1u << (i + 8);
         ia |= static_cast<uint64_t>(ka1 & 31u) << (5 * i);
         ib |= static_cast<uint64_t>(kb1 & 31u) << (5 * i);
+        // materialise this pair's decisions now: the optimiser would otherwise
+        // sink every pair's tests and index packing past the loop and keep all
+        // eight pairs' candidate keys live at once
+        asm volatile("" : "+v"(redo), "+v"(ia), "+v"(ib));
         __builtin_amdgcn_sched_barrier(0);   // keep one block pair's results live at a time
     }
     const uint64_t ilo = ia | (ib << 40);
@@ -2267,258 +2277,297 @@ __device__ __forceinline__ void fib_encode_score(const LaunchCommon& lc, const S
         else if (zero) status_fail(lc.status, sidx, 0, vi, KIND_ZERO_NORM);
         else if (!h_ok) status_fail(lc.status, sidx, 1, vi, KIND_NORM16);
     }
-    const bool queue = owner && finite_all && !zero && (small || redo != 0);
-    const uint64_t qmask = __ballot(queue);
-    if (qmask) {   // workgroup-local queue: an LDS counter, no device atomics
-        uint32_t base = 0;
-        if (lane == 0) base = atomicAdd(q_count, static_cast<uint32_t>(__popcll(qmask)));
-        base = __shfl(base, 0);
-        if (queue) {
-            const uint32_t slot = base + static_cast<uint32_t>(__popcll(qmask & ((1ull << lane) - 1ull)));
-            q_entries[slot] = (vi - tile_v0) | (small ? 0xFFFFu : redo) << 8;
-            q_nrm[slot] = nrm;
-        }
-    }
     // payload [f16 norm][16 x 5-bit indices] = 12 bytes, kept in LDS: the
-    // exact redo patches it there and the wave's 64 payloads then leave as
+    // exact redo patches it there and the wave's 32 payloads then leave as
     // one byte range
     if (owner) {
         pay[3 * n + 0] = static_cast<uint32_t>(h16) | (iw[0] << 16);
         pay[3 * n + 1] = (iw[0] >> 16) | (iw[1] << 16);
         pay[3 * n + 2] = (iw[1] >> 16) | (iw[2] << 16);
     }
-    (void)blob;
-    (void)nv;
+    return (active && finite_all && !zero) ? (small ? 0xFFFFu : redo) : 0u;
 }
 
-// Exact redo of the queued (vector, block) decisions of fib_encode_kernel,
-// run by the encoding workgroup itself once every wave has queued.  The
-// queue is cut into groups of up to 16 entries, a short queue spread over
-// all four waves (wave w takes groups w, w + 4, ...).  4 lanes per vector
-// load it; its sequential f64 norm comes from the queue (fib_encode_rotate
-// computed it in the reference's order) and the 4 lanes form
-// x_hat = f32(x / norm) (segments of fewer than 4 vectors keep x / norm in
-// f64, codec.rs:481 vs 608); then 16 undecided blocks at a time get one lane
-// per rho row -- the sequential f64 dot of row 4b + t of Pi with x_hat
-// (rotation.rs:107-113), read from Pi^T so that each step's loads of the
-// wave share one 512-byte row -- and a quarter of the codewords per lane in
-// the AVX2 distance order with strict < (simd_nearest.rs:44-104); the
-// entry's owner lane patches the 5-bit fields of the payload in LDS
-// (pay_of(local vector) -> its 3 payload words).
-struct FibFixupLds {
-    float x[WAVES][16][64 + 4];   // x, then x_hat (segments of >= 4 vectors); padded rows
-    double xh[WAVES][64];         // f64 x / norm of one entry (segments of < 4 vectors)
-    double nrm[WAVES][16];
-    float part[WAVES][16][4][2];
-    float rho[WAVES][16][4];
-    uint32_t mask[WAVES][16];
-    uint8_t res[WAVES][16][16];
+// True when every value within err of v rounds to the same f32 as v: no f32
+// rounding boundary (the midpoint of two adjacent f32 values, ties included)
+// lies within err of v.  v finite.
+__device__ __forceinline__ bool f32_rounding_stable(double v, double err) {
+    const double a = __builtin_fabs(v);
+    const float y = static_cast<float>(a);   // nearest, ties to even
+    const uint32_t b = f2u(y);
+    if (b == 0u) return a + err < 0x1p-150;   // rounds to zero: below half the smallest subnormal
+    const double yd = static_cast<double>(y);
+    // y and its neighbours are f32: their sums are exact in f64, and so are the halves
+    const double m_hi = (yd + static_cast<double>(u2f(b + 1u))) * 0.5;
+    const double m_lo = (yd + static_cast<double>(u2f(b - 1u))) * 0.5;
+    return m_hi - a > err && a - m_lo > err;
+}
+
+constexpr uint32_t FIB_UNIT = 32;                          // vectors per wave iteration (one MFMA tile)
+constexpr uint32_t FIB_UNITS_PER_TILE = TILE / FIB_UNIT;   // a segment tile of 256 vectors is 8 units
+constexpr uint32_t FIB_RING = 4;                           // units a wave holds in LDS before its redo flush
+constexpr uint32_t FIB_QCAP = 64;                          // queued vectors per wave (a flush comes first)
+constexpr int FIB_PAY_WORDS = 32 * 3 + 4;                  // one unit's payloads + lds_to_global padding
+
+struct FibRedoLds {
+    double xh[4][64];           // x_hat of the vector of each pair of a pass
+    double nrm[FIB_QCAP];       // |x| of each queued vector
+    uint64_t off[FIB_QCAP];     // its input element offset
+    uint32_t ent[FIB_QCAP];     // payload word in the ring | per-vector semantics << 15 | blocks << 16
+    uint64_t blob[FIB_RING];    // ring slot -> blob byte offset in the wire,
+    uint32_t v0[FIB_RING];      //   first vector,
+    uint32_t nv[FIB_RING];      //   vectors of the unit,
+    uint32_t nvec[FIB_RING];    //   vectors of the segment
 };
 
-template <int DIM, typename PayOf>
-__device__ void fib_fixup_wave(const LaunchCommon& lc, const void* __restrict__ in, const double* __restrict__ rot_t,
-                               const float* __restrict__ cb, const SegDev& seg, uint32_t tile_v0,
-                               const uint32_t* ents, const double* ent_nrm, uint32_t count, FibFixupLds& f,
-                               PayOf pay_of, int wave, int lane) {
-    static_assert(DIM == 64, "four lanes of 16 elements per vector");
-    constexpr int G = 16;
-    const int e = lane >> 2, t = lane & 3;
-    const bool small = seg.n_vectors < 4 || lc.per_vector != 0;
-    const uint32_t gsz = min(static_cast<uint32_t>(G), max(1u, (count + WAVES - 1) / WAVES));
-    for (uint32_t g0 = gsz * static_cast<uint32_t>(wave); g0 < count; g0 += gsz * WAVES) {
-        const uint32_t ne = min(gsz, count - g0);
-        const bool has = static_cast<uint32_t>(e) < ne;
-        uint32_t li = 0, mask = 0;
-        if (has) {
-            const uint32_t ent = ents[g0 + e];
-            li = ent & 0xFFu;
-            mask = ent >> 8;
-            const uint64_t off = vec_elem_offset(seg, tile_v0 + li) + 16u * static_cast<uint32_t>(t);
-            float4* dst = reinterpret_cast<float4*>(&f.x[wave][e][16 * t]);
-            if (!lc.in_bf16) {
-                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(in) + off);
-                const float4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
-                dst[0] = v0; dst[1] = v1; dst[2] = v2; dst[3] = v3;
-            } else {
-                const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(in) + off);
-                const uint4 w0 = src[0], w1 = src[1];
-                const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    dst[k] = make_float4(u2f(w[2 * k] << 16), u2f(w[2 * k] & 0xffff0000u), u2f(w[2 * k + 1] << 16),
-                                         u2f(w[2 * k + 1] & 0xffff0000u));
-            }
-            if (t == 0) {
-                f.mask[wave][e] = mask;
-                f.nrm[wave][e] = ent_nrm[g0 + e];
+// Exact decisions for the queued (vector, blocks) entries of one wave,
+// ent[0 .. nq): every undecided block of up to FIB_RING units at once, by the
+// reference's exact path -- x_hat = f32(x / |x|) (codec.rs:608; f64 x / |x|
+// under FibQuantizer::encode semantics, codec.rs:481), rho_r = f32(sequential
+// f64 sum of f64 products over row 4b + r of Pi) (rotation.rs:107-113), the
+// AVX2 argmin over the 32 codewords (simd_nearest.rs:44-104) -- four
+// (vector, block) pairs per pass, 16 lanes each: lane (r, k) = ((lane % 16) /
+// 4, lane % 4) sums row 4b + r over columns 16k .. 16k + 15.
+//
+// Both roundings are taken from faster forms that provably round the same:
+//  * x_hat: q = x * fl64(1 / |x|) is within 2^-50 |q| of fl64(x / |x|)
+//    (three roundings of at most 2^-53 relative and the reciprocal's
+//    2^-52), so if no f32 rounding boundary lies within that distance of q,
+//    f32(q) = f32(fl64(x / |x|)); otherwise the division is done.
+//  * rho_r: four FMA partial sums of 16 terms, then two adds, are within
+//    (gamma_19) A of the exact sum and the reference's sequential sum within
+//    (gamma_64) A, A = sum |Pi_rc x_hat_c| <= |Pi_r| |x_hat| < 1.01, so the
+//    two differ by less than 96 * 2^-53; if no f32 rounding boundary lies
+//    within 2^-46 of the partial-sum result, f32 of it is the reference's
+//    rho_r; otherwise the row is summed in the reference's order.
+template <int DIM>
+__device__ void fib_redo_flush(const LaunchCommon& lc, const void* __restrict__ in, const double* __restrict__ rot64,
+                               const float* __restrict__ cb, uint32_t* ring, FibRedoLds& R, uint32_t nq, int lane) {
+    static_assert(DIM == 64, "16 lanes of 4 rows x 4 quarters per 4-dimensional block");
+    uint32_t total = 0;
+    for (uint32_t j = 0; j < nq; ++j) total += static_cast<uint32_t>(__popc(R.ent[j] >> 16));
+    const uint32_t p = static_cast<uint32_t>(lane) >> 4, g = static_cast<uint32_t>(lane) & 15u;
+    const uint32_t r = g >> 2, k = g & 3u;
+    const bool bf16 = lc.in_bf16 != 0;
+    for (uint32_t base = 0; base < total; base += 4) {   // every lane runs every pass (cross-lane reads)
+        const uint32_t pi = base + p;
+        const bool valid = pi < total;
+        uint32_t e = 0, b = 0;   // pair pi -> (entry, block); lanes past the end keep entry 0, block 0
+        {
+            uint32_t acc = 0;
+            for (uint32_t j = 0; j < nq; ++j) {
+                const uint32_t m = R.ent[j] >> 16, c = static_cast<uint32_t>(__popc(m));
+                if (valid && pi >= acc && pi < acc + c) {
+                    uint32_t mm = m;
+                    for (uint32_t t = pi - acc; t > 0; --t) mm &= mm - 1u;
+                    e = j;
+                    b = static_cast<uint32_t>(__ffs(mm) - 1);
+                }
+                acc += c;
             }
         }
-        wave_sync();
-        if (has && !small) {
-            const double nrm = f.nrm[wave][e];
-#pragma unroll
-            for (int c = 16 * t; c < 16 * t + 16; ++c)
-                f.x[wave][e][c] = static_cast<float>(static_cast<double>(f.x[wave][e][c]) / nrm);
+        const uint32_t ent = R.ent[e];
+        const bool small = (ent >> 15) & 1u;
+        const double nv = R.nrm[e];
+        // every load of the pass goes out first: x, the row's 16 values, two codewords
+        const uint64_t off = R.off[e] + 4u * g;
+        float xv[4];
+        if (!bf16) {
+            const float4 q4 = *reinterpret_cast<const float4*>(static_cast<const float*>(in) + off);
+            xv[0] = q4.x; xv[1] = q4.y; xv[2] = q4.z; xv[3] = q4.w;
+        } else {
+            const uint2 w2 = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(in) + off);
+            xv[0] = u2f(w2.x << 16); xv[1] = u2f(w2.x & 0xffff0000u);
+            xv[2] = u2f(w2.y << 16); xv[3] = u2f(w2.y & 0xffff0000u);
         }
-        wave_sync();
-        uint32_t total = 0;
-        for (uint32_t j = 0; j < ne; ++j) total += __popc(f.mask[wave][j]);
-        for (uint32_t p0 = 0; p0 < total; p0 += G) {
-            if (small) {   // every entry queues all 16 blocks, so this pass is entry p0 / 16: its f64 x_hat once
-                const uint32_t pe0 = p0 / G;
-                f.xh[wave][lane] = static_cast<double>(f.x[wave][pe0][lane]) / f.nrm[wave][pe0];
-                wave_sync();
-            }
-            const uint32_t qi = p0 + static_cast<uint32_t>(e);
-            int pe = -1, pb = 0;
-            if (small) {   // entry qi / 16, block qi % 16
-                if (qi < total) {
-                    pe = static_cast<int>(qi >> 4);
-                    pb = static_cast<int>(qi & 15u);
-                }
-            } else if (qi < total) {
-                uint32_t acc = 0;
-                for (uint32_t j = 0; j < ne; ++j) {
-                    uint32_t m = f.mask[wave][j];
-                    const uint32_t c = __popc(m);
-                    if (qi < acc + c) {
-                        for (uint32_t k = qi - acc; k > 0; --k) m &= m - 1u;
-                        pe = static_cast<int>(j);
-                        pb = __ffs(m) - 1;
-                        break;
-                    }
-                    acc += c;
-                }
-            }
-            if (pe >= 0) {   // Pi^T: at step c all lanes read within one 512 B row
-                const double* col = rot_t + (4 * pb + t);
-                const float* xr = f.x[wave][pe];
-                double a = 0.0;
-                if (!small) {
-#pragma unroll 16
-                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * static_cast<double>(xr[c]);
+        const double* prow = rot64 + static_cast<size_t>(4u * b + r) * DIM;
+        double pr[16];
+#pragma unroll
+        for (int c = 0; c < 16; c += 2) {
+            const double2 v2 = *reinterpret_cast<const double2*>(prow + 16 * k + c);
+            pr[c] = v2.x;
+            pr[c + 1] = v2.y;
+        }
+        const float4 cw0 = reinterpret_cast<const float4*>(cb)[2 * g], cw1 = reinterpret_cast<const float4*>(cb)[2 * g + 1];
+        {   // x_hat[4g .. 4g + 3] of the pair's vector
+            const double rinv = 1.0 / nv;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const double xd = static_cast<double>(xv[j]);
+                double xh;
+                if (small) {
+                    xh = xd / nv;
                 } else {
-                    const double* xh = f.xh[wave];
-#pragma unroll 16
-                    for (int c = 0; c < DIM; ++c) a = a + col[c * DIM] * xh[c];
+                    const double q = xd * rinv;
+                    float y = static_cast<float>(q);
+                    if (!f32_rounding_stable(q, __builtin_fabs(q) * 0x1p-50)) y = static_cast<float>(xd / nv);
+                    xh = static_cast<double>(y);
                 }
-                f.rho[wave][e][t] = static_cast<float>(a);
-            }
-            wave_sync();
-            if (pe >= 0) {
-                const float s0 = f.rho[wave][e][0], s1 = f.rho[wave][e][1];
-                const float s2 = f.rho[wave][e][2], s3 = f.rho[wave][e][3];
-                float bd = u2f(0x7f800000u);
-                uint32_t bw = 0;
-#pragma unroll
-                for (int w = 0; w < 8; ++w) {
-                    const float4 cw = reinterpret_cast<const float4*>(cb)[8 * t + w];
-                    const float e0 = cw.x - s0, e1 = cw.y - s1, e2 = cw.z - s2, e3 = cw.w - s3;
-                    const float dd = (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
-                    if (dd < bd) { bd = dd; bw = static_cast<uint32_t>(8 * t + w); }
-                }
-                f.part[wave][e][t][0] = bd;
-                f.part[wave][e][t][1] = u2f(bw);
-            }
-            wave_sync();
-            if (pe >= 0 && t == 0) {
-                float bd = f.part[wave][e][0][0];
-                uint32_t bw = f2u(f.part[wave][e][0][1]);
-                for (int u = 1; u < 4; ++u)
-                    if (f.part[wave][e][u][0] < bd) { bd = f.part[wave][e][u][0]; bw = f2u(f.part[wave][e][u][1]); }
-                f.res[wave][pe][pb] = static_cast<uint8_t>(bw);
-            }
-            wave_sync();
-        }
-        if (has && t == 0) {   // index b at payload bits 16 + 5b (after the f16 norm), LSB-first
-            uint32_t* pw = pay_of(li);
-            for (int b = 0; b < DIM / 4; ++b) {
-                if (!((mask >> b) & 1u)) continue;
-                const uint32_t w = f.res[wave][e][b];
-                const int bit = 16 + 5 * b, wd = bit >> 5, sh = bit & 31;
-                pw[wd] = (pw[wd] & ~(31u << sh)) | (w << sh);
-                if (sh > 27) pw[wd + 1] = (pw[wd + 1] & ~(31u >> (32 - sh))) | (w >> (32 - sh));
+                R.xh[p][4 * g + j] = xh;
             }
         }
         wave_sync();
+        double s = 0.0;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) s = __builtin_fma(pr[c], R.xh[p][16 * k + c], s);
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        float rho = static_cast<float>(s);
+        if (valid && !f32_rounding_stable(s, 0x1p-46)) {   // the reference's order: fl64 products, sequential fl64 sum
+            double a = 0.0;
+            for (int c = 0; c < DIM; ++c) {
+                const double prod = prow[c] * R.xh[p][c];
+                a = a + prod;
+            }
+            rho = static_cast<float>(a);
+        }
+        const int gb = 16 * static_cast<int>(p);
+        const float s0 = __shfl(rho, gb), s1 = __shfl(rho, gb + 4), s2 = __shfl(rho, gb + 8), s3 = __shfl(rho, gb + 12);
+        // AVX2 distances (cw - s, (d0^2 + d1^2) + (d2^2 + d3^2)) to codewords 2g, 2g + 1
+        float bd = 0.0f;
+        uint32_t bw = 0;
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const float4 cw = w ? cw1 : cw0;
+            const float e0 = cw.x - s0, e1 = cw.y - s1, e2 = cw.z - s2, e3 = cw.w - s3;
+            const float dd = (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
+            if (w == 0 || dd < bd) { bd = dd; bw = 2 * g + w; }
+        }
+        // the first codeword with the smallest distance over the 16 lanes
+#pragma unroll
+        for (int sh = 1; sh < 16; sh <<= 1) {
+            const float od = __shfl_xor(bd, sh);
+            const uint32_t ow = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bw), sh));
+            if (od < bd || (od == bd && ow < bw)) { bd = od; bw = ow; }
+        }
+        if (valid && g == 0) {   // index b at payload bits 16 + 5b (after the f16 norm), LSB-first
+            const uint32_t bit = 16u + 5u * b, wd = bit >> 5, sh = bit & 31u;
+            uint32_t* pw = ring + (ent & 0x7FFFu) + wd;
+            atomicAnd(pw, ~(31u << sh));
+            atomicOr(pw, bw << sh);
+            if (sh > 27u) {
+                atomicAnd(pw + 1, ~(31u >> (32u - sh)));
+                atomicOr(pw + 1, bw >> (32u - sh));
+            }
+        }
+        wave_sync();   // R.xh is rewritten by the next pass
     }
 }
 
-constexpr int FIB_PAY_WORDS = 64 * 3 + 4;   // per wave: both 32-vector sub-tiles
-
+// FibQuantizer::encode_batch (codec.rs:578-668) + finish_batch_encode
+// (670-729) + FibCodeV1::encode_batch (225-320) for every segment.  Each wave
+// walks 32-vector units (unit u: 256-vector tile u / 8 of the segment table,
+// eighth u % 8) with a stride of the whole grid; the next unit's rows are
+// loaded while the current one is scored.  A unit's payloads wait in the
+// wave's LDS ring with its undecided blocks queued; every FIB_RING units (or
+// when the queue could overflow, or at the wave's last unit) the queue is
+// redone exactly and the ring's payloads are written.  No workgroup barrier
+// after the rotation operands are in LDS: the waves never wait for each other.
 template <int DIM, bool DIAG>
-__global__ __launch_bounds__(TILE) void fib_encode_kernel(LaunchCommon lc, const void* __restrict__ in,
-                                                          uint8_t* __restrict__ wire, const uint32_t* __restrict__ mf,
-                                                          float thr, const double* __restrict__ rot_t,
-                                                          const float* __restrict__ cb) {
+__global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void fib_encode_kernel(LaunchCommon lc,
+    const void* __restrict__ in, uint8_t* __restrict__ wire, const uint32_t* __restrict__ mf, float thr,
+    const double* __restrict__ rot64, const float* __restrict__ cb, uint32_t nunits) {
     static_assert(DIM == 64, "the MFMA layout is built for head_dim 64");
     extern __shared__ uint32_t smem_u[];
+    __shared__ FibRedoLds redo_lds[WAVES];
     uint32_t* rot_lds = smem_u;   // MF_ROT block (MF_SCA words)
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    uint32_t* pay = smem_u + MF_SCA + wave * FIB_PAY_WORDS;
-
-    const uint32_t blk = blockIdx.x;
-    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
-    const SegDev seg = lc.segs[sidx];
-    const uint32_t tile = blk - lc.tile_start[sidx];
-    uint8_t* blob = wire + seg.wire_offset;
+    // wave index as a wave-uniform value: the unit loop, its segment lookups
+    // and offsets then stay scalar
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
     const int h = lane >> 5, n = lane & 31;
-    const uint32_t v0 = tile * TILE + wave * WAVE;
+    uint32_t* ring = smem_u + MF_SCA + wave * FIB_RING * FIB_PAY_WORDS;
+    FibRedoLds& R = redo_lds[wave];
     const bool bf16 = lc.in_bf16 != 0;
-
-    // tile 0's input rows first: their latency overlaps the set-up (lanes
-    // past the end re-read the last vector; their results are dropped)
-    float4 xa[8], xb[8];
-    const uint32_t last = seg.n_vectors - 1;
-    if (v0 < seg.n_vectors) load_half_row(xa, in, bf16, seg, min(v0 + n, last), h);
     {
         const uint4* src = reinterpret_cast<const uint4*>(mf + MF_ROT);
         uint4* dst = reinterpret_cast<uint4*>(rot_lds);
         uint4 t[MF_SCA / 4 / TILE];
 #pragma unroll
-        for (int k = 0; k < MF_SCA / 4 / TILE; ++k) t[k] = src[threadIdx.x + k * TILE];
+        for (int q = 0; q < MF_SCA / 4 / TILE; ++q) t[q] = src[threadIdx.x + q * TILE];
 #pragma unroll
-        for (int k = 0; k < MF_SCA / 4 / TILE; ++k) dst[threadIdx.x + k * TILE] = t[k];
+        for (int q = 0; q < MF_SCA / 4 / TILE; ++q) dst[threadIdx.x + q * TILE] = t[q];
     }
     const uint4 sa4 = reinterpret_cast<const uint4*>(mf + MF_SCA)[lane];
     const v4u sa = {sa4.x, sa4.y, sa4.z, sa4.w};
-    __shared__ uint32_t q_count;
-    __shared__ uint32_t q_entries[TILE];   // (local vector) | (blocks to redo) << 8
-    __shared__ double q_nrm[TILE];         // each entry's sequential f64 norm
-    if (threadIdx.x == 0) q_count = 0;
-    const uint32_t tile_v0 = tile * TILE;
-    __syncthreads();
+    __syncthreads();   // the only barrier: the rotation operands are in LDS
 
-    // tile 1's loads are issued once tile 0's rotation has consumed its
-    // inputs, and land while tile 0 is scored
-    if (v0 < seg.n_vectors) {
+    const uint32_t stride = gridDim.x * WAVES;
+    // first unit >= u (step stride) with vectors -> its segment and first vector; nunits when none.
+    // A wave visits units in increasing order, so after a binary search for its
+    // first unit the segment search continues forward from the previous unit's
+    // segment (sidx on entry).
+    auto next_unit = [&](uint32_t u, uint32_t& sidx, uint32_t& v0) -> uint32_t {
+        if (u < nunits && sidx == 0xFFFFFFFFu) sidx = find_segment(lc.tile_start, lc.nseg, u / FIB_UNITS_PER_TILE);
+        for (; u < nunits; u += stride) {
+            const uint32_t tile = u / FIB_UNITS_PER_TILE;
+            while (sidx + 1 < lc.nseg && lc.tile_start[sidx + 1] <= tile) ++sidx;
+            v0 = (tile - lc.tile_start[sidx]) * TILE + (u % FIB_UNITS_PER_TILE) * FIB_UNIT;
+            if (v0 < lc.segs[sidx].n_vectors) return u;
+        }
+        return nunits;
+    };
+    uint32_t sidx = 0xFFFFFFFFu, v0 = 0;
+    uint32_t u = next_unit(blockIdx.x * WAVES + static_cast<uint32_t>(wave), sidx, v0);
+    float4 x[8];
+    if (u < nunits) {
+        const SegDev s = lc.segs[sidx];
+        load_half_row(x, in, bf16, s, min(v0 + static_cast<uint32_t>(n), s.n_vectors - 1), h);
+    }
+    uint32_t used = 0, nq = 0;   // ring slots filled, queued vectors
+    while (u < nunits) {   // wave-uniform
+        const SegDev seg = lc.segs[sidx];
+        uint32_t* pay = ring + used * FIB_PAY_WORDS;
         FibTileRot t;
-        fib_encode_rotate(t, xa, rot_lds, lane);
+        fib_encode_rotate(t, x, rot_lds, lane);
         __builtin_amdgcn_sched_barrier(0);
-        if (v0 + 32 < seg.n_vectors) load_half_row(xb, in, bf16, seg, min(v0 + 32 + n, last), h);
-        fib_encode_score<DIM, DIAG>(lc, seg, sidx, blob, v0, t, pay, sa, thr, &q_count, q_entries, q_nrm, tile_v0,
+        uint32_t sidx2 = sidx, v02 = 0;
+        const uint32_t u2 = next_unit(u + stride, sidx2, v02);
+        if (u2 < nunits) {   // the next unit's rows land while this one is scored
+            const SegDev s2 = lc.segs[sidx2];
+            load_half_row(x, in, bf16, s2, min(v02 + static_cast<uint32_t>(n), s2.n_vectors - 1), h);
+        }
+        const uint32_t mask = fib_encode_score<DIM, DIAG>(lc, seg, sidx, v0, t, pay, sa, thr, lane);
+        // queue this unit's undecided vectors
+        const bool small = seg.n_vectors < 4 || lc.per_vector != 0;
+        const bool queued = h == 0 && mask != 0u;
+        const uint64_t bal = __ballot(queued);
+        if (queued) {
+            const uint32_t slot = nq + static_cast<uint32_t>(__popcll(bal & ((1ull << lane) - 1ull)));
+            R.ent[slot] = (used * FIB_PAY_WORDS + 3u * static_cast<uint32_t>(n)) | (small ? 1u << 15 : 0u) |
+                          (mask << 16);
+            R.off[slot] = vec_elem_offset(seg, v0 + static_cast<uint32_t>(n));
+            R.nrm[slot] = t.nrm;
+        }
+        nq += static_cast<uint32_t>(__popcll(bal));
+        if (lane == 0) {
+            R.blob[used] = seg.wire_offset;
+            R.v0[used] = v0;
+            R.nv[used] = min(FIB_UNIT, seg.n_vectors - v0);
+            R.nvec[used] = seg.n_vectors;
+        }
+        ++used;
+        if (used == FIB_RING || nq > FIB_QCAP - FIB_UNIT || u2 >= nunits) {
+            wave_sync();
+            if (nq) fib_redo_flush<DIM>(lc, in, rot64, cb, ring, R, nq, lane);
+            wave_sync();
+            for (uint32_t q = 0; q < used; ++q) {
+                uint8_t* blob = wire + R.blob[q];
+                const uint32_t qv0 = R.v0[q];
+                lds_to_global(blob + 19 + static_cast<uint64_t>(qv0) * 12u, ring + q * FIB_PAY_WORDS, R.nv[q] * 12u,
                               lane);
+                if (qv0 == 0 && lane < 19)
+                    blob[lane] =
+                        static_cast<uint8_t>(fb2_byte(static_cast<uint32_t>(lane), 5u, DIM / 4, R.nvec[q], 10u));
+            }
+            wave_sync();   // the ring and the queue are refilled
+            used = 0;
+            nq = 0;
+        }
+        u = u2;
+        sidx = sidx2;
+        v0 = v02;
     }
-    if (v0 + 32 < seg.n_vectors) {
-        FibTileRot t;
-        fib_encode_rotate(t, xb, rot_lds, lane);
-        fib_encode_score<DIM, DIAG>(lc, seg, sidx, blob, v0 + 32, t, pay + 96, sa, thr, &q_count, q_entries, q_nrm,
-                              tile_v0, lane);
-    }
-    if (tile == 0 && threadIdx.x < 19)
-        blob[threadIdx.x] = static_cast<uint8_t>(fb2_byte(threadIdx.x, 5u, DIM / 4, seg.n_vectors, 10u));
-    __syncthreads();   // the queue is complete and every payload is in LDS
-    {
-        __shared__ FibFixupLds fx;
-        uint32_t* pay0 = smem_u + MF_SCA;
-        auto pay_of = [pay0](uint32_t li) {   // local vector -> its payload words
-            return pay0 + (li >> 6) * FIB_PAY_WORDS + 3u * (li & 63u);
-        };
-        fib_fixup_wave<DIM>(lc, in, rot_t, cb, seg, tile_v0, q_entries, q_nrm, q_count, fx, pay_of, wave, lane);
-    }
-    __syncthreads();   // patched payloads
-    if (v0 < seg.n_vectors)
-        lds_to_global(blob + 19 + static_cast<uint64_t>(v0) * 12u, pay, min(64u, seg.n_vectors - v0) * 12u, lane);
 }
 
 // ------------------------------------------------------------ fib decode
@@ -2986,15 +3035,44 @@ int launch_turbo_score(const LaunchCommon& lc, const TurboDev& td, const uint8_t
     return hipErrorInvalidValue;
 }
 
+// Workgroups of a persistent launch: every workgroup slot of the device
+// (compute units x resident workgroups of `kernel`), at most `want`.
+template <typename K>
+uint32_t persistent_grid(K kernel, size_t dyn_lds, uint32_t want) {
+    static std::mutex mu;
+    static std::map<std::pair<int, const void*>, uint32_t> slots;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return want;
+    const auto key = std::make_pair(dev, reinterpret_cast<const void*>(kernel));
+    uint32_t n = 0;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        auto it = slots.find(key);
+        if (it != slots.end()) n = it->second;
+    }
+    if (n == 0) {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0 ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), TILE,
+                                                         dyn_lds) != hipSuccess || per_cu <= 0)
+            return want;
+        n = static_cast<uint32_t>(cus) * static_cast<uint32_t>(per_cu);
+        std::lock_guard<std::mutex> lock(mu);
+        slots[key] = n;
+    }
+    return std::max(1u, std::min(n, want));
+}
+
 int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire, uint32_t nblocks,
                       void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
-    constexpr size_t lds = (MF_SCA + WAVES * FIB_PAY_WORDS) * sizeof(uint32_t);
-    if (lc.diag)
-        return launch_big_lds(fib_encode_kernel<64, true>, nblocks, lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot_t,
-                              fd.codebook);
-    return launch_big_lds(fib_encode_kernel<64, false>, nblocks, lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot_t,
-                          fd.codebook);
+    constexpr size_t lds = (MF_SCA + WAVES * FIB_RING * FIB_PAY_WORDS) * sizeof(uint32_t);
+    const uint64_t units = static_cast<uint64_t>(nblocks) * FIB_UNITS_PER_TILE;
+    if (units > 0xFFFFFFFFull) return hipErrorInvalidValue;
+    const uint32_t want = static_cast<uint32_t>((units + WAVES - 1) / WAVES);
+    auto kern = lc.diag ? fib_encode_kernel<64, true> : fib_encode_kernel<64, false>;
+    return launch_big_lds(kern, persistent_grid(kern, lds, want), lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot64,
+                          fd.codebook, static_cast<uint32_t>(units));
 }
 
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, void* out, uint32_t nblocks,
