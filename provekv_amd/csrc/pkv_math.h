@@ -12,7 +12,7 @@
 //     optimized-routines (MIT / Apache-2.0), which glibc adopted in 2.28.
 // The restatements were checked against the host libm (logf on every positive
 // float, expf on every finite float with 2 disagreements at |x| > 32, atan2f on
-// 3e8 random pairs); tests/test_host_math.py re-runs sampled versions of those
+// 3e8 random pairs); tests/test_host_side.py re-runs sampled versions of those
 // checks through pkv_host_* exports.
 //
 // Everything here must be compiled with -ffp-contract=off.

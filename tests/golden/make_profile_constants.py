@@ -2,7 +2,10 @@
 host constant generators (pkv_turbo_constants / pkv_fib_constants, no GPU).
 The file lets anyone holding the Rust reference diff the seed-42 profile
 constants once (FastHadamardRotation signs, QJL matrix, StoredRotation,
-FibCodebookV1 codewords)."""
+FibCodebookV1 codewords).
+
+The file is the library's own output, so it is a regression pin (it catches
+a change in the generators), not a parity pin against the reference."""
 import os
 import sys
 
