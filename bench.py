@@ -150,10 +150,12 @@ def profiled_traffic(summary: str, kernel: str):
     return None
 
 
-def roofline(kernel: str, alg_bytes: int, ms: float, summary: str) -> dict:
+def roofline(kernel: str, alg_bytes: int, ms: float, summary: str, tag: str = "") -> dict:
+    """`tag` picks a labelled row of the summary (" [lossy]" where one run
+    launches the same kernel for two workloads)."""
     gbs = alg_bytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "kernel": kernel, "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(summary, kernel),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(summary, kernel + tag),
             "algorithmic_bytes": int(alg_bytes)}
 
 
@@ -238,7 +240,7 @@ def pmap(fn, items, threads=8):
 
 # ================================================================ configs 0, 1, 2, 4
 def codec_workload(args, *, name, metric, prof, radii, inp, segs, wire, out, f32_bytes, enc_alg, dec_alg,
-                   kernels, summary, parity, cpu, data, config, dtype="f32"):
+                   kernels, summary, parity, cpu, data, config, dtype="f32", tag=""):
     """Encode all segments into `wire`, decode them into `out`: timed as the
     fused round trip (value) and per kernel."""
     import torch
@@ -284,9 +286,9 @@ def codec_workload(args, *, name, metric, prof, radii, inp, segs, wire, out, f32
         "kernels_gbs": {"encode": round(enc_alg / (enc_ms * 1e-3) / 1e9, 1),
                         "decode": round(dec_alg / (dec_ms * 1e-3) / 1e9, 1)},
         "algorithmic_bytes": {"encode": int(enc_alg), "decode": int(dec_alg)},
-        "roofline": roofline(kernels[dom], (enc_alg, dec_alg)[dom], (enc_ms, dec_ms)[dom], summary),
+        "roofline": roofline(kernels[dom], (enc_alg, dec_alg)[dom], (enc_ms, dec_ms)[dom], summary, tag),
         "roofline_other": roofline(kernels[1 - dom], (enc_alg, dec_alg)[1 - dom], (enc_ms, dec_ms)[1 - dom],
-                                   summary),
+                                   summary, tag),
         "parity_checked": True,
         "wall_s_timed": round(wall, 3),
         "copy_gbs": copy_gbs(stream),
@@ -473,7 +475,7 @@ def bench_config2(args):
             metric="KV codec encode+decode GB/s (f32 in) and % HBM peak, config 2 (N=8 turbo b=4 shells)",
             f32_bytes=f32, enc_alg=f32 + tier.wire_bytes, dec_alg=tier.wire_bytes + f32,
             kernels=("turbo_encode_qjl_kernel<3, false>", "turbo_decode_split_kernel<3>"),
-            summary="codec_kernels_config2.md",
+            summary="codec_kernels_config2.md", tag=" [lossy]" if lossy else " [lossless]",
             parity=lambda prof=prof, wire=wire, out=out, tier=tier, blob_in=blob_in, rc=rc: _blob_parity(
                 prof, wire, out, tier.dec, blob_in, [0, 1, 191, 383],
                 lambda v: O.turbo_encode_batch(v, SEED, radii_codec=rc, signs=signs, G=G),
