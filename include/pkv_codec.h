@@ -379,6 +379,16 @@ int pkv_encode_diagnostics(pkv_ctx* ctx, const pkv_profile* prof, int radii_code
                            uint64_t n, uint8_t* d_wire, uint64_t wire_bytes, float* d_diag,
                            uint64_t diag_elems, float* threshold, uint32_t* d_status, void* stream);
 
+/* Validation hook, no counterpart in the reference: the BlockLogU8 radii
+ * encode (radius.rs:58-77) takes each code from a hardware log and keeps it
+ * only when it lies farther from a rounding boundary than that log's error
+ * bound allows (the rest, and the block's mn / mx, use the exact logf).  The
+ * bound is measured on each device, over every normal positive float, when
+ * the first context there is created.  out[e] (256 floats, host memory) =
+ * the largest |hardware log - logf(v)| over every v whose logf(v) has a
+ * biased f32 exponent <= e. */
+int pkv_radii_log_bound(pkv_ctx* ctx, float* out);
+
 /* ---------------------------------------------------------------- host math
  * Host builds of the exact scalar routines the kernels use (test hooks):
  * angle bins of (a[i], b[i]) for pbits, and logf / expf over arrays. */

@@ -158,6 +158,22 @@ int noalloc_scratch(int device, uint8_t** out) {
     return PKV_OK;
 }
 
+std::mutex g_logb_mu;
+bool g_logb_done[kMaxDevices] = {};
+
+// The cheap-log bound table of the BlockLogU8 encodes, measured once per
+// device (the caller has made it current) before the first context there
+// returns.
+int logf_bound_once(int device, hipStream_t st) {
+    std::lock_guard<std::mutex> lock(g_logb_mu);
+    if (device >= 0 && device < kMaxDevices && g_logb_done[device]) return PKV_OK;
+    hipError_t e = static_cast<hipError_t>(launch_logf_bound(st));
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_status(e);
+    if (device >= 0 && device < kMaxDevices) g_logb_done[device] = true;
+    return PKV_OK;
+}
+
 template <typename T>
 int upload(T** dptr, const std::vector<T>& v) {
     size_t bytes = std::max<size_t>(v.size() * sizeof(T), sizeof(T));
@@ -606,7 +622,8 @@ int pkv_ctx_create(int device, pkv_ctx** out) {
     c->device = device;
     hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
     if (e != hipSuccess) { delete c; return hip_status(e); }
-    const int rc = noalloc_scratch(device, &c->noalloc);   // device is current
+    int rc = noalloc_scratch(device, &c->noalloc);   // device is current
+    if (!rc) rc = logf_bound_once(device, c->own_stream);
     if (rc) { (void)hipStreamDestroy(c->own_stream); delete c; return rc; }
     *out = c;
     return PKV_OK;
@@ -1075,6 +1092,19 @@ int pkv_encode_diagnostics(pkv_ctx* ctx, const pkv_profile* prof, int radii_code
     HIP_TRY(hipSetDevice(ctx->device));
     return run_segments_locked(ctx, prof, radii_codec, true, PKV_F32, d_in, n * prof->dim, &seg, 1, d_wire,
                                wire_bytes, d_status, static_cast<hipStream_t>(stream), false, 1, 0, 0, d_diag);
+}
+
+int pkv_radii_log_bound(pkv_ctx* ctx, float* out) {
+    if (!ctx || !out) return PKV_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    float* d = nullptr;
+    HIP_TRY(hipMalloc(&d, 256 * sizeof(float)));
+    hipError_t e = static_cast<hipError_t>(launch_logf_bound_read(d, ctx->own_stream));
+    if (e == hipSuccess) e = hipMemcpyAsync(out, d, 256 * sizeof(float), hipMemcpyDeviceToHost, ctx->own_stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->own_stream);
+    (void)hipFree(d);
+    return e == hipSuccess ? PKV_OK : hip_status(e);
 }
 
 int pkv_parse_header(const pkv_profile* p, const uint8_t* b, uint64_t len, uint64_t* n_vectors, int* radii_codec) {

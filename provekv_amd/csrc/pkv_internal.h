@@ -137,6 +137,10 @@ int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, 
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, void* out,
                       uint32_t nblocks, void* stream);
 int launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, void* stream);
+// Measure the cheap-log bound table the BlockLogU8 encodes read (once per
+// device, before any encode there); copy it (256 floats) to device memory.
+int launch_logf_bound(void* stream);
+int launch_logf_bound_read(float* out, void* stream);
 int launch_fib_product_check(const float* rot32, const float* cb, uint32_t* bad, void* stream);
 
 // Legacy per-vector records (pkv_records.hip).  Records are rec_hdr header

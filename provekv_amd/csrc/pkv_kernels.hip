@@ -56,6 +56,14 @@ struct Div255 {
 };
 __constant__ Div255 c_div255 = Div255();
 
+// Gap between cheap_logf (below) and logf, per magnitude of the result:
+// g_logb[e] = the largest |cheap_logf(v) - logf(v)| over every normal positive
+// float v whose logf(v) has biased exponent <= e, rounded up to f32.  Measured
+// on each device, over all 2,130,706,432 such v, by launch_logf_bound before
+// the library encodes anything there (pkv_ctx_create).
+__device__ uint32_t g_logb_raw[256];
+__device__ float g_logb[256];
+
 // ------------------------------------------------------------ helpers
 __device__ __forceinline__ uint32_t find_segment(const uint32_t* __restrict__ tile_start, uint32_t nseg,
                                                  uint32_t blk) {
@@ -560,6 +568,12 @@ __device__ __forceinline__ uint32_t partner(uint32_t x, int h) {
     return h ? p[0] : p[1];
 }
 
+// Value of the lane in the other 16-lane row of the same pair (l ^ 16).
+__device__ __forceinline__ uint32_t partner16(uint32_t x, int q) {
+    const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (q & 1) ? p[0] : p[1];
+}
+
 // fwht_normalized stages (turbo-quant/src/rotation.rs:379-398) on a vector
 // split over the two halves of the wave: 32 elements per lane.
 __device__ __forceinline__ void fwht_split(float (&v)[32], int h) {
@@ -575,16 +589,106 @@ __device__ __forceinline__ void fwht_split(float (&v)[32], int h) {
             }
         }
     }
-    // step 32: element c (half 0) with c + 32 (half 1): (a + b, a - b).  One
-    // v_permlane32_swap of two copies of v[c] leaves a in the first and b in
-    // the second in every lane; each half then takes fma(b, +-1, a), whose
-    // product is exact, so its single rounding is that of a + b or a - b
-    // (signed zeros included).
-    const float sgn = h ? -1.0f : 1.0f;
+    // step 32: element c (half 0) with c + 32 (half 1): (a + b, a - b).  A
+    // v_permlane32_swap of two different elements v[c], v[c + 16] leaves (a, b)
+    // of element c in the lanes of half 0 and (a, b) of element c + 16 in the
+    // lanes of half 1, so every lane forms the same a + b and a - b; a second
+    // swap returns each sum and difference to its own half.
+    (void)h;
 #pragma unroll
-    for (int c = 0; c < 32; ++c) {
-        const auto p = __builtin_amdgcn_permlane32_swap(f2u(v[c]), f2u(v[c]), false, false);
-        v[c] = __builtin_fmaf(u2f(p[1]), sgn, u2f(p[0]));
+    for (int c = 0; c < 16; ++c) {
+        auto p = __builtin_amdgcn_permlane32_swap(f2u(v[c]), f2u(v[c + 16]), false, false);
+        const float a = u2f(p[0]), b = u2f(p[1]);
+        p = __builtin_amdgcn_permlane32_swap(f2u(a + b), f2u(a - b), false, false);
+        v[c] = u2f(p[0]);
+        v[c + 16] = u2f(p[1]);
+    }
+}
+
+// The hardware log2 times ln 2 rounded to f32: within g_logb of logf.
+__device__ __forceinline__ float cheap_logf(float v) { return __builtin_amdgcn_logf(v) * 0x1.62e430p-1f; }
+
+// CompressedRadiiV1 BlockLogU8 (turbo-quant/src/radius.rs:58-77) of one
+// vector whose 64 radii sit 16 per lane on LPV = 2 (lanes l, l ^ 32; part =
+// l >> 5) or LPV = 4 lanes (l, l ^ 16, l ^ 32, l ^ 48; part = l >> 4).
+// Writes this lane's 16 codes (4 per word, radius 16 part + i in byte i) and
+// the vector's mn, mx.  Every lane of the wave must call it.
+//
+// The reference takes v_i = max(r_i, FLT_MIN), l_i = logf(v_i), mn = min l_i,
+// mx = max l_i, span = max(mx - mn, 2^-23) and
+// code_i = roundf(fl(255 * clamp(fl(fl(l_i - mn) / span), 0, 1))).
+// * logf is monotone non-decreasing on the normal floats (checked on every
+//   one), so mn = logf(min v_i) and mx = logf(max v_i): two exact logs.
+// * For the codes, t_i = fl(fl(cheap_logf(v_i) - mn) * fl(255 / span)) is
+//   within 255 delta / span + 2 * 256 * 3.0001u (u = 2^-24) of the
+//   reference's value P_i before roundf, with delta = g_logb of the larger of
+//   |mn|, |mx| (every l_i lies between them): three roundings on each side,
+//   of values at most 256 when the margin below is under 1/2.  When t_i is
+//   farther than M = 255 delta / span (1 + 2^-10) + 2^-12 from every
+//   half-integer, P_i lies in the same unit interval around rint(t_i), so
+//   roundf(P_i) = rint(t_i) (t_i >= -M > -1/2 and t_i <= 255 + M; no ties).
+//   The others -- every code when M >= 1/2, and a NaN t_i -- take the
+//   reference's chain.
+template <int LPV>
+__device__ __forceinline__ void block_log_u8(const float (&r)[16], int part, const LogfEntry* ltab, uint32_t (&code)[4],
+                                             float& mn, float& mx) {
+    constexpr float kMinPos = 1.17549435e-38f;
+    float v[16];
+    float vmin = u2f(0x7f800000u), vmax = u2f(0xff800000u);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        v[i] = r[i] < kMinPos ? kMinPos : r[i];
+        vmin = __builtin_fminf(vmin, v[i]);
+        vmax = __builtin_fmaxf(vmax, v[i]);
+    }
+    if constexpr (LPV == 4) {
+        vmin = __builtin_fminf(vmin, u2f(partner16(f2u(vmin), part)));
+        vmax = __builtin_fmaxf(vmax, u2f(partner16(f2u(vmax), part)));
+    }
+    vmin = __builtin_fminf(vmin, u2f(partner(f2u(vmin), LPV == 4 ? part >> 1 : part)));
+    vmax = __builtin_fmaxf(vmax, u2f(partner(f2u(vmax), LPV == 4 ? part >> 1 : part)));
+    // one exact log per lane: even parts the minimum, odd parts the maximum
+    const float own = og_logf_normal((part & 1) ? vmax : vmin, ltab);
+    const float other = u2f(LPV == 4 ? partner16(f2u(own), part) : partner(f2u(own), part));
+    mn = (part & 1) ? other : own;
+    mx = (part & 1) ? own : other;
+    const float span = __builtin_fmaxf(mx - mn, 1.1920929e-07f);
+    const float inv = 255.0f / span;
+    const float big = __builtin_fmaxf(__builtin_fabsf(mn), __builtin_fabsf(mx));
+    const float delta = g_logb[f2u(big) >> 23];
+    const float margin = delta * inv * (1.0f + 0x1p-10f) + 0x1p-12f;
+    const float thr = 0.5f - margin;   // decided when |t - rint(t)| < thr
+    uint32_t slow = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int i = 4 * w + t;
+            const float tv = (cheap_logf(v[i]) - mn) * inv;
+            // for t in (-1/2, 256) the sum lies in [2^23, 2^24), where the f32
+            // grid is the integers: it is 1.5 * 2^23 + rint(t), exactly
+            const float y = tv + 0x1.8p23f;
+            const float k = y - 0x1.8p23f;
+            slow |= (__builtin_fabsf(tv - k) < thr ? 0u : 1u) << i;
+            packed |= (f2u(y) & 0xffu) << (8 * t);
+        }
+        code[w] = packed;
+    }
+    if (slow) {
+        for (uint32_t m = slow; m; m &= m - 1u) {
+            const uint32_t i = static_cast<uint32_t>(__ffs(m) - 1);
+            float vi = v[0];   // v[i] by selects (a dynamic index would go through scratch)
+#pragma unroll
+            for (int j = 1; j < 16; ++j) vi = static_cast<uint32_t>(j) == i ? v[j] : vi;
+            float nrm = (og_logf_normal(vi, ltab) - mn) / span;
+            nrm = nrm < 0.0f ? 0.0f : (nrm > 1.0f ? 1.0f : nrm);
+            const uint32_t q = static_cast<uint32_t>(__builtin_roundf(nrm * 255.0f));
+            const uint32_t sh = 8u * (i & 3u), keep = ~(0xffu << sh);
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                code[w] = static_cast<uint32_t>(w) == (i >> 2) ? (code[w] & keep) | (q << sh) : code[w];
+        }
     }
 }
 
@@ -745,31 +849,12 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
                 for (int i = 0; i < HP; ++i) rw[16 * h + i] = f2u(r[i]);
         } else {
             // CompressedRadiiV1 BlockLogU8 (turbo-quant/src/radius.rs:58-77)
-            float lg[HP];
-            float mn = u2f(0x7f800000u), mx = u2f(0xff800000u);
-#pragma unroll
-            for (int i = 0; i < HP; ++i) {
-                const float v = r[i] < 1.17549435e-38f ? 1.17549435e-38f : r[i];
-                lg[i] = og_logf_normal(v, logf_lds);
-                mn = __builtin_fminf(mn, lg[i]);
-                mx = __builtin_fmaxf(mx, lg[i]);
-            }
-            mn = __builtin_fminf(mn, u2f(partner(f2u(mn), h)));
-            mx = __builtin_fmaxf(mx, u2f(partner(f2u(mx), h)));
-            const float span = __builtin_fmaxf(mx - mn, 1.1920929e-07f);
+            uint32_t code[4];
+            float mn, mx;
+            block_log_u8<2>(r, h, logf_lds, code, mn, mx);
             if (active) {
 #pragma unroll
-                for (int i = 0; i < HP; i += 4) {
-                    uint32_t packed = 0;
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        float nrm = (lg[i + t] - mn) / span;
-                        nrm = nrm < 0.0f ? 0.0f : (nrm > 1.0f ? 1.0f : nrm);
-                        const float q = __builtin_roundf(nrm * 255.0f);
-                        packed |= static_cast<uint32_t>(q) << (8 * t);
-                    }
-                    pv[4 * h + i / 4] = packed;
-                }
+                for (int w = 0; w < 4; ++w) pv[4 * h + w] = code[w];
                 if (h == 0) {
                     pv[8] = f2u(mn);
                     pv[9] = f2u(mx);
@@ -925,11 +1010,6 @@ constexpr int QA128_PER_TILE = 32 * 64;   // A operand floats of one 16-projecti
 constexpr int QB128_PER_TILE = 4 * 64;    // bound floats of one 16-projection tile
 
 // Value of lane l ^ 16 (the other quarter of the same half).
-__device__ __forceinline__ uint32_t partner16(uint32_t x, int q) {
-    const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
-    return (q & 1) ? p[0] : p[1];
-}
-
 // fwht_normalized stages (turbo-quant/src/rotation.rs:379-398) on a 128-wide
 // vector split over four lanes, 32 elements per lane.
 __device__ __forceinline__ void fwht_quarter(float (&v)[32], int q) {
@@ -946,19 +1026,25 @@ __device__ __forceinline__ void fwht_quarter(float (&v)[32], int q) {
         }
     }
     // step 32: element c of quarter 2k with c of quarter 2k + 1: (a + b, a - b);
-    // step 64: quarters 0, 1 with 2, 3.  As in fwht_split, one swap of two
-    // copies of v[c] leaves a and b in every lane, and fma(b, +-1, a) rounds
-    // exactly like a + b or a - b.
-    const float s32 = (q & 1) ? -1.0f : 1.0f, s64 = (q & 2) ? -1.0f : 1.0f;
+    // step 64: quarters 0, 1 with 2, 3.  On element pairs (c, c + 16): a
+    // v_permlane16_swap of v[c], v[c + 16] leaves step 32's (a, b) of element
+    // c in the even rows and of element c + 16 in the odd rows, and every lane
+    // forms a + b, a - b; a v_permlane32_swap of those two then holds step 64's
+    // (a, b) -- quarters 0 / 2 in rows 0, 1, quarters 1 / 3 in rows 2, 3 -- for
+    // the same a + b, a - b; the two swaps in reverse order return every
+    // result to its quarter and element.
+    (void)q;
 #pragma unroll
-    for (int c = 0; c < 32; ++c) {
-        const auto p = __builtin_amdgcn_permlane16_swap(f2u(v[c]), f2u(v[c]), false, false);
-        v[c] = __builtin_fmaf(u2f(p[1]), s32, u2f(p[0]));
-    }
-#pragma unroll
-    for (int c = 0; c < 32; ++c) {
-        const auto p = __builtin_amdgcn_permlane32_swap(f2u(v[c]), f2u(v[c]), false, false);
-        v[c] = __builtin_fmaf(u2f(p[1]), s64, u2f(p[0]));
+    for (int c = 0; c < 16; ++c) {
+        auto p = __builtin_amdgcn_permlane16_swap(f2u(v[c]), f2u(v[c + 16]), false, false);
+        float a = u2f(p[0]), b = u2f(p[1]);
+        p = __builtin_amdgcn_permlane32_swap(f2u(a + b), f2u(a - b), false, false);
+        a = u2f(p[0]);
+        b = u2f(p[1]);
+        p = __builtin_amdgcn_permlane32_swap(f2u(a + b), f2u(a - b), false, false);
+        p = __builtin_amdgcn_permlane16_swap(p[0], p[1], false, false);
+        v[c] = u2f(p[0]);
+        v[c + 16] = u2f(p[1]);
     }
 }
 
@@ -1112,33 +1198,12 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
                 for (int i = 0; i < HP; ++i) pv[16 * q + i] = f2u(r[i]);
         } else {
             // CompressedRadiiV1 BlockLogU8 (turbo-quant/src/radius.rs:58-77)
-            float lg[HP];
-            float mn = u2f(0x7f800000u), mx = u2f(0xff800000u);
-#pragma unroll
-            for (int i = 0; i < HP; ++i) {
-                const float v = r[i] < 1.17549435e-38f ? 1.17549435e-38f : r[i];
-                lg[i] = og_logf_normal(v, logf_lds);
-                mn = __builtin_fminf(mn, lg[i]);
-                mx = __builtin_fmaxf(mx, lg[i]);
-            }
-            mn = __builtin_fminf(mn, u2f(partner16(f2u(mn), q)));
-            mx = __builtin_fmaxf(mx, u2f(partner16(f2u(mx), q)));
-            mn = __builtin_fminf(mn, u2f(partner(f2u(mn), q >> 1)));
-            mx = __builtin_fmaxf(mx, u2f(partner(f2u(mx), q >> 1)));
-            const float span = __builtin_fmaxf(mx - mn, 1.1920929e-07f);
+            uint32_t code[4];
+            float mn, mx;
+            block_log_u8<4>(r, q, logf_lds, code, mn, mx);
             if (active) {
 #pragma unroll
-                for (int i = 0; i < HP; i += 4) {
-                    uint32_t packed = 0;
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        float nrm = (lg[i + t] - mn) / span;
-                        nrm = nrm < 0.0f ? 0.0f : (nrm > 1.0f ? 1.0f : nrm);
-                        const float qv = __builtin_roundf(nrm * 255.0f);
-                        packed |= static_cast<uint32_t>(qv) << (8 * t);
-                    }
-                    pv[4 * q + i / 4] = packed;
-                }
+                for (int w = 0; w < 4; ++w) pv[4 * q + w] = code[w];
                 if (q == 0) {
                     pv[16] = f2u(mn);
                     pv[17] = f2u(mx);
@@ -2873,6 +2938,54 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t value, uint64_t n) {
     if (i < n) p[i] = value;
 }
 
+// g_logb measurement: every normal positive float v in [2^-126, 2^128), a
+// contiguous run of `per` per thread.  The running maximum of
+// |cheap_logf(v) - logf(v)| (exact in f64, rounded up to f32) goes to
+// g_logb_raw[biased exponent of |logf(v)|] whenever that exponent changes.
+constexpr uint32_t kLogbLo = 0x00800000u, kLogbHi = 0x7f800000u;
+constexpr uint32_t kLogbBlocks = 2048;
+
+__global__ __launch_bounds__(256) void logf_bound_kernel(uint32_t per) {
+    __shared__ LogfEntry tab[16];
+    if (threadIdx.x < 16) tab[threadIdx.x] = c_logf_tab[threadIdx.x];
+    __syncthreads();
+    const uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+    const uint64_t b0 = kLogbLo + t * per;
+    const uint32_t u0 = static_cast<uint32_t>(b0 < kLogbHi ? b0 : kLogbHi);
+    const uint32_t u1 = static_cast<uint32_t>(b0 + per < kLogbHi ? b0 + per : kLogbHi);
+    uint32_t cur = 0xffffffffu, best = 0;
+    for (uint32_t u = u0; u < u1; ++u) {
+        const float v = u2f(u);
+        const float l = og_logf_normal(v, tab);
+        const double err = __builtin_fabs(static_cast<double>(cheap_logf(v)) - static_cast<double>(l));
+        float e = static_cast<float>(err);
+        if (static_cast<double>(e) < err) e = u2f(f2u(e) + 1u);
+        const uint32_t b = f2u(__builtin_fabsf(l)) >> 23;
+        if (b != cur) {
+            if (cur != 0xffffffffu) atomicMax(&g_logb_raw[cur], best);
+            cur = b;
+            best = 0;
+        }
+        best = f2u(e) > best ? f2u(e) : best;
+    }
+    if (cur != 0xffffffffu) atomicMax(&g_logb_raw[cur], best);
+}
+
+// g_logb[e] = max of g_logb_raw[0..e] (non-negative floats order as their bits).
+__global__ void logf_bound_finish_kernel() {
+    if (threadIdx.x == 0) {
+        uint32_t m = 0;
+        for (int e = 0; e < 256; ++e) {
+            m = g_logb_raw[e] > m ? g_logb_raw[e] : m;
+            g_logb[e] = u2f(m);
+        }
+    }
+}
+
+__global__ void logf_bound_read_kernel(float* out) {
+    if (threadIdx.x < 256) out[threadIdx.x] = g_logb[threadIdx.x];
+}
+
 template <int DIM>
 constexpr size_t stage_bytes() {
     return static_cast<size_t>(WAVES) * (WAVE * (DIM + 4) + 8) * sizeof(float);
@@ -2886,6 +2999,22 @@ hipError_t allow_lds(K kernel, size_t bytes) {
 }
 
 }  // namespace
+
+int launch_logf_bound(void* stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    constexpr uint64_t threads = static_cast<uint64_t>(kLogbBlocks) * 256;
+    const uint32_t per = static_cast<uint32_t>((static_cast<uint64_t>(kLogbHi - kLogbLo) + threads - 1) / threads);
+    hipLaunchKernelGGL(logf_bound_kernel, dim3(kLogbBlocks), dim3(256), 0, st, per);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(logf_bound_finish_kernel, dim3(1), dim3(64), 0, st);
+    return hipGetLastError();
+}
+
+int launch_logf_bound_read(float* out, void* stream) {
+    hipLaunchKernelGGL(logf_bound_read_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), out);
+    return hipGetLastError();
+}
 
 int launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, void* stream) {
     if (n == 0) return hipSuccess;

@@ -75,6 +75,14 @@ class Context:
         except Exception:
             pass
 
+    def radii_log_bound(self) -> np.ndarray:
+        """The BlockLogU8 encode's cheap-log error bounds measured on this
+        device: 256 floats, entry e covering every radius whose logf has a
+        biased f32 exponent <= e (pkv_radii_log_bound)."""
+        out = np.zeros(256, np.float32)
+        L.check(L.lib().pkv_radii_log_bound(self.ptr, out.ctypes.data), "pkv_radii_log_bound")
+        return out
+
     # profiles are cached per parameters: the reference rebuilds its codebook,
     # rotation and QJL matrix on every adapter call (proveKV/src/codec.rs:249,
     # 296, 471-499); here they are built once and stay resident.
