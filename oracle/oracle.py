@@ -65,6 +65,8 @@ I32 = C.c_int
 
 
 def _declare(L):
+    L.ora_logf_bits.argtypes = [U32, U64, P]
+    L.ora_logf_bits.restype = None
     L.ora_chacha_words.argtypes = [P, I32, U64, P, U64]
     L.ora_seed_key.argtypes = [U64, P]
     L.ora_rng_u64.argtypes = [U64, P, U64]

@@ -4,7 +4,7 @@
  * TEST INFRASTRUCTURE ONLY.  Nothing in the provekv_amd product links, loads
  * or calls this file; only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py use it, and only as the checker (or as the
- * timed CPU baseline).  Plain C, compiled with -O2 -ffp-contract=off so that
+ * timed CPU baseline).  Plain C, compiled with -O3 -ffp-contract=off so that
  * every `a*b + c` rounds twice exactly like the Rust reference (Rust never
  * contracts floating-point expressions).  Transcendentals come from the host
  * glibc, which is what Rust's f32/f64 methods lower to on linux-gnu.
@@ -1694,4 +1694,15 @@ void ora_pack_bits(const uint32_t* values, uint64_t n, int bits, uint8_t* out) {
 int ora_unpack_bits(const uint8_t* in, uint64_t n, int bits, uint32_t* out) {
     for (uint64_t i = 0; i < n; ++i) out[i] = read_bits(in, i * (uint64_t)bits, bits);
     return padding_zero(in, n * (uint64_t)bits, (n * (uint64_t)bits + 7) / 8) ? ORA_OK : ORA_ERR_MALFORMED;
+}
+
+/* Host glibc logf of the n floats whose bit patterns are u0, u0 + 1, ...
+ * (test hook: exhaustive comparisons against the product's restatement). */
+void ora_logf_bits(uint32_t u0, uint64_t n, float* out) {
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint32_t u = u0 + (uint32_t)i;
+        float x;
+        memcpy(&x, &u, 4);
+        out[i] = logf(x);
+    }
 }

@@ -98,6 +98,30 @@ def test_logf_matches_glibc():
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+def test_logf_exhaustive_equal_to_glibc_and_monotone():
+    """On every normal positive float (the radii codec clamps to FLT_MIN,
+    radius.rs:61) the restated logf equals the host glibc logf bit for bit,
+    and it never decreases -- the BlockLogU8 encode takes mn / mx as the logs
+    of the smallest / largest radius on that property."""
+    from concurrent.futures import ThreadPoolExecutor
+    lo, hi, chunk = 0x00800000, 0x7f800000, 1 << 24
+    ora = O.lib()
+
+    def run(u0):
+        n = min(chunk + 1, hi - u0)   # one overlap element joins the chunks
+        x = np.arange(u0, u0 + n, dtype=np.uint32).view(np.float32)
+        got = _host_logf(x)
+        want = np.empty(n, np.float32)
+        ora.ora_logf_bits(u0, n, want.ctypes.data)
+        return (np.array_equal(got.view(np.uint32), want.view(np.uint32)),
+                bool(np.all(np.diff(got) >= 0)))
+
+    with ThreadPoolExecutor(8) as ex:
+        res = list(ex.map(run, range(lo, hi, chunk)))
+    assert all(r[0] for r in res)
+    assert all(r[1] for r in res)
+
+
 def test_expf_matches_glibc_in_radius_range():
     rng = np.random.RandomState(1)
     x = rng.uniform(-87.0, 30.0, size=200_000).astype(np.float32)
