@@ -67,6 +67,16 @@ I32 = C.c_int
 def _declare(L):
     L.ora_logf_bits.argtypes = [U32, U64, P]
     L.ora_logf_bits.restype = None
+    L.ora_track_reset.argtypes = [I32]
+    L.ora_track_reset.restype = None
+    L.ora_track_margin.argtypes = []
+    L.ora_track_margin.restype = C.c_double
+    L.ora_track_tail_logs.argtypes = [P, P, U64]
+    L.ora_track_tail_logs.restype = U64
+    L.ora_set_codebook_perturbation.argtypes = [C.c_double]
+    L.ora_set_codebook_perturbation.restype = None
+    L.ora_set_zig_glibc.argtypes = [I32]
+    L.ora_set_zig_glibc.restype = None
     L.ora_chacha_words.argtypes = [P, I32, U64, P, U64]
     L.ora_seed_key.argtypes = [U64, P]
     L.ora_rng_u64.argtypes = [U64, P, U64]

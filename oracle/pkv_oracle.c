@@ -139,14 +139,55 @@ static double rng_open01(ora_rng* r) {
  *    x0 = V/f(R), x_i = f^-1(V/x_{i-1} + f(x_{i-1})), x_256 = 0), then
  *    round-tripped through "%.18f" exactly as the generated Rust literals
  *    were written.  Pinned against remembered literals of ziggurat_tables.rs
- *    in tests/golden.
+ *    (tests/test_oracle_rng.py) and, entry by entry, against the correctly
+ *    rounded recursion (tests/test_oracle_pins.py).
  * ====================================================================== */
 static double ZX[257], ZF[257];
 static double ZIG_R;
 static int zig_ready = 0;
 
+/* Test hooks (not part of the restatement): how far the draws are from
+ * depending on the last bit of a libm result.  While g_track is set,
+ * track() keeps the smallest relative gap between the two sides of every
+ * accept / reject comparison that involves exp or log, and the tail branch
+ * records the arguments and results of its log calls (the drawn value is
+ * built from them directly). */
+static int g_track = 0;
+static double g_margin = INFINITY;
+#define ORA_TAIL_LOGS 4096
+static double g_tail_arg[ORA_TAIL_LOGS], g_tail_val[ORA_TAIL_LOGS];
+static uint64_t g_tail_n = 0;
+
+static void track(double lhs, double rhs) {
+    if (!g_track) return;
+    const double den = fabs(lhs) > fabs(rhs) ? fabs(lhs) : fabs(rhs);
+    const double m = den > 0.0 ? fabs(lhs - rhs) / den : INFINITY;
+    if (m < g_margin) g_margin = m;
+}
+
+static double tail_log(double v) {
+    const double l = log(v);
+    if (g_track) {
+        if (g_tail_n < ORA_TAIL_LOGS) { g_tail_arg[g_tail_n] = v; g_tail_val[g_tail_n] = l; }
+        g_tail_n++;
+    }
+    return l;
+}
+
 static double zig_f(double x) { return exp(-x * x / 2.0); }
-static double zig_finv(double y) { return sqrt(-2.0 * log(y)); }
+/* The table takes the correctly rounded exp / log (x87 expl / logl rounded
+ * to double: every call of the recursion lands far enough from a midpoint
+ * for that, which tests/test_oracle_pins.py checks against mpmath), so it is
+ * the table any correctly rounded libm gives -- glibc before 2.28 among
+ * them.  glibc 2.35's exp differs at one call (F[94], 1 ulp);
+ * ora_set_zig_glibc(1) rebuilds the table with it, for that comparison. */
+static int g_zig_glibc = 0;
+static double zig_f_tab(double x) {
+    const double t = -x * x / 2.0;
+    return g_zig_glibc ? exp(t) : (double)expl((long double)t);
+}
+static double zig_finv_tab(double y) { return sqrt(-2.0 * (g_zig_glibc ? log(y) : (double)logl((long double)y))); }
+void ora_set_zig_glibc(int on) { g_zig_glibc = on; zig_ready = 0; }
 
 static double round18(double v) {
     char buf[64];
@@ -158,12 +199,12 @@ static void zig_init(void) {
     if (zig_ready) return;
     const double R = 3.6541528853610088, V = 0.00492867323399;
     double x[257];
-    x[0] = V / zig_f(R);
+    x[0] = V / zig_f_tab(R);
     x[1] = R;
-    for (int i = 2; i < 256; ++i) x[i] = zig_finv(V / x[i - 1] + zig_f(x[i - 1]));
+    for (int i = 2; i < 256; ++i) x[i] = zig_finv_tab(V / x[i - 1] + zig_f_tab(x[i - 1]));
     x[256] = 0.0;
     for (int i = 0; i < 257; ++i) {
-        ZF[i] = round18(zig_f(x[i]));
+        ZF[i] = round18(zig_f_tab(x[i]));
         ZX[i] = round18(x[i]);
     }
     ZIG_R = round18(R);
@@ -183,12 +224,15 @@ static double rng_normal(ora_rng* r) {
             while (-2.0 * yy < xx * xx) {
                 double x_ = rng_open01(r);
                 double y_ = rng_open01(r);
-                xx = log(x_) / ZIG_R;
-                yy = log(y_);
+                xx = tail_log(x_) / ZIG_R;
+                yy = tail_log(y_);
+                track(-2.0 * yy, xx * xx);
             }
             return (u < 0.0) ? xx - ZIG_R : ZIG_R - xx;
         }
-        if (ZF[i + 1] + (ZF[i] - ZF[i + 1]) * rng_f64(r) < zig_f(x)) return x;
+        const double lhs = ZF[i + 1] + (ZF[i] - ZF[i + 1]) * rng_f64(r), rhs = zig_f(x);
+        track(lhs, rhs);
+        if (lhs < rhs) return x;
     }
 }
 
@@ -211,9 +255,10 @@ static double rng_gamma(ora_rng* r, const ora_gamma* g) {
         double v = v_cbrt * v_cbrt * v_cbrt;
         double u = rng_open01(r);
         double x_sqr = x * x;
-        if (u < 1.0 - 0.0331 * x_sqr * x_sqr ||
-            log(u) < 0.5 * x_sqr + g->d * (1.0 - v + log(v)))
-            return g->d * v * g->scale;
+        if (u < 1.0 - 0.0331 * x_sqr * x_sqr) return g->d * v * g->scale;
+        const double lhs = log(u), rhs = 0.5 * x_sqr + g->d * (1.0 - v + log(v));
+        track(lhs, rhs);
+        if (lhs < rhs) return g->d * v * g->scale;
     }
 }
 
@@ -628,6 +673,23 @@ static int update_centroids(double* cb, int k, int n, const double* samples, int
     return rc;
 }
 
+/* Test hook (not part of the restatement): every initial codeword
+ * coordinate and every restart's rotated start is multiplied by
+ * 1 +- g_perturb (sign from a fixed pseudo-random pattern), standing in for
+ * last-bit differences of the inverse CDFs (statrs) and of the k x k QR
+ * (nalgebra) behind them. */
+static double g_perturb = 0.0;
+static void perturb(double* v, size_t n, uint64_t salt) {
+    if (g_perturb == 0.0) return;
+    for (size_t t = 0; t < n; ++t) {
+        uint64_t h = (t + 1) * 0x9e3779b97f4a7c15ull ^ salt;
+        h ^= h >> 29;
+        h *= 0xbf58476d1ce4e5b9ull;
+        h ^= h >> 32;
+        v[t] *= (h & 1) ? 1.0 + g_perturb : 1.0 - g_perturb;
+    }
+}
+
 /* Build the (N x k) f32 codebook; returns init/training mse. */
 static int fib_codebook(int d, int k, int n, uint64_t seed, int training, int restarts, int iterations,
                         float* out, double* init_mse_out, double* train_mse_out) {
@@ -647,6 +709,7 @@ static int fib_codebook(int d, int k, int n, uint64_t seed, int training, int re
         double rad = radius_quantile(d, k, idx + 1, n);
         for (int t = 0; t < k; ++t) init[(size_t)idx * k + t] = rad * dirs[(size_t)idx * k + t];
     }
+    perturb(init, nk, 0);
     {
         ora_rng r;
         rng_seed_from_u64(&r, cseed ^ 0x465155414e54ull);
@@ -667,6 +730,7 @@ static int fib_codebook(int d, int k, int n, uint64_t seed, int training, int re
             rc = stored_rotation(k, cseed + (uint64_t)rs * 0x9e3779b9ull, rot);
             if (rc != ORA_OK) goto done;
             for (int w = 0; w < n; ++w) rot_apply_f64(k, rot, init + (size_t)w * k, cbk + (size_t)w * k);
+            perturb(cbk, nk, (uint64_t)rs);
         }
         for (int it = 0; it < iterations; ++it) {
             for (int i = 0; i < ns; ++i) asg[i] = nearest_index_f64(samples + (size_t)i * k, cbk, k, n, NULL);
@@ -1695,6 +1759,15 @@ int ora_unpack_bits(const uint8_t* in, uint64_t n, int bits, uint32_t* out) {
     for (uint64_t i = 0; i < n; ++i) out[i] = read_bits(in, i * (uint64_t)bits, bits);
     return padding_zero(in, n * (uint64_t)bits, (n * (uint64_t)bits + 7) / 8) ? ORA_OK : ORA_ERR_MALFORMED;
 }
+
+void ora_track_reset(int on) { g_track = on; g_margin = INFINITY; g_tail_n = 0; }
+double ora_track_margin(void) { return g_margin; }
+uint64_t ora_track_tail_logs(double* args, double* vals, uint64_t cap) {
+    const uint64_t n = g_tail_n < ORA_TAIL_LOGS ? g_tail_n : ORA_TAIL_LOGS;
+    for (uint64_t i = 0; i < n && i < cap; ++i) { args[i] = g_tail_arg[i]; vals[i] = g_tail_val[i]; }
+    return g_tail_n;
+}
+void ora_set_codebook_perturbation(double rel) { g_perturb = rel; }
 
 /* Host glibc logf of the n floats whose bit patterns are u0, u0 + 1, ...
  * (test hook: exhaustive comparisons against the product's restatement). */

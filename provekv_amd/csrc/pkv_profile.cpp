@@ -111,8 +111,16 @@ struct ZigTables {
     ZigTables() {
         // rand's ziggurat_tables.py recipe, printed with "%.18f" into the
         // Rust source; the literals are reproduced by formatting the same way.
-        auto fdens = [](double v) { return std::exp(-v * v / 2.0); };
-        auto finv = [](double y) { return std::sqrt(-2.0 * std::log(y)); };
+        // exp / log correctly rounded (x87 extended precision rounded to
+        // double; every call of this recursion sits far enough from a
+        // rounding midpoint): the table of any correctly rounded libm.
+        auto fdens = [](double v) {
+            const double t = -v * v / 2.0;
+            return static_cast<double>(std::exp(static_cast<long double>(t)));
+        };
+        auto finv = [](double y) {
+            return std::sqrt(-2.0 * static_cast<double>(std::log(static_cast<long double>(y))));
+        };
         auto lit = [](double v) {
             char buf[64];
             std::snprintf(buf, sizeof buf, "%.18f", v);
