@@ -780,15 +780,11 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
             }
         };
         load_half(y);
-        bool finite = true;
         {
             uint32_t m = smask;
             asm volatile("" : "+v"(m));
 #pragma unroll
-            for (int c = 0; c < 32; ++c) {
-                finite &= isfinite_f(y[c]);
-                y[c] = flip(y[c], m, c);
-            }
+            for (int c = 0; c < 32; ++c) y[c] = flip(y[c], m, c);
         }
         fwht_split(y, h);
 #pragma unroll
@@ -801,21 +797,27 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
 
         // radii and angle bins (polar.rs:246-266, 413-421) of pairs 16h + i
         float r[HP];
-        bool rfinite = true;
+        float rsum = 0.0f;
         uint64_t pk = 0;
-        uint32_t slow = 0;
+        uint64_t unsafe[HP];   // per pair: the wave's lanes whose bin needs the exact formula
 #pragma unroll
         for (int i = 0; i < HP; ++i) {
             const float a = y[2 * i], b = y[2 * i + 1];
             const float aa = a * a, bb = b * b;
             r[i] = __builtin_sqrtf(aa + bb);
-            rfinite &= isfinite_f(r[i]);
-            uint32_t safe = 0u;
-            const uint32_t bin = PB == 3 ? octant_bin_u(a, b, safe) : 0u;
+            rsum = rsum + r[i];
+            bool safe = false;
+            const uint32_t bin = PB == 3 ? octant_bin_m(a, b, safe) : 0u;
             pk |= static_cast<uint64_t>(bin) << (static_cast<uint32_t>(i) * pbits);
-            slow |= (safe ^ 1u) << i;
+            unsafe[i] = __ballot(!safe);
         }
-        if (slow) {   // pairs near an octant line (every pair at other widths): the exact formula
+        uint64_t any_unsafe = 0;
+#pragma unroll
+        for (int i = 0; i < HP; ++i) any_unsafe |= unsafe[i];
+        if (any_unsafe) {   // pairs near an octant line (every pair at other widths): the exact formula
+            uint32_t slow = 0;
+#pragma unroll
+            for (int i = 0; i < HP; ++i) slow |= static_cast<uint32_t>((unsafe[i] >> lane) & 1u) << i;
             for (uint32_t m = slow; m; m &= m - 1u) {
                 const uint32_t i = static_cast<uint32_t>(__ffs(m) - 1);
                 // pair i by selects (a dynamic index into y would go through scratch)
@@ -828,6 +830,19 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
                 const uint64_t bin = angle_bin_exact(a, b, pbits);
                 pk = (pk & ~(static_cast<uint64_t>(levels - 1u) << (i * pbits))) | (bin << (i * pbits));
             }
+        }
+        // A non-finite input makes every FWHT output, so every radius,
+        // non-finite; a finite sum of the (non-negative) radii therefore
+        // clears both checks.  Otherwise (or on an overflowing sum) they run
+        // element by element.
+        bool finite = true, rfinite = true;
+        if (!isfinite_f(rsum)) {
+            float x[32];
+            load_half(x);
+#pragma unroll
+            for (int c = 0; c < 32; ++c) finite &= isfinite_f(x[c]);
+#pragma unroll
+            for (int i = 0; i < HP; ++i) rfinite &= isfinite_f(r[i]);
         }
         // angle indices, pbits each, LSB-first (bitpack.rs:21-35): this half's
         // 16 * pbits bits start at bit 16 * pbits * h
@@ -883,12 +898,14 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
 #pragma unroll
             for (int c = 0; c < 32; ++c) y[c] = x[c] - flip(y[c] * scale, m, c);
         }
-        bool resfinite = true;
         float rn2 = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 32; ++c) {
-            resfinite &= isfinite_f(y[c]);
-            rn2 = __builtin_fmaf(y[c], y[c], rn2);
+        for (int c = 0; c < 32; ++c) rn2 = __builtin_fmaf(y[c], y[c], rn2);
+        // squares are non-negative: a finite sum clears every element
+        bool resfinite = true;
+        if (!isfinite_f(rn2)) {
+#pragma unroll
+            for (int c = 0; c < 32; ++c) resfinite &= isfinite_f(y[c]);
         }
         rn2 = rn2 + u2f(partner(f2u(rn2), h));
         const float rn = __builtin_sqrtf(rn2) * 1.0001f;   // |res|, rounded up far past its f32 error
@@ -1129,15 +1146,11 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
             }
         };
         load_quarter(y);
-        bool finite = true;
         {
             float sg[32];
             load_signs(sg);
 #pragma unroll
-            for (int c = 0; c < 32; ++c) {
-                finite &= isfinite_f(y[c]);
-                y[c] = y[c] * sg[c];
-            }
+            for (int c = 0; c < 32; ++c) y[c] = y[c] * sg[c];
         }
         fwht_quarter(y, q);
 #pragma unroll
@@ -1150,21 +1163,27 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
 
         // radii and angle bins (polar.rs:246-266, 413-421) of pairs 16q + i
         float r[HP];
-        bool rfinite = true;
+        float rsum = 0.0f;
         uint64_t pk = 0;
-        uint32_t slow = 0;
+        uint64_t unsafe[HP];   // per pair: the wave's lanes whose bin needs the exact formula
 #pragma unroll
         for (int i = 0; i < HP; ++i) {
             const float a = y[2 * i], b = y[2 * i + 1];
             const float aa = a * a, bb = b * b;
             r[i] = __builtin_sqrtf(aa + bb);
-            rfinite &= isfinite_f(r[i]);
-            uint32_t safe = 0u;
-            const uint32_t bin = PB == 3 ? octant_bin_u(a, b, safe) : 0u;
+            rsum = rsum + r[i];
+            bool safe = false;
+            const uint32_t bin = PB == 3 ? octant_bin_m(a, b, safe) : 0u;
             pk |= static_cast<uint64_t>(bin) << (static_cast<uint32_t>(i) * pbits);
-            slow |= (safe ^ 1u) << i;
+            unsafe[i] = __ballot(!safe);
         }
-        if (slow) {   // pairs near an octant line (every pair at other widths): the exact formula
+        uint64_t any_unsafe = 0;
+#pragma unroll
+        for (int i = 0; i < HP; ++i) any_unsafe |= unsafe[i];
+        if (any_unsafe) {   // pairs near an octant line (every pair at other widths): the exact formula
+            uint32_t slow = 0;
+#pragma unroll
+            for (int i = 0; i < HP; ++i) slow |= static_cast<uint32_t>((unsafe[i] >> lane) & 1u) << i;
             for (uint32_t m = slow; m; m &= m - 1u) {
                 const uint32_t i = static_cast<uint32_t>(__ffs(m) - 1);
                 // pair i by selects (a dynamic index into y would go through scratch)
@@ -1177,6 +1196,19 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
                 const uint64_t bin = angle_bin_exact(a, b, pbits);
                 pk = (pk & ~(static_cast<uint64_t>(levels - 1u) << (i * pbits))) | (bin << (i * pbits));
             }
+        }
+        // A non-finite input makes every FWHT output, so every radius,
+        // non-finite; a finite sum of the (non-negative) radii therefore
+        // clears both checks.  Otherwise (or on an overflowing sum) they run
+        // element by element.
+        bool finite = true, rfinite = true;
+        if (!isfinite_f(rsum)) {
+            float x[32];
+            load_quarter(x);
+#pragma unroll
+            for (int c = 0; c < 32; ++c) finite &= isfinite_f(x[c]);
+#pragma unroll
+            for (int i = 0; i < HP; ++i) rfinite &= isfinite_f(r[i]);
         }
         // angle indices, pbits each, LSB-first (bitpack.rs:21-35): this
         // quarter's 16 * pbits bits start at bit 16 * pbits * q
@@ -1228,12 +1260,14 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
 #pragma unroll
             for (int c = 0; c < 32; ++c) y[c] = x[c] - (y[c] * scale) * sg[c];
         }
-        bool resfinite = true;
         float rn2 = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 32; ++c) {
-            resfinite &= isfinite_f(y[c]);
-            rn2 = __builtin_fmaf(y[c], y[c], rn2);
+        for (int c = 0; c < 32; ++c) rn2 = __builtin_fmaf(y[c], y[c], rn2);
+        // squares are non-negative: a finite sum clears every element
+        bool resfinite = true;
+        if (!isfinite_f(rn2)) {
+#pragma unroll
+            for (int c = 0; c < 32; ++c) resfinite &= isfinite_f(y[c]);
         }
         rn2 = rn2 + u2f(partner16(f2u(rn2), q));
         rn2 = rn2 + u2f(partner(f2u(rn2), q >> 1));

@@ -175,6 +175,34 @@ PKV_HD uint32_t octant_bin_u(float a, float b, uint32_t& safe) {
     return bin;
 }
 
+// octant_bin_u for the batched encodes: the bin from three sign bits
+// (bit 2: b is not negative; bit 1: sign(a) != sign(b); bit 0: (|b| < |a|)
+// == (sign(a) != sign(b)) -- the same table as octant_bin wherever a and b
+// are non-zero, which every safe pair is), and the safety test as four
+// unsigned compares of the same bit patterns (lane masks on the device, so a
+// wave can test them all at once).  safe agrees with octant_bin_u on every
+// input; the bin of an unsafe pair is not used.
+PKV_HD uint32_t octant_bin_m(float a, float b, bool& safe) {
+    uint32_t xa, xb;
+    __builtin_memcpy(&xa, &a, 4);
+    __builtin_memcpy(&xb, &b, 4);
+    const uint32_t ua = xa & 0x7fffffffu, ub = xb & 0x7fffffffu;
+    const uint32_t t = xa ^ xb;
+    const uint32_t e = ~((ub - ua) ^ t);   // bit 31: (|b| < |a|) xnor (sign(a) xor sign(b))
+    const uint32_t bin = ((~xb >> 29) & 4u) | ((t >> 30) & 2u) | (e >> 31);
+    const uint32_t mx = ua > ub ? ua : ub, mn = ua > ub ? ub : ua;
+    const uint32_t eps = mx - (16u << 23);   // wraps for mx < 2^-110, which fails the range test
+    float fa, fb;
+    __builtin_memcpy(&fa, &ua, 4);
+    __builtin_memcpy(&fb, &ub, 4);
+    const float g = fa - fb;
+    uint32_t ug;
+    __builtin_memcpy(&ug, &g, 4);
+    ug &= 0x7fffffffu;
+    safe = (eps < mn) & (eps < ug) & (0x0da24260u < mx) & (mx < 0x7149f2cau);   // 1e-30f < mx < 1e30f
+    return bin;
+}
+
 PKV_HD uint32_t angle_bin3(float a, float b) {
     bool safe;
     uint32_t bin = octant_bin(a, b, safe);
