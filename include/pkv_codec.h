@@ -61,7 +61,11 @@ typedef struct pkv_ctx pkv_ctx;
 typedef struct pkv_profile pkv_profile;
 
 /* Replaces GpuContext::init / is_available (gpu-backend/src/lib.rs:41-58):
- * binds a context to HIP device `device` (an index, 0 = first). */
+ * binds a context to HIP device `device` (an index, 0 = first).  The first
+ * context on a device also runs the device checks the encodes' proofs rest
+ * on: it measures the BlockLogU8 log bound (pkv_radii_log_bound) and checks
+ * that the f16 matrix cores keep subnormal operands (the QJL acceptance
+ * bound assumes it); PKV_ERR_UNSUPPORTED if they do not. */
 int pkv_ctx_create(int device, pkv_ctx** out);
 void pkv_ctx_destroy(pkv_ctx* ctx);
 /* 1 if a gfx950 device is usable, 0 otherwise (never errors). */

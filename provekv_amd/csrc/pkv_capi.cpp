@@ -98,11 +98,12 @@ struct pkv_profile {
     // turbo
     uint32_t bits = 0, pbits = 0, proj = 0, mode = 0;
     uint64_t seed = 0;
-    std::vector<float> signs, qjl, cs, qa, qb;
+    std::vector<float> signs, qjl, cs, qb;
+    std::vector<uint32_t> qa;
     float* d_signs = nullptr;
     float* d_qjl = nullptr;
     float* d_cs = nullptr;
-    float* d_qa = nullptr;
+    uint32_t* d_qa = nullptr;
     float* d_qb = nullptr;
     // fib
     uint32_t k = 0, n = 0, wbits = 0;
@@ -161,15 +162,23 @@ int noalloc_scratch(int device, uint8_t** out) {
 std::mutex g_logb_mu;
 bool g_logb_done[kMaxDevices] = {};
 
-// The cheap-log bound table of the BlockLogU8 encodes, measured once per
-// device (the caller has made it current) before the first context there
-// returns.
-int logf_bound_once(int device, hipStream_t st) {
+// Once per device (the caller has made it current), before the first
+// context there returns: measure the cheap-log bound table of the BlockLogU8
+// encodes, and check that the f16 matrix cores keep subnormal operands (the
+// QJL acceptance bound counts on it; a device that flushes them is refused).
+int device_checks_once(int device, hipStream_t st) {
     std::lock_guard<std::mutex> lock(g_logb_mu);
     if (device >= 0 && device < kMaxDevices && g_logb_done[device]) return PKV_OK;
+    float* d = nullptr;
+    HIP_TRY(hipMalloc(&d, 2 * sizeof(float)));
+    float got[2] = {0.0f, 0.0f};
     hipError_t e = static_cast<hipError_t>(launch_logf_bound(st));
+    if (e == hipSuccess) e = static_cast<hipError_t>(launch_f16_subnormal_probe(d, st));
+    if (e == hipSuccess) e = hipMemcpyAsync(got, d, sizeof got, hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
+    (void)hipFree(d);
     if (e != hipSuccess) return hip_status(e);
+    if (got[0] != 0x1p-10f + 0x1p-14f || got[1] != 0x1p-10f) return PKV_ERR_UNSUPPORTED;
     if (device >= 0 && device < kMaxDevices) g_logb_done[device] = true;
     return PKV_OK;
 }
@@ -623,7 +632,7 @@ int pkv_ctx_create(int device, pkv_ctx** out) {
     hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
     if (e != hipSuccess) { delete c; return hip_status(e); }
     int rc = noalloc_scratch(device, &c->noalloc);   // device is current
-    if (!rc) rc = logf_bound_once(device, c->own_stream);
+    if (!rc) rc = device_checks_once(device, c->own_stream);
     if (rc) { (void)hipStreamDestroy(c->own_stream); delete c; return rc; }
     *out = c;
     return PKV_OK;
@@ -647,32 +656,50 @@ void pkv_ctx_destroy(pkv_ctx* ctx) {
     delete ctx;
 }
 
-// Operands of the head_dim-64 QJL MFMA path (layout in TurboDev).
-// Operands of the QJL matrix-core path.  Head_dim 64 (v_mfma_f32_32x32x2_f32,
-// 32-projection tiles): qa[t][c][lane] = G[32t + lane % 32][32 (lane / 32) + c],
-// qb[t][r][lane] = bound of projection 32t + 8 (r / 4) + 4 (lane / 32) + r % 4.
-// Head_dim 128 (v_mfma_f32_16x16x4_f32, 16-projection tiles):
-// qa[t][c][lane] = G[16t + lane % 16][32 (lane / 16) + c],
-// qb[t][r][lane] = bound of projection 16t + 4 (lane / 16) + r.
-// bound_j = k u |g_j| (1 + 2^-10), rounded up, u = 2^-24, k = 200 (64) or
-// 400 (128): the reference's sequential dot is within (d + 2)u sum|g_c res_c|
-// and the matrix core's within (2d + 2)u.
+// Operands of the QJL matrix-core path: each dot is three products on the f16
+// matrix cores, Gh xh + Gh xl + Gl xh, with G = Gh + Gl + eG split here
+// (round to nearest even: Gh = f16(G), Gl = f16(G - Gh)) and the scaled
+// residual x = xh + xl + ex split in the kernel.  Per tile t (16 projections
+// on v_mfma_f32_16x16x32_f16 at head_dim 128, 32 on v_mfma_f32_32x32x16_f16 at
+// head_dim 64), K step s and half (0: Gh, 1: Gl):
+//   qa[((t * 4 + s) * 2 + half) * 64 + lane] (4 words: 8 f16, j = 0..7) =
+//       G[16t + lane % 16][32 (lane / 16) + 8s + j]      (head_dim 128)
+//       G[32t + lane % 32][32 (lane / 32) + 8s + j]      (head_dim 64)
+//   qb[((t * nb + r) * 64 + lane) * 2 + {0, 1}] = (a_j, b_j) of the projection
+//       j in accumulator register r: 16t + 4 (lane / 16) + r (128),
+//       32t + 8 (r / 4) + 4 (lane / 32) + r % 4 (64);
+// a sign is kept when |acc| > a_j xn + b_j, xn >= |x| (derivation at
+// turbo_encode_qjl_kernel):
+//   a_j = ((7.1 d + 30) u |g_j| + 1.001 * 2^-25 sqrt(d)) (1 + 2^-10),
+//   b_j = (1.002 * 2^-24 sqrt(d) |g_j| + d 2^-49) (1 + 2^-10), u = 2^-24,
+// each rounded up to f32.
 static void turbo_qjl_mfma_constants(pkv_profile* p) {
     const uint32_t dim = p->dim;
     const bool wide = dim == 128;
     const uint32_t tp = wide ? 16 : 32;                 // projections per tile
     const uint32_t tiles = p->proj / tp, nb = wide ? 4 : 16;
-    p->qa.assign(static_cast<size_t>(tiles) * 32 * 64, 0.0f);
-    p->qb.assign(static_cast<size_t>(tiles) * nb * 64, 0.0f);
-    const double u = std::ldexp(1.0, -24);
-    const double k = wide ? 400.0 : 200.0;
+    p->qa.assign(static_cast<size_t>(tiles) * 4 * 2 * 64 * 4, 0u);
+    p->qb.assign(static_cast<size_t>(tiles) * nb * 64 * 2, 0.0f);
+    const double u = std::ldexp(1.0, -24), d = static_cast<double>(dim), sd = std::sqrt(d);
+    auto up = [](double v) {
+        float f = static_cast<float>(v);
+        if (static_cast<double>(f) < v) f = std::nextafter(f, std::numeric_limits<float>::infinity());
+        return f;
+    };
     for (uint32_t t = 0; t < tiles; ++t)
         for (uint32_t lane = 0; lane < 64; ++lane) {
-            for (uint32_t c = 0; c < 32; ++c) {
-                const uint32_t row = wide ? 16 * t + lane % 16 : 32 * t + lane % 32;
-                const uint32_t col = wide ? 32 * (lane / 16) + c : 32 * (lane / 32) + c;
-                p->qa[(t * 32 + c) * 64 + lane] = p->qjl[static_cast<size_t>(row) * dim + col];
-            }
+            const uint32_t row = wide ? 16 * t + lane % 16 : 32 * t + lane % 32;
+            const uint32_t col0 = wide ? 32 * (lane / 16) : 32 * (lane / 32);
+            for (uint32_t st = 0; st < 4; ++st)
+                for (uint32_t j = 0; j < 8; ++j) {
+                    const float g = p->qjl[static_cast<size_t>(row) * dim + col0 + 8 * st + j];
+                    const uint16_t gh = f32_to_f16(g);
+                    const uint16_t gl = f32_to_f16(g - f16_to_f32(gh));   // g - gh is exact in f32
+                    const size_t w0 = (((t * 4 + st) * 2 + 0) * 64 + lane) * 4 + j / 2;
+                    const size_t w1 = (((t * 4 + st) * 2 + 1) * 64 + lane) * 4 + j / 2;
+                    p->qa[w0] |= static_cast<uint32_t>(gh) << (16 * (j & 1));
+                    p->qa[w1] |= static_cast<uint32_t>(gl) << (16 * (j & 1));
+                }
             for (uint32_t r = 0; r < nb; ++r) {
                 const uint32_t j = wide ? 16 * t + 4 * (lane / 16) + r : 32 * t + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
                 double g2 = 0.0;
@@ -680,10 +707,12 @@ static void turbo_qjl_mfma_constants(pkv_profile* p) {
                     const double g = p->qjl[static_cast<size_t>(j) * dim + c];
                     g2 += g * g;
                 }
-                const double b = k * u * std::sqrt(g2) * (1.0 + std::ldexp(1.0, -10));
-                float bf = static_cast<float>(b);
-                if (static_cast<double>(bf) < b) bf = std::nextafter(bf, std::numeric_limits<float>::infinity());
-                p->qb[(t * nb + r) * 64 + lane] = bf;
+                const double gn = std::sqrt(g2) * (1.0 + std::ldexp(1.0, -40));   // >= |g_j|
+                const double safety = 1.0 + std::ldexp(1.0, -10);
+                const double aj = ((7.1 * d + 30.0) * u * gn + 1.001 * std::ldexp(sd, -25)) * safety;
+                const double bj = (1.002 * std::ldexp(sd, -24) * gn + d * std::ldexp(1.0, -49)) * safety;
+                p->qb[((t * nb + r) * 64 + lane) * 2 + 0] = up(aj);
+                p->qb[((t * nb + r) * 64 + lane) * 2 + 1] = up(bj);
             }
         }
 }

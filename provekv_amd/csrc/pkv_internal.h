@@ -42,11 +42,10 @@ struct TurboDev {
     const float* signs;     // dim
     const float* qjl;       // proj * dim, row-major
     const float* cs;        // 2 * levels: cos, sin of each dequantized angle
-    // QJL sketch on the matrix cores (head_dim 64 with QJL), per 32-projection tile p:
-    //   qa [p][c 32][lane 64] = G[32p + lane % 32][32 (lane / 32) + c]
-    //   qb [p][q 16][lane 64] = 200 * 2^-24 * |G_j| * (1 + 2^-10), rounded up, for
-    //                           j = 32p + 8(q/4) + 4(lane/32) + q%4
-    const float* qa;
+    // QJL sketch on the f16 matrix cores (head_dim 64 / 128 with QJL): G's f16
+    // halves as MFMA A operands (qa) and per-projection acceptance-bound
+    // coefficients (qb); layouts at turbo_qjl_mfma_constants (pkv_capi.cpp)
+    const uint32_t* qa;
     const float* qb;
     uint64_t seed;
     uint32_t dim, pbits, proj, mode;
@@ -140,6 +139,8 @@ int launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, void* stream);
 // Measure the cheap-log bound table the BlockLogU8 encodes read (once per
 // device, before any encode there); copy it (256 floats) to device memory.
 int launch_logf_bound(void* stream);
+// 2 floats: matrix-core products with subnormal f16 operands (expected 2^-10 + 2^-14, 2^-10).
+int launch_f16_subnormal_probe(float* out, void* stream);
 int launch_logf_bound_read(float* out, void* stream);
 int launch_fib_product_check(const float* rot32, const float* cb, uint32_t* bad, void* stream);
 

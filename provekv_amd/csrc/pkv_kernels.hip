@@ -551,16 +551,12 @@ __global__ __launch_bounds__(TILE) void turbo_encode_kernel(
 // and stage 32 pairs the halves through v_permlane32_swap (same operands,
 // same rounding); radii and angle bins are per pair; the residual is exact.
 // Of the QJL sketch only the signs of the 32 (or 64) sequential f32 dots
-// reach the wire (qjl.rs:203-220), and this layout is already the B operand
-// of v_mfma_f32_32x32x2_f32 (K-step c: dimension 32h + c), so the dots come
-// from the matrix cores.  A sign is taken when |dot'| > bound_j * |res|,
-// where bound_j = 200 * 2^-24 * |g_j| (1 + 2^-10) covers the reference's
-// rounding (64 products and sums, <= 66u sum|g_c res_c|) and the MFMA's
-// (<= 130u, twice the sequential count) with sum|g_c res_c| <= |g_j| |res|;
-// the other dots (about 1e-4 of them) are recomputed in the reference's
-// order, the first half's partial sum handed to the second half.
-constexpr int QA_PER_TILE = 32 * 64;   // A operand floats of one 32-projection tile
-constexpr int QB_PER_TILE = 16 * 64;   // bound floats of one 32-projection tile
+// reach the wire (qjl.rs:203-220), so the dots come from the f16 matrix
+// cores (v_mfma_f32_32x32x16_f16 on the halves of the scaled residual; lane
+// (h, n) gives the B operand's column n, K step st covers dimensions
+// 32h + 8st .. 32h + 8st + 7) and a sign is taken only past the proven bound
+// at qjl_scale; the other dots are recomputed in the reference's order, the
+// first half's partial sum handed to the second half.
 
 // Value of the other half-wave's lane (l ^ 32).
 __device__ __forceinline__ uint32_t partner(uint32_t x, int h) {
@@ -692,12 +688,57 @@ __device__ __forceinline__ void block_log_u8(const float (&r)[16], int part, con
     }
 }
 
-// DIAG: also write every projection's matrix-core dot and acceptance bound to
-// lc.diag[((vector * proj) + j) * 2 + {0, 1}].
+// QJL dots on the f16 matrix cores.  Per vector the residual is scaled by
+// s = 2^k so that max |x| lies in [2^14, 2^15) (x = res * s, exact), and
+// split toward zero into f16 halves, x = xh + xl + ex with |ex| <= 2^-20 |x|
+// + 2^-24; the host splits G = Gh + Gl + eG to nearest, |eG| <= 2^-22 |G| +
+// 2^-25.  The matrix cores form acc = sum_c Gh xh + Gh xl + Gl xh (f16
+// products are exact in f32, and subnormal f16 operands are kept: checked on
+// the device by the test suite).  Per element, G x - (Gh xh + Gh xl + Gl xh)
+// = eG x + Gh ex + Gl (x - xh), at most 28.1u |G||x| + 1.001 * 2^-25 |x| +
+// 1.002 * 2^-24 |G| + 2^-49 (u = 2^-24); the 3d products accumulate with at
+// most 3d roundings, taken at 2u each: 6.03d u sum|G x|; the reference's
+// sequential f32 dot is within (d + 0.01)u sum|G_c res_c| of the exact one.
+// With sum|G x| <= |g_j| |x| and |x| <= xn, the sign of acc is the sign of
+// the reference's dot whenever |acc| > a_j xn + b_j (a_j, b_j built at
+// turbo_qjl_mfma_constants with a (1 + 2^-10) margin, which also covers the
+// rounding of the bound itself); the others are recomputed in the
+// reference's order.
+//
+__device__ __forceinline__ v16f mfma16(const v4u& a, const v4u& b, const v16f& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ v4f mfma16x32(const v4u& a, const v4u& b, const v4f& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+}
+
+// 2^(14 - e) for the exponent e of amax (clamped to [-100, 127]).
+__device__ __forceinline__ float qjl_scale(float amax) {
+    int e = static_cast<int>((f2u(amax) >> 23) & 0xffu) - 127;
+    e = e < -100 ? -100 : (e > 127 ? 127 : e);
+    return u2f(static_cast<uint32_t>(127 + 14 - e) << 23);
+}
+
+// x = v[c0 + j] * sc, j = 0..7, as f16 halves toward zero: xh = f16(x),
+// xl = f16(x - xh) (x - xh is exact in f32).
+__device__ __forceinline__ void qjl_split8(const float (&v)[32], int c0, float sc, v4u& xh, v4u& xl) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const float a = v[c0 + 2 * t] * sc, b = v[c0 + 2 * t + 1] * sc;
+        const auto h = __builtin_amdgcn_cvt_pkrtz(a, b);
+        const auto l = __builtin_amdgcn_cvt_pkrtz(a - static_cast<float>(h[0]), b - static_cast<float>(h[1]));
+        xh[t] = __builtin_bit_cast(uint32_t, h);
+        xl[t] = __builtin_bit_cast(uint32_t, l);
+    }
+}
+
+// DIAG: also write every projection's matrix-core dot and acceptance bound
+// (divided by the residual's scale) to lc.diag[((vector * proj) + j) * 2 + {0, 1}].
 template <int PB, bool DIAG>
 __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
     LaunchCommon lc, const void* __restrict__ in, uint8_t* __restrict__ wire, const float* __restrict__ signs,
-    const float* __restrict__ qjl, const float* __restrict__ cs_tab, const float* __restrict__ qa,
+    const float* __restrict__ qjl, const float* __restrict__ cs_tab, const uint32_t* __restrict__ qa,
     const float* __restrict__ qb, uint64_t seed, uint32_t pbits_rt, uint32_t proj) {
     constexpr int DIM = 64;
     constexpr int HP = 16;   // pairs per lane
@@ -910,30 +951,49 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
         rn2 = rn2 + u2f(partner(f2u(rn2), h));
         const float rn = __builtin_sqrtf(rn2) * 1.0001f;   // |res|, rounded up far past its f32 error
 
+        // QJL dots on the f16 matrix cores (v_mfma_f32_32x32x16_f16; bound at
+        // qjl_scale): K step st covers dimensions 32h + 8st + j of lane (h, n)
+        float amax = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 32; ++c) amax = __builtin_fmaxf(amax, __builtin_fabsf(y[c]));
+        amax = __builtin_fmaxf(amax, u2f(partner(f2u(amax), h)));
+        const float sc = qjl_scale(amax);
+        const float xn = rn * sc;
         uint32_t sbits[2] = {0u, 0u}, unc[2] = {0u, 0u};
         const uint32_t ptiles = proj / 32;
+        v16f acc[2] = {};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            v4u xh, xl;
+            qjl_split8(y, 8 * st, sc, xh, xl);
+#pragma unroll
+            for (uint32_t p = 0; p < 2; ++p) {
+                if (p >= ptiles) break;
+                const v4u* a = reinterpret_cast<const v4u*>(qa) + (p * 4 + st) * 2 * 64 + lane;
+                const v4u ah = a[0], al = a[64];
+                acc[p] = mfma16(ah, xh, acc[p]);
+                acc[p] = mfma16(ah, xl, acc[p]);
+                acc[p] = mfma16(al, xh, acc[p]);
+            }
+        }
 #pragma unroll
         for (uint32_t p = 0; p < 2; ++p) {
             if (p >= ptiles) break;
-            const float* qa_p = qa + p * QA_PER_TILE;
-            const float* qb_p = qb + p * QB_PER_TILE;
-            v16f acc = {};
-#pragma unroll
-            for (int c = 0; c < 32; ++c)
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa_p[c * 64 + lane], y[c], acc, 0, 0, 0);
+            const float2* ab = reinterpret_cast<const float2*>(qb) + p * 16 * 64 + lane;
             // accumulator register q: projection 32p + 8(q/4) + 4h + q%4 of vector n
             uint32_t sb = 0, un = 0;
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const uint32_t j = static_cast<uint32_t>(8 * (q >> 2) + 4 * h + (q & 3));
-                const float bnd = qb_p[q * 64 + lane] * rn;
-                sb |= (acc[q] >= 0.0f ? 1u : 0u) << j;
-                un |= (__builtin_fabsf(acc[q]) > bnd ? 0u : 1u) << j;
+                const float2 c = ab[q * 64];
+                const float bnd = __builtin_fmaf(c.x, xn, c.y);
+                sb |= (acc[p][q] >= 0.0f ? 1u : 0u) << j;
+                un |= (__builtin_fabsf(acc[p][q]) > bnd ? 0u : 1u) << j;
                 if constexpr (DIAG) {
                     if (active) {
                         float* dv = lc.diag + (static_cast<uint64_t>(t0 + static_cast<uint32_t>(n)) * proj + 32u * p + j) * 2u;
-                        dv[0] = acc[q];
-                        dv[1] = bnd;
+                        dv[0] = acc[p][q] / sc;
+                        dv[1] = bnd / sc;
                     }
                 }
             }
@@ -1014,17 +1074,12 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
 // stages 1..16 run in registers, stage 32 pairs quarters q and q ^ 1 through
 // v_permlane16_swap, stage 64 pairs q and q ^ 2 through v_permlane32_swap
 // (same operands and rounding as fwht_normalized).  The QJL dots come from
-// v_mfma_f32_16x16x4_f32: its B operand takes lane (q, n) as (K slot q,
-// column n), so K-step c covers dimensions 32q + c of the 16 vectors, and
-// a 16-projection tile accumulates in 4 registers per lane (projection
-// 16p + 4q + r of vector n in register r).  A sign is taken when
-// |dot'| > 400 * 2^-24 * |g_j| * |res| * (1 + 2^-10): the reference's 128
-// sequential products and sums stay within 130u sum|g_c res_c| and the
-// matrix core's within 258u (twice the sequential count), with
-// sum|g_c res_c| <= |g_j| |res|; the other dots are recomputed in the
-// reference's order, each quarter continuing the previous quarter's sum.
-constexpr int QA128_PER_TILE = 32 * 64;   // A operand floats of one 16-projection tile
-constexpr int QB128_PER_TILE = 4 * 64;    // bound floats of one 16-projection tile
+// v_mfma_f32_16x16x32_f16 on the f16 halves of the scaled residual (bound at
+// qjl_scale): lane (q, n) gives the B operand's column n, and K step st
+// covers dimensions 32q + 8st .. 32q + 8st + 7; a 16-projection tile
+// accumulates in 4 registers per lane (projection 16p + 4q + r of vector n in
+// register r).  The undecided dots are recomputed in the reference's order,
+// each quarter continuing the previous quarter's sum.
 
 // Value of lane l ^ 16 (the other quarter of the same half).
 // fwht_normalized stages (turbo-quant/src/rotation.rs:379-398) on a 128-wide
@@ -1074,7 +1129,7 @@ __device__ __forceinline__ uint32_t or_quarters(uint32_t x, int q) {
 template <int PB, bool DIAG>
 __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
     LaunchCommon lc, const void* __restrict__ in, uint8_t* __restrict__ wire, const float* __restrict__ signs,
-    const float* __restrict__ qjl, const float* __restrict__ cs_tab, const float* __restrict__ qa,
+    const float* __restrict__ qjl, const float* __restrict__ cs_tab, const uint32_t* __restrict__ qa,
     const float* __restrict__ qb, uint64_t seed, uint32_t pbits_rt, uint32_t proj) {
     constexpr int DIM = 128;
     constexpr int HP = 16;   // pairs per lane
@@ -1273,29 +1328,49 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
         rn2 = rn2 + u2f(partner(f2u(rn2), q >> 1));
         const float rn = __builtin_sqrtf(rn2) * 1.0001f;   // |res|, rounded up far past its f32 error
 
+        // QJL dots on the f16 matrix cores (v_mfma_f32_16x16x32_f16; bound at
+        // qjl_scale): K step st covers dimensions 32q + 8st + j of lane (q, n)
+        float amax = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 32; ++c) amax = __builtin_fmaxf(amax, __builtin_fabsf(y[c]));
+        amax = __builtin_fmaxf(amax, u2f(partner16(f2u(amax), q)));
+        amax = __builtin_fmaxf(amax, u2f(partner(f2u(amax), q >> 1)));
+        const float sc = qjl_scale(amax);
+        const float xn = rn * sc;
         uint32_t sbits[2] = {0u, 0u}, unc[2] = {0u, 0u};
         const uint32_t ptiles = proj / 16;
+        v4f acc[4] = {};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            v4u xh, xl;
+            qjl_split8(y, 8 * st, sc, xh, xl);
+#pragma unroll
+            for (uint32_t p = 0; p < 4; ++p) {
+                if (p >= ptiles) break;
+                const v4u* a = reinterpret_cast<const v4u*>(qa) + (p * 4 + st) * 2 * 64 + lane;
+                const v4u ah = a[0], al = a[64];
+                acc[p] = mfma16x32(ah, xh, acc[p]);
+                acc[p] = mfma16x32(ah, xl, acc[p]);
+                acc[p] = mfma16x32(al, xh, acc[p]);
+            }
+        }
 #pragma unroll
         for (uint32_t p = 0; p < 4; ++p) {
             if (p >= ptiles) break;
-            const float* qa_p = qa + p * QA128_PER_TILE;
-            const float* qb_p = qb + p * QB128_PER_TILE;
-            v4f acc = {};
-#pragma unroll
-            for (int c = 0; c < 32; ++c)
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa_p[c * 64 + lane], y[c], acc, 0, 0, 0);
+            const float2* ab = reinterpret_cast<const float2*>(qb) + p * 4 * 64 + lane;
             // register r: projection 16p + 4q + r of vector n
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
                 const uint32_t j = 16u * p + 4u * static_cast<uint32_t>(q) + static_cast<uint32_t>(rr);
-                const float bnd = qb_p[rr * 64 + lane] * rn;
-                sbits[j >> 5] |= (acc[rr] >= 0.0f ? 1u : 0u) << (j & 31u);
-                unc[j >> 5] |= (__builtin_fabsf(acc[rr]) > bnd ? 0u : 1u) << (j & 31u);
+                const float2 c = ab[rr * 64];
+                const float bnd = __builtin_fmaf(c.x, xn, c.y);
+                sbits[j >> 5] |= (acc[p][rr] >= 0.0f ? 1u : 0u) << (j & 31u);
+                unc[j >> 5] |= (__builtin_fabsf(acc[p][rr]) > bnd ? 0u : 1u) << (j & 31u);
                 if constexpr (DIAG) {
                     if (active) {
                         float* dv = lc.diag + (static_cast<uint64_t>(t0 + static_cast<uint32_t>(n)) * proj + j) * 2u;
-                        dv[0] = acc[rr];
-                        dv[1] = bnd;
+                        dv[0] = acc[p][rr] / sc;
+                        dv[1] = bnd / sc;
                     }
                 }
             }
@@ -2172,10 +2247,6 @@ __device__ __forceinline__ uint2 split2(float a, float b) {
     return make_uint2(__builtin_bit_cast(uint32_t, h), __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(ra, rb)));
 }
 
-__device__ __forceinline__ v16f mfma16(const v4u& a, const v4u& b, const v16f& c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
-}
-
 __device__ __forceinline__ uint32_t umed3(uint32_t a, uint32_t b, uint32_t c) {
     uint32_t r;
     asm("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
@@ -3016,6 +3087,31 @@ __global__ void logf_bound_finish_kernel() {
     }
 }
 
+// Subnormal f16 operands on the matrix cores (the QJL acceptance bound needs
+// them kept): out[0] = one 16x16x32 product sum 2^-20 * 1024 + 1024 * 2^-24,
+// out[1] = one 32x32x16 product 2^-20 * 1024.
+__global__ void f16_subnormal_probe_kernel(float* out) {
+    const int lane = threadIdx.x;
+    v8h a = {}, b = {};
+    if (lane == 0) {
+        a[0] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(0x0010));   // 2^-20
+        b[0] = static_cast<_Float16>(1024.0f);
+        a[1] = static_cast<_Float16>(1024.0f);
+        b[1] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(0x0001));   // 2^-24
+    }
+    const v4f c16 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, v4f{}, 0, 0, 0);
+    v8h a2 = {}, b2 = {};
+    if (lane == 0) {
+        a2[0] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(0x0010));
+        b2[0] = static_cast<_Float16>(1024.0f);
+    }
+    const v16f c32 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b2, v16f{}, 0, 0, 0);
+    if (lane == 0) {
+        out[0] = c16[0];
+        out[1] = c32[0];
+    }
+}
+
 __global__ void logf_bound_read_kernel(float* out) {
     if (threadIdx.x < 256) out[threadIdx.x] = g_logb[threadIdx.x];
 }
@@ -3042,6 +3138,11 @@ int launch_logf_bound(void* stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(logf_bound_finish_kernel, dim3(1), dim3(64), 0, st);
+    return hipGetLastError();
+}
+
+int launch_f16_subnormal_probe(float* out, void* stream) {
+    hipLaunchKernelGGL(f16_subnormal_probe_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), out);
     return hipGetLastError();
 }
 

@@ -83,3 +83,12 @@ def test_radii_log_bound_table(ctx):
     assert np.all(np.isfinite(t))
     assert np.all(np.diff(t.astype(np.float64)) >= 0)
     assert t[127 + 5] <= 1e-4
+
+
+def test_device_checks_ran_at_context_creation(ctx):
+    """The first context on the device measured the log bound table and
+    checked that the f16 matrix cores keep subnormal operands (the QJL
+    acceptance bound counts on it): creation fails otherwise, so a usable
+    context with a measured table is the evidence."""
+    t = ctx.radii_log_bound()
+    assert t[127] > 0.0 and np.isfinite(t[127])
