@@ -969,7 +969,7 @@ def main():
     ap.add_argument("--serial-tiers", action="store_true",
                     help="config3: the pool tier and the shell tier one after the other on one stream (default: "
                          "the shell tier on a second stream, concurrent with the pool tier)")
-    ap.add_argument("--side-workgroups", type=int, default=192,
+    ap.add_argument("--side-workgroups", type=int, default=1024,
                     help="config3: workgroups of the shell-tier rehydrate while it overlaps the pool encode")
     args = ap.parse_args()
     if args.gpus != 1:

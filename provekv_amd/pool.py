@@ -196,7 +196,7 @@ class TwoTierPlan:
         self._rehydrate_tier("shells", bufs, cache, stream)
 
     def build_and_rehydrate(self, corpus, bufs, cache: DeviceKVCache, stream=None, side=None,
-                            side_workgroups: int = 192):
+                            side_workgroups: int = 1024):
         """One whole step: each tier's encode followed by its rehydrate into
         `cache`.  The tiers share nothing but the read-only corpus (disjoint
         wires, status words and cache token ranges), so with a `side` stream
