@@ -784,19 +784,6 @@ int pkv_turbo_profile_create_with_constants(pkv_ctx* ctx, uint32_t dim, uint32_t
     return turbo_profile_common(ctx, dim, bits, projections, seed, mode, signs, qjl, out);
 }
 
-// Constants of the encode kernel's approximate argmin and its acceptance
-// margin.  key_w = |c_w|^2 + off - 2 c_w . rho' (f32 FMA) approximates the
-// reference distance D_w (+ off - |rho|^2, common to all w) within
-//   E = E_score + E_D + E_key, where
-//   E_score = 2^-23 (rounding of |c|^2 + off) + 4 * 2^-24 (FMA roundings)
-//             + 2 |c|_1 * eps_rho,  eps_rho = 69 * 2^-24 (|rho' - rho| bound:
-//             64 FMA roundings + x_hat' and Pi32 representation, with
-//             sum|Pi_rc x_c| <= |Pi_r| |x| = 1),
-//   E_D     = 8 * 2^-24 * (|c| + 1)^2 (the reference's f32 distance formula),
-//   E_key   = 31 * 2^-23 (index bits in the key, values in (0, 2)).
-// A gap above 2E between the two smallest keys proves the reference's strict
-// argmin; thr = 2.5 E leaves extra room.  With the codebook's |c| <= 0.35
-// every key stays in (0.5, 2); otherwise every block takes the exact path.
 // f16 halves of v: hi = f16(v), lo = f16(v - hi), both round-to-nearest-even.
 static void f16_split(double v, uint16_t* hi, uint16_t* lo) {
     const _Float16 h = static_cast<_Float16>(v);
@@ -829,7 +816,8 @@ static void f16_split(double v, uint16_t* hi, uint16_t* lo) {
 // a key is off by at most
 //   E = e_score + 2 l1max eps_rho + 8u (cmax + 1)^2 + 31 ulp(kmax),
 // so a gap > 2E between the two smallest keys fixes the reference's argmin;
-// thr = 2.5E.  Keys must stay positive (off - 2 cmax > 0) for the unsigned
+// thr = 2E (1 + 2^-10) (the factor covers thr's own rounding to f32).  Keys
+// must stay positive (off - 2 cmax > 0) for the unsigned
 // order to be the float order; otherwise thr = inf and every block is redone.
 static void fib_mfma_constants(pkv_profile* p) {
     const uint32_t n = p->n, k = p->k, dim = p->dim;
@@ -884,7 +872,8 @@ static void fib_mfma_constants(pkv_profile* p) {
                            16.0 * l1max * u;
     const double e = e_score + 2.0 * l1max * eps_rho + 8.0 * u * (cmax + 1.0) * (cmax + 1.0) + 31.0 * ulp;
     const bool positive = off - 2.0 * cmax * (1.0 + eps_rho) > 0.25;
-    p->thr = positive ? static_cast<float>(2.5 * e) : std::numeric_limits<float>::infinity();
+    p->thr = positive ? static_cast<float>(2.0 * e * (1.0 + std::ldexp(1.0, -10)))
+                      : std::numeric_limits<float>::infinity();
 }
 
 // The matrix-core decode is used only if every product it can form equals

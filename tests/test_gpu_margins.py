@@ -10,7 +10,7 @@ reference's exact f32 arithmetic; everything else is redone exactly:
               ((d0^2 + d1^2) + (d2^2 + d3^2), simd_nearest.rs:44-104) at the
               reference's rho = f32(Pi f64(x_hat)) (rotation.rs:107-113); a
               block is decided when its two smallest keys differ by more than
-              thr = 2.5 E, otherwise redone exactly
+              thr = 2E (1 + 2^-10), otherwise redone exactly
   QJL sign    the matrix-core dot must lie within `bound` of the reference's
               sequential f32 dot (qjl.rs:203-220) whenever |dot'| > bound
 
@@ -67,7 +67,7 @@ def test_fib_argmin_key_margin(ctx):
     D = (sq[..., 0] + sq[..., 1]) + (sq[..., 2] + sq[..., 3])  # f32, AVX2 order
     rho64 = rho.astype(np.float64)
     target = D.astype(np.float64) + 1.25 - np.sum(rho64 * rho64, axis=-1)
-    E = thr / 2.5
+    E = thr / (2.0 * (1.0 + 2.0 ** -10))   # thr = 2E (1 + 2^-10)
     ratio = float(np.max(np.abs(keys - target)) / E)
     # the kernel's decision: keys with the codeword index in the low 5 bits
     kb = (diag.reshape(n, 16, 32).view(np.uint32) & ~np.uint32(31)) | np.arange(32, dtype=np.uint32)
