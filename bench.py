@@ -975,6 +975,126 @@ def bench_score(args):
     print(json.dumps(res), flush=True)
 
 
+# ================================================================ digests
+B3_LANE_OPS_PER_BLOCK = 7 * 8 * 12 + 8   # BLAKE3 compression: rounds x G x ops, + output xors
+
+
+def bench_digest(args):
+    """BLAKE3 digests of a build (row a19: CompressedBlock::new of every blob,
+    PoolLayer / ShellLayer::compute_digest of every layer) on config 3's pool
+    and shell wires, where the encode left them; plus a bulk case (512 ranges
+    of 1 MiB) that fills the GPU.  Every digest is compared with the oracle.
+    Prints one JSON line; VALU-bound, so the roofline is the VALU issue rate."""
+    import torch
+
+    from oracle import oracle as O
+    from provekv_amd import synth
+    from provekv_amd.device import default_context
+    from provekv_amd.pool import TwoTierPlan
+    need_gpu()
+    ctx = default_context()
+    stream = torch.cuda.current_stream()
+    log("[bench] digest: config-3 build")
+    plan = TwoTierPlan(ctx, 24, 32, 64, 800, [28] * 8, seed=SEED)
+    bufs = plan.alloc()
+    corpus = torch.from_numpy(synth.corpus_tokens(3, 24, 32, plan.tokens, 64).reshape(-1)).cuda()
+    plan.encode(corpus, bufs)
+    plan.digests(bufs)
+    torch.cuda.synchronize()
+    plan.check(bufs, decode=False)
+    # parity: every payload and layer digest against the oracle
+    rep = plan.digest_report(bufs)
+    parity = True
+    wires = {}
+    for tier, name in ((plan.pool, "pool"), (plan.shells, "shell")):
+        wire = bufs[f"{name}_wire"].cpu().numpy()
+        wires[name] = wire
+        rg = np.array([(o, ln) for _, _, _, o, ln in tier.blob_offsets], np.uint64)
+        ref = O.blake3_ranges(wire, rg)
+        for i in range(len(rg) // 2):
+            owner, layer = tier.blob_offsets[2 * i][:2]
+            e = [x for x in rep[owner] if x["layer_index"] == layer][0]
+            parity &= e["key_payload_digest"] == ref[2 * i].tobytes().hex()
+            parity &= e["value_payload_digest"] == ref[2 * i + 1].tobytes().hex()
+            parity &= e["block_digest"] == O.layer_digest(layer, ref[2 * i].tobytes(), ref[2 * i + 1].tobytes()).hex()
+    log(f"[bench] digest parity vs oracle: {parity}")
+    for _ in range(args.warmup):
+        plan.digests(bufs)
+    torch.cuda.synchronize()
+    wire_bytes = plan.pool.wire_bytes + plan.shells.wire_bytes
+
+    def timed(fn, steps):
+        # events around back-to-back calls: each call takes a private table
+        # slot and may wait on the host for that slot's last use, so the
+        # calls cannot all be queued behind a spin first
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for _ in range(steps):
+            fn()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / steps
+
+    side = None if args.serial_tiers else torch.cuda.Stream()
+    for _ in range(max(1, args.warmup)):
+        plan.digests(bufs, stream=stream, side=side)
+    ms = timed(lambda: plan.digests(bufs, stream=stream, side=side), args.steps)
+    # bulk: 512 x 1 MiB
+    bulk = torch.randint(0, 256, (512 << 20,), dtype=torch.uint8, device="cuda")
+    brg = np.array([(i << 20, 1 << 20) for i in range(512)], np.uint64)
+    bout = torch.empty((512, 32), dtype=torch.uint8, device="cuda")
+    for _ in range(max(1, args.warmup)):
+        ctx.blake3_ranges(bulk, brg, out=bout)
+    torch.cuda.synchronize()
+    host = bulk[: 8 << 20].cpu().numpy()
+    parity &= np.array_equal(bout[:8].cpu().numpy(), O.blake3_ranges(host, brg[:8]))
+    bms = timed(lambda: ctx.blake3_ranges(bulk, brg, out=bout), max(3, args.steps // 4))
+    bulk_bytes = 512 << 20
+
+    def valu(nbytes, t_ms):
+        blocks = (nbytes + 63) // 64
+        ops = blocks * B3_LANE_OPS_PER_BLOCK / (t_ms * 1e-3)
+        return {"bound": "valu", "achieved": round(ops / 1e12, 2), "peak": round(VALU_PEAK_OPS / 1e12, 2),
+                "unit": "T lane-ops/s", "frac": round(ops / VALU_PEAK_OPS, 4),
+                "gbs_at_peak": round(VALU_PEAK_OPS / B3_LANE_OPS_PER_BLOCK * 64 / 1e9, 1)}
+
+    res = {"metric": "BLAKE3 digests of encoded KV (payload + layer digests), GB/s of hashed bytes",
+           "workload": "digest", "unit": "GB/s", "steps": args.steps, "warmup": args.warmup,
+           "parity_all_digests": bool(parity),
+           "config3": {"ranges": len(plan.pool.blob_offsets) + len(plan.shells.blob_offsets),
+                       "tiers": "one stream" if side is None else "pool and shell tiers on two streams",
+                       "bytes": int(wire_bytes), "ms_per_call": round(ms, 4),
+                       "gbs": round(wire_bytes / (ms * 1e-3) / 1e9, 1), "roofline": valu(wire_bytes, ms)},
+           "bulk_512x1MiB": {"bytes": bulk_bytes, "ms_per_call": round(bms, 4),
+                             "gbs": round(bulk_bytes / (bms * 1e-3) / 1e9, 1), "roofline": valu(bulk_bytes, bms)}}
+    if not args.no_cpu_baseline:
+        log("[bench] digest: CPU baseline (oracle BLAKE3, config-3 wires)")
+        jobs, job_bytes = [], []
+        for tier, name in ((plan.pool, "pool"), (plan.shells, "shell")):
+            for _, _, _, o, ln in tier.blob_offsets:
+                blob = wires[name][o:o + ln].tobytes()
+                jobs.append(lambda b=blob: O.blake3(b))
+                job_bytes.append(ln)
+        info = cpu_info()
+        t0 = time.perf_counter()
+        for j in jobs:
+            j()
+        t1 = time.perf_counter()
+        with ThreadPoolExecutor(info["threads"]) as ex:
+            t2 = time.perf_counter()
+            list(ex.map(lambda f: f(), jobs))
+            t3 = time.perf_counter()
+        res["cpu_baseline"] = {"value": round(wire_bytes / (t3 - t2) / 1e9, 3), "unit": "GB/s",
+                               "cores": info["threads"], "kind": "port",
+                               "sample": f"oracle/blake3_oracle.c (portable C, -O3) over all {len(jobs)} config-3 "
+                                         f"blobs ({wire_bytes} B), {info['threads']} threads in {t3 - t2:.3f} s",
+                               "single_thread": {"value": round(wire_bytes / (t1 - t0) / 1e9, 3), "unit": "GB/s",
+                                                 "cores": 1},
+                               "host": {"nproc": info["nproc"], "model": info["model"]}}
+    print(json.dumps(res), flush=True)
+
+
 # ================================================================ main
 def main():
     ap = argparse.ArgumentParser()
@@ -982,10 +1102,11 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", choices=("config3", "pool", "config0", "config1", "config2", "config4", "legacy",
-                                           "score"), default="config3",
+                                           "score", "digest"), default="config3",
                     help="config3 (alias pool): the metric (default); config0/1/2/4: the other BASELINE "
                          "configurations; legacy: per-vector TQW1 / FB1 records; score: attention scores on "
-                         "config-4 compressed keys")
+                         "config-4 compressed keys; digest: BLAKE3 payload and layer digests of the config-3 "
+                         "build")
     ap.add_argument("--lossy", action="store_true", help="config3: TQB1-L shells (BlockLogU8 radii)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calib", action="store_true",
@@ -1009,7 +1130,7 @@ def main():
         sys.exit(2)
     {"config3": bench_config3, "pool": bench_config3, "config0": bench_config0, "config1": bench_config1,
      "config2": bench_config2, "config4": bench_config4, "legacy": bench_legacy,
-     "score": bench_score}[args.workload](args)
+     "score": bench_score, "digest": bench_digest}[args.workload](args)
 
 
 if __name__ == "__main__":

@@ -393,6 +393,45 @@ int pkv_encode_diagnostics(pkv_ctx* ctx, const pkv_profile* prof, int radii_code
  * biased f32 exponent <= e. */
 int pkv_radii_log_bound(pkv_ctx* ctx, float* out);
 
+/* ---------------------------------------------------------------- digests
+ * BLAKE3 (the unkeyed 32-byte hash of the blake3 crate, 1.8.5 in the
+ * reference's lock file) computed on the device.  Digests are raw 32-byte
+ * hashes; the reference prints them as lower-case hex. */
+typedef struct pkv_range {
+    uint64_t offset;   /* first byte, from the buffer start */
+    uint64_t len;      /* bytes (0 allowed: the hash of the empty input) */
+} pkv_range;
+
+/* d_out[32 i .. 32 i + 32) = blake3(d_buf[ranges[i].offset .. + len]) for
+ * every range, in one pass over the bytes where they lie (an encode's wire
+ * buffer: one range per (layer, K|V) blob).  Replaces the payload digest of
+ * CompressedBlock::new (proveKV/src/codec.rs:85-95), which SharedKVPool::
+ * build_with_policy (pool.rs:268-275) and materialize_shell (shell.rs:280-282)
+ * take of every blob after copying it to the host.  Ranges may overlap and
+ * start at any byte; each must lie inside [0, buf_bytes).  d_out is 4-byte
+ * aligned device memory.  n == 0 does nothing.  The range table is copied
+ * from host memory on `stream`; it may be released when the call returns. */
+int pkv_blake3_ranges(pkv_ctx* ctx, const uint8_t* d_buf, uint64_t buf_bytes, const pkv_range* ranges,
+                      uint32_t n, uint8_t* d_out, void* stream);
+
+/* Layer digests from payload digests: entry i of d_kv_digests is 64 bytes,
+ * the key blob's digest then the value blob's, of layer i % layers (so a pool
+ * is one run of `layers` entries, N shells N runs); d_out[32 i ..) =
+ * blake3 of the compact JSON text
+ *   {"key_digests":["<hex>"],"layer_index":L,"value_digests":["<hex>"]}
+ * i.e. PoolLayer::compute_digest (proveKV/src/pool.rs:83-103) and
+ * ShellLayer::compute_digest (shell.rs:48-66) of a batched layer (one key
+ * block, one value block), whose serde_json object prints its keys sorted.
+ * Both device pointers 4-byte aligned; layers >= 1. */
+int pkv_blake3_layer_digests(pkv_ctx* ctx, const uint8_t* d_kv_digests, uint32_t n, uint32_t layers,
+                             uint8_t* d_out, void* stream);
+
+/* blake3 of host bytes, hashed on the context's device (copy in, the same
+ * kernels, copy out, synchronise): blake3::hash over a host slice, as
+ * CodecProfileDigest / ArtifactDigest::from_canonical_bytes and from_parts
+ * (quant-codec-core/src/digest.rs:14-58) use it. */
+int pkv_blake3(pkv_ctx* ctx, const void* data, uint64_t len, uint8_t out[32]);
+
 /* ---------------------------------------------------------------- host math
  * Host builds of the exact scalar routines the kernels use (test hooks):
  * angle bins of (a[i], b[i]) for pbits, and logf / expf over arrays. */

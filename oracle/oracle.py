@@ -1,4 +1,4 @@
-"""ctypes wrapper around the CPU oracle (oracle/pkv_oracle.c).
+"""ctypes wrapper around the CPU oracle (oracle/pkv_oracle.c, oracle/blake3_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()``
 and by the ``cpu_baseline`` leg of ``bench.py`` -- never by the
@@ -140,6 +140,12 @@ def _declare(L):
     L.ora_pack_bits.argtypes = [P, U64, I32, P]
     L.ora_unpack_bits.argtypes = [P, U64, I32, P]
     L.ora_unpack_bits.restype = I32
+    L.ora_blake3.argtypes = [P, U64, P]
+    L.ora_blake3.restype = None
+    L.ora_layer_digest.argtypes = [U32, P, P, P]
+    L.ora_layer_digest.restype = None
+    L.ora_blake3_ranges.argtypes = [P, P, P, U32, P]
+    L.ora_blake3_ranges.restype = None
 
 
 def _p(a: np.ndarray):
@@ -525,3 +531,30 @@ def unpack_bits(data: bytes, n: int, bits: int) -> np.ndarray:
     if rc:
         raise OracleError(rc)
     return out[:n]
+
+
+def blake3(data) -> bytes:
+    """blake3::hash (the blake3 crate's unkeyed 32-byte hash)."""
+    buf = np.frombuffer(bytes(data), dtype=np.uint8).copy() if len(data) else np.zeros(1, np.uint8)
+    out = np.zeros(32, np.uint8)
+    lib().ora_blake3(_p(buf), len(data), _p(out))
+    return out.tobytes()
+
+
+def blake3_ranges(buf: np.ndarray, ranges) -> np.ndarray:
+    """blake3 of each (offset, len) range of a uint8 array: [n, 32]."""
+    buf = np.ascontiguousarray(buf, dtype=np.uint8)
+    rg = np.ascontiguousarray(np.asarray(ranges, dtype=np.uint64).reshape(-1, 2))
+    offs, lens = np.ascontiguousarray(rg[:, 0]), np.ascontiguousarray(rg[:, 1])
+    out = np.zeros((len(rg), 32), np.uint8)
+    lib().ora_blake3_ranges(_p(buf if buf.size else np.zeros(1, np.uint8)), _p(offs), _p(lens), len(rg), _p(out))
+    return out
+
+
+def layer_digest(layer_index: int, key_digest: bytes, value_digest: bytes) -> bytes:
+    """PoolLayer / ShellLayer::compute_digest of a batched layer."""
+    k = np.frombuffer(bytes(key_digest), np.uint8).copy()
+    v = np.frombuffer(bytes(value_digest), np.uint8).copy()
+    out = np.zeros(32, np.uint8)
+    lib().ora_layer_digest(layer_index, _p(k), _p(v), _p(out))
+    return out.tobytes()

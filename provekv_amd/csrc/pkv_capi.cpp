@@ -13,6 +13,7 @@
 #include <new>
 #include <vector>
 
+#include "pkv_blake3.h"
 #include "pkv_internal.h"
 #include "pkv_math.h"
 
@@ -73,7 +74,10 @@ struct Slot {
     hipStream_t up_stream = nullptr;
     bool up_done = true;         // the host has seen up_ev complete
     Users users;                 // streams that read (or wrote status into) the slot
+    hipEvent_t done_ev = nullptr;  // private slot: recorded after the launches of the call that took it
+    bool done_recorded = false;
     bool shared = false;         // table only (no status words): reusable by equal tables
+    bool digest = false;         // a pkv_blake3_ranges table (+ its chaining-value scratch)
     uint32_t nseg = 0;
     uint64_t hash = 0;
 };
@@ -281,6 +285,41 @@ uint64_t fnv1a(const void* p, size_t n) {
     return h;
 }
 
+// Takes the next ring slot for `total` bytes (device table + pinned staging),
+// waiting first for every stream that still uses it and growing it when
+// needed.  The slot comes back private (not reusable as a shared table).
+int acquire_slot(pkv_ctx* ctx, size_t total, Slot** out) {
+    Slot& sl = ctx->slots[ctx->next];
+    ctx->next = (ctx->next + 1) % kSlots;
+    if (!sl.ev) HIP_TRY(hipEventCreateWithFlags(&sl.ev, hipEventDisableTiming));
+    if (!sl.up_ev) HIP_TRY(hipEventCreateWithFlags(&sl.up_ev, hipEventDisableTiming));
+    // the pinned copy and the device table are about to be rewritten: wait
+    // for the slot's last use (a private slot's own event), or for all work
+    // its streams had queued by now (a shared slot's users)
+    if (sl.done_recorded && sl.users.n == 1 && !sl.users.overflow) {
+        HIP_TRY(hipEventSynchronize(sl.done_ev));
+        sl.users.n = 0;
+    } else if (sl.users.n || sl.users.overflow) {
+        int rc = sl.users.drain_host(sl.ev);
+        if (rc) return rc;
+    }
+    sl.done_recorded = false;
+    sl.shared = false;
+    sl.digest = false;
+    if (sl.cap < total) {
+        if (sl.dev) HIP_TRY(hipFree(sl.dev));
+        if (sl.host) HIP_TRY(hipHostFree(sl.host));
+        sl.dev = sl.host = nullptr;
+        sl.cap = 0;
+        size_t cap = std::max<size_t>(total, 64 * 1024);
+        HIP_TRY(hipMalloc(&sl.dev, cap));
+        HIP_TRY(hipHostMalloc(&sl.host, cap, hipHostMallocDefault));
+        sl.cap = cap;
+    }
+    *out = &sl;
+    return PKV_OK;
+}
+
 // Stage the segment table + tile prefix (+ status words when the caller gave
 // none) into a ring slot and copy it to the device on `stream`.  A table the
 // device already holds in a table-only slot is reused as is: the kernels only
@@ -315,25 +354,10 @@ int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vec
             }
         }
     }
-    Slot& sl = ctx->slots[ctx->next];
-    ctx->next = (ctx->next + 1) % kSlots;
-    if (!sl.ev) HIP_TRY(hipEventCreateWithFlags(&sl.ev, hipEventDisableTiming));
-    if (!sl.up_ev) HIP_TRY(hipEventCreateWithFlags(&sl.up_ev, hipEventDisableTiming));
-    // the pinned copy and the device table are about to be rewritten
-    if (sl.users.n || sl.users.overflow) {
-        int rc = sl.users.drain_host(sl.ev);
-        if (rc) return rc;
-    }
-    sl.shared = false;
-    if (sl.cap < total) {
-        if (sl.dev) HIP_TRY(hipFree(sl.dev));
-        if (sl.host) HIP_TRY(hipHostFree(sl.host));
-        sl.dev = sl.host = nullptr;
-        size_t cap = std::max<size_t>(total, 64 * 1024);
-        HIP_TRY(hipMalloc(&sl.dev, cap));
-        HIP_TRY(hipHostMalloc(&sl.host, cap, hipHostMallocDefault));
-        sl.cap = cap;
-    }
+    Slot* slp;
+    int rc = acquire_slot(ctx, total, &slp);
+    if (rc) return rc;
+    Slot& sl = *slp;
     auto* h = static_cast<uint8_t*>(sl.host);
     std::memcpy(h, segs, seg_bytes);
     std::memcpy(h + tile_off, tiles.data(), tile_bytes);
@@ -352,8 +376,15 @@ int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vec
     return PKV_OK;
 }
 
+// After the last launch of a call that read the slot.  A private slot (this
+// call's status words or scratch) gets an event, so that taking it again
+// waits for this call only, not for everything queued after it.
 int finish_slot(Slot* sl, hipStream_t stream) {
     sl->users.add(stream);
+    if (sl->shared) return PKV_OK;
+    if (!sl->done_ev) HIP_TRY(hipEventCreateWithFlags(&sl->done_ev, hipEventDisableTiming));
+    HIP_TRY(hipEventRecord(sl->done_ev, stream));
+    sl->done_recorded = true;
     return PKV_OK;
 }
 
@@ -645,6 +676,7 @@ void pkv_ctx_destroy(pkv_ctx* ctx) {
         if (s.users.n || s.users.overflow) (void)s.users.drain_host(s.ev);
         if (s.ev) (void)hipEventDestroy(s.ev);
         if (s.up_ev) (void)hipEventDestroy(s.up_ev);
+        if (s.done_ev) (void)hipEventDestroy(s.done_ev);
         if (s.dev) (void)hipFree(s.dev);
         if (s.host) (void)hipHostFree(s.host);
     }
@@ -1123,6 +1155,150 @@ int pkv_radii_log_bound(pkv_ctx* ctx, float* out) {
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->own_stream);
     (void)hipFree(d);
     return e == hipSuccess ? PKV_OK : hip_status(e);
+}
+
+// ---- BLAKE3 digests of device bytes
+
+namespace {
+
+// Pass tables of one pkv_blake3_ranges call: [ranges | pass 0 | pass 1 | ...],
+// each pass nr + 1 B3Pass records (launch sequence in pkv_blake3.hip).
+struct B3Plan {
+    std::vector<B3Pass> passes;     // passes.size() == npass * (nr + 1)
+    std::vector<uint32_t> tiles;    // per pass
+    uint64_t cvs = 0;               // chaining values written by passes that do not finish a range
+};
+
+int plan_blake3(const pkv_range* ranges, uint32_t nr, uint64_t buf_bytes, B3Plan* plan) {
+    std::vector<uint64_t> count(nr), in_base(nr, 0);
+    for (uint32_t r = 0; r < nr; ++r) {
+        const pkv_range& g = ranges[r];
+        if (g.offset > buf_bytes || g.len > buf_bytes - g.offset) return PKV_ERR_INVALID_ARG;
+        count[r] = b3::chunks_of(g.len);
+        if (count[r] > 0xFFFFFFFFull) return PKV_ERR_INVALID_ARG;
+    }
+    for (bool more = true; more;) {
+        more = false;
+        const size_t base = plan->passes.size();
+        plan->passes.resize(base + nr + 1);
+        uint64_t tiles = 0;
+        for (uint32_t r = 0; r < nr; ++r) {
+            B3Pass& ps = plan->passes[base + r];
+            const uint64_t c = count[r], t = (c + 63) / 64;
+            ps.tile_start = static_cast<uint32_t>(tiles);
+            ps.count = static_cast<uint32_t>(c);
+            ps.in_base = static_cast<uint32_t>(in_base[r]);
+            ps.out_base = 0;
+            tiles += t;
+            if (c > 64) {   // not finished in this pass: t chaining values go on
+                ps.out_base = static_cast<uint32_t>(plan->cvs);
+                in_base[r] = plan->cvs;
+                plan->cvs += t;
+                count[r] = t;
+                more = true;
+            } else {
+                count[r] = 0;
+            }
+            if (tiles > 0xFFFFFFFFull || plan->cvs > 0xFFFFFFFFull) return PKV_ERR_INVALID_ARG;
+        }
+        plan->passes[base + nr].tile_start = static_cast<uint32_t>(tiles);
+        plan->tiles.push_back(static_cast<uint32_t>(tiles));
+    }
+    return PKV_OK;
+}
+
+// Caller holds ctx->mu and has made the device current.
+int blake3_ranges_locked(pkv_ctx* ctx, const uint8_t* d_buf, uint64_t buf_bytes, const pkv_range* ranges,
+                         uint32_t nr, uint8_t* d_out, hipStream_t stream) {
+    B3Plan plan;
+    int rc = plan_blake3(ranges, nr, buf_bytes, &plan);
+    if (rc) return rc;
+    const size_t range_bytes = sizeof(pkv_range) * nr;
+    const size_t pass_off = (range_bytes + 255) & ~static_cast<size_t>(255);
+    const size_t pass_bytes = sizeof(B3Pass) * plan.passes.size();
+    const size_t cv_off = (pass_off + pass_bytes + 255) & ~static_cast<size_t>(255);
+    const size_t total = cv_off + 32 * plan.cvs + 256;
+    const uint64_t hash = fnv1a(ranges, range_bytes);
+    // The same table again on the same stream (a serving loop's digest of
+    // every step) reuses its slot as is: no upload, and the chaining-value
+    // scratch is rewritten only after the previous call, in stream order.
+    Slot* sl = nullptr;
+    for (Slot& c : ctx->slots)
+        if (c.digest && c.nseg == nr && c.hash == hash && c.users.n == 1 && !c.users.overflow &&
+            c.users.s[0] == stream && std::memcmp(c.host, ranges, range_bytes) == 0) {
+            sl = &c;
+            break;
+        }
+    hipError_t cp = hipSuccess;
+    if (!sl) {
+        rc = acquire_slot(ctx, total, &sl);
+        if (rc) return rc;
+        auto* h = static_cast<uint8_t*>(sl->host);
+        std::memcpy(h, ranges, range_bytes);
+        std::memcpy(h + pass_off, plan.passes.data(), pass_bytes);
+        cp = hipMemcpyAsync(sl->dev, sl->host, pass_off + pass_bytes, hipMemcpyHostToDevice, stream);
+        sl->digest = true;
+        sl->nseg = nr;
+        sl->hash = hash;
+    }
+    auto* d = static_cast<uint8_t*>(sl->dev);
+    auto* d_ranges = reinterpret_cast<const B3Range*>(d);
+    auto* d_cv = reinterpret_cast<uint32_t*>(d + cv_off);
+    auto* out = reinterpret_cast<uint32_t*>(d_out);
+    int e = cp;
+    for (size_t p = 0; p < plan.tiles.size() && !e; ++p) {
+        const auto* d_pass = reinterpret_cast<const B3Pass*>(d + pass_off) + p * (nr + 1);
+        e = launch_blake3_pass(d_buf, d_ranges, d_pass, nr, plan.tiles[p], d_cv, d_cv, out, p == 0, stream);
+    }
+    const int rc2 = finish_slot(sl, stream);
+    if (e) return hip_status(static_cast<hipError_t>(e));
+    return rc2;
+}
+
+}  // namespace
+
+int pkv_blake3_ranges(pkv_ctx* ctx, const uint8_t* d_buf, uint64_t buf_bytes, const pkv_range* ranges, uint32_t n,
+                      uint8_t* d_out, void* stream) {
+    if (!ctx) return PKV_ERR_INVALID_ARG;
+    if (n == 0) return PKV_OK;
+    if (!ranges || !d_out || reinterpret_cast<uintptr_t>(d_out) % 4 || (!d_buf && buf_bytes))
+        return PKV_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    return blake3_ranges_locked(ctx, d_buf, buf_bytes, ranges, n, d_out, static_cast<hipStream_t>(stream));
+}
+
+int pkv_blake3_layer_digests(pkv_ctx* ctx, const uint8_t* d_kv_digests, uint32_t n, uint32_t layers, uint8_t* d_out,
+                             void* stream) {
+    if (!ctx || layers == 0) return PKV_ERR_INVALID_ARG;
+    if (n == 0) return PKV_OK;
+    if (!d_kv_digests || !d_out || reinterpret_cast<uintptr_t>(d_kv_digests) % 4 ||
+        reinterpret_cast<uintptr_t>(d_out) % 4)
+        return PKV_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    const int e = launch_blake3_layers(reinterpret_cast<const uint32_t*>(d_kv_digests), n, layers,
+                                       reinterpret_cast<uint32_t*>(d_out), stream);
+    return e ? hip_status(static_cast<hipError_t>(e)) : PKV_OK;
+}
+
+int pkv_blake3(pkv_ctx* ctx, const void* data, uint64_t len, uint8_t out[32]) {
+    if (!ctx || !out || (!data && len)) return PKV_ERR_INVALID_ARG;
+    const uint64_t in_pad = (len + 255) & ~static_cast<uint64_t>(255);
+    std::lock_guard<std::mutex> lock(ctx->mu);   // serialises use of ctx->io_buf
+    HIP_TRY(hipSetDevice(ctx->device));
+    int rc = ensure_io_buf(ctx, in_pad + 256);
+    if (rc) return rc;
+    auto* d_in = static_cast<uint8_t*>(ctx->io_buf);
+    uint8_t* d_hash = d_in + in_pad;
+    hipStream_t st = ctx->own_stream;
+    if (len) HIP_TRY(hipMemcpyAsync(d_in, data, len, hipMemcpyHostToDevice, st));
+    const pkv_range rg{0, len};
+    rc = blake3_ranges_locked(ctx, d_in, len, &rg, 1, d_hash, st);
+    if (rc) { (void)hipStreamSynchronize(st); return rc; }
+    HIP_TRY(hipMemcpyAsync(out, d_hash, 32, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    return PKV_OK;
 }
 
 int pkv_parse_header(const pkv_profile* p, const uint8_t* b, uint64_t len, uint64_t* n_vectors, int* radii_codec) {

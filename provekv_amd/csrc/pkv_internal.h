@@ -158,4 +158,22 @@ int launch_records_gather(const uint8_t* rec, const uint64_t* off, uint64_t n, u
 int launch_fib_decode_f64(const FibDev& fd, const uint8_t* pay, uint64_t n, uint32_t plen, float* out,
                           uint32_t* status, void* stream);
 
+// BLAKE3 digests (pkv_blake3.hip).  A range as the kernels read it (same
+// layout as pkv_range) and one pass's record per range: the pass's first
+// tile (64 elements) of the range, its element count (chunks in pass 0,
+// chaining values after), where its input chaining values start (pass > 0) and
+// where its outputs go when it does not finish the range (units of 8 words).
+// A pass table has nr + 1 records; the last one's tile_start is the tile count.
+struct B3Range {
+    uint64_t offset;
+    uint64_t len;
+};
+static_assert(sizeof(B3Range) == sizeof(pkv_range), "range layout");
+struct B3Pass {
+    uint32_t tile_start, count, in_base, out_base;
+};
+int launch_blake3_pass(const uint8_t* buf, const B3Range* ranges, const B3Pass* pass, uint32_t nr, uint32_t tiles,
+                       const uint32_t* cv_in, uint32_t* cv_out, uint32_t* out, bool leaf, void* stream);
+int launch_blake3_layers(const uint32_t* kv, uint32_t n, uint32_t layers, uint32_t* out, void* stream);
+
 }  // namespace pkv

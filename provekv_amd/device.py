@@ -83,6 +83,50 @@ class Context:
         L.check(L.lib().pkv_radii_log_bound(self.ptr, out.ctypes.data), "pkv_radii_log_bound")
         return out
 
+    # ------------------------------------------------------------ digests
+    def blake3_ranges(self, buf, ranges, out=None, stream=None):
+        """BLAKE3 of byte ranges of device uint8 tensor `buf` (rows of
+        (offset, len)), hashed where they lie: a [n, 32] uint8 device tensor
+        (CompressedBlock::new's payload digest of each range,
+        proveKV/src/codec.rs:85-95)."""
+        torch = _torch()
+        rg = np.ascontiguousarray(np.asarray(ranges, dtype=np.uint64).reshape(-1, 2))
+        if buf.dtype != torch.uint8 or not buf.is_contiguous():
+            raise TypeError("buf must be a contiguous uint8 tensor")
+        if out is None:
+            out = torch.empty((len(rg), 32), dtype=torch.uint8, device=buf.device)
+        if out.dtype != torch.uint8 or not out.is_contiguous() or out.numel() < 32 * len(rg):
+            raise ValueError(f"out must be a contiguous uint8 tensor of >= {32 * len(rg)} bytes")
+        rc = L.lib().pkv_blake3_ranges(self.ptr, buf.data_ptr(), buf.numel(), rg.ctypes.data, len(rg),
+                                       out.data_ptr(), _stream_ptr(stream))
+        L.check(rc, "pkv_blake3_ranges")
+        return out
+
+    def layer_digests(self, kv_digests, layers: int, out=None, stream=None):
+        """Layer digests (PoolLayer / ShellLayer::compute_digest,
+        proveKV/src/pool.rs:83-103, shell.rs:48-66) from [n, 2, 32] key/value
+        payload digests on the device, entry i being layer i % layers: a
+        [n, 32] uint8 device tensor."""
+        torch = _torch()
+        if kv_digests.dtype != torch.uint8 or not kv_digests.is_contiguous() or kv_digests.numel() % 64:
+            raise TypeError("kv_digests must be a contiguous uint8 tensor of 64-byte entries")
+        n = kv_digests.numel() // 64
+        if out is None:
+            out = torch.empty((n, 32), dtype=torch.uint8, device=kv_digests.device)
+        if out.dtype != torch.uint8 or not out.is_contiguous() or out.numel() < 32 * n:
+            raise ValueError(f"out must be a contiguous uint8 tensor of >= {32 * n} bytes")
+        rc = L.lib().pkv_blake3_layer_digests(self.ptr, kv_digests.data_ptr(), n, layers, out.data_ptr(),
+                                              _stream_ptr(stream))
+        L.check(rc, "pkv_blake3_layer_digests")
+        return out
+
+    def blake3(self, data: bytes) -> bytes:
+        """blake3::hash of host bytes, computed on this device."""
+        data = bytes(data)
+        out = C.create_string_buffer(32)
+        L.check(L.lib().pkv_blake3(self.ptr, data, len(data), out), "pkv_blake3")
+        return out.raw
+
     # profiles are cached per parameters: the reference rebuilds its codebook,
     # rotation and QJL matrix on every adapter call (proveKV/src/codec.rs:249,
     # 296, 471-499); here they are built once and stay resident.

@@ -44,6 +44,68 @@ def _invalid_shape(reason: str) -> QuantCodecError:
     return QuantCodecError("InvalidShape", reason)
 
 
+# ---------------------------------------------------------------- digests (digest.rs)
+class _Digest32:
+    """A 32-byte BLAKE3 digest (quant-codec-core/src/digest.rs:6-12): equality,
+    ordering and hashing by bytes; str() and to_hex() give lower-case hex.
+    The hash runs on a device context (the default one unless given)."""
+
+    __slots__ = ("_b",)
+
+    def __init__(self, digest: bytes):
+        digest = bytes(digest)
+        if len(digest) != 32:
+            raise ValueError("a digest is 32 bytes")
+        self._b = digest
+
+    @classmethod
+    def from_canonical_bytes(cls, data: bytes, ctx=None):
+        """blake3::hash(bytes) (digest.rs:15-17, 34-36)."""
+        from .device import default_context
+        return cls((ctx or default_context()).blake3(bytes(data)))
+
+    @classmethod
+    def from_parts(cls, parts, ctx=None):
+        """One hasher fed, per part, its length as a little-endian u64 and then
+        its bytes (digest.rs:19-26, 38-45): the hash of that concatenation."""
+        buf = bytearray()
+        for part in parts:
+            part = bytes(part)
+            buf += len(part).to_bytes(8, "little") + part
+        return cls.from_canonical_bytes(bytes(buf), ctx)
+
+    def as_bytes(self) -> bytes:
+        return self._b
+
+    def to_hex(self) -> str:
+        return self._b.hex()
+
+    def __str__(self) -> str:
+        return self.to_hex()
+
+    def __repr__(self) -> str:
+        return f"{type(self).__name__}({self.to_hex()!r})"
+
+    def __eq__(self, other) -> bool:
+        return type(other) is type(self) and other._b == self._b
+
+    def __lt__(self, other) -> bool:
+        if type(other) is not type(self):
+            return NotImplemented
+        return self._b < other._b
+
+    def __hash__(self) -> int:
+        return hash((type(self).__name__, self._b))
+
+
+class CodecProfileDigest(_Digest32):
+    """quant-codec-core CodecProfileDigest."""
+
+
+class ArtifactDigest(_Digest32):
+    """quant-codec-core ArtifactDigest."""
+
+
 # ---------------------------------------------------------------- shapes (shape.rs)
 class KvRole(enum.Enum):
     KEY = "Key"
@@ -264,11 +326,31 @@ class DeviceKvCodec:
     def codec_version(self) -> str:
         return "TQB1/TQW1 v1" if self.profile.kind == L.CODEC_TURBO else "FB2/FB1 v1"
 
-    def profile_digest(self):
-        # CodecProfileDigest is blake3 over the profile's canonical bytes
-        # (digest.rs:14-27); blake3 is not available to this build, and the
-        # digests are bookkeeping outside the codec path.
-        raise NotImplementedError("profile digests (blake3) are not computed by this build")
+    def canonical_profile_parts(self) -> list:
+        """The profile's canonical parts: codec id, codec version, compact
+        sorted-key JSON of the profile kind, head_dim, radii codec and
+        constructor parameters, then the resident constants themselves as
+        little-endian bytes (turbo: Hadamard signs, QJL matrix; fib: codebook
+        f32, rotation f64), so profiles built from caller constants are covered
+        too.  No codec of the reference implements CodecProfile; these parts
+        are this module's choice."""
+        import json
+        p = {k: (int(v) if isinstance(v, (int, np.integer)) else v) for k, v in self.profile.params.items()}
+        doc = {"kind": "turbo" if self.profile.kind == L.CODEC_TURBO else "fib", "dim": int(self.profile.dim),
+               "params": p}
+        if self.profile.kind == L.CODEC_TURBO:
+            doc["radii"] = "log_u8" if self.radii == L.RADII_LOG_U8 else "f32"
+        a, b = self.profile.constants()
+        return [self.codec_id().encode(), self.codec_version().encode(),
+                json.dumps(doc, sort_keys=True, separators=(",", ":")).encode(),
+                np.ascontiguousarray(a).astype(a.dtype.newbyteorder("<")).tobytes(),
+                np.ascontiguousarray(b).astype(b.dtype.newbyteorder("<")).tobytes()]
+
+    def profile_digest(self) -> CodecProfileDigest:
+        """CodecProfileDigest::from_parts over canonical_profile_parts()
+        (quant-codec-core/src/digest.rs:19-26), hashed on the profile's
+        device."""
+        return CodecProfileDigest.from_parts(self.canonical_profile_parts(), ctx=self.profile.ctx)
 
     def fixed_rate_bits(self):
         """Bits of one quantized index: the turbo profile's bits, or the fib

@@ -276,6 +276,56 @@ class TwoTierPlan:
             if err is not None:
                 raise err
 
+    # ------------------------------------------------------------ digests
+    def digests(self, bufs, stream=None, side=None) -> None:
+        """The build's digests, hashed in HBM where the encode left the blobs:
+        bufs["pool_digests"] / bufs["shell_digests"] [owners * layers, 2, 32]
+        hold every blob's payload digest (CompressedBlock::new,
+        proveKV/src/codec.rs:85-95; key then value), and
+        bufs["pool_layer_digests"] / bufs["shell_layer_digests"]
+        [owners * layers, 32] every layer's block_digest (PoolLayer /
+        ShellLayer::compute_digest, pool.rs:83-103, shell.rs:48-66).  Four
+        launches per tier at most (payload passes, then the layer digests).
+        With a `side` stream the shell tier runs there, concurrently with the
+        pool tier (each tier alone leaves most of the GPU idle); the calling
+        stream waits for both."""
+        import torch
+        main = stream if stream is not None else torch.cuda.current_stream()
+        if side is not None:
+            side.wait_stream(main)
+        for tier, name, st in ((self.pool, "pool", main), (self.shells, "shell", side or main)):
+            n = len(tier.blob_offsets) // 2
+            if f"{name}_digests" not in bufs:
+                dev = bufs[f"{name}_wire"].device
+                bufs[f"{name}_digests"] = torch.empty((n, 2, 32), dtype=torch.uint8, device=dev)
+                bufs[f"{name}_layer_digests"] = torch.empty((n, 32), dtype=torch.uint8, device=dev)
+            ranges = getattr(tier, "ranges", None)
+            if ranges is None:
+                ranges = tier.ranges = np.array([(off, ln) for _, _, _, off, ln in tier.blob_offsets], np.uint64)
+            self.ctx.blake3_ranges(bufs[f"{name}_wire"], ranges, out=bufs[f"{name}_digests"], stream=st)
+            self.ctx.layer_digests(bufs[f"{name}_digests"], self.layers, out=bufs[f"{name}_layer_digests"],
+                                   stream=st)
+        if side is not None:
+            main.wait_stream(side)
+
+    def digest_report(self, bufs) -> dict:
+        """The digests of the last digests() call as the reference prints them
+        (lower-case hex): per owner ("pool", "agent0", ...) a list over layers
+        of {"key_payload_digest", "value_payload_digest", "block_digest"}."""
+        rep = {}
+        for tier, name in ((self.pool, "pool"), (self.shells, "shell")):
+            pay = bufs[f"{name}_digests"].cpu().numpy()
+            lay = bufs[f"{name}_layer_digests"].cpu().numpy()
+            for i in range(len(tier.blob_offsets) // 2):
+                owner, layer, _, _, _ = tier.blob_offsets[2 * i]
+                rep.setdefault(owner, []).append({
+                    "layer_index": layer,
+                    "key_payload_digest": pay[i, 0].tobytes().hex(),
+                    "value_payload_digest": pay[i, 1].tobytes().hex(),
+                    "block_digest": lay[i].tobytes().hex(),
+                })
+        return rep
+
     # ------------------------------------------------------------ receipts
     def compressed_bytes(self) -> dict:
         """CLAIMS.json-style byte math: pool FB2 + shells TQB1(-L)."""

@@ -1,0 +1,166 @@
+"""BLAKE3 digests on the device against the oracle (bit-exact).
+
+* pkv_blake3 (host bytes through the device) on the published test vectors;
+* pkv_blake3_ranges over one buffer: empty ranges, every length class around
+  the block (64), chunk (1024) and pass (64 chunks, 4096 chunks) boundaries,
+  every start alignment, a range ending at the last byte of a buffer whose
+  size is not a multiple of 4, overlapping ranges;
+* a two-tier build: every blob's payload digest (CompressedBlock::new) and
+  every layer digest (PoolLayer / ShellLayer::compute_digest) against the
+  oracle over the wire bytes copied back;
+* quant-codec-core's digest types (digest_stability.rs) and profile digests;
+* argument errors.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from provekv_amd import _lib as L
+from provekv_amd import synth
+from provekv_amd.kvcodec import ArtifactDigest, CodecProfileDigest, DeviceKvCodec
+from provekv_amd.pool import TwoTierPlan
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+VECTORS = json.load(open(os.path.join(HERE, "golden", "blake3_vectors.json")))
+
+
+def test_blake3_host_bytes_known_answers(ctx):
+    for v in VECTORS["vectors"]:
+        data = bytes(i % 251 for i in range(v["input_len"]))
+        assert ctx.blake3(data).hex() == v["hash"], v["input_len"]
+    for v in VECTORS["ascii"]:
+        assert ctx.blake3(v["input"].encode()).hex() == v["hash"]
+
+
+def _ranges(buf_len: int, rng):
+    lens = [0, 1, 2, 3, 4, 5, 63, 64, 65, 127, 128, 1000, 1023, 1024, 1025, 2047, 2048, 2049, 3073,
+            63 * 1024 + 1, 64 * 1024 - 1, 64 * 1024, 64 * 1024 + 1, 65 * 1024 + 7,
+            4096 * 1024, 4096 * 1024 + 1, 4100 * 1024 + 5]
+    out = []
+    for ln in lens:
+        for align in range(4):
+            off = int(rng.integers(0, (buf_len - ln) // 4 + 1)) * 4 + align
+            off = min(off, buf_len - ln)
+            out.append((off, ln))
+    out += [(buf_len, 0), (buf_len - 1, 1), (buf_len - 3, 3), (buf_len - 1027, 1027), (0, buf_len),
+            (1, buf_len - 1), (2, buf_len - 2), (3, buf_len - 3)]
+    return out
+
+
+def test_ranges_match_oracle(ctx):
+    import torch
+    rng = np.random.default_rng(11)
+    n = 4100 * 1024 + 4099           # not a multiple of 4
+    host = rng.integers(0, 256, n, dtype=np.uint8)
+    buf = torch.from_numpy(host).cuda()
+    ranges = _ranges(n, rng)
+    print(f"{len(ranges)} ranges over {n} bytes", flush=True)
+    got = ctx.blake3_ranges(buf, ranges)
+    torch.cuda.synchronize()
+    want = O.blake3_ranges(host, ranges)
+    bad = [ranges[i] for i in range(len(ranges)) if not np.array_equal(got[i].cpu().numpy(), want[i])]
+    assert not bad, bad[:8]
+
+
+def test_ranges_twice_and_reused_output(ctx):
+    """Back-to-back calls on one stream (the ring slot and its chaining-value
+    scratch reused) give the same digests; a smaller second table too."""
+    import torch
+    rng = np.random.default_rng(12)
+    host = rng.integers(0, 256, 300_000, dtype=np.uint8)
+    buf = torch.from_numpy(host).cuda()
+    big = [(int(o), int(l)) for o, l in zip(rng.integers(0, 1000, 40), rng.integers(0, 299_000, 40))]
+    small = big[:3]
+    out = torch.full((40, 32), 0xA5, dtype=torch.uint8, device="cuda")
+    for table in (big, small, big):
+        ctx.blake3_ranges(buf, table, out=out)
+        torch.cuda.synchronize()
+        assert np.array_equal(out[:len(table)].cpu().numpy(), O.blake3_ranges(host, table))
+
+
+@pytest.mark.parametrize("lossy,two_streams", [(False, False), (True, False), (False, True)])
+def test_two_tier_digests_match_oracle(ctx, lossy, two_streams):
+    """Twice in a row (the second call reuses the first call's table slots),
+    outputs spoiled in between."""
+    import torch
+    layers, heads, dim, prefix, agents = 3, 8, 64, 200, [12, 40, 8]
+    corpus = synth.corpus_tokens(5, layers, heads, prefix + sum(agents), dim)
+    plan = TwoTierPlan(ctx, layers, heads, dim, prefix, agents, seed=42, lossy=lossy)
+    bufs = plan.alloc()
+    plan.encode(torch.from_numpy(corpus.reshape(-1)).cuda(), bufs)
+    side = torch.cuda.Stream() if two_streams else None
+    plan.digests(bufs, side=side)
+    torch.cuda.synchronize()
+    for k in ("pool_digests", "shell_digests", "pool_layer_digests", "shell_layer_digests"):
+        bufs[k].fill_(0x5A)
+    plan.digests(bufs, side=side)
+    torch.cuda.synchronize()
+    plan.check(bufs, decode=False)
+    rep = plan.digest_report(bufs)
+    for tier, name in ((plan.pool, "pool"), (plan.shells, "shell")):
+        wire = bufs[f"{name}_wire"].cpu().numpy()
+        for i in range(len(tier.blob_offsets) // 2):
+            owner, layer, _, ko, kl = tier.blob_offsets[2 * i]
+            _, _, _, vo, vl = tier.blob_offsets[2 * i + 1]
+            kd, vd = O.blake3(wire[ko:ko + kl].tobytes()), O.blake3(wire[vo:vo + vl].tobytes())
+            entry = [e for e in rep[owner] if e["layer_index"] == layer][0]
+            assert entry["key_payload_digest"] == kd.hex()
+            assert entry["value_payload_digest"] == vd.hex()
+            assert entry["block_digest"] == O.layer_digest(layer, kd, vd).hex()
+    assert sorted(rep) == ["agent0", "agent1", "agent2", "pool"]
+
+
+def test_layer_digests_entry_layout(ctx):
+    import torch
+    rng = np.random.default_rng(4)
+    kv = rng.integers(0, 256, (10, 2, 32), dtype=np.uint8)
+    got = ctx.layer_digests(torch.from_numpy(kv).cuda(), layers=4).cpu().numpy()
+    for i in range(10):
+        assert got[i].tobytes() == O.layer_digest(i % 4, kv[i, 0].tobytes(), kv[i, 1].tobytes())
+
+
+def test_digest_types(ctx):
+    # quant-codec-core/tests/digest_stability.rs
+    a = CodecProfileDigest.from_parts([b"codec", b"v1", b"profile"], ctx)
+    b = CodecProfileDigest.from_parts([b"codec", b"v1", b"profile"], ctx)
+    c = CodecProfileDigest.from_parts([b"codecv1", b"profile"], ctx)
+    assert a == b and a != c and len(str(a)) == 64
+    parts = b"".join(len(p).to_bytes(8, "little") + p for p in (b"codec", b"v1", b"profile"))
+    assert a.as_bytes() == O.blake3(parts)
+    assert CodecProfileDigest.from_canonical_bytes(b"mock", ctx).as_bytes() == O.blake3(b"mock")
+    art = ArtifactDigest.from_canonical_bytes(b"mock", ctx)
+    assert art.as_bytes() == O.blake3(b"mock") and art != CodecProfileDigest(art.as_bytes())
+
+
+def test_profile_digests(ctx):
+    turbo = ctx.turbo_profile(64, 4, 32, 42)
+    fib = ctx.fib_profile(64, 4, 32, 42)
+    dt = DeviceKvCodec(turbo, "turbo_8bit_batched")
+    dtl = DeviceKvCodec(turbo, "turbo_8bit_batched_lossy", radii=L.RADII_LOG_U8)
+    dfib = DeviceKvCodec(fib, "fib_k4_n32_batched")
+    d1 = dt.profile_digest()
+    assert d1 == dt.profile_digest()
+    parts = dt.canonical_profile_parts()
+    assert d1.as_bytes() == O.blake3(b"".join(len(p).to_bytes(8, "little") + p for p in parts))
+    others = {dtl.profile_digest(), dfib.profile_digest(),
+              DeviceKvCodec(ctx.turbo_profile(64, 4, 32, 43), "turbo_8bit_batched").profile_digest()}
+    assert d1 not in others and len(others) == 3
+
+
+def test_argument_errors(ctx):
+    import torch
+    buf = torch.zeros(100, dtype=torch.uint8, device="cuda")
+    with pytest.raises(L.PkvError) as e:
+        ctx.blake3_ranges(buf, [(90, 11)])
+    assert e.value.status == L.ERR_INVALID_ARG
+    with pytest.raises(L.PkvError):
+        ctx.blake3_ranges(buf, [(101, 0)])
+    out = torch.zeros(80, dtype=torch.uint8, device="cuda")
+    with pytest.raises(L.PkvError):
+        ctx.blake3_ranges(buf, [(0, 10)], out=out[1:33])
+    with pytest.raises(L.PkvError):
+        ctx.layer_digests(torch.zeros((2, 2, 32), dtype=torch.uint8, device="cuda"), layers=0)
