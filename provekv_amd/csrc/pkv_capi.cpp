@@ -21,7 +21,7 @@ using namespace pkv;
 
 namespace {
 
-constexpr int kSlots = 8;
+constexpr int kSlots = 32;   // table slots per context (allocated on first use)
 
 int hip_status(hipError_t e) {
     if (e == hipSuccess) return PKV_OK;
