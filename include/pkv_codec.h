@@ -393,6 +393,23 @@ int pkv_encode_diagnostics(pkv_ctx* ctx, const pkv_profile* prof, int radii_code
  * biased f32 exponent <= e. */
 int pkv_radii_log_bound(pkv_ctx* ctx, float* out);
 
+/* Lloyd-Max refinement of a codebook on the context's device: every restart
+ * at once, one workgroup each (refine_codebook's restart loop,
+ * fib-quant/src/lloyd.rs:128-147: `iterations` rounds of assign_samples and
+ * update_centroids with the SplitHighestDistortion repair, lloyd.rs:215-337,
+ * then mse_for_codebook, 339-357), bit-identical to the host computation.
+ * samples [ns][k] and starts [restarts][n][k] are f64 host arrays (the
+ * training draws and each restart's start, which the host derives from the
+ * seed); out_codebooks [restarts][n][k], out_mse [restarts] and *init_mse
+ * (the MSE of starts[0]) are host outputs.  k <= 16, n <= 256, n*k <= 2048;
+ * PKV_ERR_INVALID_ARG when an empty cell finds no donor
+ * (EmptyCellRepairFailed).  pkv_fib_profile_create refines a codebook it
+ * has not built yet in this process this way; the host generator
+ * pkv_fib_constants refines on the host. */
+int pkv_lloyd_refine(pkv_ctx* ctx, const double* samples, uint32_t ns, uint32_t k, uint32_t n,
+                     const double* starts, uint32_t restarts, uint32_t iterations, double* out_codebooks,
+                     double* out_mse, double* init_mse);
+
 /* ---------------------------------------------------------------- digests
  * BLAKE3 (the unkeyed 32-byte hash of the blake3 crate, 1.8.5 in the
  * reference's lock file) computed on the device.  Digests are raw 32-byte

@@ -140,6 +140,8 @@ def _declare(L):
     L.ora_pack_bits.argtypes = [P, U64, I32, P]
     L.ora_unpack_bits.argtypes = [P, U64, I32, P]
     L.ora_unpack_bits.restype = I32
+    L.ora_lloyd_refine.argtypes = [P, I32, I32, I32, P, I32, I32, P, P, P]
+    L.ora_lloyd_refine.restype = I32
     L.ora_blake3.argtypes = [P, U64, P]
     L.ora_blake3.restype = None
     L.ora_layer_digest.argtypes = [U32, P, P, P]
@@ -558,3 +560,19 @@ def layer_digest(layer_index: int, key_digest: bytes, value_digest: bytes) -> by
     out = np.zeros(32, np.uint8)
     lib().ora_layer_digest(layer_index, _p(k), _p(v), _p(out))
     return out.tobytes()
+
+
+def lloyd_refine(samples: np.ndarray, starts: np.ndarray, iterations: int):
+    """refine_codebook's restart loop over given samples [ns, k] and starts
+    [restarts, n, k]: (codebooks [restarts, n, k], mse [restarts], init_mse)."""
+    s = np.ascontiguousarray(samples, dtype=np.float64)
+    st = np.ascontiguousarray(starts, dtype=np.float64)
+    ns, k = s.shape
+    r, n, _ = st.shape
+    out = np.zeros_like(st)
+    mse = np.zeros(r)
+    init = np.zeros(1)
+    rc = lib().ora_lloyd_refine(_p(s), ns, k, n, _p(st), r, iterations, _p(out), _p(mse), _p(init))
+    if rc:
+        raise OracleError(rc)
+    return out, mse, float(init[0])

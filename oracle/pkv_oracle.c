@@ -673,6 +673,30 @@ static int update_centroids(double* cb, int k, int n, const double* samples, int
     return rc;
 }
 
+/* refine_codebook's restart loop (lloyd.rs:128-147) over given samples
+ * [ns][k] and starts [restarts][n][k]: each restart iterates assign_samples +
+ * update_centroids `iterations` times, then mse_for_codebook; init_mse is the
+ * MSE of starts[0].  Returns ORA_ERR_NUMERICAL when a repair finds no donor. */
+int ora_lloyd_refine(const double* samples, int ns, int k, int n, const double* starts, int restarts,
+                     int iterations, double* out_cb, double* out_mse, double* init_mse) {
+    if (ns <= 0 || k <= 0 || k > 16 || n < 2 || restarts <= 0) return ORA_ERR_INVALID_ARG;
+    size_t nk = (size_t)n * k;
+    int* asg = (int*)malloc(sizeof(int) * (size_t)ns);
+    int rc = ORA_OK;
+    *init_mse = mse_for_codebook(starts, k, n, samples, ns);
+    for (int r = 0; r < restarts && rc == ORA_OK; ++r) {
+        double* cb = out_cb + (size_t)r * nk;
+        memcpy(cb, starts + (size_t)r * nk, sizeof(double) * nk);
+        for (int it = 0; it < iterations && rc == ORA_OK; ++it) {
+            for (int i = 0; i < ns; ++i) asg[i] = nearest_index_f64(samples + (size_t)i * k, cb, k, n, NULL);
+            rc = update_centroids(cb, k, n, samples, ns, asg);
+        }
+        out_mse[r] = mse_for_codebook(cb, k, n, samples, ns);
+    }
+    free(asg);
+    return rc;
+}
+
 /* Test hook (not part of the restatement): every initial codeword
  * coordinate and every restart's rotated start is multiplied by
  * 1 +- g_perturb (sign from a fixed pseudo-random pattern), standing in for

@@ -969,6 +969,79 @@ static int fib_check(uint32_t dim, uint32_t k, uint32_t n) {
     return PKV_OK;
 }
 
+// ---- Lloyd refinement on the context's device (pkv_lloyd.hip)
+namespace {
+
+int lloyd_shape_ok(uint32_t ns, uint32_t k, uint32_t n, uint32_t restarts) {
+    if (k == 0 || n < 2 || k > LLOYD_MAX_K || n > LLOYD_MAX_N || n * k > LLOYD_MAX_NK) return PKV_ERR_UNSUPPORTED;
+    if (ns == 0 || restarts == 0 || restarts > 4096) return PKV_ERR_INVALID_ARG;
+    return PKV_OK;
+}
+
+// Caller holds ctx->mu.  Host buffers in and out; the device work runs on
+// the context's own stream, which the call waits for.
+int lloyd_on_device_locked(pkv_ctx* ctx, const double* samples, uint32_t ns, uint32_t k, uint32_t n,
+                           const double* starts, uint32_t restarts, uint32_t iterations, double* out_cb,
+                           double* out_mse, double* init_mse) {
+    int rc = lloyd_shape_ok(ns, k, n, restarts);
+    if (rc) return rc;
+    HIP_TRY(hipSetDevice(ctx->device));
+    const size_t s_bytes = sizeof(double) * ns * k, st_bytes = sizeof(double) * restarts * n * k;
+    auto pad = [](size_t b) { return (b + 255) & ~static_cast<size_t>(255); };
+    const size_t o_st = pad(s_bytes), o_cb = o_st + pad(st_bytes), o_mse = o_cb + pad(st_bytes),
+                 o_init = o_mse + pad(sizeof(double) * restarts), o_stat = o_init + 256,
+                 o_bd = o_stat + pad(sizeof(uint32_t) * restarts), o_asg = o_bd + pad(sizeof(double) * ns * restarts),
+                 total = o_asg + pad(static_cast<size_t>(ns) * restarts);
+    uint8_t* d = nullptr;
+    HIP_TRY(hipMalloc(&d, total));
+    hipStream_t st = ctx->own_stream;
+    std::vector<uint32_t> status(restarts, 1u);
+    hipError_t e = hipMemcpyAsync(d, samples, s_bytes, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(d + o_st, starts, st_bytes, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess)
+        e = static_cast<hipError_t>(launch_lloyd(
+            reinterpret_cast<const double*>(d), ns, k, n, reinterpret_cast<const double*>(d + o_st), restarts,
+            iterations, reinterpret_cast<double*>(d + o_cb), reinterpret_cast<double*>(d + o_mse),
+            reinterpret_cast<double*>(d + o_init), reinterpret_cast<uint32_t*>(d + o_stat),
+            reinterpret_cast<double*>(d + o_bd), d + o_asg, st));
+    if (e == hipSuccess) e = hipMemcpyAsync(out_cb, d + o_cb, st_bytes, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(out_mse, d + o_mse, sizeof(double) * restarts, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(init_mse, d + o_init, sizeof(double), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(status.data(), d + o_stat, sizeof(uint32_t) * restarts, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    (void)hipFree(d);
+    if (e != hipSuccess) return hip_status(e);
+    for (uint32_t v : status)
+        if (v) return PKV_ERR_INVALID_ARG;   // an empty cell with no donor (EmptyCellRepairFailed)
+    return PKV_OK;
+}
+
+struct CtxLloyd final : LloydDevice {
+    pkv_ctx* ctx;
+    explicit CtxLloyd(pkv_ctx* c) : ctx(c) {}
+    int refine(const std::vector<double>& samples, uint32_t ns, uint32_t k, uint32_t n,
+               const std::vector<double>& starts, uint32_t restarts, uint32_t iterations, std::vector<double>& out,
+               std::vector<double>& mse, double* init_mse) const override {
+        out.assign(static_cast<size_t>(restarts) * n * k, 0.0);
+        mse.assign(restarts, 0.0);
+        std::lock_guard<std::mutex> lock(ctx->mu);
+        return lloyd_on_device_locked(ctx, samples.data(), ns, k, n, starts.data(), restarts, iterations, out.data(),
+                                      mse.data(), init_mse);
+    }
+};
+
+}  // namespace
+
+int pkv_lloyd_refine(pkv_ctx* ctx, const double* samples, uint32_t ns, uint32_t k, uint32_t n, const double* starts,
+                     uint32_t restarts, uint32_t iterations, double* out_codebooks, double* out_mse,
+                     double* init_mse) {
+    if (!ctx || !samples || !starts || !out_codebooks || !out_mse || !init_mse) return PKV_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    return lloyd_on_device_locked(ctx, samples, ns, k, n, starts, restarts, iterations, out_codebooks, out_mse,
+                                  init_mse);
+}
+
 int pkv_fib_profile_create(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, uint64_t seed,
                            uint32_t training_samples, uint32_t lloyd_restarts, uint32_t lloyd_iterations,
                            pkv_profile** out) {
@@ -982,7 +1055,10 @@ int pkv_fib_profile_create(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, u
     if (training_samples < n || training_samples > 10000000) return PKV_ERR_INVALID_ARG;
     std::vector<float> cb;
     std::vector<double> rot, rot_t;
-    rc = make_fib_codebook(dim, k, n, seed, training_samples, lloyd_restarts, lloyd_iterations, cb, nullptr, nullptr);
+    // a codebook not built yet in this process is refined on the context's device
+    const CtxLloyd dev(ctx);
+    rc = make_fib_codebook(dim, k, n, seed, training_samples, lloyd_restarts, lloyd_iterations, cb, nullptr, nullptr,
+                           &dev);
     if (rc) return rc;
     rc = make_fib_rotation(dim, seed, rot);
     if (rc) return rc;

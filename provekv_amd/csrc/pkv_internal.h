@@ -114,9 +114,20 @@ struct HdrBytes {
 int make_turbo_constants(uint32_t dim, uint32_t proj, uint64_t seed, std::vector<float>& signs,
                          std::vector<float>& G);
 int make_fib_rotation(uint32_t dim, uint64_t seed, std::vector<double>& rot);
+// Runs the Lloyd iterations of every restart of a codebook build on a device
+// (pkv_capi.cpp implements it over a context, with the kernel of
+// pkv_lloyd.hip).  samples [ns][k], starts [restarts][n][k]; out [restarts][n][k],
+// mse [restarts], init_mse = MSE of starts[0].  Returns a pkv status.
+struct LloydDevice {
+    virtual ~LloydDevice() = default;
+    virtual int refine(const std::vector<double>& samples, uint32_t ns, uint32_t k, uint32_t n,
+                       const std::vector<double>& starts, uint32_t restarts, uint32_t iterations,
+                       std::vector<double>& out, std::vector<double>& mse, double* init_mse) const = 0;
+};
 int make_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint32_t training,
                       uint32_t restarts, uint32_t iterations, std::vector<float>& codebook,
-                      double* init_mse, double* train_mse);
+                      double* init_mse, double* train_mse,
+                      const LloydDevice* dev = nullptr);
 // The make_* builders above memoise per process (one build per distinct profile).
 void constants_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries);
 void constants_cache_clear();
@@ -157,6 +168,16 @@ int launch_records_gather(const uint8_t* rec, const uint64_t* off, uint64_t n, u
                           void* stream);
 int launch_fib_decode_f64(const FibDev& fd, const uint8_t* pay, uint64_t n, uint32_t plen, float* out,
                           uint32_t* status, void* stream);
+
+// Lloyd-Max refinement on the device (pkv_lloyd.hip): one workgroup per
+// restart over host-drawn samples [ns][k] and starts [restarts][n][k] (f64).
+// Outputs: refined codebooks [restarts][n][k], each restart's final MSE, the
+// MSE of restart 0's start, status[r] = 1 when an empty cell had no donor.
+// Scratch: ns f64 distances and ns u8 assignments per restart.
+constexpr uint32_t LLOYD_MAX_N = 256, LLOYD_MAX_K = 16, LLOYD_MAX_NK = 2048;
+int launch_lloyd(const double* samples, uint32_t ns, uint32_t k, uint32_t n, const double* starts, uint32_t restarts,
+                 uint32_t iterations, double* out_cb, double* out_mse, double* init_mse, uint32_t* status,
+                 double* bd_scratch, uint8_t* asg_scratch, void* stream);
 
 // BLAKE3 digests (pkv_blake3.hip).  A range as the kernels read it (same
 // layout as pkv_range) and one pass's record per range: the pass's first

@@ -430,7 +430,7 @@ int build_fib_rotation(uint32_t dim, uint64_t seed, std::vector<double>& rot) {
 
 int build_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint32_t training,
                        uint32_t restarts, uint32_t iterations, std::vector<float>& codebook,
-                       double* init_mse, double* train_mse) {
+                       double* init_mse, double* train_mse, const LloydDevice* dev) {
     if (k < 4 || k > 32 || dim % k != 0 || n < 2 || dim <= k) return PKV_ERR_UNSUPPORTED;
     const uint64_t cseed = seed + 0x9e3779b97f4a7c15ull;
     const int K = static_cast<int>(k), N = static_cast<int>(n), D = static_cast<int>(dim);
@@ -482,28 +482,55 @@ int build_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint
         double rr = std::sqrt(r2);
         for (int t = 0; t < K; ++t) samples[static_cast<size_t>(i) * K + t] = rr * dir[t];
     }
-    Lloyd lloyd{K, N, samples};
-    const double imse = lloyd.mse(init);
-    double best_mse = imse;
-    std::vector<double> best = init, cb;
+    // each restart's start: the initial codebook, then its codewords turned by
+    // a seeded k x k rotation (lloyd.rs:196-213)
     const uint32_t nr = restarts ? restarts : 1;
+    const size_t nk = init.size();
+    std::vector<double> starts(nr * nk);
     for (uint32_t rs = 0; rs < nr; ++rs) {
+        double* cb = &starts[rs * nk];
         if (rs == 0) {
-            cb = init;
-        } else {
-            std::vector<double> rot = stored_rotation(K, cseed + static_cast<uint64_t>(rs) * 0x9e3779b9ull);
-            cb.assign(init.size(), 0.0);
-            for (int w = 0; w < N; ++w)
-                for (int r = 0; r < K; ++r) {
-                    double s = 0.0;
-                    for (int c = 0; c < K; ++c) s += rot[r * K + c] * init[static_cast<size_t>(w) * K + c];
-                    cb[static_cast<size_t>(w) * K + r] = s;
-                }
+            std::copy(init.begin(), init.end(), cb);
+            continue;
         }
-        for (uint32_t it = 0; it < iterations; ++it)
-            if (!lloyd.iterate(cb)) return PKV_ERR_INVALID_ARG;
-        double m = lloyd.mse(cb);
-        if (m < best_mse || (rs == 0 && std::isinf(imse))) { best_mse = m; best = cb; }
+        std::vector<double> rot = stored_rotation(K, cseed + static_cast<uint64_t>(rs) * 0x9e3779b9ull);
+        for (int w = 0; w < N; ++w)
+            for (int r = 0; r < K; ++r) {
+                double s = 0.0;
+                for (int c = 0; c < K; ++c) s += rot[r * K + c] * init[static_cast<size_t>(w) * K + c];
+                cb[static_cast<size_t>(w) * K + r] = s;
+            }
+    }
+    // the restarts' refined codebooks and MSEs: on the device when one is
+    // given (and the shape fits its kernel), else here
+    std::vector<double> refined, mses(nr);
+    double imse;
+    if (dev && N <= static_cast<int>(LLOYD_MAX_N) && K <= static_cast<int>(LLOYD_MAX_K) &&
+        nk <= LLOYD_MAX_NK) {
+        int rc = dev->refine(samples, static_cast<uint32_t>(ns), k, n, starts, nr, iterations, refined, mses, &imse);
+        if (rc) return rc;
+    } else {
+        Lloyd lloyd{K, N, samples};
+        imse = lloyd.mse(init);
+        refined = starts;
+        for (uint32_t rs = 0; rs < nr; ++rs) {
+            std::vector<double> cb(starts.begin() + rs * nk, starts.begin() + (rs + 1) * nk);
+            for (uint32_t it = 0; it < iterations; ++it)
+                if (!lloyd.iterate(cb)) return PKV_ERR_INVALID_ARG;
+            mses[rs] = lloyd.mse(cb);
+            std::copy(cb.begin(), cb.end(), refined.begin() + rs * nk);
+        }
+    }
+    // refine_codebook's choice (lloyd.rs:148-163): a restart replaces the best
+    // so far only when strictly better; none better than the start keeps it
+    double best_mse = imse;
+    std::vector<double> best = init;
+    for (uint32_t rs = 0; rs < nr; ++rs) {
+        const double m = mses[rs];
+        if (m < best_mse || (rs == 0 && std::isinf(imse))) {
+            best_mse = m;
+            best.assign(refined.begin() + rs * nk, refined.begin() + (rs + 1) * nk);
+        }
     }
     if (best_mse > imse) { best = init; best_mse = imse; }
     codebook.resize(best.size());
@@ -592,10 +619,11 @@ int make_fib_rotation(uint32_t dim, uint64_t seed, std::vector<double>& rot) {
 
 int make_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint32_t training,
                       uint32_t restarts, uint32_t iterations, std::vector<float>& codebook,
-                      double* init_mse, double* train_mse) {
+                      double* init_mse, double* train_mse, const LloydDevice* dev) {
     std::shared_ptr<const FibCodebook> f;
     int rc = cached(cache().cb, FibKey(dim, k, n, seed, training, restarts, iterations), f, [&](FibCodebook& v) {
-        return build_fib_codebook(dim, k, n, seed, training, restarts, iterations, v.cb, &v.init_mse, &v.train_mse);
+        return build_fib_codebook(dim, k, n, seed, training, restarts, iterations, v.cb, &v.init_mse, &v.train_mse,
+                                  dev);
     });
     if (rc) return rc;
     codebook = f->cb;
