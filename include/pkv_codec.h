@@ -93,7 +93,9 @@ int pkv_turbo_profile_create_with_constants(pkv_ctx* ctx, uint32_t dim, uint32_t
 
 /* Replaces FibQuantAdapter::build_quantizer (proveKV/src/codec.rs:471-499):
  * paper_default profile with the adapter's training overrides; the codebook
- * (Lloyd-Max) and the f64 rotation are built on the host once and uploaded.
+ * and the f64 rotation are built once per process and uploaded (the host
+ * draws the training samples and restart starts, the Lloyd-Max iterations of
+ * a codebook not built yet run on this context's device, pkv_lloyd_refine).
  * The kernels implement fib_k4_n32 at head_dim 64 (dim 64, k 4, n 32);
  * other shapes return PKV_ERR_UNSUPPORTED. */
 int pkv_fib_profile_create(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, uint64_t seed,
@@ -392,6 +394,13 @@ int pkv_encode_diagnostics(pkv_ctx* ctx, const pkv_profile* prof, int radii_code
  * the largest |hardware log - logf(v)| over every v whose logf(v) has a
  * biased f32 exponent <= e. */
 int pkv_radii_log_bound(pkv_ctx* ctx, float* out);
+
+/* read_fb2_n_blocks (proveKV/src/pool.rs:108-116): the n_blocks field of a
+ * batched FB2 payload (bytes 10..14, little-endian) read without any profile
+ * check, as PoolLayer::num_blocks does for a batched layer.  PKV_OK with *n,
+ * or PKV_ERR_CORRUPT_PAYLOAD where the reference returns None (fewer than 14
+ * bytes, or no "FB2" magic).  Host only. */
+int pkv_fb2_n_blocks(const uint8_t* payload, uint64_t len, uint64_t* n);
 
 /* Lloyd-Max refinement of a codebook on the context's device: every restart
  * at once, one workgroup each (refine_codebook's restart loop,

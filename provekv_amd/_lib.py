@@ -51,7 +51,7 @@ EXPORTS = (
     "pkv_decode_batch_compact", "pkv_parse_header", "pkv_record_len", "pkv_encode_vectors", "pkv_decode_vectors",
     "pkv_constants_cache_stats", "pkv_constants_cache_clear", "pkv_prepared_len", "pkv_turbo_prepare_queries",
     "pkv_turbo_score_segments", "pkv_score_status", "pkv_turbo_score_batch", "pkv_encode_diagnostics",
-    "pkv_radii_log_bound", "pkv_lloyd_refine", "pkv_blake3_ranges", "pkv_blake3_layer_digests", "pkv_blake3",
+    "pkv_radii_log_bound", "pkv_fb2_n_blocks", "pkv_lloyd_refine", "pkv_blake3_ranges", "pkv_blake3_layer_digests", "pkv_blake3",
     "pkv_host_angle_bins", "pkv_host_logf",
     "pkv_host_expf",
 )
@@ -142,6 +142,7 @@ def _declare(L):
         "pkv_turbo_score_batch": ([P, P, P, U64, P, U32, C.c_float, P, U64, P, P], I32),
         "pkv_encode_diagnostics": ([P, P, I32, P, U64, P, U64, P, U64, P, P, P], I32),
         "pkv_radii_log_bound": ([P, P], I32),
+        "pkv_fb2_n_blocks": ([P, U64, P], I32),
         "pkv_lloyd_refine": ([P, P, U32, U32, U32, P, U32, U32, P, P, P], I32),
         "pkv_blake3_ranges": ([P, P, U64, P, U32, P, P], I32),
         "pkv_blake3_layer_digests": ([P, P, U32, U32, P, P], I32),

@@ -1377,6 +1377,13 @@ int pkv_blake3(pkv_ctx* ctx, const void* data, uint64_t len, uint8_t out[32]) {
     return PKV_OK;
 }
 
+int pkv_fb2_n_blocks(const uint8_t* payload, uint64_t len, uint64_t* n) {
+    if (!n || (!payload && len)) return PKV_ERR_INVALID_ARG;
+    if (len < 14 || std::memcmp(payload, "FB2", 3) != 0) return PKV_ERR_CORRUPT_PAYLOAD;
+    *n = rd32(payload + 10);
+    return PKV_OK;
+}
+
 int pkv_parse_header(const pkv_profile* p, const uint8_t* b, uint64_t len, uint64_t* n_vectors, int* radii_codec) {
     if (!p || !b) return PKV_ERR_INVALID_ARG;
     if (p->kind == PKV_CODEC_TURBO) {

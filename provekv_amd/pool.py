@@ -24,6 +24,20 @@ from . import _lib as L
 from .device import SEG_DTYPE
 
 
+def read_fb2_n_blocks(payload: bytes):
+    """read_fb2_n_blocks (proveKV/src/pool.rs:108-116): the FB2 n_blocks field
+    of a batched pool payload, or None for a payload shorter than 14 bytes or
+    without the "FB2" magic (no profile check)."""
+    import ctypes as C
+    buf = bytes(payload)
+    n = C.c_uint64()
+    rc = L.lib().pkv_fb2_n_blocks(buf, len(buf), C.byref(n))
+    if rc == L.ERR_CORRUPT_PAYLOAD:
+        return None
+    L.check(rc, "pkv_fb2_n_blocks")
+    return int(n.value)
+
+
 @dataclass
 class TierLayout:
     """Segment tables of one tier (pool or all shells)."""
@@ -311,19 +325,24 @@ class TwoTierPlan:
     def digest_report(self, bufs) -> dict:
         """The digests of the last digests() call as the reference prints them
         (lower-case hex): per owner ("pool", "agent0", ...) a list over layers
-        of {"key_payload_digest", "value_payload_digest", "block_digest"}."""
+        of {"key_payload_digest", "value_payload_digest", "block_digest"};
+        pool layers also carry "num_blocks", PoolLayer::num_blocks of a
+        batched layer (the key blob's FB2 n_blocks, pool.rs:60-80)."""
         rep = {}
         for tier, name in ((self.pool, "pool"), (self.shells, "shell")):
             pay = bufs[f"{name}_digests"].cpu().numpy()
             lay = bufs[f"{name}_layer_digests"].cpu().numpy()
             for i in range(len(tier.blob_offsets) // 2):
-                owner, layer, _, _, _ = tier.blob_offsets[2 * i]
-                rep.setdefault(owner, []).append({
+                owner, layer, _, ko, _ = tier.blob_offsets[2 * i]
+                entry = {
                     "layer_index": layer,
                     "key_payload_digest": pay[i, 0].tobytes().hex(),
                     "value_payload_digest": pay[i, 1].tobytes().hex(),
                     "block_digest": lay[i].tobytes().hex(),
-                })
+                }
+                if name == "pool":
+                    entry["num_blocks"] = read_fb2_n_blocks(bufs["pool_wire"][ko:ko + 14].cpu().numpy().tobytes())
+                rep.setdefault(owner, []).append(entry)
         return rep
 
     # ------------------------------------------------------------ receipts

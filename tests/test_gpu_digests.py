@@ -111,6 +111,8 @@ def test_two_tier_digests_match_oracle(ctx, lossy, two_streams):
             assert entry["key_payload_digest"] == kd.hex()
             assert entry["value_payload_digest"] == vd.hex()
             assert entry["block_digest"] == O.layer_digest(layer, kd, vd).hex()
+            if owner == "pool":
+                assert entry["num_blocks"] == prefix * heads   # one FB2 block per (token, head)
     assert sorted(rep) == ["agent0", "agent1", "agent2", "pool"]
 
 

@@ -202,3 +202,16 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode == 2
     line = json.loads(r.stdout.strip().splitlines()[-1])
     assert line["n_gpus"] == 2 and "one GPU" in line["error"]
+
+
+def test_read_fb2_n_blocks():
+    """read_fb2_n_blocks (proveKV/src/pool.rs:108-116): a structural read of
+    bytes 10..14, None below 14 bytes or without the FB2 magic."""
+    from provekv_amd.pool import read_fb2_n_blocks
+    hdr = bytearray(b"FB2\x01\x05\x00") + (16).to_bytes(4, "little") + (0x01020304).to_bytes(4, "little")
+    assert read_fb2_n_blocks(bytes(hdr)) == 0x01020304
+    assert read_fb2_n_blocks(bytes(hdr) + b"\x00" * 5) == 0x01020304   # rest of the header unchecked
+    assert read_fb2_n_blocks(bytes(hdr[:13])) is None
+    assert read_fb2_n_blocks(b"") is None
+    assert read_fb2_n_blocks(b"TQB1" + bytes(hdr[4:])) is None
+    assert read_fb2_n_blocks(b"FB2\x07" + bytes(hdr[4:])) == 0x01020304   # version not checked either
