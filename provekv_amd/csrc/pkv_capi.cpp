@@ -1313,7 +1313,8 @@ int blake3_ranges_locked(pkv_ctx* ctx, const uint8_t* d_buf, uint64_t buf_bytes,
         std::memcpy(h, ranges, range_bytes);
         std::memcpy(h + pass_off, plan.passes.data(), pass_bytes);
         cp = hipMemcpyAsync(sl->dev, sl->host, pass_off + pass_bytes, hipMemcpyHostToDevice, stream);
-        sl->digest = true;
+        // reusable by a later call only once its table is on the way to the device
+        sl->digest = cp == hipSuccess;
         sl->nseg = nr;
         sl->hash = hash;
     }
