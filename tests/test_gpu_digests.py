@@ -166,3 +166,29 @@ def test_argument_errors(ctx):
         ctx.blake3_ranges(buf, [(0, 10)], out=out[1:33])
     with pytest.raises(L.PkvError):
         ctx.layer_digests(torch.zeros((2, 2, 32), dtype=torch.uint8, device="cuda"), layers=0)
+
+
+def test_same_table_on_two_streams(ctx):
+    """One range table digested alternately on two streams, with a long
+    kernel queued ahead on each: a call reuses a table slot (and its
+    chaining-value scratch) only after an earlier call on its own stream, so
+    both streams' digests stay correct."""
+    import torch
+    rng = np.random.default_rng(21)
+    host = rng.integers(0, 256, 3_000_000, dtype=np.uint8)
+    buf = torch.from_numpy(host).cuda()
+    table = [(int(o), int(l)) for o, l in zip(rng.integers(0, 10_000, 24), rng.integers(60_000, 2_900_000, 24))]
+    want = O.blake3_ranges(host, table)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = [torch.empty((24, 32), dtype=torch.uint8, device="cuda") for _ in range(2)]
+    for _ in range(4):
+        for o in outs:
+            o.fill_(0xA5)
+        torch.cuda.synchronize()
+        for st, o in zip((s1, s2), outs):
+            with torch.cuda.stream(st):
+                torch.cuda._sleep(2_000_000)
+            ctx.blake3_ranges(buf, table, out=o, stream=st)
+        torch.cuda.synchronize()
+        for o in outs:
+            assert np.array_equal(o.cpu().numpy(), want)
