@@ -98,6 +98,80 @@ __device__ __forceinline__ void chunk_cv(const uint8_t* base, uint64_t len, uint
     }
 }
 
+// ---- four lanes per chunk (wires with too few chunks to fill the GPU one
+// lane per chunk)
+//
+// Lane i of a quad holds column i of the compression state: a = v[i],
+// b = v[4 + i], c = v[8 + i], d = v[12 + i].  The column step is the quad's
+// four G at once; for the diagonal step lane i needs b, c, d of lanes i + 1,
+// i + 2, i + 3 (mod 4), brought by DPP quad rotations and sent back after.
+// The chaining value stays split the same way (lane i: words i and 4 + i),
+// so blocks chain without moving data between lanes.  Message words come from
+// the quad's 64-byte block in LDS; lane i's four words of round r are
+// m[s_r(2i)], m[s_r(2i + 1)], m[s_r(8 + 2i)], m[s_r(9 + 2i)], whose LDS
+// addresses are computed once per kernel.
+
+__device__ __forceinline__ void wave_sync_lds() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// DPP quad rotations: lane i reads lane i + 1, i + 2, i + 3 (mod 4)
+__device__ __forceinline__ uint32_t qrot1(uint32_t x) { return __builtin_amdgcn_mov_dpp(x, 0x39, 0xf, 0xf, false); }
+__device__ __forceinline__ uint32_t qrot2(uint32_t x) { return __builtin_amdgcn_mov_dpp(x, 0x4e, 0xf, 0xf, false); }
+__device__ __forceinline__ uint32_t qrot3(uint32_t x) { return __builtin_amdgcn_mov_dpp(x, 0x93, 0xf, 0xf, false); }
+
+__device__ __forceinline__ void g1(uint32_t& a, uint32_t& b, uint32_t& c, uint32_t& d, uint32_t mx, uint32_t my) {
+    b3::g(a, b, c, d, mx, my);
+}
+
+// Word indices (0..15) of lane i's four message words in each round.
+struct QuadMsgIdx {
+    uint32_t w[7][4];
+};
+__device__ __forceinline__ QuadMsgIdx quad_msg_idx(uint32_t i) {
+    QuadMsgIdx q;
+#pragma unroll
+    for (int r = 0; r < 7; ++r) {
+        const uint8_t* s = b3::SCHED.s[r];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            q.w[r][k] = i == 0 ? s[k] : i == 1 ? s[2 + k] : i == 2 ? s[4 + k] : s[6 + k];
+            q.w[r][2 + k] = i == 0 ? s[8 + k] : i == 1 ? s[10 + k] : i == 2 ? s[12 + k] : s[14 + k];
+        }
+    }
+    return q;
+}
+
+// One compression on the quad.  (cv_lo, cv_hi) = chaining value words
+// (i, 4 + i) in and out; message word k is word(k), read from LDS.
+template <typename Word>
+__device__ __forceinline__ void quad_compress(uint32_t& cv_lo, uint32_t& cv_hi, uint32_t i, const QuadMsgIdx& q,
+                                              Word word, uint64_t counter, uint32_t block_len, uint32_t flags) {
+    uint32_t a = cv_lo, b = cv_hi;
+    uint32_t c = i == 0 ? PKV_B3_IV0 : i == 1 ? PKV_B3_IV1 : i == 2 ? PKV_B3_IV2 : PKV_B3_IV3;
+    uint32_t d = i == 0 ? static_cast<uint32_t>(counter)
+               : i == 1 ? static_cast<uint32_t>(counter >> 32)
+               : i == 2 ? block_len
+                        : flags;
+#pragma unroll
+    for (int r = 0; r < 7; ++r) {
+        const uint32_t mx = word(q.w[r][0]), my = word(q.w[r][1]);
+        const uint32_t nx = word(q.w[r][2]), ny = word(q.w[r][3]);
+        g1(a, b, c, d, mx, my);
+        b = qrot1(b);
+        c = qrot2(c);
+        d = qrot3(d);
+        g1(a, b, c, d, nx, ny);
+        b = qrot3(b);
+        c = qrot2(c);
+        d = qrot1(d);
+    }
+    cv_lo = a ^ c;
+    cv_hi = b ^ d;
+}
+
 }  // namespace
 
 // One wave per tile of 64 elements of one range (pass table: B3Pass per range
@@ -149,6 +223,110 @@ __global__ __launch_bounds__(256) void blake3_tree_kernel(const uint8_t* __restr
         uint32_t* dst = root_group ? out + 8ull * r : cv_out + 8ull * (ps.out_base + g);
 #pragma unroll
         for (int i = 0; i < 8; ++i) dst[i] = cv[i];
+    }
+}
+
+// Pass 0 with four lanes per chunk: 16 chunks per wave (one per quad), then
+// the wave merges its 16 chaining values over four levels, one parent per
+// active quad.  Tiles are 16 chunks; a range of at most 16 chunks ends here.
+__global__ __launch_bounds__(256) void blake3_quad_kernel(const uint8_t* __restrict__ buf,
+                                                          const B3Range* __restrict__ ranges,
+                                                          const B3Pass* __restrict__ pass, uint32_t nr,
+                                                          uint32_t* __restrict__ cv_out, uint32_t* __restrict__ out) {
+    __shared__ uint32_t blk_s[4][16][16];   // per wave, per quad: the current 64-byte block
+    __shared__ uint32_t cv_s[4][16][8];     // per wave, per quad: its chaining value
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t quad = lane >> 2, i = lane & 3u;
+    const uint32_t tile = __builtin_amdgcn_readfirstlane(blockIdx.x * 4u + wave);
+    if (tile >= pass[nr].tile_start) return;
+    uint32_t lo = 0, hi = nr;   // pass[lo].tile_start <= tile < pass[hi].tile_start
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (pass[mid].tile_start <= tile) lo = mid;
+        else hi = mid;
+    }
+    const uint32_t r = lo;
+    const B3Pass ps = pass[r];
+    const uint32_t g = tile - ps.tile_start;
+    const uint32_t first = g * 16u;
+    const uint32_t nq = ps.count - first < 16u ? ps.count - first : 16u;   // quads with a chunk
+    const bool root_group = ps.count <= 16u;
+    const QuadMsgIdx qi = quad_msg_idx(i);
+    const uint32_t* my_blk = blk_s[wave][quad];
+
+    uint32_t cv_lo = i == 0 ? PKV_B3_IV0 : i == 1 ? PKV_B3_IV1 : i == 2 ? PKV_B3_IV2 : PKV_B3_IV3;
+    uint32_t cv_hi = i == 0 ? PKV_B3_IV4 : i == 1 ? PKV_B3_IV5 : i == 2 ? PKV_B3_IV6 : PKV_B3_IV7;
+    {
+        const B3Range rg = ranges[r];
+        const uint64_t chunk = first + (quad < nq ? quad : 0u);
+        const uint64_t start = chunk * b3::CHUNK_BYTES;
+        const uint64_t left = rg.len - start;
+        const uint32_t clen = left < b3::CHUNK_BYTES ? static_cast<uint32_t>(left) : b3::CHUNK_BYTES;
+        // the wave runs as many blocks as its longest chunk (every chunk but
+        // a range's last is whole: 16 blocks); quads past nq and a shorter
+        // last chunk idle through the rest
+        const uint32_t nblk = clen == 0 ? 1u : (clen + 63u) / 64u;
+        const uint32_t wblk = nq > 1u ? 16u : __builtin_amdgcn_readfirstlane(nblk);
+        const uint8_t* base = buf + rg.offset + start;
+        const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(base) & 3u);
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(base - sh);
+        const bool root = ps.count == 1u;
+        for (uint32_t b = 0; b < wblk; ++b) {
+            const bool live = quad < nq && b < nblk;
+            const uint32_t blen = clen - 64u * b < 64u ? clen - 64u * b : 64u;
+            // lane i: message words 4i .. 4i + 3 from dwords 4i .. 4i + 4 of the block
+            uint32_t dw[5] = {0u, 0u, 0u, 0u, 0u};
+            if (live) {
+                const uint32_t nd = blen ? (sh + blen + 3u) >> 2 : 0u;
+#pragma unroll
+                for (uint32_t k = 0; k < 5; ++k)
+                    if (4u * i + k < nd) dw[k] = p[16u * b + 4u * i + k];
+            }
+            uint32_t w[4];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                w[j] = __builtin_amdgcn_alignbyte(dw[j + 1], dw[j], sh);
+                const int rem = static_cast<int>(blen) - static_cast<int>(4u * (4u * i + j));
+                w[j] = rem >= 4 ? w[j] : rem <= 0 ? 0u : (w[j] & ((1u << (8 * rem)) - 1u));
+            }
+            *reinterpret_cast<uint4*>(&blk_s[wave][quad][4u * i]) = make_uint4(w[0], w[1], w[2], w[3]);
+            wave_sync_lds();
+            uint32_t flags = b == 0 ? b3::CHUNK_START : 0u;
+            if (b == nblk - 1) flags |= b3::CHUNK_END | (root ? b3::ROOT : 0u);
+            uint32_t nlo = cv_lo, nhi = cv_hi;
+            quad_compress(nlo, nhi, i, qi, [&](uint32_t k) { return my_blk[k]; }, chunk, blen, flags);
+            if (live) {
+                cv_lo = nlo;
+                cv_hi = nhi;
+            }
+            wave_sync_lds();   // every quad has read its block before the next one lands
+        }
+    }
+    // merge the quads' chaining values: level s pairs quads q, q + s
+    cv_s[wave][quad][i] = cv_lo;
+    cv_s[wave][quad][4u + i] = cv_hi;
+    wave_sync_lds();
+    for (uint32_t s = 1; s < nq; s <<= 1) {
+        const uint32_t c = (nq + s - 1u) / s;
+        const bool act = (quad & (2u * s - 1u)) == 0u && quad / s + 1u < c;
+        const uint32_t partner = act ? quad + s : quad;
+        uint32_t plo = i == 0 ? PKV_B3_IV0 : i == 1 ? PKV_B3_IV1 : i == 2 ? PKV_B3_IV2 : PKV_B3_IV3;
+        uint32_t phi = i == 0 ? PKV_B3_IV4 : i == 1 ? PKV_B3_IV5 : i == 2 ? PKV_B3_IV6 : PKV_B3_IV7;
+        const uint32_t* left = cv_s[wave][quad];
+        const uint32_t* right = cv_s[wave][partner];
+        quad_compress(plo, phi, i, qi, [&](uint32_t k) { return k < 8u ? left[k] : right[k - 8u]; }, 0,
+                      b3::BLOCK_BYTES, b3::PARENT | (root_group && c == 2u ? b3::ROOT : 0u));
+        wave_sync_lds();   // all reads of this level done
+        if (act) {
+            cv_s[wave][quad][i] = plo;
+            cv_s[wave][quad][4u + i] = phi;
+        }
+        wave_sync_lds();
+    }
+    if (quad == 0) {   // out is only 4-byte aligned
+        uint32_t* dst = root_group ? out + 8ull * r : cv_out + 8ull * (ps.out_base + g);
+        dst[i] = cv_s[wave][0][i];
+        dst[4u + i] = cv_s[wave][0][4u + i];
     }
 }
 
@@ -218,6 +396,14 @@ int launch_blake3_pass(const uint8_t* buf, const B3Range* ranges, const B3Pass* 
     const uint32_t grid = (tiles + 3u) / 4u;
     hipLaunchKernelGGL(blake3_tree_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), buf, ranges, pass, nr, cv_in, cv_out,
                        out, leaf ? 1u : 0u);
+    return hipGetLastError();
+}
+
+int launch_blake3_quad(const uint8_t* buf, const B3Range* ranges, const B3Pass* pass, uint32_t nr, uint32_t tiles,
+                       uint32_t* cv_out, uint32_t* out, void* stream) {
+    if (tiles == 0) return hipSuccess;
+    hipLaunchKernelGGL(blake3_quad_kernel, dim3((tiles + 3u) / 4u), dim3(256), 0, static_cast<hipStream_t>(stream), buf,
+                       ranges, pass, nr, cv_out, out);
     return hipGetLastError();
 }
 

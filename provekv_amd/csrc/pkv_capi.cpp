@@ -1243,30 +1243,41 @@ struct B3Plan {
     std::vector<B3Pass> passes;     // passes.size() == npass * (nr + 1)
     std::vector<uint32_t> tiles;    // per pass
     uint64_t cvs = 0;               // chaining values written by passes that do not finish a range
+    bool quad = false;              // pass 0 on four lanes per chunk (16-chunk tiles)
 };
+
+// Chunks below which pass 0 puts four lanes on a chunk (16 chunks per wave,
+// ~1.4x the instructions, a quarter of the latency): one lane per chunk would
+// leave the GPU with fewer than half a wave per SIMD.  Measured at config 3:
+// the pool's 14.4 Ki chunks 47 -> 31 us, the shells' 48 Ki chunks 43 -> 50 us.
+constexpr uint64_t kB3QuadBelow = 32ull * 1024;
 
 int plan_blake3(const pkv_range* ranges, uint32_t nr, uint64_t buf_bytes, B3Plan* plan) {
     std::vector<uint64_t> count(nr), in_base(nr, 0);
+    uint64_t total = 0;
     for (uint32_t r = 0; r < nr; ++r) {
         const pkv_range& g = ranges[r];
         if (g.offset > buf_bytes || g.len > buf_bytes - g.offset) return PKV_ERR_INVALID_ARG;
         count[r] = b3::chunks_of(g.len);
         if (count[r] > 0xFFFFFFFFull) return PKV_ERR_INVALID_ARG;
+        total += count[r];
     }
+    plan->quad = total < kB3QuadBelow;
     for (bool more = true; more;) {
         more = false;
         const size_t base = plan->passes.size();
+        const uint64_t per_tile = base == 0 && plan->quad ? 16 : 64;   // elements per wave in this pass
         plan->passes.resize(base + nr + 1);
         uint64_t tiles = 0;
         for (uint32_t r = 0; r < nr; ++r) {
             B3Pass& ps = plan->passes[base + r];
-            const uint64_t c = count[r], t = (c + 63) / 64;
+            const uint64_t c = count[r], t = (c + per_tile - 1) / per_tile;
             ps.tile_start = static_cast<uint32_t>(tiles);
             ps.count = static_cast<uint32_t>(c);
             ps.in_base = static_cast<uint32_t>(in_base[r]);
             ps.out_base = 0;
             tiles += t;
-            if (c > 64) {   // not finished in this pass: t chaining values go on
+            if (t > 1) {   // not finished in this pass: t chaining values go on
                 ps.out_base = static_cast<uint32_t>(plan->cvs);
                 in_base[r] = plan->cvs;
                 plan->cvs += t;
@@ -1325,7 +1336,9 @@ int blake3_ranges_locked(pkv_ctx* ctx, const uint8_t* d_buf, uint64_t buf_bytes,
     int e = cp;
     for (size_t p = 0; p < plan.tiles.size() && !e; ++p) {
         const auto* d_pass = reinterpret_cast<const B3Pass*>(d + pass_off) + p * (nr + 1);
-        e = launch_blake3_pass(d_buf, d_ranges, d_pass, nr, plan.tiles[p], d_cv, d_cv, out, p == 0, stream);
+        e = p == 0 && plan.quad
+                ? launch_blake3_quad(d_buf, d_ranges, d_pass, nr, plan.tiles[p], d_cv, out, stream)
+                : launch_blake3_pass(d_buf, d_ranges, d_pass, nr, plan.tiles[p], d_cv, d_cv, out, p == 0, stream);
     }
     const int rc2 = finish_slot(sl, stream);
     if (e) return hip_status(static_cast<hipError_t>(e));

@@ -195,6 +195,10 @@ struct B3Pass {
 };
 int launch_blake3_pass(const uint8_t* buf, const B3Range* ranges, const B3Pass* pass, uint32_t nr, uint32_t tiles,
                        const uint32_t* cv_in, uint32_t* cv_out, uint32_t* out, bool leaf, void* stream);
+// Pass 0 with four lanes per chunk (tiles of 16 chunks; pass records as for
+// launch_blake3_pass with leaf set).
+int launch_blake3_quad(const uint8_t* buf, const B3Range* ranges, const B3Pass* pass, uint32_t nr, uint32_t tiles,
+                       uint32_t* cv_out, uint32_t* out, void* stream);
 int launch_blake3_layers(const uint32_t* kv, uint32_t n, uint32_t layers, uint32_t* out, void* stream);
 
 }  // namespace pkv

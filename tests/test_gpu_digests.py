@@ -2,7 +2,8 @@
 
 * pkv_blake3 (host bytes through the device) on the published test vectors;
 * pkv_blake3_ranges over one buffer: empty ranges, every length class around
-  the block (64), chunk (1024) and pass (64 chunks, 4096 chunks) boundaries,
+  the block (64), chunk (1024) and pass (16, 64 and 4096 chunks) boundaries,
+  with the first pass on four lanes per chunk and on one,
   every start alignment, a range ending at the last byte of a buffer whose
   size is not a multiple of 4, overlapping ranges;
 * a two-tier build: every blob's payload digest (CompressedBlock::new) and
@@ -38,7 +39,9 @@ def test_blake3_host_bytes_known_answers(ctx):
 
 def _ranges(buf_len: int, rng):
     lens = [0, 1, 2, 3, 4, 5, 63, 64, 65, 127, 128, 1000, 1023, 1024, 1025, 2047, 2048, 2049, 3073,
+            15 * 1024 + 1, 16 * 1024 - 1, 16 * 1024, 16 * 1024 + 1, 17 * 1024,
             63 * 1024 + 1, 64 * 1024 - 1, 64 * 1024, 64 * 1024 + 1, 65 * 1024 + 7,
+            1024 * 1024, 1024 * 1024 + 1,
             4096 * 1024, 4096 * 1024 + 1, 4100 * 1024 + 5]
     out = []
     for ln in lens:
@@ -51,19 +54,51 @@ def _ranges(buf_len: int, rng):
     return out
 
 
-def test_ranges_match_oracle(ctx):
+def _chunks(ranges):
+    return sum(max(1, (ln + 1023) // 1024) for _, ln in ranges)
+
+
+@pytest.mark.parametrize("mode", ["quad", "lane"])
+def test_ranges_match_oracle(ctx, mode):
+    """Both first-pass forms: a call of fewer than 32 Ki chunks runs four
+    lanes per chunk, a larger one one lane per chunk."""
     import torch
     rng = np.random.default_rng(11)
     n = 4100 * 1024 + 4099           # not a multiple of 4
     host = rng.integers(0, 256, n, dtype=np.uint8)
     buf = torch.from_numpy(host).cuda()
     ranges = _ranges(n, rng)
+    if mode == "quad":
+        keep, total = [], 0
+        for r in ranges:
+            if total + _chunks([r]) < 32 * 1024:
+                keep.append(r)
+                total += _chunks([r])
+        ranges = keep
+        assert _chunks(ranges) < 32 * 1024 and any(ln > 4096 * 1024 for _, ln in ranges)
+    else:
+        assert _chunks(ranges) >= 32 * 1024
     print(f"{len(ranges)} ranges over {n} bytes", flush=True)
     got = ctx.blake3_ranges(buf, ranges)
     torch.cuda.synchronize()
     want = O.blake3_ranges(host, ranges)
     bad = [ranges[i] for i in range(len(ranges)) if not np.array_equal(got[i].cpu().numpy(), want[i])]
     assert not bad, bad[:8]
+
+
+def test_ranges_lane_mode_match_oracle(ctx):
+    """32 Ki chunks or more in one call (here: 40 overlapping ranges of
+    ~4.1 MB) take the one-lane-per-chunk first pass; fewer take four lanes
+    per chunk (the other range tests here)."""
+    import torch
+    rng = np.random.default_rng(13)
+    n = 5 * 1024 * 1024 + 3
+    host = rng.integers(0, 256, n, dtype=np.uint8)
+    buf = torch.from_numpy(host).cuda()
+    ranges = [(int(a), 4100 * 1024 + int(b)) for a, b in zip(rng.integers(0, 900_000, 40), rng.integers(0, 2048, 40))]
+    assert sum((ln + 1023) // 1024 for _, ln in ranges) >= 32 * 1024
+    got = ctx.blake3_ranges(buf, ranges).cpu().numpy()
+    assert np.array_equal(got, O.blake3_ranges(host, ranges))
 
 
 def test_ranges_twice_and_reused_output(ctx):
