@@ -232,6 +232,58 @@ def test_bounded_fib_decode_matches_full_grid(ctx, max_workgroups, copies):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("heads,prefix,copies,bound", [(8, 256, 3, 0), (32, 96, 8, 0), (16, 48, 2, 5),
+                                                       (4, 128, 8, 3)])
+def test_head_major_fanout_rehydrate(ctx, heads, prefix, copies, bound):
+    """Pool blobs of T tokens x G heads whose vector count is a multiple of
+    256 rehydrate with each wave on tt consecutive tokens of 64 / tt heads
+    (tt = 64, 32, 16 here): every copy equals the oracle's decode, and a
+    corrupt norm is reported at its own vector index."""
+    import torch
+    from provekv_amd.pool import DeviceKVCache
+    layers, dim, agents = 2, 64, [5]
+    assert (prefix * heads) % 256 == 0
+    corpus = synth.corpus_tokens(31, layers, heads, prefix + sum(agents), dim)
+    plan = TwoTierPlan(ctx, layers, heads, dim, prefix, agents, seed=SEED)
+    bufs = plan.alloc()
+    plan.encode(torch.from_numpy(corpus.reshape(-1)).cuda(), bufs)
+    plen = plan.fib.payload_len()
+    bad_v = 3 * heads + 1                       # token 3, head 1 of blob 1 (layer 0, V)
+    _, _, _, off, _ = plan.pool.blob_offsets[1]
+    pos = off + 19 + bad_v * plen
+    bufs["pool_wire"][pos:pos + 2] = torch.tensor([0x00, 0x7C], dtype=torch.uint8, device="cuda")
+    cache = DeviceKVCache(layers, heads, prefix + sum(agents), dim, copies=copies)
+    cache.buf.fill_(5.0)
+    plan._cache_tables(bufs, cache)
+    pseg, _ = plan._cache_segs
+    st = torch.zeros(2 * len(pseg), dtype=torch.int32, device="cuda")
+    plan.fib.decode_segments(bufs["pool_wire"], pseg, cache.buf.view(-1), status=st, fanout=copies,
+                             fanout_stride=cache.copy_stride, max_workgroups=bound)
+    torch.cuda.synchronize()
+    err = plan.fib.status_error(st.cpu().numpy().view(np.uint32), pseg)
+    assert err is not None and err.segment == 1 and err.index == bad_v
+    got = cache.buf.cpu()
+    cb, rot = O.fib_constants(SEED)
+    for k, (_, layer, side, _, _) in enumerate(plan.pool.blob_offsets):
+        want = O.fib_decode_batch(plan.blob(bufs, "pool", k) if k != 1 else _restore(plan, bufs, k, bad_v),
+                                  cb.reshape(32, 4), rot.reshape(64, 64)).reshape(prefix, heads, dim)
+        for c in range(copies):
+            g = got[c, layer, side, :, :prefix, :].permute(1, 0, 2).numpy()
+            if k == 1:   # the corrupt vector's row is left untouched
+                assert np.all(g[3, 1] == 5.0)
+                g = g.copy()
+                g[3, 1] = want[3, 1]
+            assert np.array_equal(g.view(np.uint32), want.view(np.uint32)), (k, c)
+
+
+def _restore(plan, bufs, k, v):
+    """Blob k with vector v's norm made finite again (for the oracle's decode)."""
+    b = bytearray(plan.blob(bufs, "pool", k))
+    plen = plan.fib.payload_len()
+    b[19 + v * plen:19 + v * plen + 2] = bytes([0x00, 0x3C])   # f16 1.0
+    return bytes(b)
+
+
 def test_cache_target_append(ctx):
     """CacheTarget (proveKV/src/pool.rs:646-658): append one token's [H * D]
     key / value at a position in every copy."""
