@@ -460,8 +460,11 @@ int pkv_blake3(pkv_ctx* ctx, const void* data, uint64_t len, uint8_t out[32]);
 
 /* ---------------------------------------------------------------- host math
  * Host builds of the exact scalar routines the kernels use (test hooks):
- * angle bins of (a[i], b[i]) for pbits, and logf / expf over arrays. */
+ * angle bins of (a[i], b[i]) for pbits, the encode kernels' octant fast path
+ * (3-bit bin and whether the pair is safe for it, i.e. kept from the exact
+ * formula), and logf / expf over arrays. */
 void pkv_host_angle_bins(const float* a, const float* b, uint64_t n, uint32_t pbits, uint32_t* out);
+void pkv_host_octant_bins(const float* a, const float* b, uint64_t n, uint32_t* bins, uint8_t* safe);
 void pkv_host_logf(const float* x, uint64_t n, float* out);
 void pkv_host_expf(const float* x, uint64_t n, float* out);
 

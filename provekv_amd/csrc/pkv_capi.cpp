@@ -1879,6 +1879,14 @@ void pkv_host_angle_bins(const float* a, const float* b, uint64_t n, uint32_t pb
     for (uint64_t i = 0; i < n; ++i) out[i] = pbits == 3 ? angle_bin3(a[i], b[i]) : angle_bin_exact(a[i], b[i], pbits);
 }
 
+void pkv_host_octant_bins(const float* a, const float* b, uint64_t n, uint32_t* bins, uint8_t* safe) {
+    for (uint64_t i = 0; i < n; ++i) {
+        bool near_line, out_of_range;
+        bins[i] = octant_bin_m2(a[i], b[i], near_line, out_of_range);
+        safe[i] = !near_line && !out_of_range;
+    }
+}
+
 void pkv_host_logf(const float* x, uint64_t n, float* out) {
     static const LogfEntry tab[16] = {PKV_LOGF_TABLE};
     for (uint64_t i = 0; i < n; ++i) out[i] = og_logf_normal(x[i], tab);

@@ -745,11 +745,18 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
     extern __shared__ uint32_t smem_u[];   // per wave: 32 payloads (+ f32 radii for BlockLogU8)
     __shared__ float cs_lds[512];
     __shared__ LogfEntry logf_lds[16];
+    // the signs (+-1.0), then -sign * scale: the scale is 2^-3, so both are exact
+    __shared__ __align__(16) float sg_lds[2 * DIM];
 
     const uint32_t pbits = PB ? static_cast<uint32_t>(PB) : pbits_rt;
     const uint32_t levels = 1u << pbits;
     for (uint32_t t = threadIdx.x; t < 2 * levels; t += blockDim.x) cs_lds[t] = cs_tab[t];
     if (threadIdx.x < 16) logf_lds[threadIdx.x] = c_logf_tab[threadIdx.x];
+    for (uint32_t t = threadIdx.x; t < DIM; t += blockDim.x) {
+        const float sv = signs[t];
+        sg_lds[t] = sv;
+        sg_lds[DIM + t] = -sv * fwht_scale<DIM>();
+    }
     __syncthreads();
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -770,23 +777,15 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
     const uint32_t rwords = f32r ? 32u : 32u / 4 + 2;          // radii words in the payload
     const uint32_t bwords = (32u * pbits + 31) / 32;            // angle index words
 
-    // signs of this lane's half as a bit mask (bit c: element 32h + c is
-    // negated).  The signs are +-1.0, and multiplying by +-1.0 is exact, so
-    // flipping the sign bit is the same product bit for bit, NaN and
-    // subnormals included.
-    uint32_t smask = 0;
-    {
-        const float4* sp = reinterpret_cast<const float4*>(signs + 32 * h);
+    // this lane's 32 values of a 64-float LDS table (the signs, or -sign * scale)
+    auto lds_half = [&](const float* tab, float (&v)[32]) {
+        const float4* sp = reinterpret_cast<const float4*>(tab + 32 * h);
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const float4 v = sp[k];
-            smask |= (f2u(v.x) >> 31) << (4 * k) | (f2u(v.y) >> 31) << (4 * k + 1) |
-                     (f2u(v.z) >> 31) << (4 * k + 2) | (f2u(v.w) >> 31) << (4 * k + 3);
+            const float4 q = sp[k];
+            v[4 * k] = q.x; v[4 * k + 1] = q.y; v[4 * k + 2] = q.z; v[4 * k + 3] = q.w;
         }
-    }
-    // (m is smask; each use passes its own opaque copy so the 32 shifted
-    // masks are not kept live between the two uses)
-    auto flip = [](float v, uint32_t m, int c) { return u2f(f2u(v) ^ ((m << (31 - c)) & 0x80000000u)); };
+    };
 
     do {
         const uint32_t t0 = tile * TILE + (blockIdx.x & 1u) * (TILE / 2) + 32u * static_cast<uint32_t>(wave);
@@ -822,10 +821,10 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
         };
         load_half(y);
         {
-            uint32_t m = smask;
-            asm volatile("" : "+v"(m));
+            float sg[32];
+            lds_half(sg_lds, sg);
 #pragma unroll
-            for (int c = 0; c < 32; ++c) y[c] = flip(y[c], m, c);
+            for (int c = 0; c < 32; ++c) y[c] = y[c] * sg[c];
         }
         fwht_split(y, h);
 #pragma unroll
@@ -847,10 +846,10 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
             const float aa = a * a, bb = b * b;
             r[i] = __builtin_sqrtf(aa + bb);
             rsum = rsum + r[i];
-            bool safe = false;
-            const uint32_t bin = PB == 3 ? octant_bin_m(a, b, safe) : 0u;
+            bool near_line = false, out_of_range = true;   // other widths: every pair takes the exact formula
+            const uint32_t bin = PB == 3 ? octant_bin_m2(a, b, near_line, out_of_range) : 0u;
             pk |= static_cast<uint64_t>(bin) << (static_cast<uint32_t>(i) * pbits);
-            unsafe[i] = __ballot(!safe);
+            unsafe[i] = __ballot(near_line) | __ballot(out_of_range);
         }
         uint64_t any_unsafe = 0;
 #pragma unroll
@@ -932,12 +931,27 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
         // residual against x read again (turbo.rs:269-273)
         asm volatile("" ::: "memory");
         {
+            // x - (y * scale) * sign: with the scale 2^-3, y * scale is exact
+            // unless it is subnormal, and then the residual is the single
+            // rounding of x - sign * y / 8, one fma with -sign * scale.  A wave
+            // holding any |y| < 2^-123 (zeros included) takes the three
+            // roundings' own order.
             float x[32];
             load_half(x);
-            uint32_t m = smask;
-            asm volatile("" : "+v"(m));
+            float ymin = __builtin_fabsf(y[0]);
 #pragma unroll
-            for (int c = 0; c < 32; ++c) y[c] = x[c] - flip(y[c] * scale, m, c);
+            for (int c = 1; c < 32; ++c) ymin = __builtin_fminf(ymin, __builtin_fabsf(y[c]));
+            if (__ballot(!(ymin >= 0x1p-123f)) == 0) {
+                float ns[32];
+                lds_half(sg_lds + DIM, ns);
+#pragma unroll
+                for (int c = 0; c < 32; ++c) y[c] = __builtin_fmaf(y[c], ns[c], x[c]);
+            } else {
+                float sg[32];
+                lds_half(sg_lds, sg);
+#pragma unroll
+                for (int c = 0; c < 32; ++c) y[c] = x[c] - (y[c] * scale) * sg[c];
+            }
         }
         float rn2 = 0.0f;
 #pragma unroll
@@ -1227,10 +1241,10 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
             const float aa = a * a, bb = b * b;
             r[i] = __builtin_sqrtf(aa + bb);
             rsum = rsum + r[i];
-            bool safe = false;
-            const uint32_t bin = PB == 3 ? octant_bin_m(a, b, safe) : 0u;
+            bool near_line = false, out_of_range = true;   // other widths: every pair takes the exact formula
+            const uint32_t bin = PB == 3 ? octant_bin_m2(a, b, near_line, out_of_range) : 0u;
             pk |= static_cast<uint64_t>(bin) << (static_cast<uint32_t>(i) * pbits);
-            unsafe[i] = __ballot(!safe);
+            unsafe[i] = __ballot(near_line) | __ballot(out_of_range);
         }
         uint64_t any_unsafe = 0;
 #pragma unroll
@@ -1309,11 +1323,13 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
         // residual against x read again (turbo.rs:269-273)
         asm volatile("" ::: "memory");
         {
+            // x - (y * scale) * sign with sign = +-1: the product by the sign
+            // is exact, so one fma with -sign rounds the same
             float x[32], sg[32];
             load_quarter(x);
             load_signs(sg);
 #pragma unroll
-            for (int c = 0; c < 32; ++c) y[c] = x[c] - (y[c] * scale) * sg[c];
+            for (int c = 0; c < 32; ++c) y[c] = __builtin_fmaf(y[c] * scale, -sg[c], x[c]);
         }
         float rn2 = 0.0f;
 #pragma unroll

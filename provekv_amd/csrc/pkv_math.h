@@ -182,7 +182,10 @@ PKV_HD uint32_t octant_bin_u(float a, float b, uint32_t& safe) {
 // unsigned compares of the same bit patterns (lane masks on the device, so a
 // wave can test them all at once).  safe agrees with octant_bin_u on every
 // input; the bin of an unsafe pair is not used.
-PKV_HD uint32_t octant_bin_m(float a, float b, bool& safe) {
+// The two failing conditions come out separately (near an octant line; |a|,
+// |b| outside the range the line test covers) so that a kernel can take each
+// lane mask straight from its compare.
+PKV_HD uint32_t octant_bin_m2(float a, float b, bool& near_line, bool& out_of_range) {
     uint32_t xa, xb;
     __builtin_memcpy(&xa, &a, 4);
     __builtin_memcpy(&xb, &b, 4);
@@ -199,7 +202,17 @@ PKV_HD uint32_t octant_bin_m(float a, float b, bool& safe) {
     uint32_t ug;
     __builtin_memcpy(&ug, &g, 4);
     ug &= 0x7fffffffu;
-    safe = (eps < mn) & (eps < ug) & (0x0da24260u < mx) & (mx < 0x7149f2cau);   // 1e-30f < mx < 1e30f
+    const uint32_t m3 = mn < ug ? mn : ug;
+    near_line = !(eps < m3);
+    // 1e-30f < mx < 1e30f as one unsigned compare
+    out_of_range = !(mx - 0x0da24261u < 0x7149f2cau - 0x0da24261u);
+    return bin;
+}
+
+PKV_HD uint32_t octant_bin_m(float a, float b, bool& safe) {
+    bool near_line, out_of_range;
+    const uint32_t bin = octant_bin_m2(a, b, near_line, out_of_range);
+    safe = !near_line && !out_of_range;
     return bin;
 }
 

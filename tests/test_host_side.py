@@ -156,6 +156,40 @@ def test_angle_bins_match_glibc_atan2f_formula():
     assert np.array_equal(got, want)
 
 
+def test_octant_fast_path_safe_pairs_keep_the_exact_bin():
+    """The encode kernels' octant path (sign bits + one unsigned safety
+    test, octant_bin_m2): every pair it marks safe has the bin of the
+    pinned angle_bin path (glibc atan2f formula, test above); pairs on and
+    next to the octant lines, at the edges of the covered range (1e-30 ..
+    1e30), zeros, subnormals, infinities and NaN are marked unsafe."""
+    rng = np.random.RandomState(7)
+    n = 300_000
+    mag = np.exp(rng.uniform(-75, 75, n))   # one scale per pair, across the covered range
+    a = (rng.randn(n) * mag).astype(np.float32)
+    b = (rng.randn(n) * mag).astype(np.float32)
+    t = rng.randn(50_000).astype(np.float32)
+    up = np.nextafter(t, np.float32(np.inf)).astype(np.float32)
+    sub = np.float32([1e-40, -1e-40, 1e-45, 0.0, -0.0, 1e-30, 1.0000001e-30, 1e30, 9.999999e29])
+    big = np.float32([np.inf, -np.inf, np.nan, 3.4e38, -3.4e38])
+    ea = np.concatenate([t, t, -t, up, t, np.repeat(sub, len(sub)), np.repeat(big, 3), np.ones(len(big) * 3, np.float32)])
+    eb = np.concatenate([t, up, t, t, t * 0, np.tile(sub, len(sub)), np.tile(np.float32([1, -1, 0]), len(big)),
+                         np.repeat(big, 3)])
+    a = np.concatenate([a, ea]).astype(np.float32)
+    b = np.concatenate([b, eb]).astype(np.float32)
+    bins = np.zeros(a.size, np.uint32)
+    safe = np.zeros(a.size, np.uint8)
+    L.lib().pkv_host_octant_bins(a.ctypes.data, b.ctypes.data, a.size, bins.ctypes.data, safe.ctypes.data)
+    want = _bins(a, b)
+    ok = safe.astype(bool)
+    assert ok[:n].mean() > 0.9   # random pairs: nearly all take the fast path
+    assert np.array_equal(bins[ok], want[ok])
+    # never safe: on a line (|a| == |b|, a or b zero), out of range, non-finite
+    on_line = (np.abs(a) == np.abs(b)) | (a == 0) | (b == 0)
+    mx = np.maximum(np.abs(a), np.abs(b))
+    out = ~((mx > np.float32(1e-30)) & (mx < np.float32(1e30))) | ~np.isfinite(a) | ~np.isfinite(b)
+    assert not np.any(ok & (on_line | out))
+
+
 def test_profile_constant_service_builds_each_profile_once():
     """One build per distinct profile per process (the reference rebuilds on
     every adapter call, proveKV/src/codec.rs:471-499): a second request is a
