@@ -147,6 +147,17 @@ uint32_t pkv_payload_len(const pkv_profile* prof, int radii_codec);
 uint32_t pkv_header_len(const pkv_profile* prof);
 uint64_t pkv_blob_len(const pkv_profile* prof, int radii_codec, uint64_t n_vectors);
 
+/* The blob header an encode of n_vectors writes, byte for byte, into
+ * out[0 .. pkv_header_len(prof)), for a caller that lays blobs out itself.
+ * Replaces the header half of TurboCodeWireV1::encode_batch
+ * (turbo-quant/src/wire.rs:291-346: "TQB1", version, rotation, variant, dim,
+ * bits, radii codec, projections, seed, n, payload length) and of
+ * FibCodeV1::encode_batch (fib-quant/src/codec.rs:225-296: "FB2", version,
+ * bits, block count, n, norm format, norm / index lengths).  EMPTY_BATCH for
+ * n_vectors == 0 (the encodes reject an empty batch), CAPACITY when cap is
+ * short; radii_codec is ignored for fib. */
+int pkv_write_header(const pkv_profile* prof, int radii_codec, uint64_t n_vectors, uint8_t* out, uint64_t cap);
+
 /* ---------------------------------------------------------------- segments
  * One segment = one FB2/TQB1 blob <-> n_vectors dim-sized f32 (or bf16)
  * vectors of a strided tensor.  Vector i of the segment starts at element

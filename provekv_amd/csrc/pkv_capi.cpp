@@ -586,9 +586,9 @@ HdrBytes record_header(const pkv_profile* p) {
     return b.h;
 }
 
-// Header of the batched blob the records are reshaped into (TQB1 with f32
-// radii, wire.rs:267-346; FB2, codec.rs:195-320).
-HdrBytes blob_header(const pkv_profile* p, uint64_t n) {
+// Header of an n-vector batched blob (TQB1, wire.rs:267-346; FB2,
+// codec.rs:195-320); the records are reshaped into blobs with f32 radii.
+HdrBytes blob_header(const pkv_profile* p, uint64_t n, int radii = PKV_RADII_F32) {
     ByteWriter b;
     if (p->kind == PKV_CODEC_TURBO) {
         b.put(0, 'T'); b.put(1, 'Q'); b.put(2, 'B'); b.put(3, '1');
@@ -597,10 +597,11 @@ HdrBytes blob_header(const pkv_profile* p, uint64_t n) {
         b.put(8, 2);
         b.put32(10, p->dim);
         b.put(14, p->pbits);
+        b.put(15, radii == PKV_RADII_LOG_U8 ? 1u : 0u);
         b.put32(18, p->proj);
         b.put64(22, p->seed);
         b.put32(30, static_cast<uint32_t>(n));
-        b.put32(34, turbo_plen(p, PKV_RADII_F32));
+        b.put32(34, turbo_plen(p, radii));
     } else {
         b.put(0, 'F'); b.put(1, 'B'); b.put(2, '2');
         b.put(3, 1);
@@ -1122,6 +1123,20 @@ uint32_t pkv_header_len(const pkv_profile* p) { return p ? hdr_len(p) : 0; }
 uint64_t pkv_blob_len(const pkv_profile* p, int radii_codec, uint64_t n) {
     if (!p) return 0;
     return hdr_len(p) + n * pkv_payload_len(p, radii_codec);
+}
+
+int pkv_write_header(const pkv_profile* p, int radii_codec, uint64_t n_vectors, uint8_t* out, uint64_t cap) {
+    if (!p || !out) return PKV_ERR_INVALID_ARG;
+    int radii = radii_codec;
+    if (p->kind == PKV_CODEC_FIB) radii = PKV_RADII_F32;
+    else if (radii != PKV_RADII_F32 && radii != PKV_RADII_LOG_U8) return PKV_ERR_INVALID_ARG;
+    if (n_vectors == 0) return PKV_ERR_EMPTY_BATCH;   // encode_batch rejects an empty batch
+    if (n_vectors > 0xFFFFFFFFull) return PKV_ERR_INVALID_ARG;   // n is a u32 field
+    const uint32_t len = hdr_len(p);
+    if (cap < len) return PKV_ERR_CAPACITY;
+    const HdrBytes h = blob_header(p, n_vectors, radii);
+    for (uint32_t i = 0; i < len; ++i) out[i] = static_cast<uint8_t>(h.w[i >> 2] >> (8 * (i & 3)));
+    return PKV_OK;
 }
 
 int pkv_segments_status(const pkv_profile* prof, const uint32_t* host_status, uint32_t nseg, pkv_error* err) {

@@ -127,6 +127,31 @@ def test_turbo_other_bit_widths(ctx, dim, bits, mode):
         assert np.array_equal(dec.view(np.uint32), dref.view(np.uint32))
 
 
+@pytest.mark.parametrize("n", [1, 3, 1000])
+def test_write_header_matches_encoded_blobs(ctx, n):
+    """pkv_write_header: the header bytes of the blob an n-vector encode
+    writes (TQB1 with both radii codecs, QJL and PolarOnly, other polar
+    widths; FB2), equal to the oracle's blobs; an empty batch and a short
+    buffer are rejected."""
+    lib = L.lib()
+    x = kv_vectors(50 + n, n)
+    cases = []
+    for bits, mode in ((4, 1), (6, 0), (2, 1)):
+        prof = ctx.turbo_profile(64, bits, 32, SEED, mode)
+        for rc in (L.RADII_F32, L.RADII_LOG_U8):
+            cases.append((prof, rc, O.turbo_encode_batch(x, SEED, bits=bits, mode=mode, radii_codec=rc)[:38]))
+    cb, rot = O.fib_constants(SEED)
+    fprof = ctx.fib_profile_with_constants(cb, rot)
+    cases.append((fprof, L.RADII_LOG_U8, O.fib_encode_batch(x, cb.reshape(32, 4), rot.reshape(64, 64))[:19]))
+    for prof, rc, want in cases:
+        buf = np.zeros(64, np.uint8)
+        assert lib.pkv_header_len(prof._ptr) == len(want)
+        assert lib.pkv_write_header(prof._ptr, rc, n, buf.ctypes.data, buf.size) == 0
+        assert bytes(buf[:len(want)]) == want
+        assert lib.pkv_write_header(prof._ptr, rc, 0, buf.ctypes.data, buf.size) == L.ERR_EMPTY_BATCH
+        assert lib.pkv_write_header(prof._ptr, rc, n, buf.ctypes.data, len(want) - 1) == L.ERR_CAPACITY
+
+
 def test_turbo_edge_inputs(ctx):
     rng = np.random.RandomState(3)
     x = rng.randn(64, 64).astype(np.float32)
