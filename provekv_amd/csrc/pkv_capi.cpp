@@ -840,7 +840,9 @@ static void f16_split(double v, uint16_t* hi, uint16_t* lo) {
 //     hi * hi products, counted as 128 roundings of at most u (twice the
 //     sequential round-to-nearest count: truncating adders are covered)   128u
 //   the reference's own x_hat and rho roundings       2u
-// so |rho' - rho| <= eps_rho = 175u.  A key is the scoring MFMA's
+//     (under FibQuantizer::encode semantics, codec.rs:479-483, x_hat stays
+//     f64 and only rho's cast to f32 rounds: at most 1u + 2^-50)
+// so |rho' - rho| <= eps_rho = 175u for both semantics.  A key is the scoring MFMA's
 // f32(|c|^2 + off - 2 c . rho') (16 products of f16 halves, C = 0: 32u S,
 // S the largest sum of |terms|; kernel split of rho' 2 l1 17u; host splits
 // of -2c and of |c|^2 + off (8 l1 + 2 + 4 kmax)u; dropped lo * lo 16 l1 u)

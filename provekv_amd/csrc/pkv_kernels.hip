@@ -2377,9 +2377,13 @@ __device__ __forceinline__ void fib_encode_rotate(FibTileRot& t, const float4 (&
 
 // Phase 2 of a 32-vector tile: approximate argmin per block, norm status and
 // the payload words (into LDS).  Returns the blocks of this lane's vector that
-// the exact redo must decide -- every block under FibQuantizer::encode
-// semantics (segments of fewer than 4 vectors, per-vector calls) -- or 0 for
-// an inactive lane or a rejected input.
+// the exact redo must decide (gap to the second key within thr), or 0 for an
+// inactive lane or a rejected input.  The same test serves FibQuantizer::
+// encode semantics (segments of fewer than 4 vectors, per-vector calls): thr
+// bounds the keys against the exact rho = Pi (x / |x|) plus the reference's
+// own roundings, and those are smaller there (x / |x| stays f64; only rho's
+// cast to f32 remains), so only the undecided blocks go to the redo, which
+// follows the per-vector semantics.
 // DIAG: also write every block's 32 approximate keys (before the index bits
 // replace their low 5 bits) to lc.diag[(vector * 16 + block) * 32 + w].
 template <int DIM, bool DIAG>
@@ -2389,7 +2393,6 @@ __device__ __forceinline__ uint32_t fib_encode_score(const LaunchCommon& lc, con
     const int h = lane >> 5, n = lane & 31;
     const uint32_t nv = min(32u, seg.n_vectors - v0);
     const bool active = static_cast<uint32_t>(n) < nv;   // other lanes repeat the last vector
-    const bool small = seg.n_vectors < 4 || lc.per_vector != 0;
     const v16f& acc0 = t.acc0;
     const v16f& acc1 = t.acc1;
     const double nrm = t.nrm;
@@ -2471,7 +2474,7 @@ __device__ __forceinline__ uint32_t fib_encode_score(const LaunchCommon& lc, con
         pay[3 * n + 1] = (iw[0] >> 16) | (iw[1] << 16);
         pay[3 * n + 2] = (iw[1] >> 16) | (iw[2] << 16);
     }
-    return (active && finite_all && !zero) ? (small ? 0xFFFFu : redo) : 0u;
+    return (active && finite_all && !zero) ? redo : 0u;
 }
 
 // True when every value within err of v rounds to the same f32 as v: no f32

@@ -116,6 +116,19 @@ def test_fb1_decode_bit_exact(ctx, fib, n):
     assert same_f32(ad.decode(recs[-1], SEED), f64[-1])
 
 
+def test_fb1_each_encode_bit_exact_at_scale(ctx, fib):
+    """Per-vector (FibQuantizer::encode) semantics on 200,000 config-1-shaped
+    vectors: the matrix-core keys decide most blocks, the exact path the
+    rest; every record equals the oracle's per-vector encode."""
+    ad, cb, rot = fib
+    x = np.ascontiguousarray(synth.corpus_tokens(5, 2, 32, 1600, 64).reshape(-1, 64)[:200_000])
+    got = ad.build_quantizer(SEED).encode_vectors(x, each=True)
+    want = O.fib_encode_fb1(x, cb, rot, each=True)
+    assert len(got) == len(want)
+    bad = [i for i, (g, w) in enumerate(zip(got, want)) if g != w]
+    assert not bad, (len(bad), bad[:5])
+
+
 def test_fib_profile_shapes_outside_fib_k4_n32_are_refused(ctx):
     with pytest.raises(L.PkvError) as e:
         ctx.fib_profile(128, 4, 32, SEED)
@@ -123,8 +136,9 @@ def test_fib_profile_shapes_outside_fib_k4_n32_are_refused(ctx):
 
 
 def test_fb1_each_encode_near_ties(ctx, fib):
-    """Every vector takes the exact path under per-vector semantics; blocks on
-    codeword bisectors must still match the reference bytes."""
+    """Blocks on codeword bisectors (within 1e-7 .. 1e-9 of the tie): the
+    matrix-core gap test leaves them to the exact path under both
+    semantics, and the bytes must match the reference's."""
     ad, cb, rot = fib
     rng = np.random.RandomState(23)
     cb64 = cb.astype(np.float64)
