@@ -179,7 +179,8 @@ int device_checks_once(int device, hipStream_t st) {
     hipError_t e = static_cast<hipError_t>(launch_logf_bound(st));
     if (e == hipSuccess) e = static_cast<hipError_t>(launch_f16_subnormal_probe(d, st));
     if (e == hipSuccess) e = hipMemcpyAsync(got, d, sizeof got, hipMemcpyDeviceToHost, st);
-    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    const hipError_t se = hipStreamSynchronize(st);   // queued work ends before `d` is freed
+    if (e == hipSuccess) e = se;
     (void)hipFree(d);
     if (e != hipSuccess) return hip_status(e);
     if (got[0] != 0x1p-10f + 0x1p-14f || got[1] != 0x1p-10f) return PKV_ERR_UNSUPPORTED;
@@ -489,6 +490,17 @@ int run_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool encode, 
     std::lock_guard<std::mutex> lock(ctx->mu);
     return run_segments_locked(ctx, prof, radii, encode, dtype, d_f32, f32_elems, segs, nseg, d_wire, wire_bytes,
                                d_status, stream);
+}
+
+// Two device-to-host copies on `st`, then a wait for them and for all work
+// queued before: the wait happens also when the second copy fails to enqueue,
+// so no queued copy outlives the caller's (or this frame's) host buffers.
+int copy_back(hipStream_t st, void* h1, const void* d1, size_t n1, void* h2, const void* d2, size_t n2) {
+    hipError_t e = hipMemcpyAsync(h1, d1, n1, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess && n2) e = hipMemcpyAsync(h2, d2, n2, hipMemcpyDeviceToHost, st);
+    const hipError_t se = hipStreamSynchronize(st);
+    if (e == hipSuccess) e = se;
+    return e == hipSuccess ? PKV_OK : hip_status(e);
 }
 
 int ensure_io_buf(pkv_ctx* ctx, size_t bytes) {
@@ -920,7 +932,8 @@ static int fib_verify_mfma_products(pkv_ctx* ctx, pkv_profile* p) {
     hipError_t e = hipMemsetAsync(d_bad, 0, sizeof(uint32_t), ctx->own_stream);
     if (e == hipSuccess) e = static_cast<hipError_t>(launch_fib_product_check(p->d_rot32, p->d_cb, d_bad, ctx->own_stream));
     if (e == hipSuccess) e = hipMemcpyAsync(&bad, d_bad, sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->own_stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(ctx->own_stream);
+    const hipError_t se = hipStreamSynchronize(ctx->own_stream);   // queued work ends before `d_bad` is freed
+    if (e == hipSuccess) e = se;
     (void)hipFree(d_bad);
     if (e != hipSuccess) return hip_status(e);
     p->mfma_decode = bad == 0 ? 1 : 0;
@@ -1012,7 +1025,9 @@ int lloyd_on_device_locked(pkv_ctx* ctx, const double* samples, uint32_t ns, uin
     if (e == hipSuccess) e = hipMemcpyAsync(init_mse, d + o_init, sizeof(double), hipMemcpyDeviceToHost, st);
     if (e == hipSuccess)
         e = hipMemcpyAsync(status.data(), d + o_stat, sizeof(uint32_t) * restarts, hipMemcpyDeviceToHost, st);
-    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    // whatever was queued finishes before the scratch and `status` go away
+    const hipError_t se = hipStreamSynchronize(st);
+    if (e == hipSuccess) e = se;
     (void)hipFree(d);
     if (e != hipSuccess) return hip_status(e);
     for (uint32_t v : status)
@@ -1245,7 +1260,8 @@ int pkv_radii_log_bound(pkv_ctx* ctx, float* out) {
     HIP_TRY(hipMalloc(&d, 256 * sizeof(float)));
     hipError_t e = static_cast<hipError_t>(launch_logf_bound_read(d, ctx->own_stream));
     if (e == hipSuccess) e = hipMemcpyAsync(out, d, 256 * sizeof(float), hipMemcpyDeviceToHost, ctx->own_stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(ctx->own_stream);
+    const hipError_t se = hipStreamSynchronize(ctx->own_stream);   // queued work ends before `d` is freed
+    if (e == hipSuccess) e = se;
     (void)hipFree(d);
     return e == hipSuccess ? PKV_OK : hip_status(e);
 }
@@ -1478,9 +1494,8 @@ int pkv_encode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, int radii_co
                              d_stat, st);
     if (rc) { (void)hipStreamSynchronize(st); return rc; }
     uint32_t hs[2];
-    HIP_TRY(hipMemcpyAsync(hs, d_stat, sizeof hs, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(out, d_wire, blob, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipStreamSynchronize(st));
+    rc = copy_back(st, hs, d_stat, sizeof hs, out, d_wire, blob);
+    if (rc) return rc;
     return resolve_status(prof, hs, 1, &seg, err);
 }
 
@@ -1519,9 +1534,8 @@ int pkv_decode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, const uint8_
                              st);
     if (rc) { (void)hipStreamSynchronize(st); return rc; }
     uint32_t hs[2];
-    HIP_TRY(hipMemcpyAsync(hs, d_stat, sizeof hs, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(out, d_out, out_bytes, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipStreamSynchronize(st));
+    rc = copy_back(st, hs, d_stat, sizeof hs, out, d_out, out_bytes);
+    if (rc) return rc;
     rc = resolve_status(prof, hs, 1, &seg, err);
     if (rc == PKV_OK && prof->kind == PKV_CODEC_TURBO && len != blob) {   // cursor.finish(), wire.rs:566
         if (err) { err->status = PKV_ERR_CORRUPT_PAYLOAD; err->segment = -1; err->index = 0; }
@@ -1739,9 +1753,10 @@ int pkv_turbo_score_batch(pkv_ctx* ctx, const pkv_profile* prof, const uint8_t* 
                           n ? n : 1, d_st + 2, st);
     if (rc) { (void)hipStreamSynchronize(st); return rc; }
     uint32_t hs[4];
-    HIP_TRY(hipMemcpyAsync(hs, d_st, sizeof hs, hipMemcpyDeviceToHost, st));
-    if (s_bytes) HIP_TRY(hipMemcpyAsync(scores, d_s, s_bytes, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipStreamSynchronize(st));
+    {
+        const int crc = copy_back(st, hs, d_st, sizeof hs, scores, d_s, s_bytes);
+        if (crc) return crc;
+    }
     if (hs[0] != STATUS_NONE) {   // prepare_query runs before any score (turbo.rs:316-319)
         if (err) { err->status = PKV_ERR_NONFINITE_INPUT; err->segment = -1; err->index = hs[0] >> 4; }
         return PKV_ERR_NONFINITE_INPUT;
@@ -1788,9 +1803,10 @@ int pkv_encode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const fl
     int e = launch_records_pack(d_blob + hdr, base + o_rec, n, plen, rh, record_header(prof), st);
     if (e) { (void)hipStreamSynchronize(st); return hip_status(static_cast<hipError_t>(e)); }
     uint32_t hs[2];
-    HIP_TRY(hipMemcpyAsync(hs, d_stat, sizeof hs, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(out, base + o_rec, rec_bytes, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipStreamSynchronize(st));
+    {
+        const int crc = copy_back(st, hs, d_stat, sizeof hs, out, base + o_rec, rec_bytes);
+        if (crc) return crc;
+    }
     return resolve_status(prof, hs, 1, &seg, err, per_vector);
 }
 
@@ -1843,9 +1859,10 @@ int pkv_decode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const ui
         if (rc) { (void)hipStreamSynchronize(st); return rc; }
     }
     uint32_t hs[4];
-    HIP_TRY(hipMemcpyAsync(hs, d_stat, sizeof hs, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(out, base + o_out, out_bytes, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipStreamSynchronize(st));
+    {
+        const int crc = copy_back(st, hs, d_stat, sizeof hs, out, base + o_out, out_bytes);
+        if (crc) return crc;
+    }
     // FibQuantAdapter::decode_batch parses every record before decoding any
     // (codec.rs:639-665); per-record decoding stops at the first failure.
     uint32_t pick = std::min(std::min(hs[0], hs[1]), hs[3]);
