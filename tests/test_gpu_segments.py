@@ -118,3 +118,41 @@ def test_random_segment_tables(ctx, kind, dim, lossy, in_dt, out_dt, fanout, see
     for k in range(fanout):
         rest = got[k * stride:(k + 1) * stride][torch.from_numpy(~touched)]
         assert torch.all(rest == 7.0)
+
+
+@pytest.mark.parametrize("kind", ["fib", "turbo"])
+def test_header_only_blobs(ctx, kind):
+    """A blob that holds no vectors (n = 0): both batched decoders accept it
+    (fib-quant/src/codec.rs:323-402, turbo-quant/src/wire.rs:401-568) and
+    decode_batch_fast(&[]) returns nothing (fib-quant/tests/
+    decode_batch_fast_parity.rs:52-60).  The compact decode returns no
+    vectors; between two non-empty blobs of one segment table it decodes to
+    nothing while the others decode as the oracle's; its header is still
+    checked."""
+    import torch
+    from provekv_amd.device import segments
+    prof, radii, enc, dec = _codec(ctx, kind, 64, False)
+    hl = int(L.lib().pkv_header_len(prof._ptr))
+    nfield = 10 if kind == "fib" else 30          # the u32 vector count in the header
+    rng = np.random.RandomState(9)
+    xa, xb = rng.randn(5, 64).astype(np.float32), rng.randn(7, 64).astype(np.float32)
+    ba, bb = enc(xa), enc(xb)
+    empty = bytearray(ba[:hl])
+    empty[nfield:nfield + 4] = b"\0\0\0\0"
+    assert prof.decode_batch_compact(bytes(empty)).shape == (0, 64)
+    wire = torch.from_numpy(np.frombuffer(ba + bytes(empty) + bb, np.uint8).copy()).cuda()
+    segs = segments([(0, 64, 64, 0, 5, 1), (5 * 64, 64, 64, len(ba), 0, 1), (5 * 64, 64, 64, len(ba) + hl, 7, 1)])
+    want = np.concatenate([dec(ba), dec(bb)]).reshape(-1)
+    for corrupt in (False, True):
+        if corrupt:
+            wire[len(ba)] ^= 0xFF                    # the empty blob's magic
+        out = torch.full((12 * 64,), 7.0, dtype=torch.float32, device="cuda")
+        st = torch.zeros(6, dtype=torch.int32, device="cuda")
+        prof.decode_segments(wire, segs, out, radii=radii, status=st)
+        torch.cuda.synchronize()
+        err = prof.status_error(st.cpu().numpy().view(np.uint32), segs)
+        if not corrupt:
+            assert err is None
+            assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+        else:
+            assert err is not None and err.segment == 1 and err.status == L.ERR_CORRUPT_PAYLOAD
