@@ -270,6 +270,14 @@ def test_fib_errors(ctx):
     big[30] *= 1e6
     with pytest.raises(CompressionFailed, match="fp16.*vector 30"):
         ad.encode_batch_compact(big, SEED)
+    # every element the smallest subnormal: the norm underflows fp16
+    # (fib-quant/tests/norm_payload_rejection.rs:13-19), batch and per vector
+    tiny = x.copy()
+    tiny[12] = np.frombuffer(np.uint32(1).tobytes(), np.float32)[0]
+    with pytest.raises(CompressionFailed, match="fp16.*vector 12"):
+        ad.encode_batch_compact(tiny, SEED)
+    with pytest.raises(CompressionFailed, match="fp16"):
+        ad.encode(tiny[12], SEED)
     blob = bytearray(ad.encode_batch_compact(x, SEED))
     zero_norm = bytearray(blob)
     zero_norm[19 + 12 * 3] = 0
