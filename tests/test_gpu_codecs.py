@@ -152,6 +152,20 @@ def test_write_header_matches_encoded_blobs(ctx, n):
         assert lib.pkv_write_header(prof._ptr, rc, n, buf.ctypes.data, len(want) - 1) == L.ERR_CAPACITY
 
 
+def test_turbo_profile_parameters_rejected_like_the_reference(ctx):
+    """turbo-quant/tests/invalid_inputs.rs:17-27 (TurboQuantizer::new,
+    turbo.rs:148-164): an odd dimension and a QJL profile of 1 bit are
+    invalid; a valid profile outside what the kernels implement (dim 8) is
+    reported as unsupported, not as invalid."""
+    for dim, bits in ((7, 8), (8, 1)):
+        with pytest.raises(L.PkvError) as e:
+            ctx.turbo_profile(dim, bits, 8, 42, 1)
+        assert e.value.status == L.ERR_INVALID_ARG
+    with pytest.raises(L.PkvError) as e:
+        ctx.turbo_profile(8, 8, 8, 42, 1)
+    assert e.value.status == L.ERR_UNSUPPORTED
+
+
 def test_turbo_edge_inputs(ctx):
     rng = np.random.RandomState(3)
     x = rng.randn(64, 64).astype(np.float32)
