@@ -135,6 +135,17 @@ def test_fib_profile_shapes_outside_fib_k4_n32_are_refused(ctx):
     assert e.value.status == L.ERR_UNSUPPORTED
 
 
+@pytest.mark.parametrize("dim,k,n", [(0, 2, 8), (8, 0, 8), (10, 4, 8), (8, 2, 1)])
+def test_fib_profile_invalid_parts_rejected(ctx, dim, k, n):
+    """fib-quant/tests/profile_digest.rs:19-36 (FibQuantProfileV1::
+    paper_default): zero dimension, zero block dim, a dimension the block
+    does not divide and a codebook of one codeword are invalid, not merely
+    unsupported."""
+    with pytest.raises(L.PkvError) as e:
+        ctx.fib_profile(dim, k, n, SEED)
+    assert e.value.status == L.ERR_INVALID_ARG
+
+
 def test_fb1_each_encode_near_ties(ctx, fib):
     """Blocks on codeword bisectors (within 1e-7 .. 1e-9 of the tie): the
     matrix-core gap test leaves them to the exact path under both
