@@ -978,9 +978,14 @@ static int fib_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n
     return PKV_OK;
 }
 
+// FibQuantProfileV1's shape checks (fib-quant/src/profile.rs:281-318, and the
+// rotation / codebook size limits the profile applies before allocating them):
+// invalid shapes first, then the one shape the kernels implement.
 static int fib_check(uint32_t dim, uint32_t k, uint32_t n) {
-    if (dim == 0 || k == 0 || dim % k != 0) return PKV_ERR_INVALID_ARG;   // FibQuantAdapter::new
-    if (n < 2) return PKV_ERR_INVALID_ARG;
+    if (dim == 0 || k == 0 || k >= dim || dim % k != 0) return PKV_ERR_INVALID_ARG;
+    if (dim > 16384 || k > 256 || n < 2 || n > (1u << 20)) return PKV_ERR_INVALID_ARG;
+    if (static_cast<uint64_t>(dim) * dim > 16777216ull) return PKV_ERR_INVALID_ARG;    // rotation matrix values
+    if (static_cast<uint64_t>(n) * k > 67108864ull) return PKV_ERR_INVALID_ARG;       // codebook values
     if (dim != 64 || k != 4 || n != 32) return PKV_ERR_UNSUPPORTED;      // fib_k4_n32 at head_dim 64
     return PKV_OK;
 }

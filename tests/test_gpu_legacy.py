@@ -135,12 +135,14 @@ def test_fib_profile_shapes_outside_fib_k4_n32_are_refused(ctx):
     assert e.value.status == L.ERR_UNSUPPORTED
 
 
-@pytest.mark.parametrize("dim,k,n", [(0, 2, 8), (8, 0, 8), (10, 4, 8), (8, 2, 1)])
+@pytest.mark.parametrize("dim,k,n", [(0, 2, 8), (8, 0, 8), (10, 4, 8), (8, 2, 1), (8, 8, 8), (8194, 2, 8),
+                                     (256, 128, 1 << 20)])
 def test_fib_profile_invalid_parts_rejected(ctx, dim, k, n):
-    """fib-quant/tests/profile_digest.rs:19-36 (FibQuantProfileV1::
-    paper_default): zero dimension, zero block dim, a dimension the block
-    does not divide and a codebook of one codeword are invalid, not merely
-    unsupported."""
+    """fib-quant/tests/profile_digest.rs:19-36 and profile_resource_bounds.rs
+    (FibQuantProfileV1::paper_default): zero dimension, zero block dim, a
+    dimension the block does not divide, a one-codeword codebook, block dim
+    equal to the dimension, an oversized rotation matrix and oversized
+    codebook values are invalid, not merely unsupported."""
     with pytest.raises(L.PkvError) as e:
         ctx.fib_profile(dim, k, n, SEED)
     assert e.value.status == L.ERR_INVALID_ARG
