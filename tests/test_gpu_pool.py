@@ -236,9 +236,10 @@ def test_bounded_fib_decode_matches_full_grid(ctx, max_workgroups, copies):
                                                        (4, 128, 8, 3)])
 def test_head_major_fanout_rehydrate(ctx, heads, prefix, copies, bound):
     """Pool blobs of T tokens x G heads whose vector count is a multiple of
-    256 rehydrate with each wave on tt consecutive tokens of 64 / tt heads
-    (tt = 64, 32, 16 here): every copy equals the oracle's decode, and a
-    corrupt norm is reported at its own vector index."""
+    256 (whole decode tiles, no partial last tile), 2 to 8 cache copies,
+    full and bounded grids: every copy equals the oracle's decode, and a
+    corrupt norm is reported at its own vector index with its rows left
+    untouched."""
     import torch
     from provekv_amd.pool import DeviceKVCache
     layers, dim, agents = 2, 64, [5]
