@@ -234,7 +234,7 @@ def test_bounded_fib_decode_matches_full_grid(ctx, max_workgroups, copies):
 
 @pytest.mark.parametrize("heads,prefix,copies,bound", [(8, 256, 3, 0), (32, 96, 8, 0), (16, 48, 2, 5),
                                                        (4, 128, 8, 3)])
-def test_head_major_fanout_rehydrate(ctx, heads, prefix, copies, bound):
+def test_whole_tile_fanout_rehydrate(ctx, heads, prefix, copies, bound):
     """Pool blobs of T tokens x G heads whose vector count is a multiple of
     256 (whole decode tiles, no partial last tile), 2 to 8 cache copies,
     full and bounded grids: every copy equals the oracle's decode, and a
