@@ -330,6 +330,91 @@ __global__ __launch_bounds__(256) void blake3_quad_kernel(const uint8_t* __restr
     }
 }
 
+// A merge pass (after the leaf pass) with four lanes per compression: one
+// workgroup per tile of 64 values of one range.  Wave w merges values
+// 16w .. 16w + 15 of the tile on its quads, level by level as
+// blake3_quad_kernel does, then wave 0 merges the waves' results the same
+// way -- together the pairwise level-by-level order over the 64 values (an
+// aligned 16-value group is the first four levels).  A single lane per
+// compression leaves one wave per range chaining whole compressions, which is
+// most of a small wire's digest time.
+__global__ __launch_bounds__(256) void blake3_merge4_kernel(const B3Pass* __restrict__ pass, uint32_t nr,
+                                                            const uint32_t* __restrict__ cv_in,
+                                                            uint32_t* __restrict__ cv_out, uint32_t* __restrict__ out) {
+    __shared__ uint32_t cv_s[4][16][8];   // per wave, per quad: a chaining value
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t quad = lane >> 2, i = lane & 3u;
+    const uint32_t tile = blockIdx.x;
+    if (tile >= pass[nr].tile_start) return;   // the whole workgroup leaves
+    uint32_t lo = 0, hi = nr;   // pass[lo].tile_start <= tile < pass[hi].tile_start
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (pass[mid].tile_start <= tile) lo = mid;
+        else hi = mid;
+    }
+    const uint32_t r = lo;
+    const B3Pass ps = pass[r];
+    const uint32_t g = tile - ps.tile_start;
+    const uint32_t first = g * 64u;
+    const uint32_t nw = ps.count - first < 64u ? ps.count - first : 64u;   // values of this tile (>= 1)
+    const bool root_group = ps.count <= 64u;
+    const QuadMsgIdx qi = quad_msg_idx(i);
+    // level-by-level merge of the n chaining values in cv_s[wv][0 .. n) on
+    // wave wv's quads; `last` when these n values are the whole range
+    auto merge = [&](uint32_t wv, uint32_t n, bool last) {
+        for (uint32_t s = 1; s < n; s <<= 1) {
+            const uint32_t c = (n + s - 1u) / s;
+            const bool act = (quad & (2u * s - 1u)) == 0u && quad / s + 1u < c;
+            const uint32_t partner = act ? quad + s : quad;
+            uint32_t plo = i == 0 ? PKV_B3_IV0 : i == 1 ? PKV_B3_IV1 : i == 2 ? PKV_B3_IV2 : PKV_B3_IV3;
+            uint32_t phi = i == 0 ? PKV_B3_IV4 : i == 1 ? PKV_B3_IV5 : i == 2 ? PKV_B3_IV6 : PKV_B3_IV7;
+            const uint32_t* left = cv_s[wv][quad];
+            const uint32_t* right = cv_s[wv][partner];
+            quad_compress(plo, phi, i, qi, [&](uint32_t k) { return k < 8u ? left[k] : right[k - 8u]; }, 0,
+                          b3::BLOCK_BYTES, b3::PARENT | (last && c == 2u ? b3::ROOT : 0u));
+            wave_sync_lds();   // all reads of this level done
+            if (act) {
+                cv_s[wv][quad][i] = plo;
+                cv_s[wv][quad][4u + i] = phi;
+            }
+            wave_sync_lds();
+        }
+    };
+    const uint32_t base = 16u * wave;
+    const uint32_t nq = nw > base ? (nw - base < 16u ? nw - base : 16u) : 0u;   // this wave's values
+    if (quad < nq) {
+        const uint32_t* src = cv_in + 8ull * (ps.in_base + first + base + quad);
+        cv_s[wave][quad][i] = src[i];
+        cv_s[wave][quad][4u + i] = src[4u + i];
+    }
+    wave_sync_lds();
+    if (nq > 1) merge(wave, nq, root_group && nw <= 16u);
+    __syncthreads();
+    const uint32_t ng = (nw + 15u) / 16u;   // waves that held values
+    if (wave == 0) {
+        if (ng > 1) {
+            // the waves' results become quads 0 .. ng - 1 of wave 0
+            uint32_t wlo = 0, whi = 0;
+            if (quad < ng) {
+                wlo = cv_s[quad][0][i];
+                whi = cv_s[quad][0][4u + i];
+            }
+            wave_sync_lds();
+            if (quad < ng) {
+                cv_s[0][quad][i] = wlo;
+                cv_s[0][quad][4u + i] = whi;
+            }
+            wave_sync_lds();
+            merge(0, ng, root_group);
+        }
+        if (quad == 0) {   // out is only 4-byte aligned
+            uint32_t* dst = root_group ? out + 8ull * r : cv_out + 8ull * (ps.out_base + g);
+            dst[i] = cv_s[0][0][i];
+            dst[4u + i] = cv_s[0][0][4u + i];
+        }
+    }
+}
+
 // Layer digests: entry i holds the payload digests of layer i % layers, key
 // then value (16 words); out[i] = blake3 of serde_json's compact text of
 // json!({"layer_index", "key_digests": [k], "value_digests": [v]}) -- a
@@ -404,6 +489,14 @@ int launch_blake3_quad(const uint8_t* buf, const B3Range* ranges, const B3Pass* 
     if (tiles == 0) return hipSuccess;
     hipLaunchKernelGGL(blake3_quad_kernel, dim3((tiles + 3u) / 4u), dim3(256), 0, static_cast<hipStream_t>(stream), buf,
                        ranges, pass, nr, cv_out, out);
+    return hipGetLastError();
+}
+
+int launch_blake3_merge4(const B3Pass* pass, uint32_t nr, uint32_t tiles, const uint32_t* cv_in, uint32_t* cv_out,
+                         uint32_t* out, void* stream) {
+    if (tiles == 0) return hipSuccess;
+    hipLaunchKernelGGL(blake3_merge4_kernel, dim3(tiles), dim3(256), 0, static_cast<hipStream_t>(stream), pass, nr,
+                       cv_in, cv_out, out);
     return hipGetLastError();
 }
 

@@ -1374,9 +1374,11 @@ int blake3_ranges_locked(pkv_ctx* ctx, const uint8_t* d_buf, uint64_t buf_bytes,
     int e = cp;
     for (size_t p = 0; p < plan.tiles.size() && !e; ++p) {
         const auto* d_pass = reinterpret_cast<const B3Pass*>(d + pass_off) + p * (nr + 1);
-        e = p == 0 && plan.quad
-                ? launch_blake3_quad(d_buf, d_ranges, d_pass, nr, plan.tiles[p], d_cv, out, stream)
-                : launch_blake3_pass(d_buf, d_ranges, d_pass, nr, plan.tiles[p], d_cv, d_cv, out, p == 0, stream);
+        if (p == 0)
+            e = plan.quad ? launch_blake3_quad(d_buf, d_ranges, d_pass, nr, plan.tiles[p], d_cv, out, stream)
+                          : launch_blake3_pass(d_buf, d_ranges, d_pass, nr, plan.tiles[p], d_cv, d_cv, out, true, stream);
+        else
+            e = launch_blake3_merge4(d_pass, nr, plan.tiles[p], d_cv, d_cv, out, stream);
     }
     const int rc2 = finish_slot(sl, stream);
     if (e) return hip_status(static_cast<hipError_t>(e));

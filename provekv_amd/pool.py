@@ -305,8 +305,12 @@ class TwoTierPlan:
         stream waits for both."""
         import torch
         main = stream if stream is not None else torch.cuda.current_stream()
-        if side is not None:
-            side.wait_stream(main)
+        if side is not None:   # two events kept for every call (creating them is most of a wait's cost)
+            evs = getattr(self, "_digest_events", None)
+            if evs is None:
+                evs = self._digest_events = (torch.cuda.Event(), torch.cuda.Event())
+            evs[0].record(main)
+            side.wait_event(evs[0])
         for tier, name, st in ((self.pool, "pool", main), (self.shells, "shell", side or main)):
             n = len(tier.blob_offsets) // 2
             if f"{name}_digests" not in bufs:
@@ -320,7 +324,8 @@ class TwoTierPlan:
             self.ctx.layer_digests(bufs[f"{name}_digests"], self.layers, out=bufs[f"{name}_layer_digests"],
                                    stream=st)
         if side is not None:
-            main.wait_stream(side)
+            evs[1].record(side)
+            main.wait_event(evs[1])
 
     def digest_report(self, bufs) -> dict:
         """The digests of the last digests() call as the reference prints them
