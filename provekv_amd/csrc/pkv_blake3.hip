@@ -174,14 +174,13 @@ __device__ __forceinline__ void quad_compress(uint32_t& cv_lo, uint32_t& cv_hi, 
 
 }  // namespace
 
-// One wave per tile of 64 elements of one range (pass table: B3Pass per range
-// plus a sentinel whose tile_start is the pass's tile count).
+// The first pass with one lane per chunk: one wave per tile of 64 chunks of
+// one range (pass table: B3Pass per range plus a sentinel whose tile_start
+// is the pass's tile count); the wave merges its 64 chaining values.
 __global__ __launch_bounds__(256) void blake3_tree_kernel(const uint8_t* __restrict__ buf,
                                                           const B3Range* __restrict__ ranges,
                                                           const B3Pass* __restrict__ pass, uint32_t nr,
-                                                          const uint32_t* __restrict__ cv_in,
-                                                          uint32_t* __restrict__ cv_out, uint32_t* __restrict__ out,
-                                                          uint32_t leaf) {
+                                                          uint32_t* __restrict__ cv_out, uint32_t* __restrict__ out) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t tile = __builtin_amdgcn_readfirstlane(blockIdx.x * 4u + (threadIdx.x >> 6));
     if (tile >= pass[nr].tile_start) return;
@@ -199,15 +198,8 @@ __global__ __launch_bounds__(256) void blake3_tree_kernel(const uint8_t* __restr
     const bool root_group = ps.count <= 64u;
     uint32_t cv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (lane < nw) {
-        if (leaf) {
-            const B3Range rg = ranges[r];
-            chunk_cv(buf + rg.offset, rg.len, first + lane, ps.count == 1u, cv);
-        } else {
-            const uint4* src = reinterpret_cast<const uint4*>(cv_in + 8ull * (ps.in_base + first + lane));
-            const uint4 x = src[0], y = src[1];
-            cv[0] = x.x; cv[1] = x.y; cv[2] = x.z; cv[3] = x.w;
-            cv[4] = y.x; cv[5] = y.y; cv[6] = y.z; cv[7] = y.w;
-        }
+        const B3Range rg = ranges[r];
+        chunk_cv(buf + rg.offset, rg.len, first + lane, ps.count == 1u, cv);
     }
     // level s: elements are the lanes that are multiples of s, ceil(nw / s) of
     // them; even element e absorbs element e + 1 when it exists
@@ -476,11 +468,11 @@ __global__ __launch_bounds__(64) void blake3_layer_kernel(const uint32_t* __rest
 }
 
 int launch_blake3_pass(const uint8_t* buf, const B3Range* ranges, const B3Pass* pass, uint32_t nr, uint32_t tiles,
-                       const uint32_t* cv_in, uint32_t* cv_out, uint32_t* out, bool leaf, void* stream) {
+                       uint32_t* cv_out, uint32_t* out, void* stream) {
     if (tiles == 0) return hipSuccess;
     const uint32_t grid = (tiles + 3u) / 4u;
-    hipLaunchKernelGGL(blake3_tree_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), buf, ranges, pass, nr, cv_in, cv_out,
-                       out, leaf ? 1u : 0u);
+    hipLaunchKernelGGL(blake3_tree_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), buf, ranges,
+                       pass, nr, cv_out, out);
     return hipGetLastError();
 }
 

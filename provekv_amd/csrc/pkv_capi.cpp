@@ -1376,7 +1376,7 @@ int blake3_ranges_locked(pkv_ctx* ctx, const uint8_t* d_buf, uint64_t buf_bytes,
         const auto* d_pass = reinterpret_cast<const B3Pass*>(d + pass_off) + p * (nr + 1);
         if (p == 0)
             e = plan.quad ? launch_blake3_quad(d_buf, d_ranges, d_pass, nr, plan.tiles[p], d_cv, out, stream)
-                          : launch_blake3_pass(d_buf, d_ranges, d_pass, nr, plan.tiles[p], d_cv, d_cv, out, true, stream);
+                          : launch_blake3_pass(d_buf, d_ranges, d_pass, nr, plan.tiles[p], d_cv, out, stream);
         else
             e = launch_blake3_merge4(d_pass, nr, plan.tiles[p], d_cv, d_cv, out, stream);
     }

@@ -193,14 +193,15 @@ static_assert(sizeof(B3Range) == sizeof(pkv_range), "range layout");
 struct B3Pass {
     uint32_t tile_start, count, in_base, out_base;
 };
+// Pass 0 with one lane per chunk (tiles of 64 chunks).
 int launch_blake3_pass(const uint8_t* buf, const B3Range* ranges, const B3Pass* pass, uint32_t nr, uint32_t tiles,
-                       const uint32_t* cv_in, uint32_t* cv_out, uint32_t* out, bool leaf, void* stream);
+                       uint32_t* cv_out, uint32_t* out, void* stream);
 // Pass 0 with four lanes per chunk (tiles of 16 chunks; pass records as for
-// launch_blake3_pass with leaf set).
+// launch_blake3_pass).
 int launch_blake3_quad(const uint8_t* buf, const B3Range* ranges, const B3Pass* pass, uint32_t nr, uint32_t tiles,
                        uint32_t* cv_out, uint32_t* out, void* stream);
-// A merge pass (tiles of 64 values, as launch_blake3_pass without leaf) with
-// four lanes per compression, one workgroup per tile.
+// A merge pass (tiles of 64 chaining values) with four lanes per
+// compression, one workgroup per tile.
 int launch_blake3_merge4(const B3Pass* pass, uint32_t nr, uint32_t tiles, const uint32_t* cv_in, uint32_t* cv_out,
                          uint32_t* out, void* stream);
 int launch_blake3_layers(const uint32_t* kv, uint32_t n, uint32_t layers, uint32_t* out, void* stream);
