@@ -463,6 +463,18 @@ int pkv_blake3_ranges(pkv_ctx* ctx, const uint8_t* d_buf, uint64_t buf_bytes, co
 int pkv_blake3_layer_digests(pkv_ctx* ctx, const uint8_t* d_kv_digests, uint32_t n, uint32_t layers,
                              uint8_t* d_out, void* stream);
 
+/* One tier of a build in one call: pkv_blake3_ranges over its 2 n blob
+ * ranges (key, value, key, value, ... -- the pool's or the shells' blobs in
+ * layer order) into d_blob_digests (n x 64 bytes), then
+ * pkv_blake3_layer_digests of those into d_layer_digests (n x 32 bytes), on
+ * `stream`.  Replaces the per-blob CompressedBlock::new digests and the
+ * per-layer PoolLayer / ShellLayer::compute_digest of a pool or shell build
+ * (proveKV/src/codec.rs:85-95, pool.rs:83-103, shell.rs:48-66); the same
+ * bytes as the two calls, with one host round trip. */
+int pkv_blake3_tier_digests(pkv_ctx* ctx, const uint8_t* d_buf, uint64_t buf_bytes, const pkv_range* ranges,
+                            uint32_t n, uint32_t layers, uint8_t* d_blob_digests, uint8_t* d_layer_digests,
+                            void* stream);
+
 /* blake3 of host bytes, hashed on the context's device (copy in, the same
  * kernels, copy out, synchronise): blake3::hash over a host slice, as
  * CodecProfileDigest / ArtifactDigest::from_canonical_bytes and from_parts

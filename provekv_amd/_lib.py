@@ -52,7 +52,8 @@ EXPORTS = (
     "pkv_decode_batch_compact", "pkv_parse_header", "pkv_record_len", "pkv_encode_vectors", "pkv_decode_vectors",
     "pkv_constants_cache_stats", "pkv_constants_cache_clear", "pkv_prepared_len", "pkv_turbo_prepare_queries",
     "pkv_turbo_score_segments", "pkv_score_status", "pkv_turbo_score_batch", "pkv_encode_diagnostics",
-    "pkv_radii_log_bound", "pkv_fb2_n_blocks", "pkv_lloyd_refine", "pkv_blake3_ranges", "pkv_blake3_layer_digests", "pkv_blake3",
+    "pkv_radii_log_bound", "pkv_fb2_n_blocks", "pkv_lloyd_refine", "pkv_blake3_ranges", "pkv_blake3_layer_digests",
+    "pkv_blake3_tier_digests", "pkv_blake3",
     "pkv_host_angle_bins", "pkv_host_octant_bins", "pkv_host_logf",
     "pkv_host_expf",
 )
@@ -148,6 +149,7 @@ def _declare(L):
         "pkv_lloyd_refine": ([P, P, U32, U32, U32, P, U32, U32, P, P, P], I32),
         "pkv_blake3_ranges": ([P, P, U64, P, U32, P, P], I32),
         "pkv_blake3_layer_digests": ([P, P, U32, U32, P, P], I32),
+        "pkv_blake3_tier_digests": ([P, P, U64, P, U32, U32, P, P, P], I32),
         "pkv_blake3": ([P, P, U64, P], I32),
         "pkv_host_angle_bins": ([P, P, U64, U32, P], None),
         "pkv_host_octant_bins": ([P, P, U64, P, P], None),

@@ -1412,6 +1412,24 @@ int pkv_blake3_layer_digests(pkv_ctx* ctx, const uint8_t* d_kv_digests, uint32_t
     return e ? hip_status(static_cast<hipError_t>(e)) : PKV_OK;
 }
 
+int pkv_blake3_tier_digests(pkv_ctx* ctx, const uint8_t* d_buf, uint64_t buf_bytes, const pkv_range* ranges,
+                            uint32_t n, uint32_t layers, uint8_t* d_blob_digests, uint8_t* d_layer_digests,
+                            void* stream) {
+    if (!ctx || layers == 0) return PKV_ERR_INVALID_ARG;
+    if (n == 0) return PKV_OK;
+    if (n > 0x7FFFFFFFu || !ranges || !d_blob_digests || !d_layer_digests || (!d_buf && buf_bytes) ||
+        reinterpret_cast<uintptr_t>(d_blob_digests) % 4 || reinterpret_cast<uintptr_t>(d_layer_digests) % 4)
+        return PKV_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const int rc = blake3_ranges_locked(ctx, d_buf, buf_bytes, ranges, 2 * n, d_blob_digests, st);
+    if (rc) return rc;
+    const int e = launch_blake3_layers(reinterpret_cast<const uint32_t*>(d_blob_digests), n, layers,
+                                       reinterpret_cast<uint32_t*>(d_layer_digests), st);
+    return e ? hip_status(static_cast<hipError_t>(e)) : PKV_OK;
+}
+
 int pkv_blake3(pkv_ctx* ctx, const void* data, uint64_t len, uint8_t out[32]) {
     if (!ctx || !out || (!data && len)) return PKV_ERR_INVALID_ARG;
     const uint64_t in_pad = (len + 255) & ~static_cast<uint64_t>(255);

@@ -120,6 +120,23 @@ class Context:
         L.check(rc, "pkv_blake3_layer_digests")
         return out
 
+    def tier_digests(self, buf, ranges, layers: int, blob_out, layer_out, stream=None) -> None:
+        """One tier of a build (pkv_blake3_tier_digests): the payload digests
+        of its 2 n blobs (rows of `ranges`, key then value per entry) into
+        `blob_out` [n, 2, 32] and the layer digests into `layer_out` [n, 32],
+        one call for what blake3_ranges and layer_digests do in two."""
+        torch = _torch()
+        rg = np.ascontiguousarray(np.asarray(ranges, dtype=np.uint64).reshape(-1, 2))
+        if len(rg) % 2:
+            raise ValueError("ranges come in key / value pairs")
+        n = len(rg) // 2
+        for t, need in ((buf, 0), (blob_out, 64 * n), (layer_out, 32 * n)):
+            if t.dtype != torch.uint8 or not t.is_contiguous() or t.numel() < need:
+                raise ValueError("buf, blob_out and layer_out must be contiguous uint8 tensors of the needed size")
+        rc = L.lib().pkv_blake3_tier_digests(self.ptr, buf.data_ptr(), buf.numel(), rg.ctypes.data, n, layers,
+                                             blob_out.data_ptr(), layer_out.data_ptr(), _stream_ptr(stream))
+        L.check(rc, "pkv_blake3_tier_digests")
+
     def blake3(self, data: bytes) -> bytes:
         """blake3::hash of host bytes, computed on this device."""
         data = bytes(data)

@@ -299,7 +299,8 @@ class TwoTierPlan:
         bufs["pool_layer_digests"] / bufs["shell_layer_digests"]
         [owners * layers, 32] every layer's block_digest (PoolLayer /
         ShellLayer::compute_digest, pool.rs:83-103, shell.rs:48-66).  Four
-        launches per tier at most (payload passes, then the layer digests).
+        launches per tier at most (payload passes, then the layer digests), one
+        library call per tier.
         With a `side` stream the shell tier runs there, concurrently with the
         pool tier (each tier alone leaves most of the GPU idle); the calling
         stream waits for both."""
@@ -320,9 +321,8 @@ class TwoTierPlan:
             ranges = getattr(tier, "ranges", None)
             if ranges is None:
                 ranges = tier.ranges = np.array([(off, ln) for _, _, _, off, ln in tier.blob_offsets], np.uint64)
-            self.ctx.blake3_ranges(bufs[f"{name}_wire"], ranges, out=bufs[f"{name}_digests"], stream=st)
-            self.ctx.layer_digests(bufs[f"{name}_digests"], self.layers, out=bufs[f"{name}_layer_digests"],
-                                   stream=st)
+            self.ctx.tier_digests(bufs[f"{name}_wire"], ranges, self.layers, bufs[f"{name}_digests"],
+                                  bufs[f"{name}_layer_digests"], stream=st)
         if side is not None:
             evs[1].record(side)
             main.wait_event(evs[1])

@@ -203,6 +203,35 @@ def test_argument_errors(ctx):
         ctx.layer_digests(torch.zeros((2, 2, 32), dtype=torch.uint8, device="cuda"), layers=0)
 
 
+def test_tier_digests_equal_the_two_calls(ctx):
+    """pkv_blake3_tier_digests (the digests of one tier in one call) writes
+    the bytes of pkv_blake3_ranges followed by pkv_blake3_layer_digests;
+    layers == 0 and an unaligned output are rejected."""
+    import torch
+    rng = np.random.RandomState(11)
+    data = rng.randint(0, 256, size=300_000).astype(np.uint8)
+    buf = torch.from_numpy(data).cuda()
+    lens = rng.randint(0, 9000, size=12)
+    offs = [int(rng.randint(0, len(data) - l)) for l in lens]
+    ranges = np.array(list(zip(offs, lens)), np.uint64)        # 6 entries of (key, value)
+    blob = torch.zeros((6, 2, 32), dtype=torch.uint8, device="cuda")
+    layer = torch.zeros((6, 32), dtype=torch.uint8, device="cuda")
+    ctx.tier_digests(buf, ranges, 3, blob, layer)
+    want_blob = ctx.blake3_ranges(buf, ranges)
+    want_layer = ctx.layer_digests(want_blob.reshape(6, 2, 32).contiguous(), 3)
+    torch.cuda.synchronize()
+    assert torch.equal(blob.reshape(12, 32).cpu(), want_blob.cpu())
+    assert torch.equal(layer.cpu(), want_layer.cpu())
+    for i in range(6):   # and the oracle's text digest, entry i being layer i % 3
+        k, v = data[offs[2 * i]:offs[2 * i] + lens[2 * i]], data[offs[2 * i + 1]:offs[2 * i + 1] + lens[2 * i + 1]]
+        assert layer[i].cpu().numpy().tobytes() == O.layer_digest(i % 3, O.blake3(k.tobytes()), O.blake3(v.tobytes()))
+    with pytest.raises(L.PkvError):
+        ctx.tier_digests(buf, ranges, 0, blob, layer)
+    big = torch.zeros(8 * 64 + 4, dtype=torch.uint8, device="cuda")
+    with pytest.raises(L.PkvError):
+        ctx.tier_digests(buf, ranges, 3, big[1:1 + 6 * 64], layer)
+
+
 def test_same_table_on_two_streams(ctx):
     """One range table digested alternately on two streams, with a long
     kernel queued ahead on each: a call reuses a table slot (and its
