@@ -248,18 +248,25 @@ int pkv_decode_segments_bounded(pkv_ctx* ctx, const pkv_profile* prof, int radii
 
 /* pkv_decode_segments_ex without any allocation: no hipMalloc, hipFree or
  * other allocating call, here or in the kernels.  No counterpart in the
- * reference; for callers that cannot allocate device memory (code under HIP
- * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
- * arguments, checks, kernels and results as pkv_decode_segments_ex.  The
- * segment table, its workgroup prefix and (when d_status is NULL) the status
- * words live in one fixed device array of the library per GPU (about 208 KiB,
- * held until the process ends), so nseg <= PKV_NOALLOC_MAX_SEGMENTS; a larger
- * table returns PKV_ERR_SCRATCH_LIMIT before any work.  Every call on a GPU
- * shares that array and leaves its contents behind (each call rewrites what it
- * uses): calls on one stream are ordered, but calls that overlap on one GPU
- * (other streams, other contexts on the same device) race on it and must be
- * serialised by the caller.  The table is copied from the caller's host memory
- * with hipMemcpyAsync on `stream`; segs may be released when the call returns. */
+ * reference; for callers that cannot allocate device memory (tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, checks, kernels
+ * and results as pkv_decode_segments_ex, except:
+ *   - d_status is required (2*nseg device words; NULL returns
+ *     PKV_ERR_INVALID_ARG before any work): a rejected blob leaves its output
+ *     untouched and is reported only there, so the call cannot fail open;
+ *   - the segment table and its workgroup prefix live in one fixed device
+ *     array of the library per GPU (about 176 KiB, held until the process
+ *     ends), so nseg <= PKV_NOALLOC_MAX_SEGMENTS; a larger table returns
+ *     PKV_ERR_SCRATCH_LIMIT before any work;
+ *   - every call on a GPU shares that array.  The library orders the calls
+ *     on the device: each waits (hipStreamWaitEvent, no host wait) for the
+ *     previous call's kernel, on whatever stream or context of that GPU it
+ *     ran, before it rewrites the table, so overlapping calls are correct but
+ *     run one after the other;
+ *   - the table is copied from the caller's host memory with hipMemcpyAsync
+ *     on `stream` on every call (segs may be released when the call returns),
+ *     which a captured graph could not replay: on a stream under HIP graph
+ *     capture the call returns PKV_ERR_UNSUPPORTED. */
 #define PKV_NOALLOC_MAX_SEGMENTS 4096u
 int pkv_decode_segments_noalloc(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec,
                                 const uint8_t* d_wire, uint64_t wire_bytes, const pkv_seg* segs,

@@ -186,6 +186,21 @@ def gamma_f64(seed: int, shape: float, n: int) -> np.ndarray:
     return out
 
 
+PCG_DRAW = {"u32": 0, "u64": 1, "bool": 2, "f64": 3, "open01": 4, "normal": 5, "gamma": 6}
+
+
+def pcg_draws(state: int, stream: int, what: str, n: int, p0: float = 0.0, p1: float = 0.0) -> np.ndarray:
+    """n draws of a conversion of the oracle's RNG chain fed by rand_pcg's
+    Pcg32::new(state, stream) (test hook: the generator of rand 0.8's and
+    rand_distr 0.4's value-stability tests).  uint64 for u32 / u64 / bool,
+    float64 otherwise."""
+    out = np.zeros(n, dtype=np.uint64)
+    rc = lib().ora_pcg_draws(state, stream, PCG_DRAW[what], p0, p1, _p(out), n)
+    if rc != 0:
+        raise OracleError(rc)
+    return out if what in ("u32", "u64", "bool") else out.view(np.float64)
+
+
 def zig_tables():
     x = np.zeros(257)
     f = np.zeros(257)

@@ -57,6 +57,12 @@ typedef struct {
     uint32_t buf[16];
     int pos;            /* 16 = empty */
     int rounds;
+    /* test hook, not part of the restatement: when set, the stream is
+     * rand_pcg 0.3's Pcg32 (Lcg64Xsh32) instead of ChaCha, the generator the
+     * value-stability tests of rand 0.8 and rand_distr 0.4 draw from, so the
+     * conversions below can be checked against those tests' known answers */
+    int pcg;
+    uint64_t pcg_state, pcg_inc;
 } ora_rng;
 
 static uint32_t rotl32(uint32_t v, int c) { return (v << c) | (v >> (32 - c)); }
@@ -84,6 +90,26 @@ static void chacha_block(const uint32_t key[8], uint64_t counter, int rounds, ui
 static void rng_from_key(ora_rng* r, const uint32_t key[8], int rounds) {
     memcpy(r->key, key, 32);
     r->block = 0; r->pos = 16; r->rounds = rounds;
+    r->pcg = 0;
+}
+
+/* rand_pcg 0.3 Pcg32::new(state, stream): increment = stream * 2 + 1, state
+ * moved off its initial value by adding the increment and one LCG step
+ * (Lcg64Xsh32::from_state_incr), as pcg32_srandom_r of the PCG reference. */
+static void rng_pcg32(ora_rng* r, uint64_t state, uint64_t stream) {
+    memset(r, 0, sizeof *r);
+    r->pcg = 1;
+    r->pcg_inc = (stream << 1) | 1u;
+    r->pcg_state = (state + r->pcg_inc) * 6364136223846793005ull + r->pcg_inc;
+}
+
+/* Lcg64Xsh32::next_u32: XSH RR output of the old state, then one LCG step. */
+static uint32_t pcg_u32(ora_rng* r) {
+    const uint64_t old = r->pcg_state;
+    r->pcg_state = old * 6364136223846793005ull + r->pcg_inc;
+    const uint32_t xsh = (uint32_t)(((old >> 18) ^ old) >> 27);
+    const uint32_t rot = (uint32_t)(old >> 59);
+    return (xsh >> rot) | (xsh << ((32 - rot) & 31));
 }
 
 /* rand_core 0.6.4 SeedableRng::seed_from_u64: PCG32 fills the 32-byte seed. */
@@ -100,6 +126,7 @@ static void rng_seed_from_u64(ora_rng* r, uint64_t state) {
 }
 
 static uint32_t rng_u32(ora_rng* r) {
+    if (r->pcg) return pcg_u32(r);
     if (r->pos >= 16) {
         chacha_block(r->key, r->block, r->rounds, r->buf);
         r->block++;
@@ -1741,6 +1768,36 @@ void ora_gamma_f64(uint64_t seed, double shape, double* out, uint64_t n) {
     rng_seed_from_u64(&r, seed);
     gamma_init(&g, shape, 1.0);
     for (uint64_t i = 0; i < n; ++i) out[i] = rng_gamma(&r, &g);
+}
+
+/* Test hook: n draws of one of the conversions above from rand_pcg's
+ * Pcg32::new(state, stream) (the generator of rand's and rand_distr's
+ * value-stability tests); out[i] holds the u32 / u64 / bool as an integer, or
+ * the bits of the f64.  what: 0 next_u32, 1 next_u64, 2 Standard<bool>,
+ * 3 Standard<f64>, 4 Open01<f64>, 5 StandardNormal<f64>, 6 Gamma(p0, p1). */
+int ora_pcg_draws(uint64_t state, uint64_t stream, int what, double p0, double p1, uint64_t* out, uint64_t n) {
+    ora_rng r;
+    ora_gamma g;
+    rng_pcg32(&r, state, stream);
+    if (what == 6) {
+        if (!(p0 > 1.0) || !(p1 > 0.0)) return ORA_ERR_INVALID_ARG;   /* the large-shape branch only */
+        gamma_init(&g, p0, p1);
+    }
+    for (uint64_t i = 0; i < n; ++i) {
+        double v = 0.0;
+        switch (what) {
+        case 0: out[i] = rng_u32(&r); continue;
+        case 1: out[i] = rng_u64(&r); continue;
+        case 2: out[i] = (uint64_t)rng_bool(&r); continue;
+        case 3: v = rng_f64(&r); break;
+        case 4: v = rng_open01(&r); break;
+        case 5: v = rng_normal(&r); break;
+        case 6: v = rng_gamma(&r, &g); break;
+        default: return ORA_ERR_INVALID_ARG;
+        }
+        memcpy(&out[i], &v, 8);
+    }
+    return ORA_OK;
 }
 
 void ora_zig_tables(double* x257, double* f257, double* r) {

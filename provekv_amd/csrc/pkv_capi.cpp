@@ -82,6 +82,8 @@ struct Slot {
     uint64_t hash = 0;
 };
 
+struct NoallocScratch;   // pkv_decode_segments_noalloc's per-device scratch (below)
+
 }  // namespace
 
 struct pkv_ctx {
@@ -92,7 +94,7 @@ struct pkv_ctx {
     hipStream_t own_stream = nullptr;   // for the host-buffer entry points
     void* io_buf = nullptr;             // host-buffer entry points: in + out (device memory)
     size_t io_buf_cap = 0;
-    uint8_t* noalloc = nullptr;         // this device's copy of `scratch` (pkv_decode_segments_noalloc)
+    NoallocScratch* noalloc = nullptr;  // this device's `scratch` (pkv_decode_segments_noalloc)
 };
 
 struct pkv_profile {
@@ -126,16 +128,15 @@ struct pkv_profile {
 };
 
 // ---- fixed scratch of pkv_decode_segments_noalloc: [segment table | tile
-// prefix | status words] of one call, for at most PKV_NOALLOC_MAX_SEGMENTS
-// segments.  A file-scope device array: every GPU the library runs on holds
-// its own copy, at its own address, from module load to process end.  In host
-// code `scratch` names a host-side stand-in, never the device memory: host code
+// prefix] of one call, for at most PKV_NOALLOC_MAX_SEGMENTS segments.  A
+// file-scope device array: every GPU the library runs on holds its own copy,
+// at its own address, from module load to process end.  In host code
+// `scratch` names a host-side stand-in, never the device memory: host code
 // uses only the address hipGetSymbolAddress returns for the current device.
 namespace {
 constexpr size_t pad256c(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 constexpr size_t kNaTileOff = pad256c(sizeof(pkv_seg) * PKV_NOALLOC_MAX_SEGMENTS);
-constexpr size_t kNaStatusOff = kNaTileOff + pad256c(sizeof(uint32_t) * (PKV_NOALLOC_MAX_SEGMENTS + 1));
-constexpr size_t kNaBytes = kNaStatusOff + sizeof(uint32_t) * 2 * PKV_NOALLOC_MAX_SEGMENTS;
+constexpr size_t kNaBytes = kNaTileOff + sizeof(uint32_t) * (PKV_NOALLOC_MAX_SEGMENTS + 1);
 }  // namespace
 
 static __device__ __align__(256) uint8_t scratch[kNaBytes];
@@ -143,23 +144,37 @@ static __device__ __align__(256) uint8_t scratch[kNaBytes];
 namespace {
 
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-uint8_t* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of `scratch` on `device`, looked up once per device with that
-// device current (the caller has made it current).
-int noalloc_scratch(int device, uint8_t** out) {
+// One device's scratch: its address, and the event that orders the calls
+// sharing it.  Every call waits on the device for the event (the previous
+// call's kernel, on whatever stream and context it ran) before it rewrites
+// the table, and records the event after its own launch; `mu` makes that
+// wait / rewrite / launch / record sequence atomic among host threads.
+struct NoallocScratch {
+    uint8_t* ptr = nullptr;
+    hipEvent_t ev = nullptr;
+    std::mutex mu;
+};
+std::mutex g_scratch_mu;
+NoallocScratch g_scratch[kMaxDevices];
+
+// Set-up, once per device with that device current (the caller has made it
+// current): the device address of `scratch` and the ordering event.
+int noalloc_scratch(int device, NoallocScratch** out) {
+    if (device < 0 || device >= kMaxDevices) return PKV_ERR_DEVICE;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (device >= 0 && device < kMaxDevices && g_scratch_ptr[device]) {
-        *out = g_scratch_ptr[device];
-        return PKV_OK;
+    NoallocScratch& s = g_scratch[device];
+    if (!s.ptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e);
+        if (!p) return PKV_ERR_DEVICE;
+        hipEvent_t ev = nullptr;
+        HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+        s.ev = ev;
+        s.ptr = static_cast<uint8_t*>(p);
     }
-    void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess) return hip_status(e);
-    if (!p) return PKV_ERR_DEVICE;
-    if (device >= 0 && device < kMaxDevices) g_scratch_ptr[device] = static_cast<uint8_t*>(p);
-    *out = static_cast<uint8_t*>(p);
+    *out = &s;
     return PKV_OK;
 }
 
@@ -1203,13 +1218,18 @@ int pkv_decode_segments_bounded(pkv_ctx* ctx, const pkv_profile* prof, int radii
                                max_workgroups);
 }
 
-// pkv_decode_segments_ex with the table, its tile prefix and the status words
-// in this device's `scratch` (address from set-up): no allocating call.
+// pkv_decode_segments_ex with the table and its tile prefix in this device's
+// `scratch` (address from set-up): no allocating call.  Calls sharing the
+// scratch are ordered on the device by its event, whatever their stream or
+// context.
 int pkv_decode_segments_noalloc(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, const uint8_t* d_wire,
                                 uint64_t wire_bytes, const pkv_seg* segs, uint32_t nseg, void* d_out, int out_dtype,
                                 uint64_t out_elems, uint32_t fanout, uint64_t fanout_stride, uint32_t* d_status,
                                 void* stream) {
     if (!ctx || !prof) return PKV_ERR_INVALID_ARG;
+    // the caller's status words are the only report of a rejected blob (its
+    // output is left untouched): without them a decode error would pass silently
+    if (!d_status) return PKV_ERR_INVALID_ARG;
     if (nseg > PKV_NOALLOC_MAX_SEGMENTS) return PKV_ERR_SCRATCH_LIMIT;
     if (!ctx->noalloc) return PKV_ERR_DEVICE;
     if (out_dtype != PKV_F32 && out_dtype != PKV_BF16 && out_dtype != PKV_F16) return PKV_ERR_INVALID_ARG;
@@ -1224,15 +1244,26 @@ int pkv_decode_segments_noalloc(pkv_ctx* ctx, const pkv_profile* prof, int radii
     const hipStream_t st = static_cast<hipStream_t>(stream);
     std::lock_guard<std::mutex> lock(ctx->mu);
     HIP_TRY(hipSetDevice(ctx->device));
-    uint8_t* base = ctx->noalloc;
+    // the table is copied from host memory on every call, which a captured
+    // graph would replay from addresses that no longer hold it
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(st, &cap));
+    if (cap != hipStreamCaptureStatusNone) return PKV_ERR_UNSUPPORTED;
+    NoallocScratch& sc = *ctx->noalloc;
+    std::lock_guard<std::mutex> scratch_lock(sc.mu);
+    uint8_t* base = sc.ptr;
+    // the previous call's kernel (any stream, any context on this device)
+    // still reads the table until this event completes
+    HIP_TRY(hipStreamWaitEvent(st, sc.ev, 0));
     // pageable host sources: the runtime stages them before returning
     HIP_TRY(hipMemcpyAsync(base, segs, sizeof(pkv_seg) * nseg, hipMemcpyHostToDevice, st));
     HIP_TRY(hipMemcpyAsync(base + kNaTileOff, tiles, sizeof(uint32_t) * (nseg + 1), hipMemcpyHostToDevice, st));
-    uint32_t* status = d_status ? d_status : reinterpret_cast<uint32_t*>(base + kNaStatusOff);
     const int e = launch_segments(prof, radii, false, out_dtype, d_out, d_wire, reinterpret_cast<const SegDev*>(base),
-                                  reinterpret_cast<const uint32_t*>(base + kNaTileOff), nseg, tiles[nseg], status,
+                                  reinterpret_cast<const uint32_t*>(base + kNaTileOff), nseg, tiles[nseg], d_status,
                                   false, fanout, fanout_stride, 0, st);
-    return e ? hip_status(static_cast<hipError_t>(e)) : PKV_OK;
+    const hipError_t re = hipEventRecord(sc.ev, st);
+    if (e) return hip_status(static_cast<hipError_t>(e));
+    return re == hipSuccess ? PKV_OK : hip_status(re);
 }
 
 int pkv_encode_diagnostics(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, const float* d_in, uint64_t n,

@@ -14,8 +14,10 @@ and Lloyd; O.turbo_constants: signs + QJL matrix) -- never the product's.
             oracle decodes, copies 1-7 equal to copy 0
   config 4  Llama-3-8B KV 32 x {K,V} x 8 heads x 32768 tokens x 128, bf16 in,
             TQB1-L (seeded on the device, 4.3 GB): one full-size launch each
-            way; 8 blobs x 1024 sampled vectors against the oracle bit for bit,
-            every header, and size-independent checks over all 16.8 M vectors
+            way; one vector of every 64-vector workgroup tile of all 64 blobs
+            (262,144 vectors, the position inside the tile cycling over all
+            64) against the oracle bit for bit, every header, and
+            size-independent checks over all 16.8 M vectors
 
 Bars: wire bytes and decodes bit-exact (decode within 1e-6 relative is the
 stated bar; exact equality is what is checked).  Oracle calls run on a thread
@@ -220,16 +222,20 @@ def test_config4_llama_bf16_lossy_full_size(ctx):
     assert prof.status_error(st.cpu().numpy().view(np.uint32), segs) is None
     assert wire.numel() == 1_677_724_032                            # 64 x 38 + 16.8 M x 100
     signs, G = turbo_consts(Dd)
-    rng = np.random.RandomState(44)
+    # one vector of every 64-vector workgroup tile of every blob, bit for bit
+    # against the oracle: the encode and decode grids give each workgroup 64
+    # consecutive vectors (four waves of 16), and the vector taken inside a
+    # tile cycles through all 64 positions (lane groups, waves) over the tiles
+    tiles = n // 64
     hdr_ref = None
-    for k in (0, 9, 22, 31, 40, 51, 60, 63):
-        idx = np.sort(rng.choice(n, 1024, replace=False))
+    for k in range(nb):
+        idx = (np.arange(tiles, dtype=np.int64) * 64 + (np.arange(tiles) * 29 + k * 7) % 64).astype(np.int64)
         ti = torch.from_numpy(idx).cuda()
         xs = flat[k * n * Dd:(k + 1) * n * Dd].view(n, Dd)[ti].float().cpu().numpy()   # exact bf16 upcast
         ref = O.turbo_encode_batch(xs, SEED, radii_codec=1, signs=signs, G=G)
         wb = wire[k * blob:(k + 1) * blob]
         hdr = wb[:38].cpu().numpy().copy()
-        hdr[30:34] = np.frombuffer(np.uint32(1024).tobytes(), np.uint8)
+        hdr[30:34] = np.frombuffer(np.uint32(tiles).tobytes(), np.uint8)
         assert hdr.tobytes() == ref[:38], k
         pay = wb[38:].view(n, plen)[ti].cpu().numpy()
         assert pay.tobytes() == ref[38:], k
@@ -242,7 +248,7 @@ def test_config4_llama_bf16_lossy_full_size(ctx):
     assert all(h[:30].tobytes() == hdr_ref for h in heads)
     assert np.all(heads[:, 30:34].copy().view(np.uint32) == n)
     assert np.all(heads[:, 34:38].copy().view(np.uint32) == plen)
-    # every decoded vector is finite and points the way its input does
+    # and every decoded vector is finite and points the way its input does
     xf = flat.view(nb * n, Dd)
     of = out.view(nb * n, Dd)
     cos_min = 1.0

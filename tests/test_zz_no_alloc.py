@@ -1,8 +1,11 @@
 """GPU test of pkv_decode_segments_noalloc, called through the C ABI: the
-entry point that allocates nothing (segment table, tile prefix and status
-words in the library's fixed per-GPU scratch) must decode exactly what
+entry point that allocates nothing (segment table and tile prefix in the
+library's fixed per-GPU scratch) must decode exactly what
 pkv_decode_segments_ex decodes, bit for bit, on consecutive calls of
-different sizes, and report the same status words."""
+different sizes, and report the same status words; it refuses to run without
+status words (a rejected blob would otherwise pass silently) and under graph
+capture, and its calls from two streams and two contexts of one GPU, which
+share the scratch, are ordered on the device."""
 import ctypes as C
 
 import numpy as np
@@ -36,7 +39,7 @@ def _bits(t):
     return t.view(torch.int32) if t.element_size() == 4 else t.view(torch.int16)
 
 
-def _rehydrate_both_ways(ctx, layers, heads, prefix, agents, dtype, copies, lossy, corpus_seed, with_status):
+def _rehydrate_both_ways(ctx, layers, heads, prefix, agents, dtype, copies, lossy, corpus_seed):
     """Encode a two-tier plan, rehydrate it into two caches (existing entry
     point / no-allocation entry point) and compare them and the status words."""
     import torch
@@ -59,15 +62,14 @@ def _rehydrate_both_ways(ctx, layers, heads, prefix, agents, dtype, copies, loss
              (plan.turbo, bufs["shell_wire"], caches[0].segments_for(plan.shells, firsts), plan.radii)]
     for prof, wire, segs, radii in tiers:
         st_a = torch.full((2 * len(segs),), -7, dtype=torch.int32, device="cuda")
-        st_b = torch.full((2 * len(segs),), -7, dtype=torch.int32, device="cuda") if with_status else None
+        st_b = torch.full((2 * len(segs),), -7, dtype=torch.int32, device="cuda")
         prof.decode_segments(wire, segs, caches[0].buf.view(-1), radii=radii, status=st_a, fanout=copies,
                              fanout_stride=caches[0].copy_stride)
         rc = _noalloc(prof, wire, segs, caches[1].buf.view(-1), radii, copies, caches[1].copy_stride, st_b, stream)
         assert rc == L.OK, L.status_string(rc)
         torch.cuda.synchronize()
         assert prof.status_error(st_a.cpu().numpy().view(np.uint32), segs) is None
-        if with_status:
-            assert torch.equal(st_a, st_b)
+        assert torch.equal(st_a, st_b)
     torch.cuda.synchronize()
     assert torch.equal(_bits(caches[0].buf), _bits(caches[1].buf))
     assert not torch.isnan(caches[1].buf.float()).any()
@@ -82,17 +84,17 @@ def _rehydrate_both_ways(ctx, layers, heads, prefix, agents, dtype, copies, loss
 
 def test_noalloc_matches_decode_segments_ex_two_calls(ctx):
     import torch
-    # first call: the larger table (f32 caches, 3 copies, lossless shells, caller's status words)
-    _rehydrate_both_ways(ctx, 4, 8, 200, [30, 20, 10], torch.float32, 3, False, 5, True)
-    # second call: a smaller table over the same scratch (bf16, 1 copy, lossy shells, status in the scratch)
-    _rehydrate_both_ways(ctx, 2, 4, 50, [7], torch.bfloat16, 1, True, 6, False)
+    # first call: the larger table (f32 caches, 3 copies, lossless shells)
+    _rehydrate_both_ways(ctx, 4, 8, 200, [30, 20, 10], torch.float32, 3, False, 5)
+    # second call: a smaller table over the same scratch (bf16, 1 copy, lossy shells)
+    _rehydrate_both_ways(ctx, 2, 4, 50, [7], torch.bfloat16, 1, True, 6)
 
 
 def test_noalloc_rejects_header_like_decode_segments_ex(ctx):
     """A corrupt blob header: both entry points leave the segment's output
     untouched and report the same status words."""
     import torch
-    plan, bufs = _rehydrate_both_ways(ctx, 2, 4, 40, [6, 6], torch.float32, 2, False, 7, True)
+    plan, bufs = _rehydrate_both_ways(ctx, 2, 4, 40, [6, 6], torch.float32, 2, False, 7)
     wire = bufs["pool_wire"].clone()
     _, _, _, off, _ = plan.pool.blob_offsets[1]
     wire[off] = ord("X")   # FB2 magic of blob 1
@@ -118,6 +120,107 @@ def test_noalloc_rejects_tables_beyond_its_scratch(ctx):
     segs = D.segments([(0, 0, 64, 0, 0, 1)] * n)
     wire = torch.zeros(38 * n, dtype=torch.uint8, device="cuda")
     out = torch.zeros(64, dtype=torch.float32, device="cuda")
-    rc = _noalloc(prof, wire, segs, out, L.RADII_F32, 1, 0, None, torch.cuda.current_stream())
+    st = torch.zeros(2 * n, dtype=torch.int32, device="cuda")
+    rc = _noalloc(prof, wire, segs, out, L.RADII_F32, 1, 0, st, torch.cuda.current_stream())
     assert rc == L.ERR_SCRATCH_LIMIT
     assert "scratch" in L.status_string(rc)
+
+
+def _corrupt_pool(ctx):
+    import torch
+    plan, bufs = _rehydrate_both_ways(ctx, 2, 4, 40, [6, 6], torch.float32, 1, False, 8)
+    wire = bufs["pool_wire"].clone()
+    _, _, _, off, _ = plan.pool.blob_offsets[1]
+    wire[off] = ord("X")   # FB2 magic of blob 1
+    cache = DeviceKVCache(2, 4, plan.tokens, 64, copies=1)
+    return plan, wire, cache, cache.segments_for(plan.pool, [0])
+
+
+def test_noalloc_refuses_to_run_without_status_words(ctx):
+    """Fails closed: with no status words a rejected blob could not be
+    reported, so the call refuses before any work and writes nothing."""
+    import torch
+    plan, wire, cache, segs = _corrupt_pool(ctx)
+    cache.buf.fill_(float("nan"))
+    rc = _noalloc(plan.fib, wire, segs, cache.buf.view(-1), L.RADII_F32, 1, cache.copy_stride, None,
+                  torch.cuda.current_stream())
+    assert rc == L.ERR_INVALID_ARG
+    torch.cuda.synchronize()
+    assert torch.isnan(cache.buf).all()
+
+
+def test_noalloc_refuses_graph_capture(ctx):
+    """The table is copied from host memory on every call, which a graph could
+    not replay: under capture the call returns UNSUPPORTED and enqueues nothing."""
+    import torch
+    plan, wire, cache, segs = _corrupt_pool(ctx)
+    st = torch.full((2 * len(segs),), -7, dtype=torch.int32, device="cuda")
+    x = torch.zeros(16, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    codes = []
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        x.add_(1.0)
+        codes.append(_noalloc(plan.fib, wire, segs, cache.buf.view(-1), L.RADII_F32, 1, cache.copy_stride, st,
+                              torch.cuda.current_stream()))
+    torch.cuda.synchronize()
+    assert codes == [L.ERR_UNSUPPORTED]
+    assert (st == -7).all()
+    del g
+
+
+def test_noalloc_two_streams_and_two_contexts(ctx):
+    """Calls that share the per-GPU scratch from two streams, and from a second
+    context on the same device, issued back to back with no host wait between
+    them: each must decode what pkv_decode_segments_ex decodes."""
+    import torch
+    from provekv_amd.device import Context
+    ctx2 = Context(0)
+    try:
+        jobs = []
+        for c, (layers, heads, prefix, agents, seed) in zip(
+                (ctx, ctx2, ctx, ctx2),
+                ((4, 8, 300, [40, 12], 11), (3, 4, 120, [9], 12), (2, 8, 64, [5, 5, 5], 13), (5, 2, 90, [3], 14))):
+            plan = TwoTierPlan(c, layers, heads, 64, prefix, agents, seed=SEED)
+            corpus = synth.corpus_tokens(seed, layers, heads, plan.tokens, 64)
+            bufs = plan.alloc()
+            plan.encode(torch.from_numpy(corpus.reshape(-1)).cuda(), bufs)
+            firsts, t = [], prefix
+            for nt in agents:
+                firsts.append(t)
+                t += nt
+            caches = [DeviceKVCache(layers, heads, plan.tokens, 64, copies=2) for _ in range(2)]
+            for cc in caches:
+                cc.buf.fill_(float("nan"))
+            jobs.append((plan, bufs, caches, firsts))
+        calls = []
+        for plan, bufs, caches, firsts in jobs:
+            for prof, wire, segs, radii in ((plan.fib, bufs["pool_wire"], caches[1].segments_for(plan.pool, [0]),
+                                             L.RADII_F32),
+                                            (plan.turbo, bufs["shell_wire"],
+                                             caches[1].segments_for(plan.shells, firsts), plan.radii)):
+                st = torch.full((2 * len(segs),), -7, dtype=torch.int32, device="cuda")
+                calls.append((prof, wire, segs, radii, caches[1], st))
+        torch.cuda.synchronize()   # inputs, caches and status words ready before the side streams use them
+        streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+        stats = []
+        for j, (prof, wire, segs, radii, cache, st) in enumerate(calls):
+            rc = _noalloc(prof, wire, segs, cache.buf.view(-1), radii, 2, cache.copy_stride, st, streams[(j // 2) % 2])
+            assert rc == L.OK, L.status_string(rc)
+            stats.append((prof, st, segs))
+        torch.cuda.synchronize()
+        for prof, st, segs in stats:
+            assert prof.status_error(st.cpu().numpy().view(np.uint32), segs) is None
+        for plan, bufs, caches, firsts in jobs:
+            plan.fib.decode_segments(bufs["pool_wire"], caches[0].segments_for(plan.pool, [0]), caches[0].buf.view(-1),
+                                     fanout=2, fanout_stride=caches[0].copy_stride)
+            plan.turbo.decode_segments(bufs["shell_wire"], caches[0].segments_for(plan.shells, firsts),
+                                       caches[0].buf.view(-1), radii=plan.radii, fanout=2,
+                                       fanout_stride=caches[0].copy_stride)
+        torch.cuda.synchronize()
+        for plan, bufs, caches, firsts in jobs:
+            assert torch.equal(_bits(caches[0].buf), _bits(caches[1].buf))
+            assert not torch.isnan(caches[1].buf).any()
+    finally:
+        torch.cuda.synchronize()
+        ctx2.close()
