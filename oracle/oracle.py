@@ -69,6 +69,8 @@ def _declare(L):
     L.ora_logf_bits.restype = None
     L.ora_track_reset.argtypes = [I32]
     L.ora_track_reset.restype = None
+    L.ora_track_counts.argtypes = [P]
+    L.ora_track_counts.restype = None
     L.ora_track_margin.argtypes = []
     L.ora_track_margin.restype = C.c_double
     L.ora_track_tail_logs.argtypes = [P, P, U64]
@@ -83,6 +85,8 @@ def _declare(L):
     L.ora_normal_f64.argtypes = [U64, P, U64]
     L.ora_gamma_f64.argtypes = [U64, C.c_double, P, U64]
     L.ora_zig_tables.argtypes = [P, P, P]
+    L.ora_pcg_draws.argtypes = [U64, U64, I32, C.c_double, C.c_double, P, U64]
+    L.ora_pcg_draws.restype = I32
     L.ora_stored_rotation.argtypes = [U32, U64, P, P]
     L.ora_stored_rotation.restype = I32
     L.ora_fib_codebook.argtypes = [U32, U32, U32, U64, U32, U32, U32, P, P, P]

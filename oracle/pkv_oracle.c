@@ -181,6 +181,10 @@ static int zig_ready = 0;
  * built from them directly). */
 static int g_track = 0;
 static double g_margin = INFINITY;
+/* branch counts while g_track is set: ziggurat iterations, wedge tests,
+ * wedge acceptances, base-strip tail entries; gamma proposals (v > 0),
+ * squeeze acceptances, log acceptances */
+static uint64_t g_cnt[7];
 #define ORA_TAIL_LOGS 4096
 static double g_tail_arg[ORA_TAIL_LOGS], g_tail_val[ORA_TAIL_LOGS];
 static uint64_t g_tail_n = 0;
@@ -245,8 +249,10 @@ static double rng_normal(ora_rng* r) {
         int i = (int)(bits & 0xff);
         double u = bits_to_f64((bits >> 12) | ((uint64_t)(1023 + 1) << 52)) - 3.0;
         double x = u * ZX[i];
+        if (g_track) g_cnt[0]++;
         if (fabs(x) < ZX[i + 1]) return x;
         if (i == 0) {
+            if (g_track) g_cnt[3]++;
             double xx = 1.0, yy = 0.0;
             while (-2.0 * yy < xx * xx) {
                 double x_ = rng_open01(r);
@@ -259,7 +265,11 @@ static double rng_normal(ora_rng* r) {
         }
         const double lhs = ZF[i + 1] + (ZF[i] - ZF[i + 1]) * rng_f64(r), rhs = zig_f(x);
         track(lhs, rhs);
-        if (lhs < rhs) return x;
+        if (g_track) g_cnt[1]++;
+        if (lhs < rhs) {
+            if (g_track) g_cnt[2]++;
+            return x;
+        }
     }
 }
 
@@ -282,10 +292,17 @@ static double rng_gamma(ora_rng* r, const ora_gamma* g) {
         double v = v_cbrt * v_cbrt * v_cbrt;
         double u = rng_open01(r);
         double x_sqr = x * x;
-        if (u < 1.0 - 0.0331 * x_sqr * x_sqr) return g->d * v * g->scale;
+        if (g_track) g_cnt[4]++;
+        if (u < 1.0 - 0.0331 * x_sqr * x_sqr) {
+            if (g_track) g_cnt[5]++;
+            return g->d * v * g->scale;
+        }
         const double lhs = log(u), rhs = 0.5 * x_sqr + g->d * (1.0 - v + log(v));
         track(lhs, rhs);
-        if (lhs < rhs) return g->d * v * g->scale;
+        if (lhs < rhs) {
+            if (g_track) g_cnt[6]++;
+            return g->d * v * g->scale;
+        }
     }
 }
 
@@ -1841,7 +1858,8 @@ int ora_unpack_bits(const uint8_t* in, uint64_t n, int bits, uint32_t* out) {
     return padding_zero(in, n * (uint64_t)bits, (n * (uint64_t)bits + 7) / 8) ? ORA_OK : ORA_ERR_MALFORMED;
 }
 
-void ora_track_reset(int on) { g_track = on; g_margin = INFINITY; g_tail_n = 0; }
+void ora_track_reset(int on) { g_track = on; g_margin = INFINITY; g_tail_n = 0; memset(g_cnt, 0, sizeof g_cnt); }
+void ora_track_counts(uint64_t out[7]) { memcpy(out, g_cnt, sizeof g_cnt); }
 double ora_track_margin(void) { return g_margin; }
 uint64_t ora_track_tail_logs(double* args, double* vals, uint64_t cap) {
     const uint64_t n = g_tail_n < ORA_TAIL_LOGS ? g_tail_n : ORA_TAIL_LOGS;
