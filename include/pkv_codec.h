@@ -281,7 +281,10 @@ int pkv_decode_segments_noalloc(pkv_ctx* ctx, const pkv_profile* prof, int radii
  * decode_batch_compact (proveKV/src/codec.rs:248-326) and the FibQuantAdapter
  * pair (513-569).  vectors: n*dim f32 row-major.  For decode, the header is
  * parsed and validated on the host with the reference's checks
- * (turbo-quant/src/wire.rs:401-568; fib-quant/src/codec.rs:323-424). */
+ * (turbo-quant/src/wire.rs:401-568; fib-quant/src/codec.rs:323-424).  A fib
+ * payload without the FB2 magic is FibQuantAdapter::decode_batch_compact's
+ * fallback (codec.rs:542-561): one FB1 record, or else one JSON FibCodeV1,
+ * decoded as decode_batch_fast decodes it (one vector out). */
 int pkv_encode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec,
                              const float* vectors, uint64_t n, uint8_t* out, uint64_t out_cap,
                              uint64_t* out_len, pkv_error* err);
@@ -314,11 +317,71 @@ int pkv_encode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const fl
  * f64 inverse rotation, codec.rs:506-537) / decode_batch (each == 0, 639-665:
  * every record parsed first, then decode_batch_fast).  Record i is
  * records[offsets[i] .. offsets[i + 1]) (n + 1 non-decreasing offsets, the
- * flattening of a `&[&[u8]]`).  A rejected record gives
- * PKV_ERR_CORRUPT_PAYLOAD with err->index = the record the reference reports.
- * JSON-serialised codes (the pre-compact envelope) are not decoded. */
+ * flattening of a `&[&[u8]]`).  A record without the TQW1 / FB1 magic is
+ * the adapters' JSON fallback: the serde_json text of a TurboCode /
+ * FibCodeV1 (see pkv_code_from_json), parsed and checked on the host and
+ * decoded by the same kernels (fib profiles created with caller constants
+ * cannot check the JSON digests: PKV_ERR_UNSUPPORTED; so do turbo
+ * PolarOnly profiles, whose angle width the adapter's bits - 1 does not
+ * match).  A rejected record gives PKV_ERR_CORRUPT_PAYLOAD with err->index =
+ * the record the reference reports (fib decode_batch: every payload is
+ * parsed, FB1 or JSON, before any is decoded). */
 int pkv_decode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const uint8_t* records,
                        const uint64_t* offsets, uint64_t n, float* out, uint64_t out_cap_vectors, pkv_error* err);
+
+/* ---------------------------------------------------------------- JSON codes
+ * Before the compact records, proveKV stored a vector's code as the
+ * serde_json text of turbo-quant's TurboCode {polar_code, residual_sketch}
+ * (turbo-quant/src/turbo.rs:50-56, polar.rs:35-46, qjl.rs:41-50) or of
+ * fib-quant's FibCodeV1 (fib-quant/src/codec.rs:31-54), and the adapters
+ * still read it when a payload lacks the record magic:
+ * TurboQuantAdapter::decode (proveKV/src/codec.rs:386-393; the trait's
+ * decode_batch loops over it), FibQuantAdapter::decode (622-630),
+ * decode_batch (650-658) and decode_batch_compact (552-561).
+ * pkv_decode_vectors and pkv_decode_batch_compact take such payloads
+ * directly; the helpers below are their host half. */
+
+/* A codec profile by its parameters (host-only helpers; no device). */
+typedef struct pkv_codec_params {
+    int32_t kind;                  /* PKV_CODEC_TURBO or PKV_CODEC_FIB */
+    uint32_t dim;
+    uint32_t bits;                 /* turbo: the adapter's bits; its codes carry bits - 1 angle bits */
+    uint32_t projections;          /* turbo: QJL projections */
+    uint32_t k, n;                 /* fib: block dimension, codebook size */
+    uint32_t training_samples, lloyd_restarts, lloyd_iterations;   /* fib: the adapter's overrides */
+    uint64_t seed;
+} pkv_codec_params;
+
+/* Host only.  serde_json::from_slice of a JSON code (serde_json 1.0.150:
+ * object or field array, unknown fields skipped, duplicate / missing fields,
+ * trailing characters and out-of-range numbers rejected) followed by the
+ * checks the adapter's decode applies before the arithmetic: turbo
+ * PolarCode::validate_for(dim, bits - 1) (turbo-quant/src/polar.rs:107-152);
+ * fib validate_code_header (fib-quant/src/codec.rs:926-975: schema, the
+ * profile digest always, the codebook and rotation digests when not empty,
+ * dimensions, index width, norm format) and the index / norm lengths
+ * (bitpack.rs:47-66, codec.rs:1020-1031).  On success writes the payload of
+ * the equivalent TQW1 / FB1 record (turbo: f32 radii, packed angle indices,
+ * the sketch's signs when it holds one per projection -- the decode never
+ * reads them; fib: fp16 norm, packed indices; *payload_len bytes, CAPACITY
+ * when cap is short).  Errors: PKV_ERR_CORRUPT_PAYLOAD with *stage = 1 (the
+ * text does not deserialize: the adapters' "code deserialize failed") or 2
+ * (the code does not fit the profile: the decode's rejection);
+ * PKV_ERR_INVALID_ARG for parameters no reference profile accepts. */
+int pkv_code_from_json(const pkv_codec_params* params, const uint8_t* json, uint64_t len, uint8_t* payload,
+                       uint64_t cap, uint64_t* payload_len, int* stage);
+
+/* Host only.  The digest strings ("blake3:" + 64 hex digits, NUL-terminated,
+ * 72 bytes each; NULL skips one) of a fib profile, as validate_code_header
+ * compares them: FibQuantProfileV1::digest (fib-quant/src/profile.rs:256-262,
+ * the adapter's profile, proveKV/src/codec.rs:471-499),
+ * FibCodebookV1::compute_digest (codebook.rs:133-157, over the codewords,
+ * the MSEs and the Lloyd report) and StoredRotation::digest
+ * (rotation.rs:80-100), each json_digest (digest.rs:5-13).  Memoised per
+ * profile; the first codebook digest runs the codebook build on the host
+ * for its report (a few ms). */
+int pkv_fib_digests(const pkv_codec_params* params, char* profile_digest, char* codebook_digest,
+                    char* rotation_digest);
 
 /* Parses a TQB1 / FB2 header against the profile (host memory) and reports
  * the number of vectors and the radii codec; PKV_ERR_CORRUPT_PAYLOAD on any
@@ -497,6 +560,9 @@ void pkv_host_angle_bins(const float* a, const float* b, uint64_t n, uint32_t pb
 void pkv_host_octant_bins(const float* a, const float* b, uint64_t n, uint32_t* bins, uint8_t* safe);
 void pkv_host_logf(const float* x, uint64_t n, float* out);
 void pkv_host_expf(const float* x, uint64_t n, float* out);
+/* BLAKE3 of host bytes on the host, with the compression the digest
+ * kernels run (the fib digests' hash). */
+void pkv_host_blake3(const void* data, uint64_t len, uint8_t out[32]);
 
 #ifdef __cplusplus
 }

@@ -91,6 +91,8 @@ def _declare(L):
     L.ora_stored_rotation.restype = I32
     L.ora_fib_codebook.argtypes = [U32, U32, U32, U64, U32, U32, U32, P, P, P]
     L.ora_fib_codebook.restype = I32
+    L.ora_fib_codebook_report.argtypes = [U32, U32, U32, U64, U32, U32, U32, P, P, P, P, P, U32, P]
+    L.ora_fib_codebook_report.restype = I32
     L.ora_inv_norm_cdf.argtypes = [C.c_double]
     L.ora_inv_norm_cdf.restype = C.c_double
     L.ora_beta_inv.argtypes = [C.c_double, C.c_double, C.c_double]

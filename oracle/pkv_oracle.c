@@ -425,7 +425,6 @@ static void rot_apply_f64(int d, const double* M, const double* x, double* y) {
  *    boundary.  Parity of these two functions is pinned by closed forms
  *    (tests/test_oracle_profile.py), not by reference values.
  * ====================================================================== */
-static double norm_cdf(double x) { return 0.5 * erfc(-x / sqrt(2.0)); }
 
 static double inv_norm_cdf_lower(double p);
 
@@ -437,8 +436,13 @@ static double inv_norm_cdf(double p) {
     return inv_norm_cdf_lower(p);
 }
 
+static long double norm_cdf_l(long double x) { return 0.5L * erfcl(-x / sqrtl(2.0L)); }
+
 static double inv_norm_cdf_lower(double p) {
-    /* Acklam's rational approximation, then Halley steps on erfc. */
+    /* Acklam's rational approximation, then Halley steps on erfc carried in
+     * x87 long double and rounded once: the correctly rounded quantile (the
+     * exact value statrs approximates; checked against mpmath for the
+     * profiles tested, tests/test_oracle_pins.py). */
     static const double a[] = {-3.969683028665376e+01, 2.209460984245205e+02,
         -2.759285104469687e+02, 1.383577518672690e+02, -3.066479806614716e+01, 2.506628277459239e+00};
     static const double b[] = {-5.447609879822406e+01, 1.615858368580409e+02,
@@ -462,73 +466,77 @@ static double inv_norm_cdf_lower(double p) {
         x = (((((a[0] * rr + a[1]) * rr + a[2]) * rr + a[3]) * rr + a[4]) * rr + a[5]) * q /
             (((((b[0] * rr + b[1]) * rr + b[2]) * rr + b[3]) * rr + b[4]) * rr + 1);
     }
-    for (int it = 0; it < 3; ++it) {
-        double e = norm_cdf(x) - p;
-        double u = e * sqrt(2 * M_PI) * exp(x * x / 2);
-        x = x - u / (1 + x * u / 2);
+    long double xl = x;
+    for (int it = 0; it < 4; ++it) {
+        long double e = norm_cdf_l(xl) - (long double)p;
+        long double u = e * sqrtl(2.0L * 3.14159265358979323846264338327950288L) * expl(xl * xl / 2.0L);
+        xl = xl - u / (1.0L + xl * u / 2.0L);
     }
-    return x;
+    return (double)xl;
 }
 
-/* Regularized incomplete beta I_x(a,b) by Lentz's continued fraction. */
-static double betacf(double a, double b, double x) {
-    const double TINY = 1e-300;
-    double qab = a + b, qap = a + 1, qam = a - 1;
-    double c = 1, d = 1 - qab * x / qap;
-    if (fabs(d) < TINY) d = TINY;
+/* Regularized incomplete beta I_x(a,b) by Lentz's continued fraction, in
+ * long double. */
+static long double betacf(long double a, long double b, long double x) {
+    const long double TINY = 1e-300L;
+    long double qab = a + b, qap = a + 1, qam = a - 1;
+    long double c = 1, d = 1 - qab * x / qap;
+    if (fabsl(d) < TINY) d = TINY;
     d = 1 / d;
-    double h = d;
+    long double h = d;
     for (int m = 1; m <= 10000; ++m) {
         int m2 = 2 * m;
-        double aa = m * (b - m) * x / ((qam + m2) * (a + m2));
-        d = 1 + aa * d; if (fabs(d) < TINY) d = TINY;
-        c = 1 + aa / c; if (fabs(c) < TINY) c = TINY;
+        long double aa = m * (b - m) * x / ((qam + m2) * (a + m2));
+        d = 1 + aa * d; if (fabsl(d) < TINY) d = TINY;
+        c = 1 + aa / c; if (fabsl(c) < TINY) c = TINY;
         d = 1 / d; h *= d * c;
         aa = -(a + m) * (qab + m) * x / ((a + m2) * (qap + m2));
-        d = 1 + aa * d; if (fabs(d) < TINY) d = TINY;
-        c = 1 + aa / c; if (fabs(c) < TINY) c = TINY;
+        d = 1 + aa * d; if (fabsl(d) < TINY) d = TINY;
+        c = 1 + aa / c; if (fabsl(c) < TINY) c = TINY;
         d = 1 / d;
-        double del = d * c;
+        long double del = d * c;
         h *= del;
-        if (fabs(del - 1) < 1e-17) break;
+        if (fabsl(del - 1) < 1e-20L) break;
     }
     return h;
 }
 
-static double beta_reg(double a, double b, double x) {
+static long double beta_reg(long double a, long double b, long double x) {
     if (x <= 0) return 0;
     if (x >= 1) return 1;
-    double lbt = lgamma(a + b) - lgamma(a) - lgamma(b) + a * log(x) + b * log1p(-x);
-    double bt = exp(lbt);
+    long double lbt = lgammal(a + b) - lgammal(a) - lgammal(b) + a * logl(x) + b * log1pl(-x);
+    long double bt = expl(lbt);
     if (x < (a + 1) / (a + b + 2)) return bt * betacf(a, b, x) / a;
     return 1 - bt * betacf(b, a, 1 - x) / b;
 }
 
-static double beta_pdf(double a, double b, double x) {
-    return exp(lgamma(a + b) - lgamma(a) - lgamma(b) + (a - 1) * log(x) + (b - 1) * log1p(-x));
+static long double beta_pdf(long double a, long double b, long double x) {
+    return expl(lgammal(a + b) - lgammal(a) - lgammal(b) + (a - 1) * logl(x) + (b - 1) * log1pl(-x));
 }
 
-/* Beta(a,b) inverse CDF: bisection to a bracket, then safeguarded Newton. */
+/* Beta(a,b) inverse CDF: bisection to a bracket, then safeguarded Newton,
+ * in long double, rounded once (the correctly rounded quantile; see
+ * inv_norm_cdf_lower). */
 static double beta_inv(double q, double a, double b) {
     if (q <= 0) return 0;
     if (q >= 1) return 1;
-    double lo = 0, hi = 1, x = 0.5;
-    for (int it = 0; it < 60; ++it) {
-        x = 0.5 * (lo + hi);
-        if (beta_reg(a, b, x) < q) lo = x; else hi = x;
+    long double lo = 0, hi = 1, x = 0.5L;
+    for (int it = 0; it < 70; ++it) {
+        x = 0.5L * (lo + hi);
+        if (beta_reg(a, b, x) < (long double)q) lo = x; else hi = x;
     }
     for (int it = 0; it < 8; ++it) {
-        double f = beta_reg(a, b, x) - q;
-        double p = beta_pdf(a, b, x);
+        long double f = beta_reg(a, b, x) - (long double)q;
+        long double p = beta_pdf(a, b, x);
         if (!(p > 0)) break;
-        double nx = x - f / p;
+        long double nx = x - f / p;
         if (!(nx > lo && nx < hi)) break;
         if (nx == x) break;
         x = nx;
     }
     if (x < 0) x = 0;
     if (x > 1) x = 1;
-    return x;
+    return (double)x;
 }
 
 /* compiler-rt __powidf2: what Rust's f64::powi lowers to for a runtime
@@ -661,8 +669,29 @@ static double mse_for_codebook(const double* cb, int k, int n, const double* sam
     return sum / (double)ns;
 }
 
+/* LloydRepairEventV1 rows of a refinement (lloyd.rs:17-34, pushed at
+ * 297-306): restart, iteration, empty_cell, donor_cell, donor_count_before,
+ * donor_distortion, residual_norm; split_epsilon is the constant 1e-6. */
+typedef struct {
+    double* rows;   /* 7 per event */
+    int n, cap;
+    int restart, iteration;
+} ora_events;
+
+static void events_push(ora_events* ev, int empty, int donor, int count, double distortion, double rnorm) {
+    if (!ev) return;
+    if (ev->n == ev->cap) {
+        ev->cap = ev->cap ? 2 * ev->cap : 16;
+        ev->rows = (double*)realloc(ev->rows, sizeof(double) * 7 * (size_t)ev->cap);
+    }
+    double* r = ev->rows + 7 * (size_t)ev->n++;
+    r[0] = ev->restart; r[1] = ev->iteration; r[2] = empty; r[3] = donor; r[4] = count;
+    r[5] = distortion; r[6] = rnorm;
+}
+
 /* lloyd.rs:222-317 (SplitHighestDistortion policy) */
-static int update_centroids(double* cb, int k, int n, const double* samples, int ns, const int* asg) {
+static int update_centroids(double* cb, int k, int n, const double* samples, int ns, const int* asg,
+                            ora_events* ev) {
     double* sums = (double*)calloc((size_t)n * k, sizeof(double));
     int* counts = (int*)calloc(n, sizeof(int));
     double* distortion = (double*)calloc(n, sizeof(double));
@@ -708,6 +737,7 @@ static int update_centroids(double* cb, int k, int n, const double* samples, int
             cb[(size_t)donor * k + t] = cen - 1.0e-6 * dir;
             cb[(size_t)e * k + t] = cen + 1.0e-6 * dir;
         }
+        events_push(ev, e, donor, counts[donor], distortion[donor], rn);
         counts[donor] -= 1;
         counts[e] = 1;
         distortion[donor] = 0.0;
@@ -733,7 +763,7 @@ int ora_lloyd_refine(const double* samples, int ns, int k, int n, const double* 
         memcpy(cb, starts + (size_t)r * nk, sizeof(double) * nk);
         for (int it = 0; it < iterations && rc == ORA_OK; ++it) {
             for (int i = 0; i < ns; ++i) asg[i] = nearest_index_f64(samples + (size_t)i * k, cb, k, n, NULL);
-            rc = update_centroids(cb, k, n, samples, ns, asg);
+            rc = update_centroids(cb, k, n, samples, ns, asg, NULL);
         }
         out_mse[r] = mse_for_codebook(cb, k, n, samples, ns);
     }
@@ -758,9 +788,12 @@ static void perturb(double* v, size_t n, uint64_t salt) {
     }
 }
 
-/* Build the (N x k) f32 codebook; returns init/training mse. */
+/* Build the (N x k) f32 codebook; returns init/training mse, the best
+ * restart (UINT32_MAX when the start is kept, lloyd.rs:158-162) and, when
+ * `ev` is given, the repair events of every restart. */
 static int fib_codebook(int d, int k, int n, uint64_t seed, int training, int restarts, int iterations,
-                        float* out, double* init_mse_out, double* train_mse_out) {
+                        float* out, double* init_mse_out, double* train_mse_out, uint32_t* best_restart_out,
+                        ora_events* ev) {
     if (k < 4 || k > 16 || d % k != 0 || n < 2) return ORA_ERR_INVALID_ARG;
     uint64_t cseed = seed + 0x9e3779b97f4a7c15ull;
     size_t nk = (size_t)n * k;
@@ -788,6 +821,7 @@ static int fib_codebook(int d, int k, int n, uint64_t seed, int training, int re
     }
     double init_mse = mse_for_codebook(init, k, n, samples, ns);
     double best_mse = init_mse;
+    uint32_t best_restart = 0;
     memcpy(best, init, sizeof(double) * nk);
     if (restarts < 1) restarts = 1;
     for (int rs = 0; rs < restarts; ++rs) {
@@ -802,19 +836,26 @@ static int fib_codebook(int d, int k, int n, uint64_t seed, int training, int re
         }
         for (int it = 0; it < iterations; ++it) {
             for (int i = 0; i < ns; ++i) asg[i] = nearest_index_f64(samples + (size_t)i * k, cbk, k, n, NULL);
-            rc = update_centroids(cbk, k, n, samples, ns, asg);
+            if (ev) { ev->restart = rs; ev->iteration = it; }
+            rc = update_centroids(cbk, k, n, samples, ns, asg, ev);
             if (rc != ORA_OK) goto done;
         }
         double mse = mse_for_codebook(cbk, k, n, samples, ns);
         if (mse < best_mse || (rs == 0 && isinf(init_mse))) {
             best_mse = mse;
+            best_restart = (uint32_t)rs;
             memcpy(best, cbk, sizeof(double) * nk);
         }
     }
-    if (best_mse > init_mse) { memcpy(best, init, sizeof(double) * nk); best_mse = init_mse; }
+    if (best_mse > init_mse) {
+        memcpy(best, init, sizeof(double) * nk);
+        best_mse = init_mse;
+        best_restart = UINT32_MAX;
+    }
     for (size_t t = 0; t < nk; ++t) out[t] = (float)best[t];
     if (init_mse_out) *init_mse_out = init_mse;
     if (train_mse_out) *train_mse_out = best_mse;
+    if (best_restart_out) *best_restart_out = best_restart;
 done:
     free(init); free(dirs); free(samples); free(best); free(cbk); free(asg);
     return rc;
@@ -1837,7 +1878,23 @@ int ora_fib_codebook(uint32_t d, uint32_t k, uint32_t n, uint64_t seed, uint32_t
                      uint32_t restarts, uint32_t iterations, float* out, double* init_mse,
                      double* train_mse) {
     return fib_codebook((int)d, (int)k, (int)n, seed, (int)training, (int)restarts, (int)iterations, out,
-                        init_mse, train_mse);
+                        init_mse, train_mse, NULL, NULL);
+}
+
+/* The codebook build with its LloydReportV1 (lloyd.rs:165-176): best
+ * restart, repair count and up to `cap` event rows (7 doubles each); returns
+ * the event count through *n_events. */
+int ora_fib_codebook_report(uint32_t d, uint32_t k, uint32_t n, uint64_t seed, uint32_t training,
+                            uint32_t restarts, uint32_t iterations, float* out, double* init_mse,
+                            double* train_mse, uint32_t* best_restart, double* events, uint32_t cap,
+                            uint32_t* n_events) {
+    ora_events ev = {NULL, 0, 0, 0, 0};
+    int rc = fib_codebook((int)d, (int)k, (int)n, seed, (int)training, (int)restarts, (int)iterations, out,
+                          init_mse, train_mse, best_restart, &ev);
+    *n_events = (uint32_t)ev.n;
+    for (int i = 0; i < ev.n && (uint32_t)i < cap; ++i) memcpy(events + 7 * (size_t)i, ev.rows + 7 * (size_t)i, 56);
+    free(ev.rows);
+    return rc;
 }
 
 double ora_inv_norm_cdf(double p) { return inv_norm_cdf(p); }

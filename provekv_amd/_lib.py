@@ -55,7 +55,7 @@ EXPORTS = (
     "pkv_radii_log_bound", "pkv_fb2_n_blocks", "pkv_lloyd_refine", "pkv_blake3_ranges", "pkv_blake3_layer_digests",
     "pkv_blake3_tier_digests", "pkv_blake3",
     "pkv_host_angle_bins", "pkv_host_octant_bins", "pkv_host_logf",
-    "pkv_host_expf",
+    "pkv_host_expf", "pkv_code_from_json", "pkv_fib_digests", "pkv_host_blake3",
 )
 
 
@@ -68,6 +68,31 @@ class Seg(C.Structure):
         ("n_vectors", C.c_uint32),
         ("group", C.c_uint32),
     ]
+
+
+class CodecParams(C.Structure):
+    """pkv_codec_params: a codec profile by its adapter parameters."""
+    _fields_ = [
+        ("kind", C.c_int32),
+        ("dim", C.c_uint32),
+        ("bits", C.c_uint32),
+        ("projections", C.c_uint32),
+        ("k", C.c_uint32),
+        ("n", C.c_uint32),
+        ("training_samples", C.c_uint32),
+        ("lloyd_restarts", C.c_uint32),
+        ("lloyd_iterations", C.c_uint32),
+        ("seed", C.c_uint64),
+    ]
+
+
+def turbo_params(dim: int, bits: int, projections: int, seed: int) -> CodecParams:
+    return CodecParams(CODEC_TURBO, dim, bits, projections, 0, 0, 0, 0, 0, seed)
+
+
+def fib_params(dim: int, k: int, n: int, seed: int, training: int = 2048, restarts: int = 4,
+               iterations: int = 8) -> CodecParams:
+    return CodecParams(CODEC_FIB, dim, 0, 0, k, n, training, restarts, iterations, seed)
 
 
 class Error(C.Structure):
@@ -155,6 +180,9 @@ def _declare(L):
         "pkv_host_octant_bins": ([P, P, U64, P, P], None),
         "pkv_host_logf": ([P, U64, P], None),
         "pkv_host_expf": ([P, U64, P], None),
+        "pkv_code_from_json": ([P, P, U64, P, U64, P, P], I32),
+        "pkv_fib_digests": ([P, P, P, P], I32),
+        "pkv_host_blake3": ([P, U64, P], None),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -172,3 +200,27 @@ def status_string(status: int) -> str:
 def check(rc: int, where: str):
     if rc != OK:
         raise PkvError(rc, where)
+
+
+def code_from_json(params: CodecParams, text: bytes):
+    """pkv_code_from_json: (status, stage, payload bytes) of a JSON code."""
+    buf = C.create_string_buffer(bytes(text), max(len(text), 1))
+    out = C.create_string_buffer(4096)
+    n = C.c_uint64()
+    stage = C.c_int()
+    rc = lib().pkv_code_from_json(C.byref(params), buf, len(text), out, 4096, C.byref(n), C.byref(stage))
+    return rc, stage.value, out.raw[:n.value] if rc == OK else b""
+
+
+def fib_digests(params: CodecParams):
+    """pkv_fib_digests: (profile, codebook, rotation) digest strings."""
+    bufs = [C.create_string_buffer(72) for _ in range(3)]
+    check(lib().pkv_fib_digests(C.byref(params), bufs[0], bufs[1], bufs[2]), "pkv_fib_digests")
+    return tuple(b.value.decode() for b in bufs)
+
+
+def host_blake3(data: bytes) -> bytes:
+    out = C.create_string_buffer(32)
+    buf = C.create_string_buffer(bytes(data), max(len(data), 1))
+    lib().pkv_host_blake3(buf, len(data), out)
+    return out.raw

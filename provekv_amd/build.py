@@ -13,7 +13,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libpkv_hip.so")
-SOURCES = ["pkv_kernels.hip", "pkv_records.hip", "pkv_blake3.hip", "pkv_lloyd.hip", "pkv_capi.cpp", "pkv_profile.cpp"]
+SOURCES = ["pkv_kernels.hip", "pkv_records.hip", "pkv_blake3.hip", "pkv_lloyd.hip", "pkv_capi.cpp", "pkv_profile.cpp",
+           "pkv_json.cpp"]
 
 FLAGS = [
     "--offload-arch=gfx950",

@@ -7,7 +7,8 @@ inherent batch methods ``encode_batch_compact`` / ``decode_batch_compact``
 argument meaning and error classes; the work runs in libpkv_hip.so through
 ``pkv_encode_batch_compact`` / ``pkv_decode_batch_compact`` (batched TQB1 /
 FB2 blobs) and ``pkv_encode_vectors`` / ``pkv_decode_vectors`` (the trait's
-per-vector TQW1 / FB1 records).
+per-vector TQW1 / FB1 records, and the serde_json codes older proveKV
+versions stored, which the adapters still decode).
 """
 from __future__ import annotations
 
@@ -175,16 +176,15 @@ class TurboQuantAdapter(KVecCodec):
         return self.decode_batch([payload], seed)[0]
 
     def decode_batch(self, payloads, seed: int) -> np.ndarray:
+        """A TQW1 record, or else the serde_json TurboCode an older proveKV
+        stored (codec.rs:367-405), per payload; the first failing payload
+        raises."""
         payloads = [bytes(p) for p in payloads]
-        for i, p in enumerate(payloads):   # not TQW1 -> the reference tries its JSON envelope
-            if p[:4] != b"TQW1":
-                raise DecompressionFailed(f"turbo code deserialize failed: payload {i} is not a TQW1 record "
-                                          "(JSON-serialised codes are not supported)")
         prof = self._profile(seed, "decode")
         try:
             return prof.decode_vectors(payloads, each=True)
         except L.PkvError as e:
-            raise _wrap(e, DecompressionFailed, "turbo wire decode failed")
+            raise _wrap(e, DecompressionFailed, "turbo decode failed")
 
 
 class FibQuantAdapter(KVecCodec):
@@ -228,6 +228,8 @@ class FibQuantAdapter(KVecCodec):
             raise _wrap(e, CompressionFailed, "fib encode_batch failed")
 
     def decode_batch_compact(self, payload: bytes, seed: int) -> np.ndarray:
+        """An FB2 blob; else one FB1 record; else one serde_json FibCodeV1
+        (codec.rs:530-569), each through decode_batch_fast."""
         prof = self.build_quantizer(seed)
         try:
             return prof.decode_batch_compact(payload)
@@ -252,24 +254,19 @@ class FibQuantAdapter(KVecCodec):
         except L.PkvError as e:
             raise _wrap(e, CompressionFailed, "fib encode_batch failed")
 
-    def _check_magic(self, payloads):
-        for i, p in enumerate(payloads):   # not FB1 -> the reference tries its JSON envelope
-            if p[:3] != b"FB1":
-                raise DecompressionFailed(f"fib code deserialize failed: payload {i} is not an FB1 record "
-                                          "(JSON-serialised codes are not supported)")
-
     def decode(self, payload: bytes, seed: int) -> np.ndarray:
-        payload = bytes(payload)
-        self._check_magic([payload])
+        """An FB1 record, or else the serde_json FibCodeV1 an older proveKV
+        stored (codec.rs:612-637), through FibQuantizer::decode."""
         prof = self.build_quantizer(seed)
         try:
-            return prof.decode_vectors([payload], each=True)[0]
+            return prof.decode_vectors([bytes(payload)], each=True)[0]
         except L.PkvError as e:
             raise _wrap(e, DecompressionFailed, "fib decode failed")
 
     def decode_batch(self, payloads, seed: int) -> np.ndarray:
+        """Every payload parsed first (FB1 or JSON), then decode_batch_fast
+        (codec.rs:639-665)."""
         payloads = [bytes(p) for p in payloads]
-        self._check_magic(payloads)
         prof = self.build_quantizer(seed)
         try:
             return prof.decode_vectors(payloads, each=False)

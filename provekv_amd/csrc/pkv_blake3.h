@@ -7,6 +7,8 @@
 // 32-bit words, 7 rounds of the column-then-diagonal G mix, the message
 // re-indexed between rounds by a fixed permutation.  Only the unkeyed hash
 // with a 32-byte output is used, so only the first 8 output words are formed.
+// The compression is host and device code: the host hashes the small JSON
+// texts behind the fib profile / codebook / rotation digests with it.
 #pragma once
 #include <stdint.h>
 
@@ -45,9 +47,9 @@ constexpr Schedule make_schedule() {
 }
 constexpr Schedule SCHED = make_schedule();
 
-__device__ __forceinline__ uint32_t rotr(uint32_t w, uint32_t c) { return (w >> c) | (w << (32u - c)); }
+__host__ __device__ __forceinline__ uint32_t rotr(uint32_t w, uint32_t c) { return (w >> c) | (w << (32u - c)); }
 
-__device__ __forceinline__ void g(uint32_t& a, uint32_t& b, uint32_t& c, uint32_t& d, uint32_t mx, uint32_t my) {
+__host__ __device__ __forceinline__ void g(uint32_t& a, uint32_t& b, uint32_t& c, uint32_t& d, uint32_t mx, uint32_t my) {
     a = a + b + mx;
     d = rotr(d ^ a, 16);
     c = c + d;
@@ -59,7 +61,7 @@ __device__ __forceinline__ void g(uint32_t& a, uint32_t& b, uint32_t& c, uint32_
 }
 
 // cv <- first 8 words of compress(cv, m, counter, block_len, flags).
-__device__ __forceinline__ void compress(uint32_t cv[8], const uint32_t m[16], uint64_t counter, uint32_t block_len,
+__host__ __device__ __forceinline__ void compress(uint32_t cv[8], const uint32_t m[16], uint64_t counter, uint32_t block_len,
                                          uint32_t flags) {
     uint32_t v0 = cv[0], v1 = cv[1], v2 = cv[2], v3 = cv[3], v4 = cv[4], v5 = cv[5], v6 = cv[6], v7 = cv[7];
     uint32_t v8 = PKV_B3_IV0, v9 = PKV_B3_IV1, v10 = PKV_B3_IV2, v11 = PKV_B3_IV3;
@@ -92,13 +94,13 @@ __device__ __forceinline__ void compress(uint32_t cv[8], const uint32_t m[16], u
     cv[7] = v7 ^ v15;
 }
 
-__device__ __forceinline__ void set_iv(uint32_t cv[8]) {
+__host__ __device__ __forceinline__ void set_iv(uint32_t cv[8]) {
     cv[0] = PKV_B3_IV0; cv[1] = PKV_B3_IV1; cv[2] = PKV_B3_IV2; cv[3] = PKV_B3_IV3;
     cv[4] = PKV_B3_IV4; cv[5] = PKV_B3_IV5; cv[6] = PKV_B3_IV6; cv[7] = PKV_B3_IV7;
 }
 
 // Parent node: key = IV, message = left cv || right cv, counter 0, 64 bytes.
-__device__ __forceinline__ void parent(uint32_t l[8], const uint32_t r[8], uint32_t extra_flags) {
+__host__ __device__ __forceinline__ void parent(uint32_t l[8], const uint32_t r[8], uint32_t extra_flags) {
     uint32_t m[16];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {

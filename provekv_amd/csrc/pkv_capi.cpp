@@ -101,6 +101,11 @@ struct pkv_profile {
     pkv_ctx* ctx = nullptr;
     int kind = 0;
     uint32_t dim = 0;
+    // the adapter parameters the profile was built from (the JSON codes'
+    // checks need them); json_ok = 0 when unknown (fib with caller
+    // constants) or when the adapter's bits - 1 angle width does not apply
+    pkv_codec_params params{};
+    int json_ok = 0;
     // turbo
     uint32_t bits = 0, pbits = 0, proj = 0, mode = 0;
     uint64_t seed = 0;
@@ -802,6 +807,12 @@ static int turbo_profile_common(pkv_ctx* ctx, uint32_t dim, uint32_t bits, uint3
     p->proj = proj;   // written to TQB1 bytes 18..21 in every mode (wire.rs:311, 343)
     p->mode = static_cast<uint32_t>(mode);
     p->seed = seed;
+    p->params.kind = PKV_CODEC_TURBO;
+    p->params.dim = dim;
+    p->params.bits = bits;
+    p->params.projections = proj;
+    p->params.seed = seed;
+    p->json_ok = mode == PKV_TURBO_POLAR_WITH_QJL;   // TurboQuantAdapter::decode: PolarQuantizer(bits - 1)
     const uint32_t qrows = mode == PKV_TURBO_POLAR_WITH_QJL ? proj : 0;
     if (signs) {
         p->signs.assign(signs, signs + dim);
@@ -1100,7 +1111,19 @@ int pkv_fib_profile_create(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, u
     if (rc) return rc;
     rc = make_fib_rotation(dim, seed, rot);
     if (rc) return rc;
-    return fib_profile_common(ctx, dim, k, n, std::move(cb), std::move(rot), out);
+    rc = fib_profile_common(ctx, dim, k, n, std::move(cb), std::move(rot), out);
+    if (rc) return rc;
+    pkv_codec_params& pp = (*out)->params;
+    pp.kind = PKV_CODEC_FIB;
+    pp.dim = dim;
+    pp.k = k;
+    pp.n = n;
+    pp.seed = seed;
+    pp.training_samples = training_samples;
+    pp.lloyd_restarts = lloyd_restarts;
+    pp.lloyd_iterations = lloyd_iterations;
+    (*out)->json_ok = 1;
+    return PKV_OK;
 }
 
 int pkv_fib_profile_create_with_constants(pkv_ctx* ctx, uint32_t dim, uint32_t k, uint32_t n, const float* codebook,
@@ -1559,6 +1582,15 @@ int pkv_decode_batch_compact(pkv_ctx* ctx, const pkv_profile* prof, const uint8_
                              uint64_t out_cap_vectors, uint64_t* n_out, pkv_error* err) {
     if (err) { err->status = PKV_OK; err->segment = -1; err->index = 0; }
     if (!ctx || !prof || !payload) return PKV_ERR_INVALID_ARG;
+    if (prof->kind == PKV_CODEC_FIB && !(len >= 3 && std::memcmp(payload, "FB2", 3) == 0)) {
+        // FibQuantAdapter::decode_batch_compact's fallback (codec.rs:542-561):
+        // the payload is one FB1 record, or else one JSON FibCodeV1, and
+        // decode_batch_fast decodes it
+        if (n_out) *n_out = 1;
+        if (!out || out_cap_vectors < 1) return PKV_ERR_CAPACITY;
+        const uint64_t off[2] = {0, len};
+        return pkv_decode_vectors(ctx, prof, 0, payload, off, 1, out, out_cap_vectors, err);
+    }
     uint64_t n = 0;
     int radii = 0;
     int rc = pkv_parse_header(prof, payload, len, &n, &radii);
@@ -1875,11 +1907,57 @@ int pkv_decode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const ui
     if (!out || out_cap_vectors < n) return PKV_ERR_CAPACITY;
     const uint32_t plen = record_plen(prof), rh = record_hdr_len(prof), hdr = hdr_len(prof);
     const uint32_t rec_len = rh + plen;
-    bool packed = offsets[0] == 0;   // record i at i * rec_len: every valid batch
-    for (uint64_t i = 0; i < n; ++i) {
+    for (uint64_t i = 0; i < n; ++i)
         if (offsets[i + 1] < offsets[i]) return PKV_ERR_INVALID_ARG;
-        packed = packed && offsets[i + 1] - offsets[i] == rec_len;
+    // The adapters' JSON fallback: a payload without the record magic is a
+    // serde_json TurboCode / FibCodeV1 (proveKV/src/codec.rs:386-393, 552-561,
+    // 622-630, 650-658).  Each one is parsed and checked here, on the host,
+    // and stands in the batch as the record of the same code (a failed one as
+    // a valid placeholder, its failure kept by index: a deserialize failure
+    // at the parse stage, a code that does not fit the profile at the decode
+    // stage), so the kernels below decode every payload alike.
+    const bool fib = prof->kind == PKV_CODEC_FIB;
+    const char* magic = fib ? "FB1" : "TQW1";
+    const size_t mlen = fib ? 3 : 4;
+    std::vector<uint8_t> conv;          // the batch with JSON payloads replaced
+    std::vector<uint64_t> conv_off;
+    uint32_t json_parse = STATUS_NONE, json_code = STATUS_NONE;
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint64_t len_i = offsets[i + 1] - offsets[i];
+        const bool json = !(len_i >= mlen && std::memcmp(records + offsets[i], magic, mlen) == 0);
+        if (json && conv_off.empty()) {
+            if (!prof->json_ok) return PKV_ERR_UNSUPPORTED;
+            conv.assign(records + offsets[0], records + offsets[i]);
+            conv_off.assign(offsets, offsets + i + 1);
+            for (uint64_t& o : conv_off) o -= offsets[0];
+        }
+        if (conv_off.empty()) continue;
+        if (!json) {
+            conv.insert(conv.end(), records + offsets[i], records + offsets[i + 1]);
+        } else {
+            std::vector<uint8_t> pay;
+            int stage = 0;
+            const int jrc = code_from_json(prof->params, records + offsets[i], len_i, &pay, &stage);
+            if (jrc && stage == 0) return jrc;   // not a payload fault (parameters, device)
+            const HdrBytes hb = record_header(prof);
+            const uint8_t* hbytes = reinterpret_cast<const uint8_t*>(hb.w);
+            conv.insert(conv.end(), hbytes, hbytes + rh);
+            if (jrc) {
+                pay.assign(plen, 0);
+                if (fib) { pay[0] = 0x00; pay[1] = 0x3C; }   // fp16 1.0: a valid placeholder norm
+                uint32_t& slot = stage == 1 ? json_parse : json_code;
+                slot = std::min(slot, static_cast<uint32_t>(i << 4) | KIND_CORRUPT);
+            }
+            conv.insert(conv.end(), pay.begin(), pay.end());
+        }
+        conv_off.push_back(conv.size());
     }
+    if (!conv_off.empty()) {
+        records = conv.data();
+        offsets = conv_off.data();
+    }
+    bool packed = offsets[0] == 0;   // record i at i * rec_len: every valid batch
+    for (uint64_t i = 0; i < n; ++i) packed = packed && offsets[i + 1] - offsets[i] == rec_len;
     const uint64_t total = offsets[n];
     const uint64_t blob = hdr + n * static_cast<uint64_t>(plen);
     const uint64_t out_bytes = n * prof->dim * sizeof(float);
@@ -1897,7 +1975,6 @@ int pkv_decode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const ui
     hipStream_t st = ctx->own_stream;
     if (total) HIP_TRY(hipMemcpyAsync(base + o_rec, records, total, hipMemcpyHostToDevice, st));
     HIP_TRY(hipMemcpyAsync(base + o_off, offsets, 8 * (n + 1), hipMemcpyHostToDevice, st));
-    const bool fib = prof->kind == PKV_CODEC_FIB;
     int e = launch_fill_u32(d_stat, STATUS_NONE, 4, st);
     if (!e)
         e = launch_records_check(d_rec, d_off, n, rec_len, rh, fib ? 1u : 0u, packed, record_header(prof), d_stat + 2,
@@ -1921,6 +1998,8 @@ int pkv_decode_vectors(pkv_ctx* ctx, const pkv_profile* prof, int each, const ui
     }
     // FibQuantAdapter::decode_batch parses every record before decoding any
     // (codec.rs:639-665); per-record decoding stops at the first failure.
+    hs[2] = std::min(hs[2], json_parse);
+    hs[3] = std::min(hs[3], json_code);
     uint32_t pick = std::min(std::min(hs[0], hs[1]), hs[3]);
     if (fib && !each && hs[2] != STATUS_NONE) pick = hs[2];
     else pick = std::min(pick, hs[2]);

@@ -128,7 +128,30 @@ int make_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint3
                       uint32_t restarts, uint32_t iterations, std::vector<float>& codebook,
                       double* init_mse, double* train_mse,
                       const LloydDevice* dev = nullptr);
+// LloydReportV1 and LloydRepairEventV1 (fib-quant/src/lloyd.rs:17-59): the
+// refinement receipt FibCodebookV1's digest covers.
+struct LloydRepairEvent {
+    uint32_t restart, iteration, empty_cell, donor_cell, donor_count_before;
+    double donor_distortion, residual_norm;   // split_epsilon is the constant 1e-6
+};
+struct LloydReport {
+    uint32_t restarts = 0, iterations = 0, training_samples = 0;
+    double init_mse = 0.0, best_mse = 0.0;
+    uint32_t best_restart = 0, repairs = 0;
+    std::vector<LloydRepairEvent> events;
+    uint64_t seed = 0;
+};
+// The codebook build of make_fib_codebook run on the host with its report
+// (not memoised; same codewords).
+int fib_codebook_report(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint32_t training, uint32_t restarts,
+                        uint32_t iterations, std::vector<float>& codebook, LloydReport& report);
 // The make_* builders above memoise per process (one build per distinct profile).
+// A JSON-serialised TurboCode / FibCodeV1 -> the payload of the equivalent
+// TQW1 / FB1 record (pkv_json.cpp; pkv_code_from_json's contract: stage 1 =
+// does not deserialize, 2 = does not fit the profile, 0 with an error = not
+// a payload fault).
+int code_from_json(const pkv_codec_params& p, const uint8_t* json, uint64_t len, std::vector<uint8_t>* payload,
+                   int* stage);
 void constants_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries);
 void constants_cache_clear();
 

@@ -246,82 +246,85 @@ std::vector<double> stored_rotation(int dim, uint64_t seed) {
 }
 
 // ------------------------------------------------------------ special functions
-// Normal and Beta inverse CDFs to full double accuracy (statrs computes the
-// same quantities; the Lloyd refinement replaces every codeword by a sample
-// mean, so last-bit differences here do not reach the codebook).
-double normal_cdf(double x) { return 0.5 * std::erfc(-x / std::sqrt(2.0)); }
+// Normal and Beta inverse CDFs, solved in x87 long double and rounded once to
+// the nearest double (the exact quantiles statrs approximates; the Lloyd
+// refinement replaces every codeword by a sample mean, so the codebook does
+// not depend on their last bits, but the initial MSE in the codebook's
+// Lloyd report, and so its digest, does).
+long double normal_cdf(long double x) { return 0.5L * std::erfc(-x / std::sqrt(2.0L)); }
 
 double normal_quantile(double p) {
     // Lower half by bisection on erfc plus a Newton polish; the upper half by
     // symmetry (1 - p is exact for p >= 0.5), where erfc keeps full relative
     // accuracy in the tail.
     if (p > 0.5) return -normal_quantile(1.0 - p);
-    double lo = -40.0, hi = 0.0;
-    for (int it = 0; it < 200 && hi - lo > 1e-15 * (1.0 + std::fabs(lo)); ++it) {
-        double mid = 0.5 * (lo + hi);
+    long double lo = -40.0L, hi = 0.0L;
+    for (int it = 0; it < 200 && hi - lo > 1e-18L * (1.0L + std::fabs(lo)); ++it) {
+        long double mid = 0.5L * (lo + hi);
         if (normal_cdf(mid) < p) lo = mid; else hi = mid;
     }
-    double x = 0.5 * (lo + hi);
+    long double x = 0.5L * (lo + hi);
     for (int it = 0; it < 3; ++it) {
-        double pdf = std::exp(-0.5 * x * x) / std::sqrt(2.0 * M_PI);
-        if (!(pdf > 0.0)) break;
-        double nx = x - (normal_cdf(x) - p) / pdf;
-        if (!(std::fabs(nx - x) < 1e-6)) break;
+        long double pdf = std::exp(-0.5L * x * x) / std::sqrt(2.0L * 3.14159265358979323846264338327950288L);
+        if (!(pdf > 0.0L)) break;
+        long double nx = x - (normal_cdf(x) - p) / pdf;
+        if (!(std::fabs(nx - x) < 1e-6L)) break;
         x = nx;
     }
-    return x;
+    return static_cast<double>(x);
 }
 
-double incomplete_beta_cf(double a, double b, double x) {
-    const double tiny = 1e-300;
-    double c = 1.0, d = 1.0 - (a + b) * x / (a + 1.0);
+long double incomplete_beta_cf(long double a, long double b, long double x) {
+    const long double tiny = 1e-300L;
+    long double c = 1.0L, d = 1.0L - (a + b) * x / (a + 1.0L);
     if (std::fabs(d) < tiny) d = tiny;
-    d = 1.0 / d;
-    double h = d;
+    d = 1.0L / d;
+    long double h = d;
     for (int m = 1; m <= 20000; ++m) {
-        double m2 = 2.0 * m;
-        double num = m * (b - m) * x / ((a - 1.0 + m2) * (a + m2));
-        d = 1.0 + num * d; if (std::fabs(d) < tiny) d = tiny;
-        c = 1.0 + num / c; if (std::fabs(c) < tiny) c = tiny;
-        d = 1.0 / d; h *= d * c;
-        num = -(a + m) * (a + b + m) * x / ((a + m2) * (a + 1.0 + m2));
-        d = 1.0 + num * d; if (std::fabs(d) < tiny) d = tiny;
-        c = 1.0 + num / c; if (std::fabs(c) < tiny) c = tiny;
-        d = 1.0 / d;
-        double del = d * c;
+        long double m2 = 2.0L * m;
+        long double num = m * (b - m) * x / ((a - 1.0L + m2) * (a + m2));
+        d = 1.0L + num * d; if (std::fabs(d) < tiny) d = tiny;
+        c = 1.0L + num / c; if (std::fabs(c) < tiny) c = tiny;
+        d = 1.0L / d; h *= d * c;
+        num = -(a + m) * (a + b + m) * x / ((a + m2) * (a + 1.0L + m2));
+        d = 1.0L + num * d; if (std::fabs(d) < tiny) d = tiny;
+        c = 1.0L + num / c; if (std::fabs(c) < tiny) c = tiny;
+        d = 1.0L / d;
+        long double del = d * c;
         h *= del;
-        if (std::fabs(del - 1.0) < 1e-17) break;
+        if (std::fabs(del - 1.0L) < 1e-20L) break;
     }
     return h;
 }
 
-double beta_cdf(double a, double b, double x) {
-    if (x <= 0.0) return 0.0;
-    if (x >= 1.0) return 1.0;
-    double lbt = std::lgamma(a + b) - std::lgamma(a) - std::lgamma(b) + a * std::log(x) + b * std::log1p(-x);
-    double bt = std::exp(lbt);
-    if (x < (a + 1.0) / (a + b + 2.0)) return bt * incomplete_beta_cf(a, b, x) / a;
-    return 1.0 - bt * incomplete_beta_cf(b, a, 1.0 - x) / b;
+long double beta_cdf(long double a, long double b, long double x) {
+    if (x <= 0.0L) return 0.0L;
+    if (x >= 1.0L) return 1.0L;
+    long double lbt = std::lgamma(a + b) - std::lgamma(a) - std::lgamma(b) + a * std::log(x) + b * std::log1p(-x);
+    long double bt = std::exp(lbt);
+    if (x < (a + 1.0L) / (a + b + 2.0L)) return bt * incomplete_beta_cf(a, b, x) / a;
+    return 1.0L - bt * incomplete_beta_cf(b, a, 1.0L - x) / b;
 }
 
 double beta_quantile(double q, double a, double b) {
     if (q <= 0.0) return 0.0;
     if (q >= 1.0) return 1.0;
-    double lo = 0.0, hi = 1.0;
-    for (int it = 0; it < 64; ++it) {
-        double mid = 0.5 * (lo + hi);
+    long double lo = 0.0L, hi = 1.0L;
+    for (int it = 0; it < 72; ++it) {
+        long double mid = 0.5L * (lo + hi);
         if (beta_cdf(a, b, mid) < q) lo = mid; else hi = mid;
     }
-    double x = 0.5 * (lo + hi);
+    long double x = 0.5L * (lo + hi);
+    const long double la = a, lb = b;
     for (int it = 0; it < 6; ++it) {
-        double pdf = std::exp(std::lgamma(a + b) - std::lgamma(a) - std::lgamma(b) +
-                              (a - 1.0) * std::log(x) + (b - 1.0) * std::log1p(-x));
-        if (!(pdf > 0.0)) break;
-        double nx = x - (beta_cdf(a, b, x) - q) / pdf;
+        long double pdf = std::exp(std::lgamma(la + lb) - std::lgamma(la) - std::lgamma(lb) +
+                                   (la - 1.0L) * std::log(x) + (lb - 1.0L) * std::log1p(-x));
+        if (!(pdf > 0.0L)) break;
+        long double nx = x - (beta_cdf(la, lb, x) - q) / pdf;
         if (!(nx > lo && nx < hi) || nx == x) break;
         x = nx;
     }
-    return x < 0.0 ? 0.0 : (x > 1.0 ? 1.0 : x);
+    return static_cast<double>(x < 0.0L ? 0.0L : (x > 1.0L ? 1.0L : x));
 }
 
 // compiler-rt __powidf2 (f64::powi with a run-time exponent).
@@ -359,7 +362,11 @@ struct Lloyd {
         for (int i = 0; i < ns; ++i) { double bd; nearest(&samples[static_cast<size_t>(i) * k], cb.data(), &bd); sum += bd; }
         return sum / static_cast<double>(ns);
     }
-    bool iterate(std::vector<double>& cb) const {
+    // One assign_samples + update_centroids round (lloyd.rs:215-317); each
+    // empty-cell repair is appended to `events` (when given) as the
+    // reference's RepairRecorder does.
+    bool iterate(std::vector<double>& cb, std::vector<LloydRepairEvent>* events = nullptr, uint32_t restart = 0,
+                 uint32_t iteration = 0) const {
         const int ns = static_cast<int>(samples.size()) / k;
         std::vector<double> sums(cb.size(), 0.0), dist(n, 0.0), far(cb.size(), 0.0), fard(n, -1.0);
         std::vector<int> counts(n, 0), asg(ns);
@@ -395,6 +402,9 @@ struct Lloyd {
                 cb[donor * k + t] = cen - 1.0e-6 * dir;
                 cb[e * k + t] = cen + 1.0e-6 * dir;
             }
+            if (events)
+                events->push_back({restart, iteration, static_cast<uint32_t>(e), static_cast<uint32_t>(donor),
+                                   static_cast<uint32_t>(counts[donor]), dist[donor], rn});
             counts[donor] -= 1;
             counts[e] = 1;
             dist[donor] = 0.0;
@@ -430,7 +440,8 @@ int build_fib_rotation(uint32_t dim, uint64_t seed, std::vector<double>& rot) {
 
 int build_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint32_t training,
                        uint32_t restarts, uint32_t iterations, std::vector<float>& codebook,
-                       double* init_mse, double* train_mse, const LloydDevice* dev) {
+                       double* init_mse, double* train_mse, const LloydDevice* dev,
+                       LloydReport* report = nullptr) {
     if (k < 4 || k > 32 || dim % k != 0 || n < 2 || dim <= k) return PKV_ERR_UNSUPPORTED;
     const uint64_t cseed = seed + 0x9e3779b97f4a7c15ull;
     const int K = static_cast<int>(k), N = static_cast<int>(n), D = static_cast<int>(dim);
@@ -503,9 +514,12 @@ int build_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint
     }
     // the restarts' refined codebooks and MSEs: on the device when one is
     // given (and the shape fits its kernel), else here
+    // given (and the shape fits its kernel), else here; the repair events of
+    // a report are recorded by the host iterations only
     std::vector<double> refined, mses(nr);
+    std::vector<LloydRepairEvent> events;
     double imse;
-    if (dev && N <= static_cast<int>(LLOYD_MAX_N) && K <= static_cast<int>(LLOYD_MAX_K) &&
+    if (dev && !report && N <= static_cast<int>(LLOYD_MAX_N) && K <= static_cast<int>(LLOYD_MAX_K) &&
         nk <= LLOYD_MAX_NK) {
         int rc = dev->refine(samples, static_cast<uint32_t>(ns), k, n, starts, nr, iterations, refined, mses, &imse);
         if (rc) return rc;
@@ -516,27 +530,41 @@ int build_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint
         for (uint32_t rs = 0; rs < nr; ++rs) {
             std::vector<double> cb(starts.begin() + rs * nk, starts.begin() + (rs + 1) * nk);
             for (uint32_t it = 0; it < iterations; ++it)
-                if (!lloyd.iterate(cb)) return PKV_ERR_INVALID_ARG;
+                if (!lloyd.iterate(cb, report ? &events : nullptr, rs, it)) return PKV_ERR_INVALID_ARG;
             mses[rs] = lloyd.mse(cb);
             std::copy(cb.begin(), cb.end(), refined.begin() + rs * nk);
         }
     }
     // refine_codebook's choice (lloyd.rs:148-163): a restart replaces the best
     // so far only when strictly better; none better than the start keeps it
+    // (best_restart u32::MAX)
     double best_mse = imse;
+    uint32_t best_restart = 0;
     std::vector<double> best = init;
     for (uint32_t rs = 0; rs < nr; ++rs) {
         const double m = mses[rs];
         if (m < best_mse || (rs == 0 && std::isinf(imse))) {
             best_mse = m;
+            best_restart = rs;
             best.assign(refined.begin() + rs * nk, refined.begin() + (rs + 1) * nk);
         }
     }
-    if (best_mse > imse) { best = init; best_mse = imse; }
+    if (best_mse > imse) { best = init; best_mse = imse; best_restart = 0xFFFFFFFFu; }
     codebook.resize(best.size());
     for (size_t t = 0; t < best.size(); ++t) codebook[t] = static_cast<float>(best[t]);
     if (init_mse) *init_mse = imse;
     if (train_mse) *train_mse = best_mse;
+    if (report) {   // LloydReportV1 (lloyd.rs:165-176)
+        report->restarts = nr;
+        report->iterations = iterations;
+        report->training_samples = static_cast<uint32_t>(ns);
+        report->init_mse = imse;
+        report->best_mse = best_mse;
+        report->best_restart = best_restart;
+        report->repairs = static_cast<uint32_t>(std::min<size_t>(events.size(), 0xFFFFFFFFu));
+        report->events = std::move(events);
+        report->seed = cseed;
+    }
     return PKV_OK;
 }
 
@@ -630,6 +658,12 @@ int make_fib_codebook(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint3
     if (init_mse) *init_mse = f->init_mse;
     if (train_mse) *train_mse = f->train_mse;
     return PKV_OK;
+}
+
+int fib_codebook_report(uint32_t dim, uint32_t k, uint32_t n, uint64_t seed, uint32_t training, uint32_t restarts,
+                        uint32_t iterations, std::vector<float>& codebook, LloydReport& report) {
+    return build_fib_codebook(dim, k, n, seed, training, restarts, iterations, codebook, nullptr, nullptr, nullptr,
+                              &report);
 }
 
 void constants_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries) {

@@ -438,12 +438,14 @@ class Profile:
         return out[: out_len.value].tobytes()
 
     def decode_batch_compact(self, payload: bytes) -> np.ndarray:
-        buf = np.frombuffer(payload, dtype=np.uint8)
-        n = C.c_uint64()
+        buf = np.frombuffer(bytes(payload) or b"\0", dtype=np.uint8)
+        n = C.c_uint64(1)
         radii = C.c_int()
-        rc = L.lib().pkv_parse_header(self._ptr, buf.ctypes.data, len(payload), C.byref(n), C.byref(radii))
-        if rc:
-            raise L.PkvError(rc, "decode_batch_compact")
+        # a fib payload without the FB2 magic is one FB1 record or one JSON code
+        if self.kind != L.CODEC_FIB or payload[:3] == b"FB2":
+            rc = L.lib().pkv_parse_header(self._ptr, buf.ctypes.data, len(payload), C.byref(n), C.byref(radii))
+            if rc:
+                raise L.PkvError(rc, "decode_batch_compact")
         out = np.zeros((max(n.value, 1), self.dim), np.float32)
         n_out = C.c_uint64()
         err = L.Error()
