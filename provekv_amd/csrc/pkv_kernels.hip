@@ -79,6 +79,12 @@ __device__ __forceinline__ uint64_t vec_elem_offset(const SegDev& s, uint64_t i)
     return s.elem_offset + (i / s.group) * s.stride_outer + (i % s.group) * s.stride_inner;
 }
 
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+    const uint32_t lo = static_cast<uint32_t>(__shfl(static_cast<int>(v), src));
+    const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(v >> 32), src));
+    return static_cast<uint64_t>(hi) << 32 | lo;
+}
+
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -1560,16 +1566,26 @@ __global__ __launch_bounds__(TILE) void turbo_decode_kernel(
     stage_rows_out<DIM>(out, lc, stage, seg, v0, nv, skip_lo, skip_hi, lane);
 }
 
-// LDS words per wave of turbo_decode_split_kernel: max(payloads, rows).
-__host__ __device__ constexpr uint32_t turbo_split_wave_words(uint32_t pwd) {
-    return (32 * pwd + 4 > 32 * (64 + 4) + 4) ? 32 * pwd + 4 : 32 * (64 + 4) + 4;
+// LDS words per wave of turbo_decode_split_kernel: two buffers, each the
+// aligned windows of two runs of 16 payloads (the decoded rows are staged
+// over the buffer just consumed, 16 rows at a time).
+__host__ __device__ constexpr uint32_t turbo_split_run_words(uint32_t pwd) { return 16 * pwd + 2; }
+__host__ __device__ constexpr uint32_t turbo_split_buf_words(uint32_t pwd) {
+    return (2 * turbo_split_run_words(pwd) > 16 * (64 + 4)) ? 2 * turbo_split_run_words(pwd) : 16 * (64 + 4);
 }
+__host__ __device__ constexpr uint32_t turbo_split_wave_words(uint32_t pwd) { return 2 * turbo_split_buf_words(pwd); }
 
 // Turbo decode at head_dim 64 (TurboQuantizer::decode, turbo.rs:302-330:
 // the polar part; the QJL words are validated, not used): two lanes per
-// vector as in turbo_encode_qjl_kernel, one 32-vector group per wave, two
-// workgroups per tile.  Each lane rebuilds the 32 elements of its half and
-// stores them straight from registers.
+// vector as in turbo_encode_qjl_kernel, 32 vectors per wave.  A resident grid
+// walks the 128-vector half-tiles, each workgroup a contiguous share, and a
+// wave's payloads for the next half-tile travel to LDS by direct loads
+// (global_load_lds) while it decodes and stores the current one.  Wave w of a
+// half-tile takes the two runs of 16 vectors starting at 64 (w / 2) +
+// 16 (w % 2) and 32 later: when a blob holds 32 heads (vector = token * H +
+// head) those are 16 heads at two consecutive tokens, so each store
+// instruction writes two runs of two adjacent 256 B rows (tokens t, t + 1 of
+// one head).  Any other layout is only another order of the same stores.
 template <int PB>
 __global__ __launch_bounds__(TILE) void turbo_decode_split_kernel(
     LaunchCommon lc, const uint8_t* __restrict__ wire, void* __restrict__ out,
@@ -1577,8 +1593,9 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split_kernel(
     uint32_t proj, uint32_t mode) {
     constexpr int DIM = 64;
     constexpr int HP = 16;
-    extern __shared__ uint32_t smem_u[];   // per wave: 32 payloads
-    __shared__ float cs_lds[512];
+    constexpr int PITCH = DIM + 4;
+    extern __shared__ uint32_t smem_u[];   // per wave: two buffers of turbo_split_buf_words
+    __shared__ float cs_lds[32];           // levels <= 16
     __shared__ uint64_t exp_lds[32];
     __shared__ float div255_lds[256];
 
@@ -1589,103 +1606,175 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split_kernel(
     for (uint32_t t = threadIdx.x; t < 256; t += blockDim.x) div255_lds[t] = c_div255.v[t];
     __syncthreads();
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
     const int h = lane >> 5, n = lane & 31;
-    // half-tiles vb = 2 * tile + half; a grid smaller than the count loops
-    // (a bounded share of the GPU, so another kernel can run beside it)
+    const uint32_t j = static_cast<uint32_t>(n) & 15u, run = static_cast<uint32_t>(n) >> 4;
+    const uint32_t plen = lc.plen, pwd = plen >> 2, winw = turbo_split_run_words(pwd);
+    const uint32_t bufw = turbo_split_buf_words(pwd);
+    uint32_t* wbuf = smem_u + wave * turbo_split_wave_words(pwd);
+    // half-tiles vb = 2 * tile + half, a contiguous share per workgroup (a
+    // grid smaller than the count is a bounded share of the GPU, so another
+    // kernel can run beside it); the next half-tile's segment is the current
+    // one or a later one found by stepping on
     const uint32_t nvb = 2u * lc.tile_start[lc.nseg];
-    for (uint32_t vb = blockIdx.x; vb < nvb; vb += gridDim.x) {
-    wave_sync();   // the previous half-tile's rows are out of LDS
-    const uint32_t blk = vb >> 1;
-    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
-    const SegDev seg = lc.segs[sidx];
-    const uint32_t tile = blk - lc.tile_start[sidx];
-    const uint32_t plen = lc.plen, pwd = plen >> 2;
-    const uint8_t* blob = wire + seg.wire_offset;
+    const uint32_t per = (nvb + gridDim.x - 1) / gridDim.x;
+    const uint32_t vb0 = blockIdx.x * per;
+    if (vb0 >= nvb) return;
+    const uint32_t vb_end = min(nvb, vb0 + per);
+    uint32_t sidx = find_segment(lc.tile_start, lc.nseg, vb0 >> 1);
 
-    // header check (every wave; 38 bytes)
-    const uint32_t hb = lane < 38 ? blob[lane] : 0u;
-    const bool hbad = lane < 38 && tqb1_checked(lane) &&
-                      hb != tqb1_byte(lane, DIM, pbits, lc.radii, proj, seed, seg.n_vectors, plen);
-    if (__ballot(hbad) != 0ull) {
-        if (lane == 0) status_fail(lc.status, sidx, 0, 0u, KIND_HEADER);
-        continue;
-    }
-    const uint32_t t0 = tile * TILE + (vb & 1u) * (TILE / 2) + 32u * static_cast<uint32_t>(wave);
-    if (t0 >= seg.n_vectors) continue;
-    const uint32_t nv = min(32u, seg.n_vectors - t0);
-    // per wave: the 32 payloads, later the 32 decoded rows (pitch DIM + 4)
-    uint32_t* sw = smem_u + wave * turbo_split_wave_words(pwd);
-    global_to_lds(sw, blob + 38 + static_cast<uint64_t>(t0) * plen, nv * plen, lane);
-    wave_sync();
-
-    const bool active = static_cast<uint32_t>(n) < nv;
-    const uint32_t* pw = sw + min(static_cast<uint32_t>(n), nv - 1) * pwd;
-    const bool f32r = lc.radii == PKV_RADII_F32;
-    const uint32_t rwords = f32r ? 32u : 32u / 4 + 2;
-    bool ok = true;
-    float r[HP];
-    if (f32r) {
+    // One half-tile's share of this wave: segment, the two runs, and its
+    // header bytes (lanes 0-37); fetch() also starts the payload copies of
+    // both runs into `dst` (run q's aligned window at dst + q * winw).
+    struct Item {
+        uint32_t sidx, r0, r1, n0, n1;
+        uint32_t hb;
+    };
+    auto fetch = [&](uint32_t vb, uint32_t* dst) -> Item {
+        Item it;
+        const uint32_t blk = vb >> 1;
+        while (sidx + 1 < lc.nseg && lc.tile_start[sidx + 1] <= blk) ++sidx;
+        it.sidx = sidx;
+        const SegDev seg = lc.segs[sidx];
+        const uint32_t tile = blk - lc.tile_start[sidx];
+        it.r0 = tile * TILE + (vb & 1u) * (TILE / 2) + 64u * static_cast<uint32_t>(wave >> 1) +
+                16u * static_cast<uint32_t>(wave & 1);
+        it.r1 = it.r0 + 32u;
+        it.n0 = it.r0 < seg.n_vectors ? min(16u, seg.n_vectors - it.r0) : 0u;
+        it.n1 = it.r1 < seg.n_vectors ? min(16u, seg.n_vectors - it.r1) : 0u;
+        const uint8_t* blob = wire + seg.wire_offset;
+        it.hb = lane < 38 ? blob[lane] : 0u;
+        // the aligned dwords holding each run's payload bytes (the segment's
+        // extent was checked on the host, so they lie in the wire buffer)
 #pragma unroll
-        for (int i = 0; i < HP; ++i) {
-            r[i] = u2f(pw[16 * h + i]);
-            ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);   // radius.rs:88-104
+        for (uint32_t q = 0; q < 2; ++q) {
+            const uint32_t cnt = q ? it.n1 : it.n0;
+            if (!cnt) continue;
+            const uintptr_t a = reinterpret_cast<uintptr_t>(blob + 38 + static_cast<uint64_t>(q ? it.r1 : it.r0) * plen);
+            const uintptr_t a0 = a & ~static_cast<uintptr_t>(3);
+            const uint32_t ndw = static_cast<uint32_t>((((a + cnt * plen + 3u) & ~static_cast<uintptr_t>(3)) - a0) >> 2);
+            for (uint32_t k0 = 0; k0 < ndw; k0 += WAVE)
+                if (k0 + static_cast<uint32_t>(lane) < ndw)
+                    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(a0) + k0 + lane,
+                                                     dst + q * winw + k0, 4, 0, 0);
         }
-    } else {
-        const float mn = u2f(pw[8]), mx = u2f(pw[9]);
-        ok &= isfinite_f(mn) && isfinite_f(mx) && !(mn > mx);   // radius.rs:171-177
-        const float span = mx - mn;
+        return it;
+    };
+
+    Item cur = fetch(vb0, wbuf);
+    uint32_t bsel = 0;
+    for (uint32_t vb = vb0; vb < vb_end; ++vb) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this half-tile's payload copies have landed
+        wave_sync();
+        uint32_t* buf = wbuf + bsel * bufw;
+        const Item it = cur;
+        if (vb + 1 < vb_end) cur = fetch(vb + 1, wbuf + (bsel ^ 1u) * bufw);
+        bsel ^= 1u;
+        const SegDev seg = lc.segs[it.sidx];
+        // header check (every wave; 38 bytes)
+        const bool hbad = lane < 38 && tqb1_checked(lane) &&
+                          it.hb != tqb1_byte(lane, DIM, pbits, lc.radii, proj, seed, seg.n_vectors, plen);
+        if (__ballot(hbad) != 0ull) {
+            if (lane == 0) status_fail(lc.status, it.sidx, 0, 0u, KIND_HEADER);
+            continue;
+        }
+        if (!it.n0) continue;
+        const uint32_t sh = static_cast<uint32_t>((seg.wire_offset + 38u) & 3u);   // payload lengths are whole words
+        const uint32_t cnt = run ? it.n1 : it.n0;
+        const bool active = j < cnt;
+        // lanes past a run's end repeat its last vector (run 1 empty: run 0's first)
+        const uint32_t* win = buf + (cnt ? run : 0u) * winw + (cnt ? min(j, cnt - 1u) : 0u) * pwd;
+        auto pword = [&](uint32_t k) -> uint32_t {
+            return sh ? __builtin_amdgcn_alignbyte(win[k + 1], win[k], sh) : win[k];
+        };
+        const uint32_t vi = (run ? it.r1 : it.r0) + j;
+        // this lane's output row offset, computed once (one division by the
+        // segment's group) and handed to the storing lanes by a shuffle
+        const uint64_t my_off = vec_elem_offset(seg, vi);
+        const bool f32r = lc.radii == PKV_RADII_F32;
+        const uint32_t rwords = f32r ? 32u : 32u / 4 + 2;
+        bool ok = true;
+        float r[HP];
+        if (f32r) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t q = pw[4 * h + k];
+            for (int i = 0; i < HP; ++i) {
+                r[i] = u2f(pword(16 * h + i));
+                ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);   // radius.rs:88-104
+            }
+        } else {
+            const float mn = u2f(pword(8)), mx = u2f(pword(9));
+            ok &= isfinite_f(mn) && isfinite_f(mx) && !(mn > mx);   // radius.rs:171-177
+            const float span = mx - mn;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint32_t u = (q >> (8 * t)) & 0xffu;
-                const int i = 4 * k + t;
-                r[i] = og_expf(mn + span * div255_lds[u], exp_lds);   // radius.rs:128-145
-                ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);             // polar.rs:127-133
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t q = pword(4 * h + k);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t u = (q >> (8 * t)) & 0xffu;
+                    const int i = 4 * k + t;
+                    r[i] = og_expf(mn + span * div255_lds[u], exp_lds);   // radius.rs:128-145
+                    ok &= isfinite_f(r[i]) && !(r[i] < 0.0f);             // polar.rs:127-133
+                }
             }
         }
-    }
-    // this half's 16 angle indices: bits 16 pbits h .. (pbits <= 4: <= 64 bits)
-    const uint32_t bit0 = 16u * pbits * static_cast<uint32_t>(h);
-    const uint32_t* aw = pw + rwords + (bit0 >> 5);
-    const uint32_t sh = bit0 & 31u;
-    const uint64_t lo64 = static_cast<uint64_t>(aw[0]) | static_cast<uint64_t>(aw[1]) << 32;
-    uint64_t pk = lo64 >> sh;
-    if (sh) pk |= static_cast<uint64_t>(aw[2]) << (64 - sh);
-    // the angle field is 32 * pbits bits, a whole number of words: no padding
-    // bits to check (bitpack.rs:88-109); nor in the 32/64-bit QJL field
-    (void)mode;
+        // this half's 16 angle indices: bits 16 pbits h .. (pbits <= 4: <= 64 bits)
+        const uint32_t bit0 = 16u * pbits * static_cast<uint32_t>(h);
+        const uint32_t aw0 = rwords + (bit0 >> 5);
+        const uint32_t ash = bit0 & 31u;
+        const uint64_t lo64 = static_cast<uint64_t>(pword(aw0)) | static_cast<uint64_t>(pword(aw0 + 1)) << 32;
+        uint64_t pk = lo64 >> ash;
+        if (ash) pk |= static_cast<uint64_t>(pword(aw0 + 2)) << (64 - ash);
+        // the angle field is 32 * pbits bits, a whole number of words: no padding
+        // bits to check (bitpack.rs:88-109); nor in the 32/64-bit QJL field
+        (void)mode;
 
-    float y[32];
+        float y[32];
 #pragma unroll
-    for (int i = 0; i < HP; ++i) {
-        const uint32_t bin = static_cast<uint32_t>(pk >> (static_cast<uint32_t>(i) * pbits)) & (levels - 1u);
-        y[2 * i] = r[i] * cs_lds[2 * bin];
-        y[2 * i + 1] = r[i] * cs_lds[2 * bin + 1];
-    }
-    fwht_split(y, h);
-    const float scale = fwht_scale<DIM>();
-    const bool vok = ok && partner(ok ? 1u : 0u, h);
-    if (active && h == 0 && !vok) status_fail(lc.status, sidx, 1, t0 + n, KIND_CORRUPT);
-    // rows through LDS (over the consumed payloads) so they leave coalesced
-    wave_sync();
-    float* stage = reinterpret_cast<float*>(sw);
-    {
-        float* srow = stage + n * (DIM + 4) + 32 * h;
-        const float4* sp = reinterpret_cast<const float4*>(signs + 32 * h);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float4 sg = sp[k];
-            *reinterpret_cast<float4*>(srow + 4 * k) =
-                make_float4((y[4 * k] * scale) * sg.x, (y[4 * k + 1] * scale) * sg.y, (y[4 * k + 2] * scale) * sg.z,
-                            (y[4 * k + 3] * scale) * sg.w);
+        for (int i = 0; i < HP; ++i) {
+            const uint32_t bin = static_cast<uint32_t>(pk >> (static_cast<uint32_t>(i) * pbits)) & (levels - 1u);
+            y[2 * i] = r[i] * cs_lds[2 * bin];
+            y[2 * i + 1] = r[i] * cs_lds[2 * bin + 1];
         }
-    }
-    const uint64_t badm = __ballot(active && h == 0 && !vok);
-    wave_sync();
-    stage_rows_out<DIM>(out, lc, stage, seg, t0, nv, static_cast<uint32_t>(badm), 0u, lane);
+        fwht_split(y, h);
+        const float scale = fwht_scale<DIM>();
+        const bool vok = ok && partner(ok ? 1u : 0u, h);
+        if (active && h == 0 && !vok) status_fail(lc.status, it.sidx, 1, vi, KIND_CORRUPT);
+        // rows to write: the active, good vectors (lane n's vector: run n / 16, j)
+        const uint32_t wmask = static_cast<uint32_t>(__ballot(active && h == 0 && vok));
+        // Rows leave through LDS (staged over the consumed payload buffer), 16
+        // at a time: pass p stages the vectors j = 8p .. 8p + 7 of both runs
+        // (row (j % 8) + 8 run), and store k writes rows 2k, 2k + 8 (one head,
+        // tokens t and t + 1: lanes 0-31) and 2k + 1, 2k + 9 (the next head:
+        // lanes 32-63).
+        float* stage = reinterpret_cast<float*>(buf);
+        const uint32_t sel = static_cast<uint32_t>(lane) >> 4, c = static_cast<uint32_t>(lane) & 15u;
+#pragma unroll
+        for (uint32_t pass = 0; pass < 2; ++pass) {
+            wave_sync();   // payload words / the previous pass's rows are no longer read
+            if ((j >> 3) == pass) {
+                float* srow = stage + ((j & 7u) + 8u * run) * PITCH + 32 * h;
+                const float4* sp = reinterpret_cast<const float4*>(signs + 32 * h);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float4 sg = sp[k];
+                    *reinterpret_cast<float4*>(srow + 4 * k) =
+                        make_float4((y[4 * k] * scale) * sg.x, (y[4 * k + 1] * scale) * sg.y,
+                                    (y[4 * k + 2] * scale) * sg.z, (y[4 * k + 3] * scale) * sg.w);
+                }
+            }
+            wave_sync();
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k) {
+                const uint32_t row = 2u * k + (sel >> 1) + 8u * (sel & 1u);
+                const uint32_t src = 8u * pass + (row & 7u) + 16u * (row >> 3);   // the lane of the row's vector
+                const uint64_t off = shfl_u64(my_off, static_cast<int>(src));
+                if ((wmask >> src) & 1u)   // whole rows per instruction: streaming stores (the L2 stays with
+                                           // the pool encode that runs beside this decode in a rehydrate step)
+                    store_out4<true>(out, lc, off + 4 * c,
+                                     *reinterpret_cast<const float4*>(stage + row * PITCH + 4 * c));
+            }
+        }
     }
 }
 
@@ -2996,8 +3085,10 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
             }
             continue;
         }
-        // vectors (of the 32) to write: active and good
+        // vectors (of the 32) to write: active and good; each lane's row
+        // offset is computed once and handed to the storing lanes by a shuffle
         const uint32_t wmask = static_cast<uint32_t>(__ballot(active && !vbad && h == 0));
+        const uint64_t my_off = vec_elem_offset(seg, min(vi, seg.n_vectors - 1));
         // Fan-out: rows go through LDS, 16 whole rows (8 heads x 2 tokens) per
         // pass, so each store instruction writes 4 whole 256 B rows -- two
         // runs of two adjacent rows -- instead of 32 B into each of 32 rows
@@ -3024,11 +3115,9 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
                 const uint32_t sel = static_cast<uint32_t>(lane) >> 4, c = lane & 15;
                 const uint32_t row = 2u * kk + (sel >> 1) + 8u * (sel & 1u);
                 const uint32_t ln = (row & 7u) + 8u * pass + 16u * (row >> 3);
-                if ((wmask >> ln) & 1u) {
-                    const uint32_t wv = (ln & 15u) + 16u * sub + 32u * (ln >> 4);
-                    store_out4(out, lc, vec_elem_offset(seg, v0 + wv) + 4 * c,
-                               *reinterpret_cast<const float4*>(hs + row * RPITCH + 4 * c));
-                }
+                const uint64_t off = shfl_u64(my_off, static_cast<int>(ln));
+                if ((wmask >> ln) & 1u)
+                    store_out4(out, lc, off + 4 * c, *reinterpret_cast<const float4*>(hs + row * RPITCH + 4 * c));
             }
             wave_sync();   // the next pass overwrites the staging rows
         }
@@ -3229,7 +3318,8 @@ int launch_turbo_decode(const LaunchCommon& lc, const TurboDev& td, const uint8_
     if (td.dim == 64 && td.pbits <= 4) {
         const size_t lds = static_cast<size_t>(WAVES) * turbo_split_wave_words(lc.plen >> 2) * sizeof(uint32_t);
         if (nblocks > (1u << 30)) return hipErrorInvalidValue;   // 2 workgroups per tile
-        const uint32_t grid = lc.grid_cap ? std::min(2 * nblocks, lc.grid_cap) : 2 * nblocks;
+        // a resident grid (four workgroups per CU) walking contiguous shares
+        const uint32_t grid = std::min(2 * nblocks, lc.grid_cap ? lc.grid_cap : 1024u);
         return td.pbits == 3 ? launch_big_lds(turbo_decode_split_kernel<3>, grid, lds, st, lc, wire, out,
                                               td.signs, td.cs, td.seed, td.pbits, td.proj, td.mode)
                              : launch_big_lds(turbo_decode_split_kernel<0>, grid, lds, st, lc, wire, out,
