@@ -188,22 +188,26 @@ bool g_logb_done[kMaxDevices] = {};
 
 // Once per device (the caller has made it current), before the first
 // context there returns: measure the cheap-log bound table of the BlockLogU8
-// encodes, and check that the f16 matrix cores keep subnormal operands (the
-// QJL acceptance bound counts on it; a device that flushes them is refused).
+// encodes, check that the f16 matrix cores keep subnormal operands (the QJL
+// acceptance bound counts on it) and that the encodes' short sqrt fix-up
+// agrees with the correctly rounded sqrt on every input it is used on; a
+// device that fails either check is refused.
 int device_checks_once(int device, hipStream_t st) {
     std::lock_guard<std::mutex> lock(g_logb_mu);
     if (device >= 0 && device < kMaxDevices && g_logb_done[device]) return PKV_OK;
     float* d = nullptr;
-    HIP_TRY(hipMalloc(&d, 2 * sizeof(float)));
-    float got[2] = {0.0f, 0.0f};
+    HIP_TRY(hipMalloc(&d, 4 * sizeof(float)));
+    float got[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     hipError_t e = static_cast<hipError_t>(launch_logf_bound(st));
     if (e == hipSuccess) e = static_cast<hipError_t>(launch_f16_subnormal_probe(d, st));
+    if (e == hipSuccess) e = static_cast<hipError_t>(launch_sqrt_check(reinterpret_cast<uint32_t*>(d + 2), st));
     if (e == hipSuccess) e = hipMemcpyAsync(got, d, sizeof got, hipMemcpyDeviceToHost, st);
     const hipError_t se = hipStreamSynchronize(st);   // queued work ends before `d` is freed
     if (e == hipSuccess) e = se;
     (void)hipFree(d);
     if (e != hipSuccess) return hip_status(e);
     if (got[0] != 0x1p-10f + 0x1p-14f || got[1] != 0x1p-10f) return PKV_ERR_UNSUPPORTED;
+    if (f2u(got[2]) != 0u) return PKV_ERR_UNSUPPORTED;
     if (device >= 0 && device < kMaxDevices) g_logb_done[device] = true;
     return PKV_OK;
 }
@@ -728,7 +732,8 @@ void pkv_ctx_destroy(pkv_ctx* ctx) {
 // on v_mfma_f32_16x16x32_f16 at head_dim 128, 32 on v_mfma_f32_32x32x16_f16 at
 // head_dim 64), K step s and half (0: Gh, 1: Gl):
 //   qa[((t * 4 + s) * 2 + half) * 64 + lane] (4 words: 8 f16, j = 0..7) =
-//       G[16t + lane % 16][32 (lane / 16) + 8s + j]      (head_dim 128)
+//       G[16t + lane % 16][16 B(lane / 16) + 64 (s / 2) + 8 (s % 2) + j]
+//           (head_dim 128; B = (0, 2, 1, 3): the encode's residual layout)
 //       G[32t + lane % 32][32 (lane / 32) + 8s + j]      (head_dim 64)
 //   qb[((t * nb + r) * 64 + lane) * 2 + {0, 1}] = (a_j, b_j) of the projection
 //       j in accumulator register r: 16t + 4 (lane / 16) + r (128),
@@ -754,10 +759,11 @@ static void turbo_qjl_mfma_constants(pkv_profile* p) {
     for (uint32_t t = 0; t < tiles; ++t)
         for (uint32_t lane = 0; lane < 64; ++lane) {
             const uint32_t row = wide ? 16 * t + lane % 16 : 32 * t + lane % 32;
-            const uint32_t col0 = wide ? 32 * (lane / 16) : 32 * (lane / 32);
+            const uint32_t rq = lane / 16, blk = ((rq & 1) << 1) | (rq >> 1);
             for (uint32_t st = 0; st < 4; ++st)
                 for (uint32_t j = 0; j < 8; ++j) {
-                    const float g = p->qjl[static_cast<size_t>(row) * dim + col0 + 8 * st + j];
+                    const uint32_t col = wide ? 16 * blk + 64 * (st / 2) + 8 * (st % 2) + j : 32 * (lane / 32) + 8 * st + j;
+                    const float g = p->qjl[static_cast<size_t>(row) * dim + col];
                     const uint16_t gh = f32_to_f16(g);
                     const uint16_t gl = f32_to_f16(g - f16_to_f32(gh));   // g - gh is exact in f32
                     const size_t w0 = (((t * 4 + st) * 2 + 0) * 64 + lane) * 4 + j / 2;
@@ -2050,9 +2056,12 @@ void pkv_host_angle_bins(const float* a, const float* b, uint64_t n, uint32_t pb
 
 void pkv_host_octant_bins(const float* a, const float* b, uint64_t n, uint32_t* bins, uint8_t* safe) {
     for (uint64_t i = 0; i < n; ++i) {
-        bool near_line, out_of_range;
-        bins[i] = octant_bin_m2(a[i], b[i], near_line, out_of_range);
-        safe[i] = !near_line && !out_of_range;
+        bool unsafe;
+        bins[i] = octant_bin_f(a[i], b[i], unsafe);
+        // the encode kernels also send a pair whose squares do not sum to a
+        // finite value down the exact path (its lane's radius sum is not finite)
+        const float aa = a[i] * a[i], bb = b[i] * b[i];
+        safe[i] = !unsafe && isfinite_f(aa + bb);
     }
 }
 

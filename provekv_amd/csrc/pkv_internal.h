@@ -176,6 +176,7 @@ int launch_logf_bound(void* stream);
 // 2 floats: matrix-core products with subnormal f16 operands (expected 2^-10 + 2^-14, 2^-10).
 int launch_f16_subnormal_probe(float* out, void* stream);
 int launch_logf_bound_read(float* out, void* stream);
+int launch_sqrt_check(uint32_t* bad, void* stream);
 int launch_fib_product_check(const float* rot32, const float* cb, uint32_t* bad, void* stream);
 
 // Legacy per-vector records (pkv_records.hip).  Records are rec_hdr header

@@ -578,9 +578,10 @@ __device__ __forceinline__ uint32_t partner16(uint32_t x, int q) {
 
 // fwht_normalized stages (turbo-quant/src/rotation.rs:379-398) on a vector
 // split over the two halves of the wave: 32 elements per lane.
+template <int FIRST = 1>
 __device__ __forceinline__ void fwht_split(float (&v)[32], int h) {
 #pragma unroll
-    for (int step = 1; step < 32; step *= 2) {
+    for (int step = FIRST; step < 32; step *= 2) {
 #pragma unroll
         for (int start = 0; start < 32; start += 2 * step) {
 #pragma unroll
@@ -607,8 +608,37 @@ __device__ __forceinline__ void fwht_split(float (&v)[32], int h) {
     }
 }
 
+// The sign flips of the rotation (x_c * s_c, s_c = +-1, exact) fused with
+// the FWHT's first stage (step 1): (x0 s0 + x1 s1, x0 s0 - x1 s1) as two fmas
+// around the exact product x1 s1 -- the same single roundings.
+__device__ __forceinline__ void signs_stage1(float (&v)[32], const float (&sg)[32]) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float t = v[2 * i + 1] * sg[2 * i + 1];
+        const float a = v[2 * i];
+        v[2 * i] = __builtin_fmaf(a, sg[2 * i], t);
+        v[2 * i + 1] = __builtin_fmaf(a, sg[2 * i], -t);
+    }
+}
+
 // The hardware log2 times ln 2 rounded to f32: within g_logb of logf.
 __device__ __forceinline__ float cheap_logf(float v) { return __builtin_amdgcn_logf(v) * 0x1.62e430p-1f; }
+
+// Correctly rounded sqrt of x >= 2^-96, +0, +inf or NaN: the hardware root s
+// (v_sqrt_f32, within 1 ulp) moved to a neighbour s -+ 1 ulp when the exact
+// remainder fma(-s', s, x) shows the root lies past the midpoint -- the
+// fix-up of the compiler's own f32 sqrt expansion, without the rescaling it
+// applies below 2^-96 or the +-0 / +inf select, which this fix-up already
+// gets right (+0: the neighbours' remainders are NaN and -0; +inf: NaN).
+// Below 2^-96 (callers route such inputs to __builtin_sqrtf) the remainder
+// may underflow.
+__device__ __forceinline__ float sqrt_normal(float x) {
+    const float s = __builtin_amdgcn_sqrtf(x);
+    const float sd = u2f(f2u(s) - 1u), su = u2f(f2u(s) + 1u);
+    float r = __builtin_fmaf(-sd, s, x) <= 0.0f ? sd : s;
+    r = __builtin_fmaf(-su, s, x) > 0.0f ? su : r;
+    return r;
+}
 
 // CompressedRadiiV1 BlockLogU8 (turbo-quant/src/radius.rs:58-77) of one
 // vector whose 64 radii sit 16 per lane on LPV = 2 (lanes l, l ^ 32; part =
@@ -631,18 +661,28 @@ __device__ __forceinline__ float cheap_logf(float v) { return __builtin_amdgcn_l
 //   roundf(P_i) = rint(t_i) (t_i >= -M > -1/2 and t_i <= 255 + M; no ties).
 //   The others -- every code when M >= 1/2, and a NaN t_i -- take the
 //   reference's chain.
+// * rint(t_i) comes from v_rndne_f32 and goes into its byte by
+//   v_cvt_pk_u8_f32, exact for the integers 0..255 the decided codes have;
+//   whether any code is undecided is a wave-wide OR of compare masks, and
+//   only then does a lane rebuild its per-code flags.  A lane holding a
+//   radius below FLT_MIN (zero, subnormal) or NaN takes the chain for every
+//   code: there v_i = FLT_MIN (or NaN) differs from the radius the hardware
+//   log sees.
 template <int LPV>
 __device__ __forceinline__ void block_log_u8(const float (&r)[16], int part, const LogfEntry* ltab, uint32_t (&code)[4],
                                              float& mn, float& mx) {
     constexpr float kMinPos = 1.17549435e-38f;
-    float v[16];
-    float vmin = u2f(0x7f800000u), vmax = u2f(0xff800000u);
+    // min / max of v_i = max(r_i, FLT_MIN): the same clamp applied to the
+    // extremes of the radii (NaN radii skipped by fmin / fmax, as before)
+    float rmin = u2f(0x7f800000u), rmax = u2f(0xff800000u);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        v[i] = r[i] < kMinPos ? kMinPos : r[i];
-        vmin = __builtin_fminf(vmin, v[i]);
-        vmax = __builtin_fmaxf(vmax, v[i]);
+        rmin = __builtin_fminf(rmin, r[i]);
+        rmax = __builtin_fmaxf(rmax, r[i]);
     }
+    const bool tiny = rmin < kMinPos;   // NaN radii show up as NaN codes below
+    float vmin = tiny ? kMinPos : rmin;
+    float vmax = rmax < kMinPos && rmax != u2f(0xff800000u) ? kMinPos : rmax;
     if constexpr (LPV == 4) {
         vmin = __builtin_fminf(vmin, u2f(partner16(f2u(vmin), part)));
         vmax = __builtin_fmaxf(vmax, u2f(partner16(f2u(vmax), part)));
@@ -660,29 +700,33 @@ __device__ __forceinline__ void block_log_u8(const float (&r)[16], int part, con
     const float delta = g_logb[f2u(big) >> 23];
     const float margin = delta * inv * (1.0f + 0x1p-10f) + 0x1p-12f;
     const float thr = 0.5f - margin;   // decided when |t - rint(t)| < thr
-    uint32_t slow = 0;
+    uint64_t undecided = __ballot(tiny);
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
         uint32_t packed = 0;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int i = 4 * w + t;
-            const float tv = (cheap_logf(v[i]) - mn) * inv;
-            // for t in (-1/2, 256) the sum lies in [2^23, 2^24), where the f32
-            // grid is the integers: it is 1.5 * 2^23 + rint(t), exactly
-            const float y = tv + 0x1.8p23f;
-            const float k = y - 0x1.8p23f;
-            slow |= (__builtin_fabsf(tv - k) < thr ? 0u : 1u) << i;
-            packed |= (f2u(y) & 0xffu) << (8 * t);
+            const float tv = (cheap_logf(r[i]) - mn) * inv;
+            const float k = __builtin_rintf(tv);
+            undecided |= __ballot(!(__builtin_fabsf(tv - k) < thr));
+            packed = __builtin_amdgcn_cvt_pk_u8_f32(k, static_cast<uint32_t>(t), packed);
         }
         code[w] = packed;
     }
-    if (slow) {
+    if (undecided) {
+        uint32_t slow = tiny ? 0xffffu : 0u;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float tv = (cheap_logf(r[i]) - mn) * inv;
+            slow |= (__builtin_fabsf(tv - __builtin_rintf(tv)) < thr ? 0u : 1u) << i;
+        }
         for (uint32_t m = slow; m; m &= m - 1u) {
             const uint32_t i = static_cast<uint32_t>(__ffs(m) - 1);
-            float vi = v[0];   // v[i] by selects (a dynamic index would go through scratch)
+            float ri = r[0];   // r[i] by selects (a dynamic index would go through scratch)
 #pragma unroll
-            for (int j = 1; j < 16; ++j) vi = static_cast<uint32_t>(j) == i ? v[j] : vi;
+            for (int j = 1; j < 16; ++j) ri = static_cast<uint32_t>(j) == i ? r[j] : ri;
+            const float vi = ri < kMinPos ? kMinPos : ri;
             float nrm = (og_logf_normal(vi, ltab) - mn) / span;
             nrm = nrm < 0.0f ? 0.0f : (nrm > 1.0f ? 1.0f : nrm);
             const uint32_t q = static_cast<uint32_t>(__builtin_roundf(nrm * 255.0f));
@@ -694,8 +738,89 @@ __device__ __forceinline__ void block_log_u8(const float (&r)[16], int part, con
     }
 }
 
+// Radii and angle bins (polar.rs:246-266, 413-421) of a lane's 16 pairs
+// (y[2i], y[2i + 1]): r[i] = sqrt(fl(a^2) + fl(b^2)), the bins pbits apart
+// in pk, rsum the lane's radius sum (its finiteness stands for every radius
+// and input element).  At pbits = 3 a pair octant_bin_f passes takes the
+// octant's bin and sqrt_normal's radius (its fl(a^2) + fl(b^2) >= 2^-94);
+// the other pairs -- near an octant line or outside the covered range, every
+// pair of a lane whose radius sum is not finite, every pair at other widths
+// -- take angle_bin_exact and __builtin_sqrtf.  Every lane of the wave must
+// call it.
+template <int PB>
+__device__ __forceinline__ void radii_bins(const float (&y)[32], uint32_t pbits, int lane, float (&r)[16],
+                                           uint64_t& pk, float& rsum) {
+    constexpr int HP = 16;
+    uint64_t unsafe[HP];   // per pair: the wave's lanes that need the exact formulas
+    rsum = 0.0f;
+    pk = 0;
+    // octant_bin_f's bins, bit by bit: each pair shifts the sign bits of g,
+    // a ^ b and b into a shift register (v_alignbit), ascending bit order,
+    // pairs 0..9 and two bits of pair 10 into w0, the rest into w1; a bit
+    // reversal then puts pair i at bits 3i (g), 3i + 1 (a ^ b), 3i + 2 (b),
+    // and one xor per word turns them into octant_bin_f's (sign(g) ^ sign(a ^
+    // b), sign(a ^ b), !sign(b)).
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int i = 0; i < HP; ++i) {
+        const float a = y[2 * i], b = y[2 * i + 1];
+        const float aa = a * a, bb = b * b;
+        r[i] = sqrt_normal(aa + bb);
+        rsum = rsum + r[i];
+        bool uns = true;
+        if constexpr (PB == 3) {
+            const float fa = __builtin_fabsf(a), fb = __builtin_fabsf(b);
+            const float g = fa - fb;
+            const float mx = __builtin_fmaxf(__builtin_fmaxf(fa, fb), 0x1p-31f);
+            const float m3 = __builtin_fminf(__builtin_fminf(fa, fb), __builtin_fabsf(g));
+            uns = !(mx < m3 * 65536.0f);   // octant_bin_f's test
+            const uint32_t src[3] = {f2u(g), f2u(a) ^ f2u(b), f2u(b)};
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                if (3 * i + k < 32) w0 = __builtin_amdgcn_alignbit(w0, src[k], 31);
+                else w1 = __builtin_amdgcn_alignbit(w1, src[k], 31);
+            }
+        }
+        unsafe[i] = __ballot(uns);
+    }
+    if constexpr (PB == 3) {
+        w0 = __builtin_bitreverse32(w0);
+        w1 = __builtin_bitreverse32(w1) >> 16;
+        w0 ^= ((w0 >> 1) & 0x49249249u) ^ 0x24924924u;   // bits 3i ^= 3i + 1; bits 3i + 2 flipped
+        w1 ^= ((w1 >> 1) & 0x2492u) ^ 0x9249u;           // the same fields, one bit up (pair 10 straddles)
+        pk = (static_cast<uint64_t>(w1) << 32) | w0;
+    }
+    const bool force = !isfinite_f(rsum);
+    uint64_t any_unsafe = __ballot(force);
+#pragma unroll
+    for (int i = 0; i < HP; ++i) any_unsafe |= unsafe[i];
+    if (any_unsafe) {
+        const uint32_t levels = 1u << pbits;
+        uint32_t slow = force ? 0xffffu : 0u;
+#pragma unroll
+        for (int i = 0; i < HP; ++i) slow |= static_cast<uint32_t>((unsafe[i] >> lane) & 1u) << i;
+        for (uint32_t m = slow; m; m &= m - 1u) {
+            const uint32_t i = static_cast<uint32_t>(__ffs(m) - 1);
+            // pair i by selects (a dynamic index into y would go through scratch)
+            float a = y[0], b = y[1];
+#pragma unroll
+            for (int j = 1; j < HP; ++j) {
+                a = static_cast<uint32_t>(j) == i ? y[2 * j] : a;
+                b = static_cast<uint32_t>(j) == i ? y[2 * j + 1] : b;
+            }
+            const uint64_t bin = angle_bin_exact(a, b, pbits);
+            pk = (pk & ~(static_cast<uint64_t>(levels - 1u) << (i * pbits))) | (bin << (i * pbits));
+            const float aa = a * a, bb = b * b;
+            const float ri = __builtin_sqrtf(aa + bb);
+#pragma unroll
+            for (int j = 0; j < HP; ++j) r[j] = static_cast<uint32_t>(j) == i ? ri : r[j];
+        }
+    }
+}
+
 // QJL dots on the f16 matrix cores.  Per vector the residual is scaled by
-// s = 2^k so that max |x| lies in [2^14, 2^15) (x = res * s, exact), and
+// s = 2^k so that an upper bound of |x|_2 lies in [2^14, 2^15) (x = res * s,
+// exact; qjl_scale), and
 // split toward zero into f16 halves, x = xh + xl + ex with |ex| <= 2^-20 |x|
 // + 2^-24; the host splits G = Gh + Gl + eG to nearest, |eG| <= 2^-22 |G| +
 // 2^-25.  The matrix cores form acc = sum_c Gh xh + Gh xl + Gl xh (f16
@@ -719,11 +844,33 @@ __device__ __forceinline__ v4f mfma16x32(const v4u& a, const v4u& b, const v4f& 
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
 }
 
-// 2^(14 - e) for the exponent e of amax (clamped to [-100, 127]).
-__device__ __forceinline__ float qjl_scale(float amax) {
-    int e = static_cast<int>((f2u(amax) >> 23) & 0xffu) - 127;
-    e = e < -100 ? -100 : (e > 127 ? 127 : e);
+// |res| rounded up: rn2 is the f32 sum of the squares (one fma each, then
+// the lanes' partial sums added), within (1 + 35u) rn2 + 2^-144 of the exact
+// one (relative roundings while normal, at most 2^-150 each while subnormal),
+// so |res| <= sqrt(rn2) (1 + 19u) + 2^-72, which 1.0001 and 2^-70 cover.
+__device__ __forceinline__ float qjl_norm_bound(float rn2) {
+    return __builtin_fmaf(__builtin_sqrtf(rn2), 1.0001f, 0x1p-70f);
+}
+
+// 2^(14 - e) for the exponent e of rn >= |res| (clamped to [-60, 127]): every
+// |x_c| = |res_c| 2^(14 - e) <= rn 2^(14 - e) < 2^15, inside the f16 range
+// (and below 2^14 when rn < 2^-60).
+__device__ __forceinline__ float qjl_scale(float rn) {
+    int e = static_cast<int>((f2u(rn) >> 23) & 0xffu) - 127;
+    e = e < -60 ? -60 : (e > 127 ? 127 : e);
     return u2f(static_cast<uint32_t>(127 + 14 - e) << 23);
+}
+
+// a - f32(f16 half `hi` of h), one v_fma_mix_f32 (exact: a's f16 truncation
+// removed from a).
+template <int HI>
+__device__ __forceinline__ float sub_f16(float a, uint32_t h) {
+    float r;
+    if constexpr (HI)
+        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(a));
+    else
+        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(a));
+    return r;
 }
 
 // x = v[c0 + j] * sc, j = 0..7, as f16 halves toward zero: xh = f16(x),
@@ -732,10 +879,9 @@ __device__ __forceinline__ void qjl_split8(const float (&v)[32], int c0, float s
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const float a = v[c0 + 2 * t] * sc, b = v[c0 + 2 * t + 1] * sc;
-        const auto h = __builtin_amdgcn_cvt_pkrtz(a, b);
-        const auto l = __builtin_amdgcn_cvt_pkrtz(a - static_cast<float>(h[0]), b - static_cast<float>(h[1]));
-        xh[t] = __builtin_bit_cast(uint32_t, h);
-        xl[t] = __builtin_bit_cast(uint32_t, l);
+        const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+        xh[t] = h;
+        xl[t] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(sub_f16<0>(a, h), sub_f16<1>(b, h)));
     }
 }
 
@@ -829,10 +975,9 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
         {
             float sg[32];
             lds_half(sg_lds, sg);
-#pragma unroll
-            for (int c = 0; c < 32; ++c) y[c] = y[c] * sg[c];
+            signs_stage1(y, sg);
         }
-        fwht_split(y, h);
+        fwht_split<2>(y, h);
 #pragma unroll
         for (int c = 0; c < 32; ++c) y[c] *= scale;
 
@@ -843,40 +988,9 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
 
         // radii and angle bins (polar.rs:246-266, 413-421) of pairs 16h + i
         float r[HP];
-        float rsum = 0.0f;
-        uint64_t pk = 0;
-        uint64_t unsafe[HP];   // per pair: the wave's lanes whose bin needs the exact formula
-#pragma unroll
-        for (int i = 0; i < HP; ++i) {
-            const float a = y[2 * i], b = y[2 * i + 1];
-            const float aa = a * a, bb = b * b;
-            r[i] = __builtin_sqrtf(aa + bb);
-            rsum = rsum + r[i];
-            bool near_line = false, out_of_range = true;   // other widths: every pair takes the exact formula
-            const uint32_t bin = PB == 3 ? octant_bin_m2(a, b, near_line, out_of_range) : 0u;
-            pk |= static_cast<uint64_t>(bin) << (static_cast<uint32_t>(i) * pbits);
-            unsafe[i] = __ballot(near_line) | __ballot(out_of_range);
-        }
-        uint64_t any_unsafe = 0;
-#pragma unroll
-        for (int i = 0; i < HP; ++i) any_unsafe |= unsafe[i];
-        if (any_unsafe) {   // pairs near an octant line (every pair at other widths): the exact formula
-            uint32_t slow = 0;
-#pragma unroll
-            for (int i = 0; i < HP; ++i) slow |= static_cast<uint32_t>((unsafe[i] >> lane) & 1u) << i;
-            for (uint32_t m = slow; m; m &= m - 1u) {
-                const uint32_t i = static_cast<uint32_t>(__ffs(m) - 1);
-                // pair i by selects (a dynamic index into y would go through scratch)
-                float a = y[0], b = y[1];
-#pragma unroll
-                for (int j = 1; j < HP; ++j) {
-                    a = static_cast<uint32_t>(j) == i ? y[2 * j] : a;
-                    b = static_cast<uint32_t>(j) == i ? y[2 * j + 1] : b;
-                }
-                const uint64_t bin = angle_bin_exact(a, b, pbits);
-                pk = (pk & ~(static_cast<uint64_t>(levels - 1u) << (i * pbits))) | (bin << (i * pbits));
-            }
-        }
+        float rsum;
+        uint64_t pk;
+        radii_bins<PB>(y, pbits, lane, r, pk, rsum);
         // A non-finite input makes every FWHT output, so every radius,
         // non-finite; a finite sum of the (non-negative) radii therefore
         // clears both checks.  Otherwise (or on an overflowing sum) they run
@@ -969,17 +1083,12 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
             for (int c = 0; c < 32; ++c) resfinite &= isfinite_f(y[c]);
         }
         rn2 = rn2 + u2f(partner(f2u(rn2), h));
-        const float rn = __builtin_sqrtf(rn2) * 1.0001f;   // |res|, rounded up far past its f32 error
+        const float rn = qjl_norm_bound(rn2);
 
         // QJL dots on the f16 matrix cores (v_mfma_f32_32x32x16_f16; bound at
         // qjl_scale): K step st covers dimensions 32h + 8st + j of lane (h, n)
-        float amax = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 32; ++c) amax = __builtin_fmaxf(amax, __builtin_fabsf(y[c]));
-        amax = __builtin_fmaxf(amax, u2f(partner(f2u(amax), h)));
-        const float sc = qjl_scale(amax);
+        const float sc = qjl_scale(rn);
         const float xn = rn * sc;
-        uint32_t sbits[2] = {0u, 0u}, unc[2] = {0u, 0u};
         const uint32_t ptiles = proj / 32;
         v16f acc[2] = {};
 #pragma unroll
@@ -996,33 +1105,57 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
                 acc[p] = mfma16(al, xh, acc[p]);
             }
         }
+        // accumulator register k of tile p: projection 32p + 8(k/4) + 4h + k%4
+        // of vector n.  The sign bits shift in (v_alignbit) as negative flags,
+        // register 15 first, so bit k of neg is register k; a dot is undecided
+        // when |acc| <= a_j xn + b_j, collected wave-wide.
+        uint32_t sbits[2] = {0u, 0u};
+        uint64_t undecided = 0;
 #pragma unroll
         for (uint32_t p = 0; p < 2; ++p) {
             if (p >= ptiles) break;
             const float2* ab = reinterpret_cast<const float2*>(qb) + p * 16 * 64 + lane;
-            // accumulator register q: projection 32p + 8(q/4) + 4h + q%4 of vector n
-            uint32_t sb = 0, un = 0;
+            uint32_t neg = 0;
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const uint32_t j = static_cast<uint32_t>(8 * (q >> 2) + 4 * h + (q & 3));
-                const float2 c = ab[q * 64];
+            for (int k = 15; k >= 0; --k) {
+                const float2 c = ab[k * 64];
                 const float bnd = __builtin_fmaf(c.x, xn, c.y);
-                sb |= (acc[p][q] >= 0.0f ? 1u : 0u) << j;
-                un |= (__builtin_fabsf(acc[p][q]) > bnd ? 0u : 1u) << j;
+                undecided |= __ballot(!(__builtin_fabsf(acc[p][k]) > bnd));
+                neg = __builtin_amdgcn_alignbit(neg, f2u(acc[p][k]), 31);
                 if constexpr (DIAG) {
                     if (active) {
+                        const uint32_t j = static_cast<uint32_t>(8 * (k >> 2) + 4 * h + (k & 3));
                         float* dv = lc.diag + (static_cast<uint64_t>(t0 + static_cast<uint32_t>(n)) * proj + 32u * p + j) * 2u;
-                        dv[0] = acc[p][q] / sc;
+                        dv[0] = acc[p][k] / sc;
                         dv[1] = bnd / sc;
                     }
                 }
             }
+            // nibble m of neg -> bits 8m + 4h .. 8m + 4h + 3; a dot >= 0 (or -0,
+            // always undecided) gives bit 1
+            uint32_t sp = (neg | (neg << 8)) & 0x00ff00ffu;
+            sp = (sp | (sp << 4)) & 0x0f0f0f0fu;
+            const uint32_t sb = (sp ^ 0x0f0f0f0fu) << (4 * h);
             sbits[p] = sb | partner(sb, h);
-            unc[p] = un | partner(un, h);
         }
         // undecided signs: the reference's sequential dot, half 0's partial
         // sum continued by half 1
-        if (__ballot(active && (unc[0] | unc[1]) != 0u)) {
+        if (undecided & __ballot(active)) {
+            uint32_t unc[2] = {0u, 0u};
+#pragma unroll
+            for (uint32_t p = 0; p < 2; ++p) {
+                if (p >= ptiles) break;
+                const float2* ab = reinterpret_cast<const float2*>(qb) + p * 16 * 64 + lane;
+                uint32_t un = 0;
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const uint32_t j = static_cast<uint32_t>(8 * (k >> 2) + 4 * h + (k & 3));
+                    const float2 c = ab[k * 64];
+                    const float bnd = __builtin_fmaf(c.x, xn, c.y);
+                    un |= (__builtin_fabsf(acc[p][k]) > bnd ? 0u : 1u) << j;
+                }
+                unc[p] = un | partner(un, h);
+            }
 #pragma unroll
             for (uint32_t p = 0; p < 2; ++p) {
                 if (p >= ptiles) break;
@@ -1053,14 +1186,13 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
         }
 
         // status (per vector, first failure in vector order) and the QJL words
-        const bool fin_v = finite && partner(finite ? 1u : 0u, h);
-        const bool rfin_v = rfinite && partner(rfinite ? 1u : 0u, h);
-        const bool resfin_v = resfinite && partner(resfinite ? 1u : 0u, h);
+        uint32_t bad = (finite ? 0u : 1u) | (rfinite ? 0u : 2u) | (resfinite ? 0u : 4u);
+        bad |= partner(bad, h);
         if (active && h == 0) {
             const uint32_t vi = t0 + n;
-            if (!fin_v) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_INPUT);
-            else if (!rfin_v) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RADIUS);
-            else if (!resfin_v) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RESIDUAL);
+            if (bad & 1u) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_INPUT);
+            else if (bad & 2u) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RADIUS);
+            else if (bad & 4u) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RESIDUAL);
             pv[rwords + bwords] = sbits[0];
             if (proj > 32) pv[rwords + bwords + 1] = sbits[1];
         }
@@ -1089,24 +1221,31 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
     }
 }
 
-// Head_dim 128: four lanes per vector.  Lane (q, n) = (lane / 16, lane % 16)
-// holds elements 32q .. 32q + 31 of vector n of a 16-vector group.  FWHT
-// stages 1..16 run in registers, stage 32 pairs quarters q and q ^ 1 through
-// v_permlane16_swap, stage 64 pairs q and q ^ 2 through v_permlane32_swap
-// (same operands and rounding as fwht_normalized).  The QJL dots come from
+// Head_dim 128: four lanes per vector, lane (q, n) = (lane / 16, lane % 16)
+// of a 16-vector group.  The encode reads elements 32q .. 32q + 31; FWHT
+// stages 1..16 run in registers, stages 32 and 64 on v_permlane16_swap /
+// v_permlane32_swap (same operands and rounding as fwht_normalized), and the
+// transform stops in layout F: lane q holds 16-element blocks q and 4 + q
+// (elements 16q + c in v[c], 64 + 16q + c in v[16 + c]) -- its pairs are
+// 8q .. 8q + 7 and 32 + 8q .. 32 + 8q + 7.  The inverse transform runs on
+// layout F (stages 1..8 in registers, 16, 32 and 64 across lanes) and stops in
+// layout G: lane q holds blocks B(q) and 4 + B(q), B = (0, 2, 1, 3), where the
+// residual and its QJL dots are formed.  The QJL dots come from
 // v_mfma_f32_16x16x32_f16 on the f16 halves of the scaled residual (bound at
 // qjl_scale): lane (q, n) gives the B operand's column n, and K step st
-// covers dimensions 32q + 8st .. 32q + 8st + 7; a 16-projection tile
-// accumulates in 4 registers per lane (projection 16p + 4q + r of vector n in
-// register r).  The undecided dots are recomputed in the reference's order,
-// each quarter continuing the previous quarter's sum.
+// covers its elements y[8st .. 8st + 7] (dimensions 16B(q) + 8st + j for st <
+// 2, 64 + 16B(q) + 8(st - 2) + j after); a 16-projection tile accumulates in
+// 4 registers per lane (projection 16p + 4q + r of vector n in register r).
+// The undecided dots are recomputed in the reference's order, block by block,
+// each block's holder continuing the previous block's sum.
 
 // Value of lane l ^ 16 (the other quarter of the same half).
 // fwht_normalized stages (turbo-quant/src/rotation.rs:379-398) on a 128-wide
 // vector split over four lanes, 32 elements per lane.
+template <int FIRST = 1>
 __device__ __forceinline__ void fwht_quarter(float (&v)[32], int q) {
 #pragma unroll
-    for (int step = 1; step < 32; step *= 2) {
+    for (int step = FIRST; step < 32; step *= 2) {
 #pragma unroll
         for (int start = 0; start < 32; start += 2 * step) {
 #pragma unroll
@@ -1137,6 +1276,74 @@ __device__ __forceinline__ void fwht_quarter(float (&v)[32], int q) {
         p = __builtin_amdgcn_permlane16_swap(p[0], p[1], false, false);
         v[c] = u2f(p[0]);
         v[c + 16] = u2f(p[1]);
+    }
+}
+
+// Stages 2..64 of fwht_normalized on the standard layout (element 32q + c in
+// v[c]; stage 1 already applied), ending in layout F.  Per c: a
+// v_permlane16_swap of v[c], v[c + 16] gives each row the stage-32 pair
+// (lower, upper) of one element -- row q: elements (c, 32 + c) + 16 (q & 1)
+// + 64 (q >> 1) -- and a v_permlane32_swap of the sums and differences the
+// stage-64 pair, (16q + c, 64 + 16q + c) in row q, which stays there.
+__device__ __forceinline__ void fwht128_fwd(float (&v)[32]) {
+#pragma unroll
+    for (int step = 2; step < 32; step *= 2) {
+#pragma unroll
+        for (int start = 0; start < 32; start += 2 * step) {
+#pragma unroll
+            for (int off = 0; off < step; ++off) {
+                const float a = v[start + off], b = v[start + off + step];
+                v[start + off] = a + b;
+                v[start + off + step] = a - b;
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+        auto p = __builtin_amdgcn_permlane16_swap(f2u(v[c]), f2u(v[c + 16]), false, false);
+        float a = u2f(p[0]), b = u2f(p[1]);
+        p = __builtin_amdgcn_permlane32_swap(f2u(a + b), f2u(a - b), false, false);
+        a = u2f(p[0]);
+        b = u2f(p[1]);
+        v[c] = a + b;
+        v[c + 16] = a - b;
+    }
+}
+
+// fwht_normalized on layout F, ending in layout G.  Stages 1..8 pair elements
+// inside a 16-element block (registers); per c the three cross-lane stages:
+// a v_permlane16_swap of v[c], v[c + 16] gives rows 0..3 the stage-16 pairs
+// (c, 16 + c), (64 + c, 80 + c), (32 + c, 48 + c), (96 + c, 112 + c), a
+// v_permlane32_swap of the sums and
+// differences the stage-32 pairs (c, 32 + c), (64 + c, 96 + c), (16 + c,
+// 48 + c), (80 + c, 112 + c), and a v_permlane16_swap of those results the
+// stage-64 pairs (c, 64 + c), (32 + c, 96 + c), (16 + c, 80 + c),
+// (48 + c, 112 + c): blocks B(q) and 4 + B(q), B = (0, 2, 1, 3).
+__device__ __forceinline__ void fwht128_inv(float (&v)[32]) {
+#pragma unroll
+    for (int step = 1; step < 16; step *= 2) {
+#pragma unroll
+        for (int start = 0; start < 32; start += 2 * step) {
+#pragma unroll
+            for (int off = 0; off < step; ++off) {
+                const float a = v[start + off], b = v[start + off + step];
+                v[start + off] = a + b;
+                v[start + off + step] = a - b;
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+        auto p = __builtin_amdgcn_permlane16_swap(f2u(v[c]), f2u(v[c + 16]), false, false);
+        float a = u2f(p[0]), b = u2f(p[1]);
+        p = __builtin_amdgcn_permlane32_swap(f2u(a + b), f2u(a - b), false, false);
+        a = u2f(p[0]);
+        b = u2f(p[1]);
+        p = __builtin_amdgcn_permlane16_swap(f2u(a + b), f2u(a - b), false, false);
+        a = u2f(p[0]);
+        b = u2f(p[1]);
+        v[c] = a + b;
+        v[c + 16] = a - b;
     }
 }
 
@@ -1180,37 +1387,40 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
     const uint32_t rwords = f32r ? 64u : 64u / 4 + 2;          // radii words in the payload
     const uint32_t bwords = (64u * pbits + 31) / 32;            // angle index words
 
-    auto load_signs = [&](float (&sg)[32]) {
-        const float4* sp = reinterpret_cast<const float4*>(signs + 32 * q);
+    // this lane's 32 sign values, elements e0 + c (c < 16) and e1 + c - 16
+    auto load_signs = [&](float (&sg)[32], uint32_t e0, uint32_t e1) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const float4 v = sp[k];
+            const float4 v = reinterpret_cast<const float4*>(signs + (k < 4 ? e0 : e1))[k & 3];
             sg[4 * k] = v.x; sg[4 * k + 1] = v.y; sg[4 * k + 2] = v.z; sg[4 * k + 3] = v.w;
         }
     };
+    // layout G: blocks B(q) and 4 + B(q), B = (0, 2, 1, 3)
+    const uint32_t g0 = 16u * static_cast<uint32_t>(((q & 1) << 1) | (q >> 1)), g1 = 64u + g0;
 
     do {
         const uint32_t t0 = tile * TILE + (blockIdx.x & 3u) * (TILE / 4) + GV * static_cast<uint32_t>(wave);
         if (t0 >= seg.n_vectors) break;
         const uint32_t nv = min(static_cast<uint32_t>(GV), seg.n_vectors - t0);
         const bool active = static_cast<uint32_t>(n) < nv;   // other lanes repeat the last vector
-        const uint64_t off = vec_elem_offset(seg, t0 + min(static_cast<uint32_t>(n), nv - 1)) + 32u * q;
+        const uint64_t vbase = vec_elem_offset(seg, t0 + min(static_cast<uint32_t>(n), nv - 1));
         uint32_t* pv = pay + n * pwd;   // this vector's payload
 
         float y[32];
-        auto load_quarter = [&](float (&v)[32]) {
+        // elements e0 + c (c < 16) and e1 + c - 16 of this lane's vector
+        auto load_x = [&](float (&v)[32], uint32_t e0, uint32_t e1) {
             if (!bf16) {
-                const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(in) + off);
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
-                    const float4 w = src[k];
+                    const float4 w = reinterpret_cast<const float4*>(static_cast<const float*>(in) + vbase +
+                                                                     (k < 4 ? e0 : e1))[k & 3];
                     v[4 * k] = w.x; v[4 * k + 1] = w.y; v[4 * k + 2] = w.z; v[4 * k + 3] = w.w;
                 }
             } else {
-                const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(in) + off);
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const uint4 w = src[k];
+                    const uint4 w = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(in) + vbase +
+                                                                   (k < 2 ? e0 : e1))[k & 1];
                     const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
@@ -1220,14 +1430,14 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
                 }
             }
         };
-        load_quarter(y);
+        const uint32_t q0 = 32u * static_cast<uint32_t>(q);   // standard layout: elements 32q .. 32q + 31
+        load_x(y, q0, q0 + 16);
         {
             float sg[32];
-            load_signs(sg);
-#pragma unroll
-            for (int c = 0; c < 32; ++c) y[c] = y[c] * sg[c];
+            load_signs(sg, q0, q0 + 16);
+            signs_stage1(y, sg);
         }
-        fwht_quarter(y, q);
+        fwht128_fwd(y);   // -> layout F
 #pragma unroll
         for (int c = 0; c < 32; ++c) y[c] *= scale;
 
@@ -1236,42 +1446,12 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
             for (uint32_t k = 0; k < bwords; ++k) pv[rwords + k] = 0u;
         wave_sync();
 
-        // radii and angle bins (polar.rs:246-266, 413-421) of pairs 16q + i
+        // radii and angle bins (polar.rs:246-266, 413-421) of pairs 8q + i
+        // (i < 8) and 32 + 8q + i - 8 (layout F)
         float r[HP];
-        float rsum = 0.0f;
-        uint64_t pk = 0;
-        uint64_t unsafe[HP];   // per pair: the wave's lanes whose bin needs the exact formula
-#pragma unroll
-        for (int i = 0; i < HP; ++i) {
-            const float a = y[2 * i], b = y[2 * i + 1];
-            const float aa = a * a, bb = b * b;
-            r[i] = __builtin_sqrtf(aa + bb);
-            rsum = rsum + r[i];
-            bool near_line = false, out_of_range = true;   // other widths: every pair takes the exact formula
-            const uint32_t bin = PB == 3 ? octant_bin_m2(a, b, near_line, out_of_range) : 0u;
-            pk |= static_cast<uint64_t>(bin) << (static_cast<uint32_t>(i) * pbits);
-            unsafe[i] = __ballot(near_line) | __ballot(out_of_range);
-        }
-        uint64_t any_unsafe = 0;
-#pragma unroll
-        for (int i = 0; i < HP; ++i) any_unsafe |= unsafe[i];
-        if (any_unsafe) {   // pairs near an octant line (every pair at other widths): the exact formula
-            uint32_t slow = 0;
-#pragma unroll
-            for (int i = 0; i < HP; ++i) slow |= static_cast<uint32_t>((unsafe[i] >> lane) & 1u) << i;
-            for (uint32_t m = slow; m; m &= m - 1u) {
-                const uint32_t i = static_cast<uint32_t>(__ffs(m) - 1);
-                // pair i by selects (a dynamic index into y would go through scratch)
-                float a = y[0], b = y[1];
-#pragma unroll
-                for (int j = 1; j < HP; ++j) {
-                    a = static_cast<uint32_t>(j) == i ? y[2 * j] : a;
-                    b = static_cast<uint32_t>(j) == i ? y[2 * j + 1] : b;
-                }
-                const uint64_t bin = angle_bin_exact(a, b, pbits);
-                pk = (pk & ~(static_cast<uint64_t>(levels - 1u) << (i * pbits))) | (bin << (i * pbits));
-            }
-        }
+        float rsum;
+        uint64_t pk;
+        radii_bins<PB>(y, pbits, lane, r, pk, rsum);
         // A non-finite input makes every FWHT output, so every radius,
         // non-finite; a finite sum of the (non-negative) radii therefore
         // clears both checks.  Otherwise (or on an overflowing sum) they run
@@ -1279,38 +1459,40 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
         bool finite = true, rfinite = true;
         if (!isfinite_f(rsum)) {
             float x[32];
-            load_quarter(x);
+            load_x(x, q0, q0 + 16);
 #pragma unroll
             for (int c = 0; c < 32; ++c) finite &= isfinite_f(x[c]);
 #pragma unroll
             for (int i = 0; i < HP; ++i) rfinite &= isfinite_f(r[i]);
         }
         // angle indices, pbits each, LSB-first (bitpack.rs:21-35): this
-        // quarter's 16 * pbits bits start at bit 16 * pbits * q
+        // lane's two runs of 8 pairs, 8 * pbits <= 32 bits each, start at
+        // bits 8 * pbits * q and 8 * pbits * (4 + q)
         if (active) {
-            const uint32_t bit0 = 16u * pbits * static_cast<uint32_t>(q);
-            const uint32_t nb = 16u * pbits;   // <= 64 bits (pbits <= 4)
-            uint32_t* bwp = pv + rwords + (bit0 >> 5);
-            const uint32_t sh = bit0 & 31u;
-            const uint32_t w0 = static_cast<uint32_t>(pk << sh);
-            const uint32_t w1 = static_cast<uint32_t>((pk << sh) >> 32) | (sh ? static_cast<uint32_t>(pk >> (64 - sh)) : 0u);
-            const uint32_t w2 = sh ? static_cast<uint32_t>(pk >> (96 - sh)) : 0u;
-            atomicOr(bwp, w0);
-            if (sh + nb > 32) atomicOr(bwp + 1, w1);
-            if (sh + nb > 64) atomicOr(bwp + 2, w2);
+            const uint32_t nb = 8u * pbits;
+            const uint64_t lo = pk & ((1ull << nb) - 1u), hi = pk >> nb;
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const uint32_t bit0 = nb * (static_cast<uint32_t>(q) + 4u * half);
+                const uint64_t run = (half ? hi : lo) << (bit0 & 31u);
+                uint32_t* bwp = pv + rwords + (bit0 >> 5);
+                atomicOr(bwp, static_cast<uint32_t>(run));
+                if ((bit0 & 31u) + nb > 32) atomicOr(bwp + 1, static_cast<uint32_t>(run >> 32));
+            }
         }
         if (f32r) {
             if (active)
 #pragma unroll
-                for (int i = 0; i < HP; ++i) pv[16 * q + i] = f2u(r[i]);
+                for (int i = 0; i < HP; ++i) pv[(i < 8 ? 8 * q : 24 + 8 * q) + i] = f2u(r[i]);
         } else {
             // CompressedRadiiV1 BlockLogU8 (turbo-quant/src/radius.rs:58-77)
             uint32_t code[4];
             float mn, mx;
             block_log_u8<4>(r, q, logf_lds, code, mn, mx);
             if (active) {
+                // radius j in byte j: local codes 0..7 are radii 8q.., 8..15 are 32 + 8q..
 #pragma unroll
-                for (int w = 0; w < 4; ++w) pv[4 * q + w] = code[w];
+                for (int w = 0; w < 4; ++w) pv[(w < 2 ? 2 * q : 6 + 2 * q) + w] = code[w];
                 if (q == 0) {
                     pv[16] = f2u(mn);
                     pv[17] = f2u(mx);
@@ -1325,15 +1507,15 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
             y[2 * i] = r[i] * cs_lds[2 * bin];
             y[2 * i + 1] = r[i] * cs_lds[2 * bin + 1];
         }
-        fwht_quarter(y, q);
+        fwht128_inv(y);   // layout F -> layout G
         // residual against x read again (turbo.rs:269-273)
         asm volatile("" ::: "memory");
         {
             // x - (y * scale) * sign with sign = +-1: the product by the sign
             // is exact, so one fma with -sign rounds the same
             float x[32], sg[32];
-            load_quarter(x);
-            load_signs(sg);
+            load_x(x, g0, g1);
+            load_signs(sg, g0, g1);
 #pragma unroll
             for (int c = 0; c < 32; ++c) y[c] = __builtin_fmaf(y[c] * scale, -sg[c], x[c]);
         }
@@ -1348,18 +1530,13 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
         }
         rn2 = rn2 + u2f(partner16(f2u(rn2), q));
         rn2 = rn2 + u2f(partner(f2u(rn2), q >> 1));
-        const float rn = __builtin_sqrtf(rn2) * 1.0001f;   // |res|, rounded up far past its f32 error
+        const float rn = qjl_norm_bound(rn2);
 
         // QJL dots on the f16 matrix cores (v_mfma_f32_16x16x32_f16; bound at
-        // qjl_scale): K step st covers dimensions 32q + 8st + j of lane (q, n)
-        float amax = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 32; ++c) amax = __builtin_fmaxf(amax, __builtin_fabsf(y[c]));
-        amax = __builtin_fmaxf(amax, u2f(partner16(f2u(amax), q)));
-        amax = __builtin_fmaxf(amax, u2f(partner(f2u(amax), q >> 1)));
-        const float sc = qjl_scale(amax);
+        // qjl_scale): K step st covers y[8st + j] of lane (q, n), dimensions
+        // g0 + 8st + j (st < 2) and g1 + 8(st - 2) + j
+        const float sc = qjl_scale(rn);
         const float xn = rn * sc;
-        uint32_t sbits[2] = {0u, 0u}, unc[2] = {0u, 0u};
         const uint32_t ptiles = proj / 16;
         v4f acc[4] = {};
 #pragma unroll
@@ -1376,20 +1553,25 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
                 acc[p] = mfma16x32(al, xh, acc[p]);
             }
         }
+        // register r of tile p: projection j = 16p + 4q + r of vector n.  The
+        // sign bits shift in (v_alignbit) as negative flags, tile 2w + 1 first,
+        // so bit 4k + r of neg[w] is register r of tile 2w + k; a dot is
+        // undecided when |acc| <= a_j xn + b_j, collected wave-wide.
+        const float2* ab = reinterpret_cast<const float2*>(qb) + lane;
+        uint32_t neg[2] = {0u, 0u};
+        uint64_t undecided = 0;
 #pragma unroll
-        for (uint32_t p = 0; p < 4; ++p) {
-            if (p >= ptiles) break;
-            const float2* ab = reinterpret_cast<const float2*>(qb) + p * 4 * 64 + lane;
-            // register r: projection 16p + 4q + r of vector n
+        for (int p = 3; p >= 0; --p) {
+            if (static_cast<uint32_t>(p) >= ptiles) continue;
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const uint32_t j = 16u * p + 4u * static_cast<uint32_t>(q) + static_cast<uint32_t>(rr);
-                const float2 c = ab[rr * 64];
+            for (int rr = 3; rr >= 0; --rr) {
+                const float2 c = ab[(p * 4 + rr) * 64];
                 const float bnd = __builtin_fmaf(c.x, xn, c.y);
-                sbits[j >> 5] |= (acc[p][rr] >= 0.0f ? 1u : 0u) << (j & 31u);
-                unc[j >> 5] |= (__builtin_fabsf(acc[p][rr]) > bnd ? 0u : 1u) << (j & 31u);
+                undecided |= __ballot(!(__builtin_fabsf(acc[p][rr]) > bnd));
+                neg[p >> 1] = __builtin_amdgcn_alignbit(neg[p >> 1], f2u(acc[p][rr]), 31);
                 if constexpr (DIAG) {
                     if (active) {
+                        const uint32_t j = 16u * p + 4u * static_cast<uint32_t>(q) + static_cast<uint32_t>(rr);
                         float* dv = lc.diag + (static_cast<uint64_t>(t0 + static_cast<uint32_t>(n)) * proj + j) * 2u;
                         dv[0] = acc[p][rr] / sc;
                         dv[1] = bnd / sc;
@@ -1397,50 +1579,69 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
                 }
             }
         }
+        // word w: bits 4q + r (tile 2w) and 16 + 4q + r (tile 2w + 1); a dot
+        // >= 0 (or -0, always undecided) gives bit 1
+        uint32_t sbits[2];
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
+            const uint32_t pos = ~neg[w] & 0xffu;
+            sbits[w] = ((pos & 0xfu) | ((pos << 12) & 0xf0000u)) << (4 * q);
             sbits[w] = or_quarters(sbits[w], q);
-            unc[w] = or_quarters(unc[w], q);
         }
         // undecided signs: the reference's sequential dot, each quarter
         // continuing the previous quarter's partial sum
-        if (__ballot(active && (unc[0] | unc[1]) != 0u)) {
+        if (undecided & __ballot(active)) {
+            uint32_t unc[2] = {0u, 0u};
+#pragma unroll
+            for (uint32_t p = 0; p < 4; ++p) {
+                if (p >= ptiles) break;
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const uint32_t j = 16u * p + 4u * static_cast<uint32_t>(q) + static_cast<uint32_t>(rr);
+                    const float2 c = ab[(p * 4 + rr) * 64];
+                    const float bnd = __builtin_fmaf(c.x, xn, c.y);
+                    unc[j >> 5] |= (__builtin_fabsf(acc[p][rr]) > bnd ? 0u : 1u) << (j & 31u);
+                }
+            }
 #pragma unroll
             for (uint32_t w = 0; w < 2; ++w) {
                 if (32u * w >= proj) break;
-                const uint32_t m = active ? unc[w] : 0u;
+                const uint32_t uq = or_quarters(unc[w], q);   // every lane swaps
+                const uint32_t m = active ? uq : 0u;
                 uint32_t any = m;
                 for (int sh2 = 1; sh2 < 64; sh2 <<= 1) any |= __shfl_xor(any, sh2);
                 while (any) {
                     const uint32_t j = static_cast<uint32_t>(__ffs(any) - 1);
                     any &= any - 1u;
-                    const float* g = qjl + static_cast<size_t>(32 * w + j) * DIM + 32 * q;
+                    const float* g = qjl + static_cast<size_t>(32 * w + j) * DIM;
+                    // blocks 0..7 in order: block b sits in row B(b & 3), in
+                    // y[0..15] (b < 4) or y[16..31]; its row continues the sum
+                    // and every lane takes it
                     float run = 0.0f;
-                    for (int st = 0; st < 4; ++st) {
-                        if (q == st) {
+#pragma unroll
+                    for (int b = 0; b < 8; ++b) {
+                        const int hb = ((b & 1) << 1) | ((b >> 1) & 1);
+                        if (q == hb) {
                             float d = run;
 #pragma unroll
-                            for (int c = 0; c < 32; ++c) d = d + g[c] * y[c];
+                            for (int c = 0; c < 16; ++c) d = d + g[16 * b + c] * y[(b < 4 ? 0 : 16) + c];
                             run = d;
                         }
-                        const float prev = __shfl(run, lane >= 16 ? lane - 16 : lane);
-                        if (q == st + 1) run = prev;
+                        run = __shfl(run, 16 * hb + n);
                     }
-                    const float full = __shfl(run, 48 + n);   // quarter 3 holds the whole sum
+                    const float full = run;
                     if ((m >> j) & 1u) sbits[w] = (sbits[w] & ~(1u << j)) | (full >= 0.0f ? 1u << j : 0u);
                 }
             }
         }
 
         // status (per vector, first failure in vector order) and the QJL words
-        const bool fin_v = or_quarters(finite ? 0u : 1u, q) == 0u;
-        const bool rfin_v = or_quarters(rfinite ? 0u : 1u, q) == 0u;
-        const bool resfin_v = or_quarters(resfinite ? 0u : 1u, q) == 0u;
+        const uint32_t bad = or_quarters((finite ? 0u : 1u) | (rfinite ? 0u : 2u) | (resfinite ? 0u : 4u), q);
         if (active && q == 0) {
             const uint32_t vi = t0 + n;
-            if (!fin_v) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_INPUT);
-            else if (!rfin_v) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RADIUS);
-            else if (!resfin_v) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RESIDUAL);
+            if (bad & 1u) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_INPUT);
+            else if (bad & 2u) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RADIUS);
+            else if (bad & 4u) status_fail(lc.status, sidx, 1, vi, KIND_NONFINITE_RESIDUAL);
             pv[rwords + bwords] = sbits[0];
             if (proj > 32) pv[rwords + bwords + 1] = sbits[1];
         }
@@ -3220,6 +3421,24 @@ __global__ void f16_subnormal_probe_kernel(float* out) {
     }
 }
 
+// sqrt_normal against __builtin_sqrtf on every float it is used on (2^-96 ..
+// +inf) and on +0 and NaN; *bad counts the disagreements.
+constexpr uint32_t kSqrtLo = 0x0f800000u, kSqrtHi = 0x7f800001u;
+
+__global__ __launch_bounds__(256) void sqrt_check_kernel(uint32_t per, uint32_t* bad) {
+    const uint64_t t = blockIdx.x * static_cast<uint64_t>(blockDim.x) + threadIdx.x;
+    const uint64_t b0 = kSqrtLo + t * per;
+    const uint32_t u0 = static_cast<uint32_t>(b0 < kSqrtHi ? b0 : kSqrtHi);
+    const uint32_t u1 = static_cast<uint32_t>(b0 + per < kSqrtHi ? b0 + per : kSqrtHi);
+    uint32_t n = 0;
+    for (uint32_t u = u0; u < u1; ++u) n += f2u(sqrt_normal(u2f(u))) != f2u(__builtin_sqrtf(u2f(u))) ? 1u : 0u;
+    if (t == 0) {
+        n += f2u(sqrt_normal(0.0f)) != 0u ? 1u : 0u;
+        n += isfinite_f(sqrt_normal(u2f(0x7fc00000u))) || (f2u(sqrt_normal(u2f(0x7fc00000u))) & 0x7fffffu) == 0u ? 1u : 0u;
+    }
+    if (n) atomicAdd(bad, n);
+}
+
 __global__ void logf_bound_read_kernel(float* out) {
     if (threadIdx.x < 256) out[threadIdx.x] = g_logb[threadIdx.x];
 }
@@ -3251,6 +3470,17 @@ int launch_logf_bound(void* stream) {
 
 int launch_f16_subnormal_probe(float* out, void* stream) {
     hipLaunchKernelGGL(f16_subnormal_probe_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), out);
+    return hipGetLastError();
+}
+
+int launch_sqrt_check(uint32_t* bad, void* stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    constexpr uint64_t threads = static_cast<uint64_t>(kLogbBlocks) * 256;
+    const uint32_t per = static_cast<uint32_t>((static_cast<uint64_t>(kSqrtHi - kSqrtLo) + threads - 1) / threads);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, st, bad, 0u, static_cast<uint64_t>(1));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(sqrt_check_kernel, dim3(kLogbBlocks), dim3(256), 0, st, per, bad);
     return hipGetLastError();
 }
 

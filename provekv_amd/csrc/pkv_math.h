@@ -209,6 +209,35 @@ PKV_HD uint32_t octant_bin_m2(float a, float b, bool& near_line, bool& out_of_ra
     return bin;
 }
 
+// octant_bin_m2 in float form, for the batched encodes' fast path (five
+// instructions for the test on gfx950, |.| being a free source modifier):
+// g = |a| - |b|, unsafe = !(max(|a|, |b|, 2^-31) < min(|a|, |b|, |g|) * 2^16).
+// A pair it passes is one octant_bin_m2 passes, with the same bin, provided
+// fl(fl(a^2) + fl(b^2)) is finite (the kernels send every pair of a vector
+// whose radii do not sum to a finite value down the exact path):
+//   * m3 * 2^16 is exact (no overflow: m3 <= mx < 2^64 when a^2, b^2 are
+//     finite), so m3 > mx 2^-16 = eps of octant_bin_m2 (exact for mx >
+//     2^-110), and m3 > 2^-47, so mx > 2^-47 > 1e-30; mx < 2^64 < 1e30;
+//   * bin bit 0: the sign of g is set exactly when |a| < |b| (a difference of
+//     unequal floats keeps its sign; |a| == |b| fails the test through
+//     |g| = 0), so sign(g) xor sign(a) xor sign(b) is octant_bin_m2's
+//     ~((ub - ua) ^ t) >> 31.
+// The 2^-31 floor also keeps every passed pair's fl(a^2) + fl(b^2) >= 2^-94,
+// inside sqrt_normal's domain.
+PKV_HD uint32_t octant_bin_f(float a, float b, bool& unsafe) {
+    const float fa = __builtin_fabsf(a), fb = __builtin_fabsf(b);
+    const float g = fa - fb;
+    const float mx = __builtin_fmaxf(__builtin_fmaxf(fa, fb), 0x1p-31f);
+    const float m3 = __builtin_fminf(__builtin_fminf(fa, fb), __builtin_fabsf(g));
+    unsafe = !(mx < m3 * 65536.0f);
+    uint32_t xa, xb, xg;
+    __builtin_memcpy(&xa, &a, 4);
+    __builtin_memcpy(&xb, &b, 4);
+    __builtin_memcpy(&xg, &g, 4);
+    const uint32_t t = xa ^ xb, c = xg ^ t;
+    return ((~xb >> 29) & 4u) | ((t >> 30) & 2u) | (c >> 31);
+}
+
 PKV_HD uint32_t octant_bin_m(float a, float b, bool& safe) {
     bool near_line, out_of_range;
     const uint32_t bin = octant_bin_m2(a, b, near_line, out_of_range);

@@ -157,14 +157,15 @@ def test_angle_bins_match_glibc_atan2f_formula():
 
 
 def test_octant_fast_path_safe_pairs_keep_the_exact_bin():
-    """The encode kernels' octant path (sign bits + one unsigned safety
-    test, octant_bin_m2): every pair it marks safe has the bin of the
-    pinned angle_bin path (glibc atan2f formula, test above); pairs on and
-    next to the octant lines, at the edges of the covered range (1e-30 ..
-    1e30), zeros, subnormals, infinities and NaN are marked unsafe."""
+    """The encode kernels' octant path (sign bits + the float safety test of
+    octant_bin_f, and a finite fl(a^2) + fl(b^2)): every pair it marks safe
+    has the bin of the pinned angle_bin path (glibc atan2f formula, test
+    above); pairs on and next to the octant lines, outside the covered range
+    (2^-47 .. 2^64), zeros, subnormals, infinities and NaN are marked
+    unsafe."""
     rng = np.random.RandomState(7)
     n = 300_000
-    mag = np.exp(rng.uniform(-75, 75, n))   # one scale per pair, across the covered range
+    mag = np.exp(rng.uniform(-30, 42, n))   # one scale per pair, across the covered range
     a = (rng.randn(n) * mag).astype(np.float32)
     b = (rng.randn(n) * mag).astype(np.float32)
     t = rng.randn(50_000).astype(np.float32)
@@ -186,8 +187,10 @@ def test_octant_fast_path_safe_pairs_keep_the_exact_bin():
     # never safe: on a line (|a| == |b|, a or b zero), out of range, non-finite
     on_line = (np.abs(a) == np.abs(b)) | (a == 0) | (b == 0)
     mx = np.maximum(np.abs(a), np.abs(b))
-    out = ~((mx > np.float32(1e-30)) & (mx < np.float32(1e30))) | ~np.isfinite(a) | ~np.isfinite(b)
+    out = ~((mx > np.float32(2.0 ** -47)) & (mx < np.float32(2.0 ** 64))) | ~np.isfinite(a) | ~np.isfinite(b)
     assert not np.any(ok & (on_line | out))
+    # and inside the range octant_bin_m2 (the integer form) covers
+    assert np.all(mx[ok] > np.float32(1e-30)) and np.all(mx[ok] < np.float32(1e30))
 
 
 def test_profile_constant_service_builds_each_profile_once():
