@@ -656,7 +656,7 @@ __device__ __forceinline__ float sqrt_normal(float x) {
 //   reference's value P_i before roundf, with delta = g_logb of the larger of
 //   |mn|, |mx| (every l_i lies between them): three roundings on each side,
 //   of values at most 256 when the margin below is under 1/2.  When t_i is
-//   farther than M = 255 delta / span (1 + 2^-10) + 2^-12 from every
+//   farther than M = 255 delta / span (1 + 2^-10) + 1552u from every
 //   half-integer, P_i lies in the same unit interval around rint(t_i), so
 //   roundf(P_i) = rint(t_i) (t_i >= -M > -1/2 and t_i <= 255 + M; no ties).
 //   The others -- every code when M >= 1/2, and a NaN t_i -- take the
@@ -698,7 +698,7 @@ __device__ __forceinline__ void block_log_u8(const float (&r)[16], int part, con
     const float inv = 255.0f / span;
     const float big = __builtin_fmaxf(__builtin_fabsf(mn), __builtin_fabsf(mx));
     const float delta = g_logb[f2u(big) >> 23];
-    const float margin = delta * inv * (1.0f + 0x1p-10f) + 0x1p-12f;
+    const float margin = delta * inv * (1.0f + 0x1p-10f) + 0x1.84p-14f;   // 1552u >= 6 * 256 * 1.0001u
     const float thr = 0.5f - margin;   // decided when |t - rint(t)| < thr
     uint64_t undecided = __ballot(tiny);
 #pragma unroll
@@ -748,10 +748,10 @@ __device__ __forceinline__ void block_log_u8(const float (&r)[16], int part, con
 // -- take angle_bin_exact and __builtin_sqrtf.  Every lane of the wave must
 // call it.
 template <int PB>
-__device__ __forceinline__ void radii_bins(const float (&y)[32], uint32_t pbits, int lane, float (&r)[16],
-                                           uint64_t& pk, float& rsum) {
+__device__ __forceinline__ void radii_bins(const float (&y)[32], uint32_t pbits, float (&r)[16], uint64_t& pk,
+                                           float& rsum) {
     constexpr int HP = 16;
-    uint64_t unsafe[HP];   // per pair: the wave's lanes that need the exact formulas
+    uint64_t any_unsafe = 0;   // the wave's lanes with a pair that needs the exact formulas
     rsum = 0.0f;
     pk = 0;
     // octant_bin_f's bins, bit by bit: each pair shifts the sign bits of g,
@@ -781,7 +781,7 @@ __device__ __forceinline__ void radii_bins(const float (&y)[32], uint32_t pbits,
                 else w1 = __builtin_amdgcn_alignbit(w1, src[k], 31);
             }
         }
-        unsafe[i] = __ballot(uns);
+        any_unsafe |= __ballot(uns);
     }
     if constexpr (PB == 3) {
         w0 = __builtin_bitreverse32(w0);
@@ -791,14 +791,17 @@ __device__ __forceinline__ void radii_bins(const float (&y)[32], uint32_t pbits,
         pk = (static_cast<uint64_t>(w1) << 32) | w0;
     }
     const bool force = !isfinite_f(rsum);
-    uint64_t any_unsafe = __ballot(force);
-#pragma unroll
-    for (int i = 0; i < HP; ++i) any_unsafe |= unsafe[i];
+    any_unsafe |= __ballot(force);
     if (any_unsafe) {
+        // this lane's pairs again (the fast loop keeps only the wave's OR)
         const uint32_t levels = 1u << pbits;
         uint32_t slow = force ? 0xffffu : 0u;
 #pragma unroll
-        for (int i = 0; i < HP; ++i) slow |= static_cast<uint32_t>((unsafe[i] >> lane) & 1u) << i;
+        for (int i = 0; i < HP; ++i) {
+            bool uns = true;
+            if constexpr (PB == 3) (void)octant_bin_f(y[2 * i], y[2 * i + 1], uns);
+            slow |= (uns ? 1u : 0u) << i;
+        }
         for (uint32_t m = slow; m; m &= m - 1u) {
             const uint32_t i = static_cast<uint32_t>(__ffs(m) - 1);
             // pair i by selects (a dynamic index into y would go through scratch)
@@ -990,7 +993,7 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
         float r[HP];
         float rsum;
         uint64_t pk;
-        radii_bins<PB>(y, pbits, lane, r, pk, rsum);
+        radii_bins<PB>(y, pbits, r, pk, rsum);
         // A non-finite input makes every FWHT output, so every radius,
         // non-finite; a finite sum of the (non-negative) radii therefore
         // clears both checks.  Otherwise (or on an overflowing sum) they run
@@ -1451,7 +1454,7 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
         float r[HP];
         float rsum;
         uint64_t pk;
-        radii_bins<PB>(y, pbits, lane, r, pk, rsum);
+        radii_bins<PB>(y, pbits, r, pk, rsum);
         // A non-finite input makes every FWHT output, so every radius,
         // non-finite; a finite sum of the (non-negative) radii therefore
         // clears both checks.  Otherwise (or on an overflowing sum) they run
