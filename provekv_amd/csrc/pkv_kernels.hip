@@ -2998,6 +2998,15 @@ __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void 
     }
     uint32_t used = 0, nq = 0;   // ring slots filled, queued vectors
     while (u < nunits) {   // wave-uniform
+        {   // a wave near its last units steps down so the ones with more left issue
+            // first (the arbiter otherwise favours the oldest waves, which then
+            // finish early and leave the late ones at low occupancy)
+            const uint32_t rem = (nunits - u + stride - 1) / stride;
+            if (rem >= 4) __builtin_amdgcn_s_setprio(3);
+            else if (rem == 3) __builtin_amdgcn_s_setprio(2);
+            else if (rem == 2) __builtin_amdgcn_s_setprio(1);
+            else __builtin_amdgcn_s_setprio(0);
+        }
         const SegDev seg = lc.segs[sidx];
         uint32_t* pay = ring + used * FIB_PAY_WORDS;
         FibTileRot t;
