@@ -191,8 +191,12 @@ int pkv_segments_status(const pkv_profile* prof, const uint32_t* host_status, ui
  * d_wire.  Replaces the per-(layer, K|V) loops of TurboQuantAdapter /
  * FibQuantAdapter::encode_batch_compact (proveKV/src/codec.rs:248-291,
  * 513-525) driven by materialize_shell / SharedKVPool::build_with_policy.
- * d_status: 2*nseg uint32 device words (may be NULL).  The call validates the
- * segment table against in_elems / wire_bytes before launching. */
+ * d_status: 2*nseg uint32 device words, or NULL.  With status words the call
+ * is asynchronous and a rejected input is reported only there
+ * (pkv_segments_status); with NULL it waits for its kernels and returns the
+ * first error's code itself, as the reference's encode does (not under graph
+ * capture: PKV_ERR_UNSUPPORTED).  The call validates the segment table
+ * against in_elems / wire_bytes before launching. */
 int pkv_encode_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, int in_dtype,
                         const void* d_in, uint64_t in_elems, const pkv_seg* segs, uint32_t nseg,
                         uint8_t* d_wire, uint64_t wire_bytes, uint32_t* d_status, void* stream);
@@ -201,6 +205,8 @@ int pkv_encode_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, 
  * radii_codec: the TQB1 radii codec the caller expects (ignored for fib);
  * each header is checked against the profile and the segment on the device
  * (a mismatch marks the segment corrupt and leaves its output untouched).
+ * d_status as in pkv_encode_segments: a NULL one makes the call wait and
+ * return a rejected blob's error, so it never fails open.
  * Replaces decode_batch_compact (proveKV/src/codec.rs:295-326, 530-569) under
  * SharedKVPool::decompress_layer (pool.rs:471-614) and
  * AgentShell::decompress_all_layers_with_seed (shell.rs:92-141). */

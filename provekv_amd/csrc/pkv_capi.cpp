@@ -477,6 +477,10 @@ int launch_segments(const pkv_profile* prof, int radii, bool encode, int dtype, 
 }
 
 // Caller holds ctx->mu.
+int copy_back(hipStream_t st, void* h1, const void* d1, size_t n1, void* h2, const void* d2, size_t n2);
+int resolve_status(const pkv_profile* p, const uint32_t* st, uint32_t nseg, const pkv_seg* segs, pkv_error* err,
+                   bool per_vector);
+
 int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool encode, int dtype,
                         const void* d_f32, uint64_t f32_elems, const pkv_seg* segs, uint32_t nseg,
                         const uint8_t* d_wire, uint64_t wire_bytes, uint32_t* d_status, hipStream_t stream,
@@ -494,6 +498,14 @@ int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool e
                                fanout, fanout_stride);
     if (rc) return rc;
     HIP_TRY(hipSetDevice(ctx->device));
+    if (!d_status) {
+        // Without the caller's status words the call reports a rejected input
+        // or blob itself (the reference's encode / decode return the error),
+        // so it waits for its kernels; that wait cannot be captured.
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        HIP_TRY(hipStreamIsCapturing(stream, &cap));
+        if (cap != hipStreamCaptureStatusNone) return PKV_ERR_UNSUPPORTED;
+    }
     Slot* sl;
     SegDev* dsegs;
     uint32_t *dtiles, *dstat;
@@ -504,7 +516,14 @@ int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool e
                                   per_vector, fanout, fanout_stride, grid_cap, stream, diag);
     int rc2 = finish_slot(sl, stream);
     if (e) return hip_status(static_cast<hipError_t>(e));
-    return rc2;
+    if (rc2 || d_status) return rc2;
+    // the private status words, read back into the slot's pinned mirror
+    uint32_t* host_status = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(sl->host) +
+                                                        (reinterpret_cast<uint8_t*>(dstat) -
+                                                         static_cast<uint8_t*>(sl->dev)));
+    rc = copy_back(stream, host_status, dstat, sizeof(uint32_t) * 2 * nseg, nullptr, nullptr, 0);
+    if (rc) return rc;
+    return resolve_status(prof, host_status, nseg, segs, nullptr, per_vector);
 }
 
 int run_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool encode, int dtype, const void* d_f32,

@@ -156,3 +156,39 @@ def test_header_only_blobs(ctx, kind):
             assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
         else:
             assert err is not None and err.segment == 1 and err.status == L.ERR_CORRUPT_PAYLOAD
+
+
+@pytest.mark.parametrize("kind", ["fib", "turbo"])
+def test_calls_without_status_words_fail_closed(ctx, kind):
+    """Without the caller's status words (d_status = NULL) a segment call
+    reports a rejected blob or input itself, as the reference's decode /
+    encode return the error: the call waits for its kernels and returns the
+    error's code (the segment and vector are in the status words, for a
+    caller that passes them); a clean call returns normally with the same
+    bytes."""
+    import torch
+    prof, radii, enc, dec = _codec(ctx, kind, 64, False)
+    rng = np.random.RandomState(11)
+    xa, xb = rng.randn(9, 64).astype(np.float32), rng.randn(6, 64).astype(np.float32)
+    ba, bb = enc(xa), enc(xb)
+    segs = segments([(0, 64, 64, 0, 9, 1), (9 * 64, 64, 64, len(ba), 6, 1)])
+    wire = torch.from_numpy(np.frombuffer(ba + bb, np.uint8).copy()).cuda()
+    out = torch.zeros(15 * 64, dtype=torch.float32, device="cuda")
+    prof.decode_segments(wire, segs, out, radii=radii)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), np.concatenate([dec(ba), dec(bb)]).reshape(-1).view(np.uint32))
+    wire[len(ba)] ^= 0xFF                                   # the second blob's magic
+    with pytest.raises(L.PkvError) as e:
+        prof.decode_segments(wire, segs, out, radii=radii)
+    assert e.value.status == L.ERR_CORRUPT_PAYLOAD
+    # encode: a non-finite input in the second segment
+    x = np.concatenate([xa, xb])
+    x[11, 5] = np.inf
+    inp = torch.from_numpy(x.reshape(-1)).cuda()
+    wout = torch.empty(len(ba) + len(bb), dtype=torch.uint8, device="cuda")
+    with pytest.raises(L.PkvError) as e:
+        prof.encode_segments(inp, segs, wout, radii=radii)
+    assert e.value.status == L.ERR_NONFINITE_INPUT
+    x[11, 5] = 0.5
+    inp = torch.from_numpy(x.reshape(-1)).cuda()
+    prof.encode_segments(inp, segs, wout, radii=radii)
+    assert wout.cpu().numpy().tobytes()[:len(ba)] == ba
