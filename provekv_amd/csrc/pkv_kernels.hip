@@ -2537,15 +2537,16 @@ turbo_score_lut_kernel(
 //           products and |c_w|^2 + off (times 1.0); codeword index in the 5
 //           low bits; each half-wave keeps its two smallest keys and the
 //           halves meet through v_permlane32_swap.
-// If the second smallest key exceeds the smallest by more than `thr` (2.5x
+// If the second smallest key exceeds the smallest by more than `thr` (twice
 // the host-derived worst-case error of a key against the reference's f32
-// distance), the smallest key's codeword is the reference's strict argmin.
-// Otherwise the vector is queued (in the workgroup's LDS queue) with the mask
-// of its undecided blocks (a few % of vectors), and once every wave has
-// queued, the workgroup redoes those blocks exactly (fib_fixup_wave): f64
-// sequential rows of the exact x_hat and the AVX2-order f32 distances.
-// Segments of fewer than 4 vectors and per-vector encodes (the reference's
-// single-vector path with an f64 x_hat) queue all 16 blocks.
+// distance, rounded up), the smallest key's codeword is the reference's
+// strict argmin.  Otherwise the vector goes to its wave's LDS list with the
+// mask of its undecided blocks (a few % of vectors), and the wave redoes
+// those blocks exactly once it has encoded its units (fib_redo_list): f64
+// sequential rows of the exact x_hat and the AVX2-order f32 distances.  Segments of fewer than 4
+// vectors and per-vector encodes (the reference's single-vector path with an
+// f64 x_hat) take the same test; their undecided blocks are redone under the
+// per-vector semantics.
 
 
 // f16 halves of a, b by round-toward-zero: hi = (a_hi, b_hi), lo = the
@@ -2787,179 +2788,257 @@ __device__ __forceinline__ bool f32_rounding_stable(double v, double err) {
 
 constexpr uint32_t FIB_UNIT = 32;                          // vectors per wave iteration (one MFMA tile)
 constexpr uint32_t FIB_UNITS_PER_TILE = TILE / FIB_UNIT;   // a segment tile of 256 vectors is 8 units
-constexpr uint32_t FIB_RING = 4;                           // units a wave holds in LDS before its redo flush
-constexpr uint32_t FIB_QCAP = 64;                          // queued vectors per wave (a flush comes first)
 constexpr int FIB_PAY_WORDS = 32 * 3 + 4;                  // one unit's payloads + lds_to_global padding
+constexpr uint32_t FIB_LCAP = 96;                          // a wave's list of undecided vectors (LDS)
 
-struct FibRedoLds {
-    double xh[4][64];           // x_hat of the vector of each pair of a pass
-    double nrm[FIB_QCAP];       // |x| of each queued vector
-    uint64_t off[FIB_QCAP];     // its input element offset
-    uint32_t ent[FIB_QCAP];     // payload word in the ring | per-vector semantics << 15 | blocks << 16
-    uint64_t blob[FIB_RING];    // ring slot -> blob byte offset in the wire,
-    uint32_t v0[FIB_RING];      //   first vector,
-    uint32_t nv[FIB_RING];      //   vectors of the unit,
-    uint32_t nvec[FIB_RING];    //   vectors of the segment
+// Lane permutations inside each row of 16 lanes (DPP, no LDS round trip):
+// quad xor 1, quad xor 2, i <-> 7 - i within 8, i <-> 15 - i within 16.
+constexpr int DPP_QUAD_XOR1 = 0xB1, DPP_QUAD_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = dpp_u32<CTRL>(static_cast<uint32_t>(b)), hi = dpp_u32<CTRL>(static_cast<uint32_t>(b >> 32));
+    return __builtin_bit_cast(double, static_cast<uint64_t>(hi) << 32 | lo);
+}
+// (d, w) := the smaller of (d, w) and the pair from the permuted lane (ties: the lower index)
+template <int CTRL>
+__device__ __forceinline__ void argmin_step(float& d, uint32_t& w) {
+    const float od = u2f(dpp_u32<CTRL>(f2u(d)));
+    const uint32_t ow = dpp_u32<CTRL>(w);
+    if (od < d || (od == d && ow < w)) { d = od; w = ow; }
+}
+
+// A vector with undecided argmin blocks, in its encode wave's LDS list.
+struct FibRedoEntry {
+    uint64_t in_off;      // the vector's first input element
+    uint64_t field_off;   // wire byte of its payload's index field (payload byte 2)
+    double nrm;           // |x| (the reference's sequential f64 l2_norm)
+    uint32_t flags;       // undecided blocks (bits 0..15) | FibQuantizer::encode semantics << 16
+    uint32_t field[3];    // the index field as encoded (bits 0..31, 32..63, 64..79), patched by the redo
 };
 
-// Exact decisions for the queued (vector, blocks) entries of one wave,
-// ent[0 .. nq): every undecided block of up to FIB_RING units at once, by the
-// reference's exact path -- x_hat = f32(x / |x|) (codec.rs:608; f64 x / |x|
+// Exact decisions for the nq (<= FIB_LCAP) listed vectors of one wave, then
+// their index fields back to the wire.  The wave's four groups of 16 lanes
+// take one entry each per round; with PREFETCH (after the wave's last unit,
+// when nothing else is live) the next round's x and Pi rows load while the
+// current one is redone, without it (a full list in the middle of the unit
+// loop, rare) each round loads its own.  Per undecided block b, the
+// reference's exact path: x_hat = f32(x / |x|) (codec.rs:608; f64 x / |x|
 // under FibQuantizer::encode semantics, codec.rs:481), rho_r = f32(sequential
 // f64 sum of f64 products over row 4b + r of Pi) (rotation.rs:107-113), the
-// AVX2 argmin over the 32 codewords (simd_nearest.rs:44-104) -- four
-// (vector, block) pairs per pass, 16 lanes each: lane (r, k) = ((lane % 16) /
-// 4, lane % 4) sums row 4b + r over columns 16k .. 16k + 15.
+// AVX2 argmin over the 32 codewords (simd_nearest.rs:44-104).  Lane g of a
+// group converts elements 4g .. 4g + 3 and holds codewords 2g, 2g + 1; rows
+// 4b .. 4b + 3 of Pi are 2 KB in a row, which the group loads as 16-byte
+// pieces g + 16c (c = 0 .. 7, 256 contiguous bytes per load), so lane g holds
+// columns 2g, 2g + 1, 2g + 32, 2g + 33 of every one of the four rows.
 //
 // Both roundings are taken from faster forms that provably round the same:
 //  * x_hat: q = x * fl64(1 / |x|) is within 2^-50 |q| of fl64(x / |x|)
 //    (three roundings of at most 2^-53 relative and the reciprocal's
 //    2^-52), so if no f32 rounding boundary lies within that distance of q,
 //    f32(q) = f32(fl64(x / |x|)); otherwise the division is done.
-//  * rho_r: four FMA partial sums of 16 terms, then two adds, are within
-//    (gamma_19) A of the exact sum and the reference's sequential sum within
-//    (gamma_64) A, A = sum |Pi_rc x_hat_c| <= |Pi_r| |x_hat| < 1.01, so the
-//    two differ by less than 96 * 2^-53; if no f32 rounding boundary lies
-//    within 2^-46 of the partial-sum result, f32 of it is the reference's
-//    rho_r; otherwise the row is summed in the reference's order.
-template <int DIM>
-__device__ void fib_redo_flush(const LaunchCommon& lc, const void* __restrict__ in, const double* __restrict__ rot64,
-                               const float* __restrict__ cb, uint32_t* ring, FibRedoLds& R, uint32_t nq, int lane) {
-    static_assert(DIM == 64, "16 lanes of 4 rows x 4 quarters per 4-dimensional block");
-    uint32_t total = 0;
-    for (uint32_t j = 0; j < nq; ++j) total += static_cast<uint32_t>(__popc(R.ent[j] >> 16));
-    const uint32_t p = static_cast<uint32_t>(lane) >> 4, g = static_cast<uint32_t>(lane) & 15u;
-    const uint32_t r = g >> 2, k = g & 3u;
+//  * rho_r: each lane's FMA chain over its four columns, then a 16-lane
+//    butterfly of adds, rounds every term at most 8 times, so it is within
+//    gamma_8 A of the exact sum, and the reference's sequential sum is within
+//    gamma_64 A, A = sum |Pi_rc x_hat_c| <= |Pi_r| |x_hat| < 1.01: the two
+//    differ by less than 96 * 2^-53; if no f32 rounding boundary lies within
+//    2^-46 of the fast result, f32 of it is the reference's rho_r; otherwise
+//    the row is summed in the reference's order.
+// A vector is listed once, so every wave writes only its own vectors' index
+// fields (after the encode wrote their payloads: the same wave's stores to the
+// same bytes, in order).
+template <int DIM, bool PREFETCH>
+__device__ __forceinline__ void fib_redo_list(const LaunchCommon& lc, const void* __restrict__ in,
+                                              uint8_t* __restrict__ wire, const double* __restrict__ rot64,
+                                              const float* __restrict__ cb, FibRedoEntry* list, double* xh_wave,
+                                              uint32_t nq, int lane) {
+    static_assert(DIM == 64, "16 lanes x 4 columns of 4 rows per 4-dimensional block");
+    const uint32_t grp = static_cast<uint32_t>(lane) >> 4, g = static_cast<uint32_t>(lane) & 15u;
+    double* xh = xh_wave + grp * DIM;
     const bool bf16 = lc.in_bf16 != 0;
-    for (uint32_t base = 0; base < total; base += 4) {   // every lane runs every pass (cross-lane reads)
-        const uint32_t pi = base + p;
-        const bool valid = pi < total;
-        uint32_t e = 0, b = 0;   // pair pi -> (entry, block); lanes past the end keep entry 0, block 0
-        {
-            uint32_t acc = 0;
-            for (uint32_t j = 0; j < nq; ++j) {
-                const uint32_t m = R.ent[j] >> 16, c = static_cast<uint32_t>(__popc(m));
-                if (valid && pi >= acc && pi < acc + c) {
-                    uint32_t mm = m;
-                    for (uint32_t t = pi - acc; t > 0; --t) mm &= mm - 1u;
-                    e = j;
-                    b = static_cast<uint32_t>(__ffs(mm) - 1);
-                }
-                acc += c;
-            }
+    const float4 cw0 = reinterpret_cast<const float4*>(cb)[2 * g], cw1 = reinterpret_cast<const float4*>(cb)[2 * g + 1];
+    // p[4r + 0..3] = Pi[4b + r][2g], [2g + 1], [2g + 32], [2g + 33]
+    auto load_rows = [&](uint32_t b, double (&p)[16]) {
+        const double2* base = reinterpret_cast<const double2*>(rot64 + static_cast<size_t>(4u * b) * DIM) + g;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const double2 v2 = base[16 * c];
+            p[2 * c] = v2.x;
+            p[2 * c + 1] = v2.y;
         }
-        const uint32_t ent = R.ent[e];
-        const bool small = (ent >> 15) & 1u;
-        const double nv = R.nrm[e];
-        // every load of the pass goes out first: x, the row's 16 values, two codewords
-        const uint64_t off = R.off[e] + 4u * g;
-        float xv[4];
+    };
+    // round j: group grp redoes entry 4j + grp; its x elements 4g .. 4g + 3
+    // and its first undecided block's rows (every round loads: past the end,
+    // the last entry again)
+    struct In {
+        float x[4];
+        double p[16];
+    };
+    auto fetch = [&](uint32_t j, In& d) {
+        const FibRedoEntry& e = list[min(4u * j + grp, nq - 1u)];
+        const uint64_t off = e.in_off + 4u * g;
         if (!bf16) {
             const float4 q4 = *reinterpret_cast<const float4*>(static_cast<const float*>(in) + off);
-            xv[0] = q4.x; xv[1] = q4.y; xv[2] = q4.z; xv[3] = q4.w;
+            d.x[0] = q4.x; d.x[1] = q4.y; d.x[2] = q4.z; d.x[3] = q4.w;
         } else {
             const uint2 w2 = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(in) + off);
-            xv[0] = u2f(w2.x << 16); xv[1] = u2f(w2.x & 0xffff0000u);
-            xv[2] = u2f(w2.y << 16); xv[3] = u2f(w2.y & 0xffff0000u);
+            d.x[0] = u2f(w2.x << 16); d.x[1] = u2f(w2.x & 0xffff0000u);
+            d.x[2] = u2f(w2.y << 16); d.x[3] = u2f(w2.y & 0xffff0000u);
         }
-        const double* prow = rot64 + static_cast<size_t>(4u * b + r) * DIM;
-        double pr[16];
-#pragma unroll
-        for (int c = 0; c < 16; c += 2) {
-            const double2 v2 = *reinterpret_cast<const double2*>(prow + 16 * k + c);
-            pr[c] = v2.x;
-            pr[c + 1] = v2.y;
-        }
-        const float4 cw0 = reinterpret_cast<const float4*>(cb)[2 * g], cw1 = reinterpret_cast<const float4*>(cb)[2 * g + 1];
-        {   // x_hat[4g .. 4g + 3] of the pair's vector
+        if constexpr (PREFETCH) load_rows(static_cast<uint32_t>(__ffs((e.flags & 0xFFFFu) | 0x10000u) - 1) & 15u, d.p);
+    };
+    auto redo = [&](uint32_t j, const In& d) {
+        const uint32_t idx = 4u * j + grp;
+        if (idx >= nq) return;   // group-uniform
+        FibRedoEntry& e = list[idx];
+        const uint32_t flags = e.flags;
+        const bool small = (flags >> 16) & 1u;
+        const double nv = e.nrm;
+        {   // x_hat[4g .. 4g + 3]
             const double rinv = 1.0 / nv;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const double xd = static_cast<double>(xv[j]);
-                double xh;
+            for (int q = 0; q < 4; ++q) {
+                const double xd = static_cast<double>(d.x[q]);
+                double x1;
                 if (small) {
-                    xh = xd / nv;
+                    x1 = xd / nv;
                 } else {
-                    const double q = xd * rinv;
-                    float y = static_cast<float>(q);
-                    if (!f32_rounding_stable(q, __builtin_fabs(q) * 0x1p-50)) y = static_cast<float>(xd / nv);
-                    xh = static_cast<double>(y);
+                    const double qq = xd * rinv;
+                    float y = static_cast<float>(qq);
+                    if (!f32_rounding_stable(qq, __builtin_fabs(qq) * 0x1p-50)) y = static_cast<float>(xd / nv);
+                    x1 = static_cast<double>(y);
                 }
-                R.xh[p][4 * g + j] = xh;
+                xh[4 * g + q] = x1;
             }
         }
+        uint64_t ilo = e.field[0] | static_cast<uint64_t>(e.field[1]) << 32;   // field bits 0..63
+        uint32_t ihi = e.field[2];                                               // and 64..79
         wave_sync();
-        double s = 0.0;
+        const double2 xa = *reinterpret_cast<const double2*>(xh + 2 * g);
+        const double2 xb = *reinterpret_cast<const double2*>(xh + 2 * g + 32);
+        bool first = true;
+        for (uint32_t m = flags & 0xFFFFu; m != 0u; m &= m - 1u) {
+            const uint32_t b = static_cast<uint32_t>(__ffs(m) - 1);
+            double p[16];
+            if (PREFETCH && first) {
 #pragma unroll
-        for (int c = 0; c < 16; ++c) s = __builtin_fma(pr[c], R.xh[p][16 * k + c], s);
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        float rho = static_cast<float>(s);
-        if (valid && !f32_rounding_stable(s, 0x1p-46)) {   // the reference's order: fl64 products, sequential fl64 sum
-            double a = 0.0;
-            for (int c = 0; c < DIM; ++c) {
-                const double prod = prow[c] * R.xh[p][c];
-                a = a + prod;
+                for (int c = 0; c < 16; ++c) p[c] = d.p[c];
+            } else {
+                load_rows(b, p);
             }
-            rho = static_cast<float>(a);
-        }
-        const int gb = 16 * static_cast<int>(p);
-        const float s0 = __shfl(rho, gb), s1 = __shfl(rho, gb + 4), s2 = __shfl(rho, gb + 8), s3 = __shfl(rho, gb + 12);
-        // AVX2 distances (cw - s, (d0^2 + d1^2) + (d2^2 + d3^2)) to codewords 2g, 2g + 1
-        float bd = 0.0f;
-        uint32_t bw = 0;
+            first = false;
+            float rho[4];
 #pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            const float4 cw = w ? cw1 : cw0;
-            const float e0 = cw.x - s0, e1 = cw.y - s1, e2 = cw.z - s2, e3 = cw.w - s3;
-            const float dd = (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
-            if (w == 0 || dd < bd) { bd = dd; bw = 2 * g + w; }
-        }
-        // the first codeword with the smallest distance over the 16 lanes
+            for (int r = 0; r < 4; ++r) {
+                double s = __builtin_fma(p[4 * r], xa.x, 0.0);
+                s = __builtin_fma(p[4 * r + 1], xa.y, s);
+                s = __builtin_fma(p[4 * r + 2], xb.x, s);
+                s = __builtin_fma(p[4 * r + 3], xb.y, s);
+                s += dpp_f64<DPP_QUAD_XOR1>(s);
+                s += dpp_f64<DPP_QUAD_XOR2>(s);
+                s += dpp_f64<DPP_HALF_MIRROR>(s);
+                s += dpp_f64<DPP_MIRROR>(s);
+                rho[r] = static_cast<float>(s);
+                if (!f32_rounding_stable(s, 0x1p-46)) {   // the reference's order: fl64 products, sequential fl64 sum
+                    const double* prow = rot64 + static_cast<size_t>(4u * b + static_cast<uint32_t>(r)) * DIM;
+                    double a = 0.0;
+                    for (int c = 0; c < DIM; ++c) {
+                        const double prod = prow[c] * xh[c];
+                        a = a + prod;
+                    }
+                    rho[r] = static_cast<float>(a);
+                }
+            }
+            // AVX2 distances (cw - s, (d0^2 + d1^2) + (d2^2 + d3^2)) to codewords 2g, 2g + 1
+            float bd = 0.0f;
+            uint32_t bw = 0;
 #pragma unroll
-        for (int sh = 1; sh < 16; sh <<= 1) {
-            const float od = __shfl_xor(bd, sh);
-            const uint32_t ow = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bw), sh));
-            if (od < bd || (od == bd && ow < bw)) { bd = od; bw = ow; }
-        }
-        if (valid && g == 0) {   // index b at payload bits 16 + 5b (after the f16 norm), LSB-first
-            const uint32_t bit = 16u + 5u * b, wd = bit >> 5, sh = bit & 31u;
-            uint32_t* pw = ring + (ent & 0x7FFFu) + wd;
-            atomicAnd(pw, ~(31u << sh));
-            atomicOr(pw, bw << sh);
-            if (sh > 27u) {
-                atomicAnd(pw + 1, ~(31u >> (32u - sh)));
-                atomicOr(pw + 1, bw >> (32u - sh));
+            for (int w = 0; w < 2; ++w) {
+                const float4 cw = w ? cw1 : cw0;
+                const float e0 = cw.x - rho[0], e1 = cw.y - rho[1], e2 = cw.z - rho[2], e3 = cw.w - rho[3];
+                const float dd = (e0 * e0 + e1 * e1) + (e2 * e2 + e3 * e3);
+                if (w == 0 || dd < bd) { bd = dd; bw = 2 * g + w; }
+            }
+            // the first codeword with the smallest distance over the 16 lanes
+            argmin_step<DPP_QUAD_XOR1>(bd, bw);
+            argmin_step<DPP_QUAD_XOR2>(bd, bw);
+            argmin_step<DPP_HALF_MIRROR>(bd, bw);
+            argmin_step<DPP_MIRROR>(bd, bw);
+            const uint32_t pos = 5u * b;   // field bits pos .. pos + 4
+            if (pos + 5u <= 64u) {
+                ilo = (ilo & ~(31ull << pos)) | (static_cast<uint64_t>(bw) << pos);
+            } else if (pos >= 64u) {
+                ihi = (ihi & ~(31u << (pos - 64u))) | (bw << (pos - 64u));
+            } else {   // bits pos .. 63 in ilo, the rest in ihi
+                ilo = (ilo & ~(~0ull << pos)) | (static_cast<uint64_t>(bw) << pos);
+                ihi = (ihi & ~(31u >> (64u - pos))) | (bw >> (64u - pos));
             }
         }
-        wave_sync();   // R.xh is rewritten by the next pass
+        if (g == 0) {
+            e.field[0] = static_cast<uint32_t>(ilo);
+            e.field[1] = static_cast<uint32_t>(ilo >> 32);
+            e.field[2] = ihi;
+        }
+        wave_sync();   // xh is rewritten in the group's next round
+    };
+    const uint32_t rounds = (nq + 3u) / 4u;
+    if constexpr (PREFETCH) {
+        In da, db;
+        fetch(0, da);
+        for (uint32_t j = 0; j < rounds; j += 2) {   // two rounds per pass: no register copies of loads in flight
+            fetch(j + 1, db);
+            redo(j, da);
+            fetch(j + 2, da);
+            redo(j + 1, db);
+        }
+    } else {
+        for (uint32_t j = 0; j < rounds; ++j) {
+            In d;
+            fetch(j, d);
+            redo(j, d);
+        }
     }
+    wave_sync();
+    if (static_cast<uint32_t>(lane) < nq) {   // lane i writes entry i's index field
+        const FibRedoEntry& e = list[lane];
+        const uint64_t lo = e.field[0] | static_cast<uint64_t>(e.field[1]) << 32;
+        const uint16_t hi = static_cast<uint16_t>(e.field[2]);
+        __builtin_memcpy(wire + e.field_off, &lo, 8);
+        __builtin_memcpy(wire + e.field_off + 8, &hi, 2);
+    }
+    wave_sync();   // the list is refilled
 }
 
 // FibQuantizer::encode_batch (codec.rs:578-668) + finish_batch_encode
 // (670-729) + FibCodeV1::encode_batch (225-320) for every segment.  Each wave
 // walks 32-vector units (unit u: 256-vector tile u / 8 of the segment table,
 // eighth u % 8) with a stride of the whole grid; the next unit's rows are
-// loaded while the current one is scored.  A unit's payloads wait in the
-// wave's LDS ring with its undecided blocks queued; every FIB_RING units (or
-// when the queue could overflow, or at the wave's last unit) the queue is
-// redone exactly and the ring's payloads are written.  No workgroup barrier
-// after the rotation operands are in LDS: the waves never wait for each other.
+// loaded while the current one is scored, and each unit's payloads leave as
+// one byte range.  A vector with undecided blocks goes to the wave's LDS list
+// with a copy of its index field; the wave redoes its list after its last
+// unit, or earlier when the next unit could overflow it.  No workgroup
+// barrier after the rotation operands are in LDS: the waves never wait for
+// each other.
 template <int DIM, bool DIAG>
 __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void fib_encode_kernel(LaunchCommon lc,
     const void* __restrict__ in, uint8_t* __restrict__ wire, const uint32_t* __restrict__ mf, float thr,
     const double* __restrict__ rot64, const float* __restrict__ cb, uint32_t nunits) {
     static_assert(DIM == 64, "the MFMA layout is built for head_dim 64");
     extern __shared__ uint32_t smem_u[];
-    __shared__ FibRedoLds redo_lds[WAVES];
     uint32_t* rot_lds = smem_u;   // MF_ROT block (MF_SCA words)
     // wave index as a wave-uniform value: the unit loop, its segment lookups
     // and offsets then stay scalar
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int h = lane >> 5, n = lane & 31;
-    uint32_t* ring = smem_u + MF_SCA + wave * FIB_RING * FIB_PAY_WORDS;
-    FibRedoLds& R = redo_lds[wave];
+    uint32_t* pay = smem_u + MF_SCA + wave * FIB_PAY_WORDS;
+    FibRedoEntry* list = reinterpret_cast<FibRedoEntry*>(smem_u + MF_SCA + WAVES * FIB_PAY_WORDS) + wave * FIB_LCAP;
+    double* xh = reinterpret_cast<double*>(reinterpret_cast<FibRedoEntry*>(smem_u + MF_SCA + WAVES * FIB_PAY_WORDS) +
+                                           WAVES * FIB_LCAP) + wave * 4 * DIM;
     const bool bf16 = lc.in_bf16 != 0;
     {
         const uint4* src = reinterpret_cast<const uint4*>(mf + MF_ROT);
@@ -2996,7 +3075,7 @@ __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void 
         const SegDev s = lc.segs[sidx];
         load_half_row(x, in, bf16, s, min(v0 + static_cast<uint32_t>(n), s.n_vectors - 1), h);
     }
-    uint32_t used = 0, nq = 0;   // ring slots filled, queued vectors
+    uint32_t nq = 0;   // listed vectors
     while (u < nunits) {   // wave-uniform
         {   // a wave near its last units steps down so the ones with more left issue
             // first (the arbiter otherwise favours the oldest waves, which then
@@ -3008,7 +3087,6 @@ __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void 
             else __builtin_amdgcn_s_setprio(0);
         }
         const SegDev seg = lc.segs[sidx];
-        uint32_t* pay = ring + used * FIB_PAY_WORDS;
         FibTileRot t;
         fib_encode_rotate(t, x, rot_lds, lane);
         __builtin_amdgcn_sched_barrier(0);
@@ -3019,45 +3097,40 @@ __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void 
             load_half_row(x, in, bf16, s2, min(v02 + static_cast<uint32_t>(n), s2.n_vectors - 1), h);
         }
         const uint32_t mask = fib_encode_score<DIM, DIAG>(lc, seg, sidx, v0, t, pay, sa, thr, lane);
-        // queue this unit's undecided vectors
+        wave_sync();   // the unit's payloads are in LDS
+        // list this unit's undecided vectors, with their index fields
         const bool small = seg.n_vectors < 4 || lc.per_vector != 0;
         const bool queued = h == 0 && mask != 0u;
         const uint64_t bal = __ballot(queued);
         if (queued) {
-            const uint32_t slot = nq + static_cast<uint32_t>(__popcll(bal & ((1ull << lane) - 1ull)));
-            R.ent[slot] = (used * FIB_PAY_WORDS + 3u * static_cast<uint32_t>(n)) | (small ? 1u << 15 : 0u) |
-                          (mask << 16);
-            R.off[slot] = vec_elem_offset(seg, v0 + static_cast<uint32_t>(n));
-            R.nrm[slot] = t.nrm;
+            const uint32_t vi = v0 + static_cast<uint32_t>(n);
+            const uint32_t w0 = pay[3 * n], w1 = pay[3 * n + 1], w2 = pay[3 * n + 2];
+            FibRedoEntry& en = list[nq + static_cast<uint32_t>(__popcll(bal & ((1ull << lane) - 1ull)))];
+            en.in_off = vec_elem_offset(seg, vi);
+            en.field_off = seg.wire_offset + 19u + 12ull * vi + 2u;   // payload bytes 2 .. 11
+            en.nrm = t.nrm;
+            en.flags = mask | (small ? 1u << 16 : 0u);
+            en.field[0] = (w0 >> 16) | (w1 << 16);
+            en.field[1] = (w1 >> 16) | (w2 << 16);
+            en.field[2] = w2 >> 16;
         }
         nq += static_cast<uint32_t>(__popcll(bal));
-        if (lane == 0) {
-            R.blob[used] = seg.wire_offset;
-            R.v0[used] = v0;
-            R.nv[used] = min(FIB_UNIT, seg.n_vectors - v0);
-            R.nvec[used] = seg.n_vectors;
-        }
-        ++used;
-        if (used == FIB_RING || nq > FIB_QCAP - FIB_UNIT || u2 >= nunits) {
-            wave_sync();
-            if (nq) fib_redo_flush<DIM>(lc, in, rot64, cb, ring, R, nq, lane);
-            wave_sync();
-            for (uint32_t q = 0; q < used; ++q) {
-                uint8_t* blob = wire + R.blob[q];
-                const uint32_t qv0 = R.v0[q];
-                lds_to_global(blob + 19 + static_cast<uint64_t>(qv0) * 12u, ring + q * FIB_PAY_WORDS, R.nv[q] * 12u,
-                              lane);
-                if (qv0 == 0 && lane < 19)
-                    blob[lane] =
-                        static_cast<uint8_t>(fb2_byte(static_cast<uint32_t>(lane), 5u, DIM / 4, R.nvec[q], 10u));
-            }
-            wave_sync();   // the ring and the queue are refilled
-            used = 0;
+        uint8_t* blob = wire + seg.wire_offset;
+        lds_to_global(blob + 19 + static_cast<uint64_t>(v0) * 12u, pay, min(FIB_UNIT, seg.n_vectors - v0) * 12u, lane);
+        if (v0 == 0 && lane < 19)
+            blob[lane] = static_cast<uint8_t>(fb2_byte(static_cast<uint32_t>(lane), 5u, DIM / 4, seg.n_vectors, 10u));
+        wave_sync();   // the payload words are rewritten by the next unit
+        if (nq > FIB_LCAP - FIB_UNIT) {   // the next unit could overflow the list
+            fib_redo_list<DIM, false>(lc, in, wire, rot64, cb, list, xh, nq, lane);
             nq = 0;
         }
         u = u2;
         sidx = sidx2;
         v0 = v02;
+    }
+    if (nq) {   // the list's rounds are latency-bound and short: issued ahead of the other waves' units
+        __builtin_amdgcn_s_setprio(3);
+        fib_redo_list<DIM, true>(lc, in, wire, rot64, cb, list, xh, nq, lane);
     }
 }
 
@@ -3681,7 +3754,8 @@ uint32_t persistent_grid(K kernel, size_t dyn_lds, uint32_t want) {
 int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, uint8_t* wire, uint32_t nblocks,
                       void* stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
-    constexpr size_t lds = (MF_SCA + WAVES * FIB_RING * FIB_PAY_WORDS) * sizeof(uint32_t);
+    constexpr size_t lds = (MF_SCA + WAVES * FIB_PAY_WORDS) * sizeof(uint32_t) +
+                           WAVES * (FIB_LCAP * sizeof(FibRedoEntry) + 4 * 64 * sizeof(double));
     const uint64_t units = static_cast<uint64_t>(nblocks) * FIB_UNITS_PER_TILE;
     if (units > 0xFFFFFFFFull) return hipErrorInvalidValue;
     const uint32_t want = static_cast<uint32_t>((units + WAVES - 1) / WAVES);

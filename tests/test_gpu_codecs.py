@@ -328,3 +328,24 @@ def test_fib_encode_near_ties_take_exact_path(ctx):
     x = np.array(xs, np.float32)
     blob = ad.encode_batch_compact(x, SEED)
     assert blob == O.fib_encode_batch(x, cb.astype(np.float32), rot)
+
+
+def test_fib_encode_full_wave_lists(ctx):
+    """300,000 vectors with every block near a codeword bisector: every
+    vector is undecided, each encode wave lists 32 per unit, and a wave with
+    more than two units redoes a full list in the middle of its unit loop
+    (the path ordinary data never takes) as well as after its last unit; the
+    bytes must still equal the reference's."""
+    ad = FibQuantAdapter(64, 4, 32, 2048, 4, 8)
+    cb, rot = O.fib_constants(SEED)
+    cb = cb.reshape(32, 4).astype(np.float64)
+    rot = rot.reshape(64, 64)
+    rng = np.random.RandomState(29)
+    n = 300_000
+    w1 = rng.randint(0, 32, (n, 16))
+    w2 = (w1 + rng.randint(1, 32, (n, 16))) % 32
+    t = 0.5 + rng.choice([0.0, 1e-9, -1e-9, 1e-7], (n, 16))
+    rho = t[..., None] * cb[w1] + (1 - t[..., None]) * cb[w2]
+    x = ((rho.reshape(n, 64) @ rot) * rng.uniform(0.5, 4.0, (n, 1))).astype(np.float32)
+    blob = ad.encode_batch_compact(x, SEED)
+    assert blob == O.fib_encode_batch(x, cb.astype(np.float32), rot)
