@@ -2794,6 +2794,7 @@ constexpr uint32_t FIB_LCAP = 96;                          // a wave's list of u
 // Lane permutations inside each row of 16 lanes (DPP, no LDS round trip):
 // quad xor 1, quad xor 2, i <-> 7 - i within 8, i <-> 15 - i within 16.
 constexpr int DPP_QUAD_XOR1 = 0xB1, DPP_QUAD_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+constexpr int DPP_ROW_ROR4 = 0x124, DPP_ROW_ROR8 = 0x128;   // rotate by 4 / 8 lanes within the 16
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
     return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
@@ -2841,13 +2842,15 @@ struct FibRedoEntry {
 //    (three roundings of at most 2^-53 relative and the reciprocal's
 //    2^-52), so if no f32 rounding boundary lies within that distance of q,
 //    f32(q) = f32(fl64(x / |x|)); otherwise the division is done.
-//  * rho_r: each lane's FMA chain over its four columns, then a 16-lane
-//    butterfly of adds, rounds every term at most 8 times, so it is within
-//    gamma_8 A of the exact sum, and the reference's sequential sum is within
-//    gamma_64 A, A = sum |Pi_rc x_hat_c| <= |Pi_r| |x_hat| < 1.01: the two
-//    differ by less than 96 * 2^-53; if no f32 rounding boundary lies within
-//    2^-46 of the fast result, f32 of it is the reference's rho_r; otherwise
-//    the row is summed in the reference's order.
+//  * rho_r: each lane's FMA chain over its four columns, then four levels of
+//    adds over the 16 lanes (two that halve the rows a lane keeps, then two
+//    rotations, after which lane 2 (r % 2) + r / 2 of the group holds row r),
+//    rounds every term at most 8 times, so it is within gamma_8 A of the
+//    exact sum, and the reference's sequential sum is within gamma_64 A,
+//    A = sum |Pi_rc x_hat_c| <= |Pi_r| |x_hat| < 1.01: the two differ by less
+//    than 96 * 2^-53; if no f32 rounding boundary lies within 2^-46 of the
+//    fast result, f32 of it is the reference's rho_r; otherwise that lane
+//    sums the row in the reference's order.
 // A vector is listed once, so every wave writes only its own vectors' index
 // fields (after the encode wrote their payloads: the same wave's stores to the
 // same bytes, in order).
@@ -2858,6 +2861,9 @@ __device__ __forceinline__ void fib_redo_list(const LaunchCommon& lc, const void
                                               uint32_t nq, int lane) {
     static_assert(DIM == 64, "16 lanes x 4 columns of 4 rows per 4-dimensional block");
     const uint32_t grp = static_cast<uint32_t>(lane) >> 4, g = static_cast<uint32_t>(lane) & 15u;
+    const bool b0 = (g & 1u) != 0, b1 = (g & 2u) != 0;
+    const uint32_t my_row = (b0 ? 2u : 0u) + (b1 ? 1u : 0u);   // the row whose sum this lane ends with (g < 4)
+    const int gb = lane & ~15;   // the group's first lane
     double* xh = xh_wave + grp * DIM;
     const bool bf16 = lc.in_bf16 != 0;
     const float4 cw0 = reinterpret_cast<const float4*>(cb)[2 * g], cw1 = reinterpret_cast<const float4*>(cb)[2 * g + 1];
@@ -2931,28 +2937,35 @@ __device__ __forceinline__ void fib_redo_list(const LaunchCommon& lc, const void
                 load_rows(b, p);
             }
             first = false;
-            float rho[4];
+            double sr[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                double s = __builtin_fma(p[4 * r], xa.x, 0.0);
-                s = __builtin_fma(p[4 * r + 1], xa.y, s);
-                s = __builtin_fma(p[4 * r + 2], xb.x, s);
-                s = __builtin_fma(p[4 * r + 3], xb.y, s);
-                s += dpp_f64<DPP_QUAD_XOR1>(s);
-                s += dpp_f64<DPP_QUAD_XOR2>(s);
-                s += dpp_f64<DPP_HALF_MIRROR>(s);
-                s += dpp_f64<DPP_MIRROR>(s);
-                rho[r] = static_cast<float>(s);
-                if (!f32_rounding_stable(s, 0x1p-46)) {   // the reference's order: fl64 products, sequential fl64 sum
-                    const double* prow = rot64 + static_cast<size_t>(4u * b + static_cast<uint32_t>(r)) * DIM;
-                    double a = 0.0;
-                    for (int c = 0; c < DIM; ++c) {
-                        const double prod = prow[c] * xh[c];
-                        a = a + prod;
-                    }
-                    rho[r] = static_cast<float>(a);
-                }
+                double t = __builtin_fma(p[4 * r], xa.x, 0.0);
+                t = __builtin_fma(p[4 * r + 1], xa.y, t);
+                t = __builtin_fma(p[4 * r + 2], xb.x, t);
+                sr[r] = __builtin_fma(p[4 * r + 3], xb.y, t);
             }
+            // lanes g, g ^ 1: even lanes keep rows 0, 1, odd lanes rows 2, 3
+            const double ka = b0 ? sr[2] : sr[0], kb = b0 ? sr[3] : sr[1];
+            const double ra = ka + dpp_f64<DPP_QUAD_XOR1>(b0 ? sr[0] : sr[2]);
+            const double rb = kb + dpp_f64<DPP_QUAD_XOR1>(b0 ? sr[1] : sr[3]);
+            // lanes g, g ^ 2: row 2 (g % 2) + (g / 2) % 2
+            double t = (b1 ? rb : ra) + dpp_f64<DPP_QUAD_XOR2>(b1 ? ra : rb);
+            // lanes g, g + 4, g + 8, g + 12 hold the same row
+            t += dpp_f64<DPP_ROW_ROR4>(t);
+            t += dpp_f64<DPP_ROW_ROR8>(t);
+            float rho_l = static_cast<float>(t);
+            if (!f32_rounding_stable(t, 0x1p-46)) {   // the reference's order: fl64 products, sequential fl64 sum
+                const double* prow = rot64 + static_cast<size_t>(4u * b + my_row) * DIM;
+                double a = 0.0;
+                for (int c = 0; c < DIM; ++c) {
+                    const double prod = prow[c] * xh[c];
+                    a = a + prod;
+                }
+                rho_l = static_cast<float>(a);
+            }
+            const float rho[4] = {__shfl(rho_l, gb), __shfl(rho_l, gb + 2), __shfl(rho_l, gb + 1),
+                                  __shfl(rho_l, gb + 3)};
             // AVX2 distances (cw - s, (d0^2 + d1^2) + (d2^2 + d3^2)) to codewords 2g, 2g + 1
             float bd = 0.0f;
             uint32_t bw = 0;
