@@ -12,7 +12,8 @@ Workloads (`--workload`, default config3):
            T, D] per layer and K|V, f32; decode: 2 launches; 3,221,225,472 B
            written).  The shell encode runs first, then the shell rehydrate on
            a second stream (on at most --side-workgroups workgroups) beside the
-           pool encode, then the pool rehydrate (`--serial-tiers`: in order).
+           pool encode (on at most --pool-workgroups), then the pool rehydrate
+           (`--serial-tiers`: in order).
   config0  one layer, turbo b=4 lossless: K and V [32 heads, 1024 tokens, 64]
            (seed 0) -> 2 TQB1 blobs -> f32
   config1  fib_k4_n32 pool: 24 layers x {K,V} x 32 heads x 800 tokens (seed 1)
@@ -603,7 +604,8 @@ def bench_config3(args):
     side = None if args.serial_tiers else torch.cuda.Stream()   # default priority
 
     def step():
-        plan.build_and_rehydrate(dev, bufs, cache, stream=stream, side=side, side_workgroups=args.side_workgroups)
+        plan.build_and_rehydrate(dev, bufs, cache, stream=stream, side=side, side_workgroups=args.side_workgroups,
+                                 pool_workgroups=args.pool_workgroups)
 
     def launches():
         pseg, sseg = plan._cache_segs
@@ -633,7 +635,7 @@ def bench_config3(args):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=torch.cuda.Stream()):
             plan.build_and_rehydrate(dev, bufs, cache, stream=torch.cuda.current_stream(), side=side,
-                                     side_workgroups=args.side_workgroups)
+                                     side_workgroups=args.side_workgroups, pool_workgroups=args.pool_workgroups)
         torch.cuda.synchronize()
         # a replay must reproduce the eager step's bytes: outputs spoiled first
         names_out = ("pool_wire", "shell_wire", "pool_status", "shell_status", "pool_cstatus", "shell_cstatus")
@@ -705,7 +707,8 @@ def bench_config3(args):
                    "cache_dtype": args.cache_dtype, "cache_copies": args.copies,
                    "tier_streams": 1 if args.serial_tiers else 2,
                    "hip_graph": graph_ok is not None,
-                   "side_workgroups": None if args.serial_tiers else args.side_workgroups},
+                   "side_workgroups": None if args.serial_tiers else args.side_workgroups,
+                   "pool_workgroups": None if args.serial_tiers else args.pool_workgroups},
         "hbm_fraction_codec": round(sum(alg.values()) / (step_gpu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "kernels_ms": {n: round(per[n], 4) for n in names},
         "kernels_gbs": {n: round(kern_gbs[n], 1) for n in names},
@@ -1121,8 +1124,11 @@ def main():
     ap.add_argument("--graph", action="store_true",
                     help="config3: replay one captured HIP graph per step instead of launching it eagerly "
                          "(checked against the eager step's bytes; slower here: 0.92 against 0.87 ms)")
-    ap.add_argument("--side-workgroups", type=int, default=1024,
+    ap.add_argument("--side-workgroups", type=int, default=512,
                     help="config3: workgroups of the shell-tier rehydrate while it overlaps the pool encode")
+    ap.add_argument("--pool-workgroups", type=int, default=640,
+                    help="config3: workgroups of the pool encode while the shell-tier rehydrate runs beside it "
+                         "(0: every workgroup slot)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1",

@@ -201,6 +201,19 @@ int pkv_encode_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, 
                         const void* d_in, uint64_t in_elems, const pkv_seg* segs, uint32_t nseg,
                         uint8_t* d_wire, uint64_t wire_bytes, uint32_t* d_status, void* stream);
 
+/* pkv_encode_segments on a bounded share of the GPU: the fib encode, a
+ * persistent grid that otherwise takes every workgroup slot of the device,
+ * runs on at most max_workgroups workgroups (0: no bound), its waves stepping
+ * over more 32-vector units, so a kernel queued on another stream (the shell
+ * rehydrate of the same step) keeps compute units beside it.  Turbo encodes
+ * (one workgroup per tile group) launch as by pkv_encode_segments.  No
+ * counterpart in the reference (its tiers run one after the other); for
+ * callers that overlap the pool and shell tiers of one pool build. */
+int pkv_encode_segments_bounded(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, int in_dtype,
+                                const void* d_in, uint64_t in_elems, const pkv_seg* segs, uint32_t nseg,
+                                uint8_t* d_wire, uint64_t wire_bytes, uint32_t max_workgroups,
+                                uint32_t* d_status, void* stream);
+
 /* Decode every segment into f32 at the segment's strided positions.
  * radii_codec: the TQB1 radii codec the caller expects (ignored for fib);
  * each header is checked against the profile and the segment on the device

@@ -46,7 +46,7 @@ EXPORTS = (
     "pkv_fib_profile_create_with_constants", "pkv_profile_destroy", "pkv_fib_decode_path", "pkv_turbo_constants",
     "pkv_fib_constants", "pkv_profile_constants", "pkv_payload_len", "pkv_header_len", "pkv_blob_len",
     "pkv_write_header",
-    "pkv_segments_status", "pkv_encode_segments", "pkv_decode_segments", "pkv_decode_segments_ex",
+    "pkv_segments_status", "pkv_encode_segments", "pkv_encode_segments_bounded", "pkv_decode_segments", "pkv_decode_segments_ex",
     "pkv_decode_segments_bounded", "pkv_decode_segments_noalloc",
     "pkv_encode_batch_compact",
     "pkv_decode_batch_compact", "pkv_parse_header", "pkv_record_len", "pkv_encode_vectors", "pkv_decode_vectors",
@@ -150,6 +150,7 @@ def _declare(L):
         "pkv_write_header": ([P, I32, U64, P, U64], I32),
         "pkv_segments_status": ([P, P, U32, P], I32),
         "pkv_encode_segments": ([P, P, I32, I32, P, U64, P, U32, P, U64, P, P], I32),
+        "pkv_encode_segments_bounded": ([P, P, I32, I32, P, U64, P, U32, P, U64, U32, P, P], I32),
         "pkv_decode_segments": ([P, P, I32, P, U64, P, U32, P, U64, P, P], I32),
         "pkv_decode_segments_ex": ([P, P, I32, P, U64, P, U32, P, I32, U64, U32, U64, P, P], I32),
         "pkv_decode_segments_bounded": ([P, P, I32, P, U64, P, U32, P, I32, U64, U32, U64, U32, P, P], I32),

@@ -1236,6 +1236,16 @@ int pkv_encode_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, 
                         d_status, static_cast<hipStream_t>(stream));
 }
 
+int pkv_encode_segments_bounded(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, int in_dtype,
+                                const void* d_in, uint64_t in_elems, const pkv_seg* segs, uint32_t nseg,
+                                uint8_t* d_wire, uint64_t wire_bytes, uint32_t max_workgroups, uint32_t* d_status,
+                                void* stream) {
+    if (!ctx) return PKV_ERR_INVALID_ARG;
+    std::lock_guard<std::mutex> lock(ctx->mu);
+    return run_segments_locked(ctx, prof, radii_codec, true, in_dtype, d_in, in_elems, segs, nseg, d_wire, wire_bytes,
+                               d_status, static_cast<hipStream_t>(stream), false, 1, 0, max_workgroups);
+}
+
 int pkv_decode_segments(pkv_ctx* ctx, const pkv_profile* prof, int radii_codec, const uint8_t* d_wire,
                         uint64_t wire_bytes, const pkv_seg* segs, uint32_t nseg, float* d_out, uint64_t out_elems,
                         uint32_t* d_status, void* stream) {

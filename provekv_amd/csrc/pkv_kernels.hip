@@ -3773,8 +3773,10 @@ int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, 
     if (units > 0xFFFFFFFFull) return hipErrorInvalidValue;
     const uint32_t want = static_cast<uint32_t>((units + WAVES - 1) / WAVES);
     auto kern = lc.diag ? fib_encode_kernel<64, true> : fib_encode_kernel<64, false>;
-    return launch_big_lds(kern, persistent_grid(kern, lds, want), lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot64,
-                          fd.codebook, static_cast<uint32_t>(units));
+    uint32_t grid = persistent_grid(kern, lds, want);
+    if (lc.grid_cap) grid = std::min(grid, lc.grid_cap);   // a bounded share of the GPU
+    return launch_big_lds(kern, grid, lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot64, fd.codebook,
+                          static_cast<uint32_t>(units));
 }
 
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, void* out, uint32_t nblocks,

@@ -262,9 +262,10 @@ class Profile:
         return status.data_ptr()
 
     def encode_segments(self, inp, segs: np.ndarray, wire, radii: int = L.RADII_F32, status=None,
-                        stream=None) -> None:
+                        stream=None, max_workgroups: int = 0) -> None:
         """Encode every segment of `segs` from device tensor `inp` (f32 or
-        bf16) into device uint8 tensor `wire` in one launch."""
+        bf16) into device uint8 tensor `wire` in one launch.  max_workgroups
+        > 0 bounds the fib encode's persistent grid (pkv_encode_segments_bounded)."""
         torch = _torch()
         segs = np.ascontiguousarray(segs, dtype=SEG_DTYPE)
         dtype = L.DT_BF16 if inp.dtype == torch.bfloat16 else L.DT_F32
@@ -275,6 +276,12 @@ class Profile:
         if not (inp.is_contiguous() and wire.is_contiguous()):
             raise ValueError("tensors must be contiguous")
         st = self._status_ptr(status, len(segs))
+        if max_workgroups:
+            rc = L.lib().pkv_encode_segments_bounded(self.ctx.ptr, self._ptr, radii, dtype, inp.data_ptr(),
+                                                     inp.numel(), segs.ctypes.data, len(segs), wire.data_ptr(),
+                                                     wire.numel(), max_workgroups, st, _stream_ptr(stream))
+            L.check(rc, "pkv_encode_segments_bounded")
+            return
         rc = L.lib().pkv_encode_segments(self.ctx.ptr, self._ptr, radii, dtype, inp.data_ptr(), inp.numel(),
                                          segs.ctypes.data, len(segs), wire.data_ptr(), wire.numel(), st,
                                          _stream_ptr(stream))

@@ -210,14 +210,15 @@ class TwoTierPlan:
         self._rehydrate_tier("shells", bufs, cache, stream)
 
     def build_and_rehydrate(self, corpus, bufs, cache: DeviceKVCache, stream=None, side=None,
-                            side_workgroups: int = 1024):
+                            side_workgroups: int = 512, pool_workgroups: int = 640):
         """One whole step: each tier's encode followed by its rehydrate into
         `cache`.  The tiers share nothing but the read-only corpus (disjoint
         wires, status words and cache token ranges), so with a `side` stream
         they overlap: the shell encode runs first on `stream`; then the shell
         rehydrate (HBM writes) runs on `side` on at most `side_workgroups`
-        workgroups while the pool encode (VALU and matrix cores) takes the rest
-        of the GPU on `stream`; then the pool rehydrate.  `stream` waits for
+        workgroups while the pool encode (VALU and matrix cores), on at most
+        `pool_workgroups` (0: every slot), takes the rest of the GPU on
+        `stream`; then the pool rehydrate.  `stream` waits for
         `side` at the end, so work queued after this call sees both tiers
         done.  Without `side` the four launches run in order on `stream`."""
         import torch
@@ -232,7 +233,8 @@ class TwoTierPlan:
         shells_encoded.record(main)
         side.wait_event(shells_encoded)
         self._rehydrate_tier("shells", bufs, cache, side, max_workgroups=side_workgroups)
-        self.fib.encode_segments(corpus, self.pool.enc, bufs["pool_wire"], status=bufs["pool_status"], stream=main)
+        self.fib.encode_segments(corpus, self.pool.enc, bufs["pool_wire"], status=bufs["pool_status"], stream=main,
+                                 max_workgroups=pool_workgroups)
         self._rehydrate_tier("pool", bufs, cache, main)
         join.record(side)
         main.wait_event(join)

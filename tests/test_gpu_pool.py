@@ -191,6 +191,43 @@ def test_bounded_turbo_decode_matches_full_grid(ctx, max_workgroups):
     assert err is not None and err.segment == 5 and err.index == 123
 
 
+@pytest.mark.parametrize("max_workgroups", [1, 5, 64, 640])
+def test_bounded_fib_encode_matches_full_grid(ctx, max_workgroups):
+    """pkv_encode_segments_bounded: the fib encode's persistent grid held to a
+    few workgroups (each wave then walks more units, and its list of
+    undecided vectors spans them) writes the same FB2 blobs as the full grid,
+    equal to the oracle's, and reports a non-finite input the same way; the
+    turbo encode ignores the bound."""
+    import torch
+    layers, heads, dim, prefix, agents = 3, 8, 64, 500, [30, 7]
+    corpus = synth.corpus_tokens(13, layers, heads, prefix + sum(agents), dim)
+    corpus[5, 1, 3, 1, 17] = np.inf   # token 5, layer 1, head 3, V: pool blob (layer 1, V), vector 5 * 8 + 3
+    plan = TwoTierPlan(ctx, layers, heads, dim, prefix, agents, seed=SEED)
+    dev = torch.from_numpy(corpus.reshape(-1)).cuda()
+    wires, stats, swires = [], [], []
+    for bound in (0, max_workgroups):
+        bufs = plan.alloc()
+        st = torch.zeros(2 * len(plan.pool.enc), dtype=torch.int32, device="cuda")
+        plan.fib.encode_segments(dev, plan.pool.enc, bufs["pool_wire"], status=st, max_workgroups=bound)
+        plan.turbo.encode_segments(dev, plan.shells.enc, bufs["shell_wire"], radii=plan.radii,
+                                   status=bufs["shell_status"], max_workgroups=bound)
+        torch.cuda.synchronize()
+        wires.append(bufs["pool_wire"].cpu())
+        swires.append(bufs["shell_wire"].cpu())
+        stats.append(st.cpu().numpy().view(np.uint32).copy())
+    assert torch.equal(wires[0], wires[1]) and torch.equal(swires[0], swires[1])
+    assert np.array_equal(stats[0], stats[1])
+    err = plan.fib.status_error(stats[1], plan.pool.enc)
+    assert err is not None and err.index == 5 * heads + 3
+    cb, rot = O.fib_constants(SEED)
+    for b, (_, layer, side, off, nbytes) in enumerate(plan.pool.blob_offsets):
+        if (layer, side) == (1, 1):
+            continue   # the rejected blob
+        x = np.ascontiguousarray(corpus[:prefix, layer, :, side, :]).reshape(-1, dim)
+        assert bytes(wires[1][off:off + nbytes].numpy()) == O.fib_encode_batch(x, cb.reshape(32, 4),
+                                                                              rot.reshape(64, 64))
+
+
 @pytest.mark.parametrize("max_workgroups,copies", [(1, 2), (3, 1), (7, 2), (5, 8)])
 def test_bounded_fib_decode_matches_full_grid(ctx, max_workgroups, copies):
     """The fib matrix-core decode on a bounded grid (workgroups looping over
