@@ -2728,16 +2728,28 @@ __device__ __forceinline__ uint32_t fib_encode_score(const LaunchCommon& lc, con
             b2 = min(b2, umed3(b1, kb, kB));
             b1 = min(b1, min(kb, kB));
         }
+        // merge the halves for the owner lanes (h = 0), whose results are the
+        // only ones used: with (a, b) = this block's two smallest keys in half
+        // 0 and (c, d) in half 1, the smallest is min(a, c) and the second
+        // min(max(a, c), min(b, d)).  Swapping (a1, a2) gives lanes 0-31 the
+        // pair (a, c) and lanes 32-63 (b, d); one more swap brings the upper
+        // lanes' min(b, d) down.  Only the smallest keys need the half bit
+        // (index bit 2) of their codeword; the gap test compares keys with
+        // their index bits in place, which the bound E already covers (31 ulp
+        // per key).
         const uint32_t hb = static_cast<uint32_t>(h) << 2;
-        a1 |= hb; a2 |= hb; b1 |= hb; b2 |= hb;
-        const auto pa = __builtin_amdgcn_permlane32_swap(a1, a1, false, false);
-        const auto pA = __builtin_amdgcn_permlane32_swap(a2, a2, false, false);
-        const auto pb = __builtin_amdgcn_permlane32_swap(b1, b1, false, false);
-        const auto pB = __builtin_amdgcn_permlane32_swap(b2, b2, false, false);
-        const uint32_t ka1 = min(pa[0], pa[1]), ka2 = min(max(pa[0], pa[1]), min(pA[0], pA[1]));
-        const uint32_t kb1 = min(pb[0], pb[1]), kb2 = min(max(pb[0], pb[1]), min(pB[0], pB[1]));
-        if (!(u2f(ka2 & ~31u) - u2f(ka1 & ~31u) > thr)) redo |= 1u << i;
-        if (!(u2f(kb2 & ~31u) - u2f(kb1 & ~31u) > thr)) redo |= 1u << (i + 8);
+        a1 |= hb;
+        b1 |= hb;
+        const auto pa = __builtin_amdgcn_permlane32_swap(a1, a2, false, false);
+        const auto pb = __builtin_amdgcn_permlane32_swap(b1, b2, false, false);
+        const uint32_t ma = min(pa[0], pa[1]), Ma = max(pa[0], pa[1]);
+        const uint32_t mb = min(pb[0], pb[1]), Mb = max(pb[0], pb[1]);
+        const auto qa2 = __builtin_amdgcn_permlane32_swap(ma, pa[0], false, false);
+        const auto qb2 = __builtin_amdgcn_permlane32_swap(mb, pb[0], false, false);
+        const uint32_t ka1 = qa2[0], ka2 = min(Ma, qa2[1]);
+        const uint32_t kb1 = qb2[0], kb2 = min(Mb, qb2[1]);
+        if (!(u2f(ka2) - u2f(ka1) > thr)) redo |= 1u << i;
+        if (!(u2f(kb2) - u2f(kb1) > thr)) redo |= 1u << (i + 8);
         ia |= static_cast<uint64_t>(ka1 & 31u) << (5 * i);
         ib |= static_cast<uint64_t>(kb1 & 31u) << (5 * i);
         // materialise this pair's decisions now: the optimiser would otherwise
