@@ -2550,11 +2550,10 @@ turbo_score_lut_kernel(
 
 
 // f16 halves of a, b by round-toward-zero: hi = (a_hi, b_hi), lo = the
-// rounded remainders; a - a_hi is exact in f32.
+// rounded remainders; a - a_hi is exact in f32 (one v_fma_mix_f32 each).
 __device__ __forceinline__ uint2 split2(float a, float b) {
-    const auto h = __builtin_amdgcn_cvt_pkrtz(a, b);
-    const float ra = a - static_cast<float>(h[0]), rb = b - static_cast<float>(h[1]);
-    return make_uint2(__builtin_bit_cast(uint32_t, h), __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(ra, rb)));
+    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+    return make_uint2(h, __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(sub_f16<0>(a, h), sub_f16<1>(b, h))));
 }
 
 __device__ __forceinline__ uint32_t umed3(uint32_t a, uint32_t b, uint32_t c) {
