@@ -2699,7 +2699,10 @@ __device__ __forceinline__ uint32_t fib_encode_score(const LaunchCommon& lc, con
         // B: (p0 hi, p1 hi), (p0 lo, p1 lo), (p0 hi, p1 hi), (1, 1) with
         // p0 = rho'[4b + h], p1 = rho'[4b + 2 + h]
         const uint2 qa = split2(acc0[2 * i], acc0[2 * i + 1]), qb = split2(acc1[2 * i], acc1[2 * i + 1]);
-        const v4u ba = {qa.x, qa.y, qa.x, 0x3C003C00u}, bb = {qb.x, qb.y, qb.x, 0x3C003C00u};
+        // (built by a shuffle: the tuples then take the split results in place, one copy each)
+        const v2u one2 = {0x3C003C00u, 0x3C003C00u};
+        const v4u ba = __builtin_shufflevector(v2u{qa.x, qa.y}, one2, 0, 1, 0, 2);
+        const v4u bb = __builtin_shufflevector(v2u{qb.x, qb.y}, one2, 0, 1, 0, 2);
         const v16f d0 = mfma16(sa, ba, zero16);
         const v16f d1 = mfma16(sa, bb, zero16);
         if constexpr (DIAG) {
