@@ -3053,7 +3053,8 @@ __device__ __forceinline__ void fib_redo_list(const LaunchCommon& lc, const void
 template <int DIM, bool DIAG>
 __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void fib_encode_kernel(LaunchCommon lc,
     const void* __restrict__ in, uint8_t* __restrict__ wire, const uint32_t* __restrict__ mf, float thr,
-    const double* __restrict__ rot64, const float* __restrict__ cb, uint32_t nunits) {
+    const double* __restrict__ rot64, const float* __restrict__ cb, uint32_t nunits,
+    const SegDev* __restrict__ segs, const uint32_t* __restrict__ tile_start) {
     static_assert(DIM == 64, "the MFMA layout is built for head_dim 64");
     extern __shared__ uint32_t smem_u[];
     uint32_t* rot_lds = smem_u;   // MF_ROT block (MF_SCA words)
@@ -3086,12 +3087,12 @@ __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void 
     // first unit the segment search continues forward from the previous unit's
     // segment (sidx on entry).
     auto next_unit = [&](uint32_t u, uint32_t& sidx, uint32_t& v0) -> uint32_t {
-        if (u < nunits && sidx == 0xFFFFFFFFu) sidx = find_segment(lc.tile_start, lc.nseg, u / FIB_UNITS_PER_TILE);
+        if (u < nunits && sidx == 0xFFFFFFFFu) sidx = find_segment(tile_start, lc.nseg, u / FIB_UNITS_PER_TILE);
         for (; u < nunits; u += stride) {
             const uint32_t tile = u / FIB_UNITS_PER_TILE;
-            while (sidx + 1 < lc.nseg && lc.tile_start[sidx + 1] <= tile) ++sidx;
-            v0 = (tile - lc.tile_start[sidx]) * TILE + (u % FIB_UNITS_PER_TILE) * FIB_UNIT;
-            if (v0 < lc.segs[sidx].n_vectors) return u;
+            while (sidx + 1 < lc.nseg && tile_start[sidx + 1] <= tile) ++sidx;
+            v0 = (tile - tile_start[sidx]) * TILE + (u % FIB_UNITS_PER_TILE) * FIB_UNIT;
+            if (v0 < segs[sidx].n_vectors) return u;
         }
         return nunits;
     };
@@ -3099,7 +3100,7 @@ __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void 
     uint32_t u = next_unit(blockIdx.x * WAVES + static_cast<uint32_t>(wave), sidx, v0);
     float4 x[8];
     if (u < nunits) {
-        const SegDev s = lc.segs[sidx];
+        const SegDev s = segs[sidx];
         load_half_row(x, in, bf16, s, min(v0 + static_cast<uint32_t>(n), s.n_vectors - 1), h);
     }
     uint32_t nq = 0;   // listed vectors
@@ -3113,14 +3114,14 @@ __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void 
             else if (rem == 2) __builtin_amdgcn_s_setprio(1);
             else __builtin_amdgcn_s_setprio(0);
         }
-        const SegDev seg = lc.segs[sidx];
+        const SegDev seg = segs[sidx];
         FibTileRot t;
         fib_encode_rotate(t, x, rot_lds, lane);
         __builtin_amdgcn_sched_barrier(0);
         uint32_t sidx2 = sidx, v02 = 0;
         const uint32_t u2 = next_unit(u + stride, sidx2, v02);
         if (u2 < nunits) {   // the next unit's rows land while this one is scored
-            const SegDev s2 = lc.segs[sidx2];
+            const SegDev s2 = segs[sidx2];
             load_half_row(x, in, bf16, s2, min(v02 + static_cast<uint32_t>(n), s2.n_vectors - 1), h);
         }
         const uint32_t mask = fib_encode_score<DIM, DIAG>(lc, seg, sidx, v0, t, pay, sa, thr, lane);
@@ -3790,7 +3791,7 @@ int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, 
     uint32_t grid = persistent_grid(kern, lds, want);
     if (lc.grid_cap) grid = std::min(grid, lc.grid_cap);   // a bounded share of the GPU
     return launch_big_lds(kern, grid, lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot64, fd.codebook,
-                          static_cast<uint32_t>(units));
+                          static_cast<uint32_t>(units), lc.segs, lc.tile_start);
 }
 
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, void* out, uint32_t nblocks,
