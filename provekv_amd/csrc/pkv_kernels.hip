@@ -3289,7 +3289,9 @@ template <int DIM, bool STAGED>
 __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, const uint8_t* __restrict__ wire,
                                                                void* __restrict__ out,
                                                                const float* __restrict__ rot32,
-                                                               const float* __restrict__ cb) {
+                                                               const float* __restrict__ cb,
+                                                               const SegDev* __restrict__ segs,
+                                                               const uint32_t* __restrict__ tile_start) {
     static_assert(DIM == 64, "two 32-column MFMA blocks");
     constexpr int BLOCKS = DIM / 4;
     constexpr uint32_t PLEN = 2 + (BLOCKS * 5 + 7) / 8;   // 12
@@ -3314,7 +3316,7 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
     const int wave = threadIdx.x >> 6;
     // one tile per workgroup, or (grid capped) a workgroup walks the tiles
     // blockIdx.x, blockIdx.x + gridDim.x, ... with the tables loaded once
-    const uint32_t nblk = lc.tile_start[lc.nseg];
+    const uint32_t nblk = tile_start[lc.nseg];
     for (uint32_t blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
     wave_sync();   // the previous tile's LDS reads are done
     // opaque per tile: the loop must not keep lane-derived addresses or table
@@ -3322,9 +3324,9 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
     int zoff = 0, lane = threadIdx.x & 63;
     asm volatile("" : "+s"(zoff), "+v"(lane));
     const int h = lane >> 5, n = lane & 31;
-    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
-    const SegDev seg = lc.segs[sidx];
-    const uint32_t tile = blk - lc.tile_start[sidx];
+    const uint32_t sidx = find_segment(tile_start, lc.nseg, blk);
+    const SegDev seg = segs[sidx];
+    const uint32_t tile = blk - tile_start[sidx];
     const uint32_t v0 = tile * TILE + wave * WAVE;
     const uint8_t* blob = wire + seg.wire_offset;
 
@@ -3799,10 +3801,12 @@ int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* w
     const uint32_t grid = lc.grid_cap ? std::min(nblocks, lc.grid_cap) : nblocks;
     if (fd.mfma_decode && lc.fanout > 1)
         hipLaunchKernelGGL((fib_decode_mfma_kernel<64, true>), dim3(grid), dim3(TILE), 0,
-                           static_cast<hipStream_t>(stream), lc, wire, out, fd.rot32, fd.codebook);
+                           static_cast<hipStream_t>(stream), lc, wire, out, fd.rot32, fd.codebook, lc.segs,
+                           lc.tile_start);
     else if (fd.mfma_decode)
         hipLaunchKernelGGL((fib_decode_mfma_kernel<64, false>), dim3(grid), dim3(TILE), 0,
-                           static_cast<hipStream_t>(stream), lc, wire, out, fd.rot32, fd.codebook);
+                           static_cast<hipStream_t>(stream), lc, wire, out, fd.rot32, fd.codebook, lc.segs,
+                           lc.tile_start);
     else
         hipLaunchKernelGGL(fib_decode_kernel<64>, dim3(nblocks), dim3(TILE), 0, static_cast<hipStream_t>(stream), lc,
                            wire, out, fd.rot32t, fd.codebook);
