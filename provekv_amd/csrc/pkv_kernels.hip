@@ -2691,8 +2691,12 @@ __device__ __forceinline__ uint32_t fib_encode_score(const LaunchCommon& lc, con
     const double nrm = t.nrm;
     const bool finite_all = t.finite_all, zero = t.zero;
 
-    uint64_t ia = 0, ib = 0;   // indices of blocks 0..7 and 8..15, 5 bits each
-    uint32_t redo = 0;
+    // Both decisions are shifted in by v_alignbit, one instruction per block:
+    // the 5-bit indices from the top (blocks 0..5 in ra, 6..7 in ra2, 8..13 in
+    // rb, 14..15 in rb2; the newest block highest) and the acceptance bits from
+    // the bottom (da, db: bit 0 the newest block, set when thr - gap < 0, which
+    // is gap > thr exactly: a difference's sign is never lost to rounding)
+    uint32_t ra = 0, ra2 = 0, rb = 0, rb2 = 0, da = 0, db = 0;
     const v16f zero16 = {};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {   // blocks i (row tile 0) and i + 8 (row tile 1)
@@ -2750,19 +2754,28 @@ __device__ __forceinline__ uint32_t fib_encode_score(const LaunchCommon& lc, con
         const auto qb2 = __builtin_amdgcn_permlane32_swap(mb, pb[0], false, false);
         const uint32_t ka1 = qa2[0], ka2 = min(Ma, qa2[1]);
         const uint32_t kb1 = qb2[0], kb2 = min(Mb, qb2[1]);
-        if (!(u2f(ka2) - u2f(ka1) > thr)) redo |= 1u << i;
-        if (!(u2f(kb2) - u2f(kb1) > thr)) redo |= 1u << (i + 8);
-        ia |= static_cast<uint64_t>(ka1 & 31u) << (5 * i);
-        ib |= static_cast<uint64_t>(kb1 & 31u) << (5 * i);
+        const float ta = thr - (u2f(ka2) - u2f(ka1)), tb = thr - (u2f(kb2) - u2f(kb1));
+        da = __builtin_amdgcn_alignbit(da, f2u(ta), 31);   // (da << 1) | sign(ta)
+        db = __builtin_amdgcn_alignbit(db, f2u(tb), 31);
+        if (i < 6) {
+            ra = __builtin_amdgcn_alignbit(ka1, ra, 5);     // (ra >> 5) | (ka1 << 27)
+            rb = __builtin_amdgcn_alignbit(kb1, rb, 5);
+        } else {
+            ra2 = __builtin_amdgcn_alignbit(ka1, ra2, 5);
+            rb2 = __builtin_amdgcn_alignbit(kb1, rb2, 5);
+        }
         // materialise this pair's decisions now: the optimiser would otherwise
         // sink every pair's tests and index packing past the loop and keep all
         // eight pairs' candidate keys live at once
-        asm volatile("" : "+v"(redo), "+v"(ia), "+v"(ib));
+        asm volatile("" : "+v"(da), "+v"(db), "+v"(ra), "+v"(ra2), "+v"(rb), "+v"(rb2));
         __builtin_amdgcn_sched_barrier(0);   // keep one block pair's results live at a time
     }
-    const uint64_t ilo = ia | (ib << 40);
-    const uint32_t iw[3] = {static_cast<uint32_t>(ilo), static_cast<uint32_t>(ilo >> 32),
-                            static_cast<uint32_t>(ib >> 24)};
+    // the 80-bit index field: blocks 0..5 = ra >> 2, 6..7 = x, 8..13 = rb >> 2,
+    // 14..15 = y at bits 0, 30, 40, 70
+    const uint32_t x = ra2 >> 22, y = rb2 >> 22;
+    const uint32_t iw[3] = {__builtin_amdgcn_alignbit(x, ra, 2), (x >> 2) | (rb << 6), (rb >> 26) | (y << 6)};
+    // undecided blocks: bit j of the bit-reversed da / db is block j's (j + 8's) acceptance
+    const uint32_t redo = (~(__builtin_bitreverse32(da) >> 24) & 0xFFu) | ((~(__builtin_bitreverse32(db) >> 24) & 0xFFu) << 8);
 
     // encode_norm Fp16Paper (codec.rs:994-1020)
     const uint16_t h16 = f32_to_f16(static_cast<float>(nrm));
