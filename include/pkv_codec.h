@@ -579,6 +579,9 @@ void pkv_host_angle_bins(const float* a, const float* b, uint64_t n, uint32_t pb
 void pkv_host_octant_bins(const float* a, const float* b, uint64_t n, uint32_t* bins, uint8_t* safe);
 void pkv_host_logf(const float* x, uint64_t n, float* out);
 void pkv_host_expf(const float* x, uint64_t n, float* out);
+/* The fib encode redo's test that f32 rounds every value within |v| 2^-50
+ * of v[i] like v[i] (1) or that the exact division must decide (0). */
+void pkv_host_f32_stable_rel50(const double* v, uint64_t n, uint8_t* out);
 /* BLAKE3 of host bytes on the host, with the compression the digest
  * kernels run (the fib digests' hash). */
 void pkv_host_blake3(const void* data, uint64_t len, uint8_t out[32]);

@@ -55,7 +55,7 @@ EXPORTS = (
     "pkv_radii_log_bound", "pkv_fb2_n_blocks", "pkv_lloyd_refine", "pkv_blake3_ranges", "pkv_blake3_layer_digests",
     "pkv_blake3_tier_digests", "pkv_blake3",
     "pkv_host_angle_bins", "pkv_host_octant_bins", "pkv_host_logf",
-    "pkv_host_expf", "pkv_code_from_json", "pkv_fib_digests", "pkv_host_blake3",
+    "pkv_host_expf", "pkv_host_f32_stable_rel50", "pkv_code_from_json", "pkv_fib_digests", "pkv_host_blake3",
 )
 
 
@@ -180,6 +180,7 @@ def _declare(L):
         "pkv_host_angle_bins": ([P, P, U64, U32, P], None),
         "pkv_host_octant_bins": ([P, P, U64, P, P], None),
         "pkv_host_logf": ([P, U64, P], None),
+        "pkv_host_f32_stable_rel50": ([P, U64, P], None),
         "pkv_host_expf": ([P, U64, P], None),
         "pkv_code_from_json": ([P, P, U64, P, U64, P, P], I32),
         "pkv_fib_digests": ([P, P, P, P], I32),

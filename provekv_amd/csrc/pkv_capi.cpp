@@ -2104,4 +2104,8 @@ void pkv_host_expf(const float* x, uint64_t n, float* out) {
     for (uint64_t i = 0; i < n; ++i) out[i] = og_expf(x[i], tab);
 }
 
+void pkv_host_f32_stable_rel50(const double* v, uint64_t n, uint8_t* out) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = f32_rounding_stable_rel50(v[i]) ? 1 : 0;
+}
+
 }  // extern "C"

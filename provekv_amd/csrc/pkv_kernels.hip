@@ -2867,8 +2867,9 @@ struct FibRedoEntry {
 // Both roundings are taken from faster forms that provably round the same:
 //  * x_hat: q = x * fl64(1 / |x|) is within 2^-50 |q| of fl64(x / |x|)
 //    (three roundings of at most 2^-53 relative and the reciprocal's
-//    2^-52), so if no f32 rounding boundary lies within that distance of q,
-//    f32(q) = f32(fl64(x / |x|)); otherwise the division is done.
+//    2^-52), so if no f32 rounding boundary lies within that distance of q
+//    (tested on q's bits, f32_rounding_stable_rel50), f32(q) =
+//    f32(fl64(x / |x|)); otherwise the division is done.
 //  * rho_r: each lane's FMA chain over its four columns, then four levels of
 //    adds over the 16 lanes (two that halve the rows a lane keeps, then two
 //    rotations, after which lane 2 (r % 2) + r / 2 of the group holds row r),
@@ -2942,7 +2943,7 @@ __device__ __forceinline__ void fib_redo_list(const LaunchCommon& lc, const void
                 } else {
                     const double qq = xd * rinv;
                     float y = static_cast<float>(qq);
-                    if (!f32_rounding_stable(qq, __builtin_fabs(qq) * 0x1p-50)) y = static_cast<float>(xd / nv);
+                    if (!f32_rounding_stable_rel50(qq)) y = static_cast<float>(xd / nv);   // |qq| <= 1 + 2^-50
                     x1 = static_cast<double>(y);
                 }
                 xh[4 * g + q] = x1;

@@ -34,6 +34,19 @@ PKV_HD double u2d(uint64_t u) { return __builtin_bit_cast(double, u); }
 PKV_HD float fabs_f(float x) { return u2f(f2u(x) & 0x7fffffffu); }
 PKV_HD bool isfinite_f(float x) { return (f2u(x) & 0x7f800000u) != 0x7f800000u; }
 
+// f32_rounding_stable(v, |v| 2^-50), read off v's bits, for 2^-126 <= |v| <
+// 2^127: the f32 rounding boundaries inside v's binade [2^e, 2^(e+1)) are the
+// values whose low 29 f64 mantissa bits are 2^28 (the one below the binade
+// lies 2^(e-25) away), and |v| 2^-50 < 8 ulp64(v), so a distance of more
+// than 8 ulp64 from the nearest such value leaves every value within |v|
+// 2^-50 rounding like v.  False below 2^-126 (zero included): the caller then
+// takes its exact path.
+PKV_HD bool f32_rounding_stable_rel50(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(b), hi = static_cast<uint32_t>(b >> 32) & 0x7fffffffu;
+    return hi >= 0x38100000u && (lo & 0x1fffffffu) - 0x10000000u + 8u > 16u;
+}
+
 // ---------------------------------------------------------------- atan2f
 // fdlibm s_atanf.c / e_atan2f.c (single precision).
 PKV_HD float fd_atanf(float x) {

@@ -252,3 +252,51 @@ def test_read_fb2_n_blocks():
     assert read_fb2_n_blocks(b"") is None
     assert read_fb2_n_blocks(b"TQB1" + bytes(hdr[4:])) is None
     assert read_fb2_n_blocks(b"FB2\x07" + bytes(hdr[4:])) == 0x01020304   # version not checked either
+
+
+def _stable_rel50(v):
+    v = np.ascontiguousarray(v, np.float64)
+    out = np.zeros(v.size, np.uint8)
+    L.lib().pkv_host_f32_stable_rel50(v.ctypes.data, v.size, out.ctypes.data)
+    return out.astype(bool)
+
+
+def test_redo_xhat_stability_test_is_sufficient():
+    """The fib encode redo keeps f32(q) for q = x * fl64(1 / |x|) only when
+    the bit test says no f32 rounding boundary (midpoint of two adjacent f32
+    values, ties included) lies within |q| 2^-50 of q; here every value it
+    accepts is checked exactly, in rationals, against its two neighbouring
+    midpoints -- on values placed 0..40 f64 ulps either side of midpoints,
+    of f32 values themselves, of binade edges and of 2^-126 (below which it
+    must refuse), signs mixed.  It must also accept almost every random q,
+    or the redo would divide far more often than it needs to."""
+    from fractions import Fraction
+    rng = np.random.RandomState(5)
+    base = []
+    ys = rng.randint(0x00800000, 0x3f800001, size=3000).astype(np.uint32).view(np.float32).astype(np.float64)
+    yn = np.nextafter(ys.astype(np.float32), np.float32(np.inf)).astype(np.float64)
+    base.append((ys + yn) / 2)                                    # midpoints (exact in f64)
+    base.append(ys)                                               # f32 values
+    base.append(np.ldexp(1.0, np.arange(-130, 2)).astype(np.float64))   # binade edges, 2^-126 among them
+    base = np.concatenate(base)
+    k = np.concatenate([np.arange(-40, 41), [-(1 << 20), 1 << 20]]).astype(np.int64)
+    bits = (base.view(np.int64)[:, None] + k[None, :]).reshape(-1)
+    v = bits.view(np.float64)
+    v = v[np.isfinite(v) & (v > 0)]
+    v = np.concatenate([v, -v[::7], [0.0, -0.0, 5e-324]])
+    ok = _stable_rel50(v)
+    assert not ok[np.abs(v) < 2.0 ** -126].any()
+    acc = v[ok]
+    assert acc.size > 0.5 * v.size
+    for q in acc:
+        a = abs(float(q))
+        y = np.float32(a)
+        lo = float(np.nextafter(y, np.float32(0)))
+        hi = float(np.nextafter(y, np.float32(np.inf)))
+        fa, fy = Fraction(a), Fraction(float(y))
+        err = fa * Fraction(1, 1 << 50)
+        m_lo, m_hi = (fy + Fraction(lo)) / 2, (fy + Fraction(hi)) / 2
+        assert m_hi - fa > err and fa - m_lo > err, q
+    # random rotated components: refused about 17 times in 2^29
+    r = rng.standard_normal(200_000) / 8.0
+    assert _stable_rel50(r).mean() > 0.9999
