@@ -2563,10 +2563,11 @@ __device__ __forceinline__ uint32_t umed3(uint32_t a, uint32_t b, uint32_t c) {
 }
 
 // Elements 32h .. 32h + 31 of vector vi as 8 float4 (f32, or bf16 widened);
-// all loads are issued before any use.
-__device__ __forceinline__ void load_half_row(float4 (&v)[8], const void* __restrict__ in, bool bf16,
-                                              const SegDev& s, uint32_t vi, int h) {
-    const uint64_t off = vec_elem_offset(s, vi) + 32u * static_cast<uint32_t>(h);
+// all loads are issued before any use.  Returns the vector's first element.
+__device__ __forceinline__ uint64_t load_half_row(float4 (&v)[8], const void* __restrict__ in, bool bf16,
+                                                  const SegDev& s, uint32_t vi, int h) {
+    const uint64_t row = vec_elem_offset(s, vi);
+    const uint64_t off = row + 32u * static_cast<uint32_t>(h);
     if (!bf16) {
         const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(in) + off);
 #pragma unroll
@@ -2584,6 +2585,7 @@ __device__ __forceinline__ void load_half_row(float4 (&v)[8], const void* __rest
                                        u2f(w[k].w & 0xffff0000u));
         }
     }
+    return row;
 }
 
 // Value of `x` in lane (l % 32) + 32 * from_h, for every lane l.
@@ -3113,9 +3115,10 @@ __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void 
     uint32_t sidx = 0xFFFFFFFFu, v0 = 0;
     uint32_t u = next_unit(blockIdx.x * WAVES + static_cast<uint32_t>(wave), sidx, v0);
     float4 x[8];
+    uint64_t xrow = 0;   // first element of the vector whose rows x holds
     if (u < nunits) {
         const SegDev s = segs[sidx];
-        load_half_row(x, in, bf16, s, min(v0 + static_cast<uint32_t>(n), s.n_vectors - 1), h);
+        xrow = load_half_row(x, in, bf16, s, min(v0 + static_cast<uint32_t>(n), s.n_vectors - 1), h);
     }
     uint32_t nq = 0;   // listed vectors
     while (u < nunits) {   // wave-uniform
@@ -3129,6 +3132,7 @@ __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void 
             else __builtin_amdgcn_s_setprio(0);
         }
         const SegDev seg = segs[sidx];
+        const uint64_t row = xrow;
         FibTileRot t;
         fib_encode_rotate(t, x, rot_lds, lane);
         __builtin_amdgcn_sched_barrier(0);
@@ -3136,7 +3140,7 @@ __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void 
         const uint32_t u2 = next_unit(u + stride, sidx2, v02);
         if (u2 < nunits) {   // the next unit's rows land while this one is scored
             const SegDev s2 = segs[sidx2];
-            load_half_row(x, in, bf16, s2, min(v02 + static_cast<uint32_t>(n), s2.n_vectors - 1), h);
+            xrow = load_half_row(x, in, bf16, s2, min(v02 + static_cast<uint32_t>(n), s2.n_vectors - 1), h);
         }
         const uint32_t mask = fib_encode_score<DIM, DIAG>(lc, seg, sidx, v0, t, pay, sa, thr, lane);
         wave_sync();   // the unit's payloads are in LDS
@@ -3148,7 +3152,7 @@ __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void 
             const uint32_t vi = v0 + static_cast<uint32_t>(n);
             const uint32_t w0 = pay[3 * n], w1 = pay[3 * n + 1], w2 = pay[3 * n + 2];
             FibRedoEntry& en = list[nq + static_cast<uint32_t>(__popcll(bal & ((1ull << lane) - 1ull)))];
-            en.in_off = vec_elem_offset(seg, vi);
+            en.in_off = row;   // (a listed lane is active: its vector's own offset)
             en.field_off = seg.wire_offset + 19u + 12ull * vi + 2u;   // payload bytes 2 .. 11
             en.nrm = t.nrm;
             en.flags = mask | (small ? 1u << 16 : 0u);
