@@ -352,13 +352,21 @@ int acquire_slot(pkv_ctx* ctx, size_t total, Slot** out) {
 // over the same segments (every step of a serving loop) upload nothing.  A
 // caller on another stream than the one that uploaded the table waits (on the
 // device) for that upload unless the host has already seen it complete.
+// Tables up to this many tiles also get a per-tile segment map (one scalar
+// load per workgroup instead of a binary search of the tile prefix).
+constexpr uint64_t kMaxMapTiles = 1u << 20;
+
 int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vector<uint32_t>& tiles,
                 bool need_status, hipStream_t stream, Slot** out_slot, SegDev** d_segs, uint32_t** d_tiles,
-                uint32_t** d_status) {
+                uint32_t** d_status, uint32_t** d_map) {
     const size_t seg_bytes = sizeof(pkv_seg) * nseg;
     const size_t tile_bytes = sizeof(uint32_t) * (nseg + 1);
+    const uint64_t ntiles = tiles[nseg];
+    const bool with_map = ntiles <= kMaxMapTiles;
     const size_t tile_off = (seg_bytes + 255) & ~static_cast<size_t>(255);
-    const size_t stat_off = (tile_off + tile_bytes + 255) & ~static_cast<size_t>(255);
+    const size_t map_off = (tile_off + tile_bytes + 255) & ~static_cast<size_t>(255);
+    const size_t map_bytes = with_map ? sizeof(uint32_t) * ntiles : 0;
+    const size_t stat_off = (map_off + map_bytes + 255) & ~static_cast<size_t>(255);
     const size_t total = stat_off + (need_status ? sizeof(uint32_t) * 2 * nseg : 0) + 256;
     const uint64_t hash = fnv1a(segs, seg_bytes);
     if (!need_status) {
@@ -373,6 +381,7 @@ int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vec
                 auto* d = static_cast<uint8_t*>(c.dev);
                 *d_segs = reinterpret_cast<SegDev*>(d);
                 *d_tiles = reinterpret_cast<uint32_t*>(d + tile_off);
+                *d_map = with_map ? reinterpret_cast<uint32_t*>(d + map_off) : nullptr;
                 *d_status = nullptr;
                 *out_slot = &c;
                 return PKV_OK;
@@ -386,6 +395,10 @@ int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vec
     auto* h = static_cast<uint8_t*>(sl.host);
     std::memcpy(h, segs, seg_bytes);
     std::memcpy(h + tile_off, tiles.data(), tile_bytes);
+    if (with_map) {
+        auto* m = reinterpret_cast<uint32_t*>(h + map_off);
+        for (uint32_t i = 0; i < nseg; ++i) std::fill(m + tiles[i], m + tiles[i + 1], i);
+    }
     HIP_TRY(hipMemcpyAsync(sl.dev, sl.host, stat_off, hipMemcpyHostToDevice, stream));
     HIP_TRY(hipEventRecord(sl.up_ev, stream));
     sl.up_stream = stream;
@@ -396,6 +409,7 @@ int stage_table(pkv_ctx* ctx, const pkv_seg* segs, uint32_t nseg, const std::vec
     auto* d = static_cast<uint8_t*>(sl.dev);
     *d_segs = reinterpret_cast<SegDev*>(d);
     *d_tiles = reinterpret_cast<uint32_t*>(d + tile_off);
+    *d_map = with_map ? reinterpret_cast<uint32_t*>(d + map_off) : nullptr;
     *d_status = need_status ? reinterpret_cast<uint32_t*>(d + stat_off) : nullptr;
     *out_slot = &sl;
     return PKV_OK;
@@ -452,12 +466,13 @@ FibDev fib_dev(const pkv_profile* p) {
 int launch_segments(const pkv_profile* prof, int radii, bool encode, int dtype, const void* d_f32,
                     const uint8_t* d_wire, const SegDev* dsegs, const uint32_t* dtiles, uint32_t nseg,
                     uint32_t nblocks, uint32_t* status, bool per_vector, uint32_t fanout, uint64_t fanout_stride,
-                    uint32_t grid_cap, hipStream_t stream, float* diag = nullptr) {
+                    uint32_t grid_cap, hipStream_t stream, float* diag = nullptr, const uint32_t* dmap = nullptr) {
     int e = launch_fill_u32(status, STATUS_NONE, 2ull * nseg, stream);
     if (e) return e;
     LaunchCommon lc;
     lc.segs = dsegs;
     lc.tile_start = dtiles;
+    lc.tile_seg = dmap;
     lc.nseg = nseg;
     lc.status = status;
     lc.radii = static_cast<uint32_t>(radii);
@@ -508,12 +523,12 @@ int run_segments_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, bool e
     }
     Slot* sl;
     SegDev* dsegs;
-    uint32_t *dtiles, *dstat;
-    rc = stage_table(ctx, segs, nseg, tiles, d_status == nullptr, stream, &sl, &dsegs, &dtiles, &dstat);
+    uint32_t *dtiles, *dstat, *dmap;
+    rc = stage_table(ctx, segs, nseg, tiles, d_status == nullptr, stream, &sl, &dsegs, &dtiles, &dstat, &dmap);
     if (rc) return rc;
     uint32_t* status = d_status ? d_status : dstat;
     const int e = launch_segments(prof, radii, encode, dtype, d_f32, d_wire, dsegs, dtiles, nseg, tiles[nseg], status,
-                                  per_vector, fanout, fanout_stride, grid_cap, stream, diag);
+                                  per_vector, fanout, fanout_stride, grid_cap, stream, diag, dmap);
     int rc2 = finish_slot(sl, stream);
     if (e) return hip_status(static_cast<hipError_t>(e));
     if (rc2 || d_status) return rc2;
@@ -1757,8 +1772,8 @@ int score_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, const uint8_t
     if (rc) return rc;
     Slot* sl;
     SegDev* dsegs;
-    uint32_t *dtiles, *dstat;
-    rc = stage_table(ctx, segs, nseg, tiles, d_status == nullptr, stream, &sl, &dsegs, &dtiles, &dstat);
+    uint32_t *dtiles, *dstat, *dmap;
+    rc = stage_table(ctx, segs, nseg, tiles, d_status == nullptr, stream, &sl, &dsegs, &dtiles, &dstat, &dmap);
     if (rc) return rc;
     uint32_t* status = d_status ? d_status : dstat;
     rc = launch_fill_u32(status, STATUS_NONE, 2ull * nseg, stream);
@@ -1766,6 +1781,7 @@ int score_locked(pkv_ctx* ctx, const pkv_profile* prof, int radii, const uint8_t
     LaunchCommon lc;
     lc.segs = dsegs;
     lc.tile_start = dtiles;
+    lc.tile_seg = dmap;
     lc.nseg = nseg;
     lc.status = status;
     lc.radii = static_cast<uint32_t>(radii);

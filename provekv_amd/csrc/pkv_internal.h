@@ -88,6 +88,7 @@ struct FibDev {
 struct LaunchCommon {
     const SegDev* segs;
     const uint32_t* tile_start;   // nseg + 1 prefix of workgroups per segment
+    const uint32_t* tile_seg = nullptr;   // segment of every tile (tile_start[nseg] entries), or null
     uint32_t nseg;
     uint32_t* status;             // 2 * nseg words, or a dummy
     uint32_t radii;               // turbo radii codec

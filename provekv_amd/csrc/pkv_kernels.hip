@@ -75,6 +75,13 @@ __device__ __forceinline__ uint32_t find_segment(const uint32_t* __restrict__ ti
     return lo;
 }
 
+// Segment of workgroup tile blk: one load from the launch's per-tile map when
+// it has one, otherwise a binary search of the tile prefix.
+__device__ __forceinline__ uint32_t segment_of(const uint32_t* __restrict__ tile_seg,
+                                               const uint32_t* __restrict__ tile_start, uint32_t nseg, uint32_t blk) {
+    return tile_seg ? tile_seg[blk] : find_segment(tile_start, nseg, blk);
+}
+
 __device__ __forceinline__ uint64_t vec_elem_offset(const SegDev& s, uint64_t i) {
     return s.elem_offset + (i / s.group) * s.stride_outer + (i % s.group) * s.stride_inner;
 }
@@ -357,7 +364,7 @@ __global__ __launch_bounds__(TILE) void turbo_encode_kernel(
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     float* stage = smem + wave * WAVE_FLOATS;
     const uint32_t blk = blockIdx.x;
-    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const uint32_t sidx = segment_of(lc.tile_seg, lc.tile_start, lc.nseg, blk);
     const SegDev seg = lc.segs[sidx];
     const uint32_t tile = blk - lc.tile_start[sidx];
     const uint32_t v0 = tile * TILE + wave * WAVE;
@@ -918,7 +925,7 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl_kernel(
     const int h = lane >> 5, n = lane & 31;
     // two workgroups per TILE-vector tile, one 32-vector group per wave
     const uint32_t blk = blockIdx.x >> 1;
-    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const uint32_t sidx = segment_of(lc.tile_seg, lc.tile_start, lc.nseg, blk);
     const SegDev seg = lc.segs[sidx];
     const uint32_t tile = blk - lc.tile_start[sidx];
     const uint32_t plen = lc.plen, pwd = plen >> 2;
@@ -1378,7 +1385,7 @@ __global__ __launch_bounds__(TILE) void turbo_encode_qjl128_kernel(
     const int q = lane >> 4, n = lane & 15;
     // four workgroups per TILE-vector tile, one 16-vector group per wave
     const uint32_t blk = blockIdx.x >> 2;
-    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const uint32_t sidx = segment_of(lc.tile_seg, lc.tile_start, lc.nseg, blk);
     const SegDev seg = lc.segs[sidx];
     const uint32_t tile = blk - lc.tile_start[sidx];
     const uint32_t plen = lc.plen, pwd = plen >> 2;
@@ -1681,7 +1688,7 @@ __global__ __launch_bounds__(TILE) void turbo_decode_kernel(
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     float* stage = smem + wave * WAVE_FLOATS;
     const uint32_t blk = blockIdx.x;
-    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const uint32_t sidx = segment_of(lc.tile_seg, lc.tile_start, lc.nseg, blk);
     const SegDev seg = lc.segs[sidx];
     const uint32_t tile = blk - lc.tile_start[sidx];
     const uint32_t v0 = tile * TILE + wave * WAVE;
@@ -1826,7 +1833,7 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split_kernel(
     const uint32_t vb0 = blockIdx.x * per;
     if (vb0 >= nvb) return;
     const uint32_t vb_end = min(nvb, vb0 + per);
-    uint32_t sidx = find_segment(lc.tile_start, lc.nseg, vb0 >> 1);
+    uint32_t sidx = segment_of(lc.tile_seg, lc.tile_start, lc.nseg, vb0 >> 1);
 
     // One half-tile's share of this wave: segment, the two runs, and its
     // header bytes (lanes 0-37); fetch() also starts the payload copies of
@@ -2012,7 +2019,7 @@ __global__ __launch_bounds__(TILE) void turbo_decode_split128_kernel(
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int q = lane >> 4, n = lane & 15;
     const uint32_t blk = blockIdx.x >> 2;
-    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const uint32_t sidx = segment_of(lc.tile_seg, lc.tile_start, lc.nseg, blk);
     const SegDev seg = lc.segs[sidx];
     const uint32_t tile = blk - lc.tile_start[sidx];
     const uint32_t plen = lc.plen, pwd = plen >> 2;
@@ -2213,7 +2220,7 @@ __global__ __launch_bounds__(TILE) void turbo_score_kernel(
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint32_t blk = blockIdx.x;
-    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const uint32_t sidx = segment_of(lc.tile_seg, lc.tile_start, lc.nseg, blk);
     const SegDev seg = lc.segs[sidx];
     const uint32_t tile = blk - lc.tile_start[sidx];
     const uint32_t plen = lc.plen, pwd = plen >> 2;
@@ -2366,7 +2373,7 @@ turbo_score_lut_kernel(
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint32_t blk = blockIdx.x;
-    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const uint32_t sidx = segment_of(lc.tile_seg, lc.tile_start, lc.nseg, blk);
     const SegDev seg = lc.segs[sidx];
     const uint32_t tile = blk - lc.tile_start[sidx];
     const uint32_t plen = lc.plen, pwd = plen >> 2;
@@ -3070,7 +3077,7 @@ template <int DIM, bool DIAG>
 __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void fib_encode_kernel(LaunchCommon lc,
     const void* __restrict__ in, uint8_t* __restrict__ wire, const uint32_t* __restrict__ mf, float thr,
     const double* __restrict__ rot64, const float* __restrict__ cb, uint32_t nunits,
-    const SegDev* __restrict__ segs, const uint32_t* __restrict__ tile_start) {
+    const SegDev* __restrict__ segs, const uint32_t* __restrict__ tile_start, const uint32_t* __restrict__ tile_seg) {
     static_assert(DIM == 64, "the MFMA layout is built for head_dim 64");
     extern __shared__ uint32_t smem_u[];
     uint32_t* rot_lds = smem_u;   // MF_ROT block (MF_SCA words)
@@ -3103,7 +3110,7 @@ __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void 
     // first unit the segment search continues forward from the previous unit's
     // segment (sidx on entry).
     auto next_unit = [&](uint32_t u, uint32_t& sidx, uint32_t& v0) -> uint32_t {
-        if (u < nunits && sidx == 0xFFFFFFFFu) sidx = find_segment(tile_start, lc.nseg, u / FIB_UNITS_PER_TILE);
+        if (u < nunits && sidx == 0xFFFFFFFFu) sidx = segment_of(tile_seg, tile_start, lc.nseg, u / FIB_UNITS_PER_TILE);
         for (; u < nunits; u += stride) {
             const uint32_t tile = u / FIB_UNITS_PER_TILE;
             while (sidx + 1 < lc.nseg && tile_start[sidx + 1] <= tile) ++sidx;
@@ -3205,7 +3212,7 @@ __global__ __launch_bounds__(TILE) void fib_decode_kernel(LaunchCommon lc, const
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint32_t blk = blockIdx.x;
-    const uint32_t sidx = find_segment(lc.tile_start, lc.nseg, blk);
+    const uint32_t sidx = segment_of(lc.tile_seg, lc.tile_start, lc.nseg, blk);
     const SegDev seg = lc.segs[sidx];
     const uint32_t tile = blk - lc.tile_start[sidx];
     const uint32_t v0 = tile * TILE + wave * WAVE;
@@ -3309,7 +3316,8 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
                                                                const float* __restrict__ rot32,
                                                                const float* __restrict__ cb,
                                                                const SegDev* __restrict__ segs,
-                                                               const uint32_t* __restrict__ tile_start) {
+                                                               const uint32_t* __restrict__ tile_start,
+                                                               const uint32_t* __restrict__ tile_seg) {
     static_assert(DIM == 64, "two 32-column MFMA blocks");
     constexpr int BLOCKS = DIM / 4;
     constexpr uint32_t PLEN = 2 + (BLOCKS * 5 + 7) / 8;   // 12
@@ -3342,7 +3350,7 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
     int zoff = 0, lane = threadIdx.x & 63;
     asm volatile("" : "+s"(zoff), "+v"(lane));
     const int h = lane >> 5, n = lane & 31;
-    const uint32_t sidx = find_segment(tile_start, lc.nseg, blk);
+    const uint32_t sidx = segment_of(tile_seg, tile_start, lc.nseg, blk);
     const SegDev seg = segs[sidx];
     const uint32_t tile = blk - tile_start[sidx];
     const uint32_t v0 = tile * TILE + wave * WAVE;
@@ -3811,7 +3819,7 @@ int launch_fib_encode(const LaunchCommon& lc, const FibDev& fd, const void* in, 
     uint32_t grid = persistent_grid(kern, lds, want);
     if (lc.grid_cap) grid = std::min(grid, lc.grid_cap);   // a bounded share of the GPU
     return launch_big_lds(kern, grid, lds, st, lc, in, wire, fd.mf, fd.thr, fd.rot64, fd.codebook,
-                          static_cast<uint32_t>(units), lc.segs, lc.tile_start);
+                          static_cast<uint32_t>(units), lc.segs, lc.tile_start, lc.tile_seg);
 }
 
 int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* wire, void* out, uint32_t nblocks,
@@ -3820,11 +3828,11 @@ int launch_fib_decode(const LaunchCommon& lc, const FibDev& fd, const uint8_t* w
     if (fd.mfma_decode && lc.fanout > 1)
         hipLaunchKernelGGL((fib_decode_mfma_kernel<64, true>), dim3(grid), dim3(TILE), 0,
                            static_cast<hipStream_t>(stream), lc, wire, out, fd.rot32, fd.codebook, lc.segs,
-                           lc.tile_start);
+                           lc.tile_start, lc.tile_seg);
     else if (fd.mfma_decode)
         hipLaunchKernelGGL((fib_decode_mfma_kernel<64, false>), dim3(grid), dim3(TILE), 0,
                            static_cast<hipStream_t>(stream), lc, wire, out, fd.rot32, fd.codebook, lc.segs,
-                           lc.tile_start);
+                           lc.tile_start, lc.tile_seg);
     else
         hipLaunchKernelGGL(fib_decode_kernel<64>, dim3(nblocks), dim3(TILE), 0, static_cast<hipStream_t>(stream), lc,
                            wire, out, fd.rot32t, fd.codebook);
