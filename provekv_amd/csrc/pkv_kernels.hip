@@ -2784,7 +2784,8 @@ __device__ __forceinline__ uint32_t fib_encode_score(const LaunchCommon& lc, con
     const uint32_t x = ra2 >> 22, y = rb2 >> 22;
     const uint32_t iw[3] = {__builtin_amdgcn_alignbit(x, ra, 2), (x >> 2) | (rb << 6), (rb >> 26) | (y << 6)};
     // undecided blocks: bit j of the bit-reversed da / db is block j's (j + 8's) acceptance
-    const uint32_t redo = (~(__builtin_bitreverse32(da) >> 24) & 0xFFu) | ((~(__builtin_bitreverse32(db) >> 24) & 0xFFu) << 8);
+    const uint32_t redo = (~(__builtin_bitreverse32(da) >> 24) & 0xFFu) |
+                          ((~(__builtin_bitreverse32(db) >> 24) & 0xFFu) << 8);
 
     // encode_norm Fp16Paper (codec.rs:994-1020)
     const uint16_t h16 = f32_to_f16(static_cast<float>(nrm));
@@ -3078,6 +3079,11 @@ __global__ __launch_bounds__(TILE) __attribute__((amdgpu_waves_per_eu(3))) void 
     const void* __restrict__ in, uint8_t* __restrict__ wire, const uint32_t* __restrict__ mf, float thr,
     const double* __restrict__ rot64, const float* __restrict__ cb, uint32_t nunits,
     const SegDev* __restrict__ segs, const uint32_t* __restrict__ tile_start, const uint32_t* __restrict__ tile_seg) {
+    // (the segment tables come as restrict arguments, not through lc: the
+    // compiler then reads them with scalar loads, which wait on their own
+    // counter; vector loads share vmcnt with the prefetched rows and the
+    // payload stores, whose in-order count would make each segment read wait
+    // for them)
     static_assert(DIM == 64, "the MFMA layout is built for head_dim 64");
     extern __shared__ uint32_t smem_u[];
     uint32_t* rot_lds = smem_u;   // MF_ROT block (MF_SCA words)
