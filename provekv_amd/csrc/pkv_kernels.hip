@@ -3324,6 +3324,8 @@ __global__ __launch_bounds__(TILE) void fib_decode_mfma_kernel(LaunchCommon lc, 
                                                                const SegDev* __restrict__ segs,
                                                                const uint32_t* __restrict__ tile_start,
                                                                const uint32_t* __restrict__ tile_seg) {
+    // (segment tables as restrict arguments: scalar loads, so a tile's segment
+    // lookup does not wait for the previous tile's stores to drain)
     static_assert(DIM == 64, "two 32-column MFMA blocks");
     constexpr int BLOCKS = DIM / 4;
     constexpr uint32_t PLEN = 2 + (BLOCKS * 5 + 7) / 8;   // 12
